@@ -1,0 +1,274 @@
+"""Torch-tensor wrappers over the C ABI of libtrmoe (include/trmoe.h).
+
+Every function here launches HIP kernels on the current stream of the
+tensors' device and returns freshly allocated outputs (torch's caching
+allocator); inputs are never modified.  There is no fallback: if the library
+is missing or a call fails, an exception is raised.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _native as N
+
+ORDER_TOKEN = N.ORDER_TOKEN
+ORDER_ASSIGNMENT = N.ORDER_ASSIGNMENT
+
+# Padding the packed layouts use (must match the kernel tiles).
+SHARED_GATE_UP_ALIGN = 256   # rows = 2 * round_up(S, 128)
+EXPERT_GATE_UP_ALIGN = 128   # rows = 2 * round_up(W, 64)
+DOWN_ALIGN = 128             # rows = round_up(H, 128)
+
+_DTYPES = {torch.float32: N.F32, torch.bfloat16: N.BF16, torch.float8_e4m3fn: N.FP8_E4M3}
+
+
+def _round_up(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise NotImplementedError(f"TR-MoE HIP kernels do not support {dtype}") from None
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _lib():
+    return N.load()
+
+
+def _require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("TR-MoE HIP ops need tensors on a ROCm device")
+
+
+# ---------------------------------------------------------------------------
+# K1
+# ---------------------------------------------------------------------------
+
+def route_sort(token_ids: torch.Tensor, route_table: torch.Tensor, num_experts: int,
+               order: int = ORDER_TOKEN, return_routes: bool = False):
+    """(sorted int64[kN], inverse int64[kN], offsets int32[E+1], counts int32[E][, routes int64[k,N]])."""
+    lib = _lib()
+    _require_cuda(token_ids, route_table)
+    ids = token_ids.reshape(-1)
+    if ids.dtype != torch.int64:
+        ids = ids.to(torch.int64)
+    ids = ids.contiguous()
+    table = route_table.contiguous()
+    if table.dtype != torch.int64 or table.ndim != 2:
+        raise ValueError("route_table must be int64 [top_k, vocab]")
+    k, vocab = table.shape
+    n = ids.numel()
+    dev = ids.device
+    sorted_idx = torch.empty(k * n, dtype=torch.int64, device=dev)
+    inverse = torch.empty(k * n, dtype=torch.int64, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    routes = torch.empty(k, n, dtype=torch.int64, device=dev) if return_routes else None
+    ws_bytes = lib.trmoe_route_sort_workspace_bytes(n, k, num_experts, order)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
+    st = lib.trmoe_route_sort(_p(ids), n, _p(table), vocab, k, num_experts, order, _p(routes),
+                              _p(sorted_idx), _p(inverse), _p(offsets), _p(counts), _p(ws), ws_bytes,
+                              _stream(ids))
+    N.check(st, "trmoe_route_sort")
+    if return_routes:
+        return sorted_idx, inverse, offsets, counts, routes
+    return sorted_idx, inverse, offsets, counts
+
+
+# ---------------------------------------------------------------------------
+# packing
+# ---------------------------------------------------------------------------
+
+def pack_dims(kind: int, out_features: int, in_features: int, row_align: int) -> Tuple[int, int]:
+    lib = _lib()
+    rows, cols = ctypes.c_int64(), ctypes.c_int64()
+    N.check(lib.trmoe_pack_dims(kind, out_features, in_features, row_align, ctypes.byref(rows),
+                                ctypes.byref(cols)), "trmoe_pack_dims")
+    return rows.value, cols.value
+
+
+def _pack(kind: int, a: torch.Tensor, b: Optional[torch.Tensor], groups: int, out_f: int, in_f: int,
+          strides: Tuple[int, int, int], row_align: int, scale_a=None, scale_b=None):
+    """Scales are [groups, out_f] (or [out_f] for one group); made contiguous here."""
+    lib = _lib()
+    _require_cuda(a, b)
+    rows, cols = pack_dims(kind, out_f, in_f, row_align)
+    dst = torch.empty(groups, rows, cols, dtype=a.dtype, device=a.device)
+    dst_scale = None
+    scale_stride = 0
+    if scale_a is not None:
+        dst_scale = torch.empty(groups, rows, dtype=torch.float32, device=a.device)
+        scale_a = scale_a.float().contiguous().reshape(groups, out_f)
+        scale_b = scale_b.float().contiguous().reshape(groups, out_f) if scale_b is not None else None
+        scale_stride = out_f
+    st = lib.trmoe_pack_weight(kind, dtype_code(a.dtype), _p(a), _p(b), groups, out_f, in_f,
+                               strides[0], strides[1], strides[2], _p(scale_a), _p(scale_b),
+                               scale_stride, row_align, _p(dst), _p(dst_scale), _stream(a))
+    N.check(st, "trmoe_pack_weight")
+    return dst, dst_scale
+
+
+def pack_linear_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor, scale_gate=None, scale_up=None):
+    """nn.Linear weights [S, H] (gate, up) -> packed [2*round_up(S,128), round_up(H,8)]."""
+    S, H = w_gate.shape
+    if w_up.shape != w_gate.shape or w_up.stride() != w_gate.stride():
+        raise ValueError("gate and up weights must have the same shape and strides")
+    dst, sc = _pack(N.PACK_GATE_UP, w_gate, w_up, 1, S, H, (0, w_gate.stride(0), w_gate.stride(1)),
+                    SHARED_GATE_UP_ALIGN, scale_gate, scale_up)
+    return dst[0], (sc[0] if sc is not None else None)
+
+
+def pack_linear_down(w_down: torch.Tensor, scale=None):
+    """nn.Linear weight [H, S] -> packed [round_up(H,128), round_up(S,8)]."""
+    H, S = w_down.shape
+    dst, sc = _pack(N.PACK_PLAIN, w_down, None, 1, H, S, (0, w_down.stride(0), w_down.stride(1)),
+                    DOWN_ALIGN, scale, None)
+    return dst[0], (sc[0] if sc is not None else None)
+
+
+def pack_expert_gate_up(gate: torch.Tensor, up: torch.Tensor, scale_gate=None, scale_up=None):
+    """Expert tensors [E, H, W] (any strides, e.g. an active-capacity slice)
+    -> packed [E, 2*round_up(W,64), round_up(H,8)]; scales [E, W] (stride given)."""
+    E, H, W = gate.shape
+    if up.shape != gate.shape or up.stride() != gate.stride():
+        raise ValueError("gate and up expert weights must have the same shape and strides")
+    return _pack(N.PACK_GATE_UP, gate, up, E, W, H, (gate.stride(0), gate.stride(2), gate.stride(1)),
+                 EXPERT_GATE_UP_ALIGN, scale_gate, scale_up)
+
+
+def pack_expert_down(down: torch.Tensor, scale=None):
+    """Expert down [E, W, H] -> packed [E, round_up(H,128), round_up(W,8)]; scale [E, H]."""
+    E, W, H = down.shape
+    return _pack(N.PACK_PLAIN, down, None, E, H, W, (down.stride(0), down.stride(2), down.stride(1)),
+                 DOWN_ALIGN, scale, None)
+
+
+# ---------------------------------------------------------------------------
+# compute
+# ---------------------------------------------------------------------------
+
+def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[torch.Tensor],
+                   shared_width: int) -> torch.Tensor:
+    """h[N, round_up(S,128)] = silu(x Wg^T) * (x Wu^T)."""
+    lib = _lib()
+    _require_cuda(x, w_packed)
+    n, hidden = x.shape
+    ldh = _round_up(shared_width, 128)
+    h = torch.empty(n, ldh, dtype=x.dtype, device=x.device)
+    st = lib.trmoe_shared_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
+                                  x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(h), ldh,
+                                  _stream(x))
+    N.check(st, "trmoe_shared_gate_up")
+    return h
+
+
+def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Tensor, num_experts: int,
+                   top_k: int, w_gate_up: torch.Tensor, s_gate_up, w_down: torch.Tensor, s_down,
+                   expert_width: int) -> torch.Tensor:
+    """y[k*N, H] in partition order."""
+    lib = _lib()
+    _require_cuda(x, sorted_idx, offsets, w_gate_up, w_down)
+    n, hidden = x.shape
+    y = torch.empty(top_k * n, hidden, dtype=x.dtype, device=x.device)
+    st = lib.trmoe_routed_experts(dtype_code(x.dtype), dtype_code(w_gate_up.dtype), _p(x), n, hidden,
+                                  x.stride(0), _p(sorted_idx), _p(offsets), num_experts, top_k,
+                                  _p(w_gate_up), _p(s_gate_up), _p(w_down), _p(s_down), expert_width,
+                                  _p(y), hidden, _stream(x))
+    N.check(st, "trmoe_routed_experts")
+    return y
+
+
+def _weights_arg(route_weights: Sequence[float]):
+    arr = (ctypes.c_float * 4)(*[float(w) for w in list(route_weights)[:4]])
+    return arr
+
+
+def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor, w_scale, hidden: int,
+                        y: Optional[torch.Tensor], inverse: Optional[torch.Tensor], top_k: int,
+                        route_weights: Sequence[float], shared_scale: float, routed_scale: float,
+                        residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    lib = _lib()
+    _require_cuda(h, w_down, y, inverse, residual)
+    n = h.shape[0]
+    out = torch.empty(n, hidden, dtype=h.dtype, device=h.device)
+    rw = _weights_arg(route_weights)
+    st = lib.trmoe_shared_down_combine(
+        dtype_code(h.dtype), dtype_code(w_down.dtype), _p(h), n, shared_width, h.stride(0), _p(w_down),
+        _p(w_scale), hidden, _p(y), hidden, _p(inverse), top_k, ctypes.cast(rw, ctypes.c_void_p),
+        float(shared_scale), float(routed_scale), _p(residual),
+        residual.stride(0) if residual is not None else 0, _p(out), hidden, _stream(h))
+    N.check(st, "trmoe_shared_down_combine")
+    return out
+
+
+def combine(y: torch.Tensor, inverse: torch.Tensor, n_tokens: int, top_k: int,
+            route_weights: Sequence[float], routed_scale: float,
+            residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    lib = _lib()
+    _require_cuda(y, inverse, residual)
+    hidden = y.shape[1]
+    out = torch.empty(n_tokens, hidden, dtype=y.dtype, device=y.device)
+    rw = _weights_arg(route_weights)
+    st = lib.trmoe_combine(dtype_code(y.dtype), n_tokens, hidden, _p(y), hidden, _p(inverse), top_k,
+                           ctypes.cast(rw, ctypes.c_void_p), float(routed_scale), _p(residual),
+                           residual.stride(0) if residual is not None else 0, _p(out), hidden, _stream(y))
+    N.check(st, "trmoe_combine")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# whole layer
+# ---------------------------------------------------------------------------
+
+@dataclass
+class PackedLayer:
+    """Weights of one layer in kernel layout (built by TRHashEngine)."""
+
+    act_dtype: torch.dtype
+    expert_gate_up: torch.Tensor
+    expert_gate_up_scale: Optional[torch.Tensor]
+    expert_down: torch.Tensor
+    expert_down_scale: Optional[torch.Tensor]
+    num_experts: int
+    expert_width: int
+    shared_width: int = 0
+    shared_gate_up: Optional[torch.Tensor] = None
+    shared_gate_up_scale: Optional[torch.Tensor] = None
+    shared_down: Optional[torch.Tensor] = None
+    shared_down_scale: Optional[torch.Tensor] = None
+
+
+def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
+                  route_weights: Sequence[float], shared_scale: float, routed_scale: float,
+                  order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual) -- K1..K4."""
+    n, hidden = x.shape
+    top_k = route_table.shape[0]
+    if n == 0:
+        return torch.empty(0, hidden, dtype=x.dtype, device=x.device)
+    sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, packed.num_experts, order)
+    y = routed_experts(x, sorted_idx, offsets, packed.num_experts, top_k, packed.expert_gate_up,
+                       packed.expert_gate_up_scale, packed.expert_down, packed.expert_down_scale,
+                       packed.expert_width)
+    if packed.shared_width > 0:
+        h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width)
+        return shared_down_combine(h, packed.shared_width, packed.shared_down, packed.shared_down_scale,
+                                   hidden, y, inverse, top_k, route_weights, shared_scale, routed_scale,
+                                   residual)
+    return combine(y, inverse, n, top_k, route_weights, routed_scale, residual)

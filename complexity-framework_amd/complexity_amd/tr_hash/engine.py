@@ -1,0 +1,554 @@
+"""TR-Hash SwiGLU engine with a native HIP backend (mirror of complexity/tr_hash/engine.py).
+
+Module surface kept identical to the reference (engine.py:107-716): the
+``route_table`` / ``fused_route_codes`` / ``fused_expert_pairs`` buffers,
+``expert_{gate,up,down}`` parameters, ``shared_{gate,up,down}`` linears,
+``set_active_capacity``, ``load_route_table``, ``capability_summary`` (same
+21 keys), ``last_backend`` and the graph-bucket path, so state dicts and call
+sites move over unchanged.
+
+Backends:
+
+* ``PYTORCH`` -- the universal definition (engine.py:66-104, 333-349, 578),
+  used for CPU tensors and for differentiable forwards;
+* ``HIP`` -- the gfx950 kernels of ``libtrmoe`` (route partition, shared
+  SwiGLU GEMM, grouped routed experts, down GEMM with the un-permute and
+  combine in its epilogue), forward-only;
+* ``CUDA_GRAPH`` -- HIP (or PYTORCH) captured per static bucket.
+
+``precision=fp8`` keeps e4m3 copies of every weight with per-output-channel
+scales (``*_fp8`` / ``*_scale`` buffers, saved in the state dict); both
+backends then compute with the dequantised values q * scale.
+"""
+
+from __future__ import annotations
+
+import logging
+from dataclasses import replace
+from typing import Callable, Dict, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import ops
+from .buckets import GraphBucketPlanner
+from .capabilities import (
+    PARTITION_ASSIGNMENT,
+    BackendDecision,
+    select_backend,
+    supports_fused_cuda,
+)
+from .config import SUPPORTED_EXPERT_COUNTS, GraphBucket, TRHashBackend, TRHashEngineConfig, TRHashPhase, TRHashPrecision
+from .routing import build_route_table, compile_top2_pair_metadata
+
+logger = logging.getLogger(__name__)
+
+E4M3_MAX = 448.0
+_FP8_WEIGHTS = ("expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up", "shared_down")
+
+
+def _silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    return F.silu(gate) * up
+
+
+def reference_topk_swiglu(
+    flat_x: torch.Tensor,
+    routes: torch.Tensor,
+    gate_weights: torch.Tensor,
+    up_weights: torch.Tensor,
+    down_weights: torch.Tensor,
+    route_weights: torch.Tensor,
+    *,
+    activation: Callable[[torch.Tensor, torch.Tensor], torch.Tensor] = _silu_mul,
+    intermediate_transform: Optional[Callable[[torch.Tensor, int], torch.Tensor]] = None,
+) -> torch.Tensor:
+    """Universal routed formula: masked dense loop over experts (engine.py:66-104).
+
+    For each expert e the tokens routed to it (token weight tw = sum of the
+    route weights of the slots that selected e) run the expert SwiGLU; the
+    result scaled by tw is accumulated in expert order in ``flat_x.dtype``.
+    """
+    if flat_x.ndim != 2:
+        raise ValueError("flat_x must be [tokens, hidden]")
+    if routes.ndim != 2 or routes.size(1) != flat_x.size(0):
+        raise ValueError("routes must be [top_k, tokens]")
+    if route_weights.shape != routes.shape:
+        raise ValueError("route_weights must match routes")
+    if gate_weights.shape != up_weights.shape:
+        raise ValueError("gate and up expert weights must have the same shape")
+    if gate_weights.ndim != 3 or down_weights.ndim != 3:
+        raise ValueError("expert weights must be rank-3 tensors")
+    if gate_weights.size(0) != down_weights.size(0):
+        raise ValueError("expert weight tensors must have the same expert count")
+    total = torch.zeros_like(flat_x)
+    for e in range(gate_weights.size(0)):
+        tw = (routes.eq(e).to(flat_x.dtype) * route_weights).sum(dim=0)
+        xe = flat_x * tw.ne(0).to(flat_x.dtype).unsqueeze(-1)
+        inner = activation(xe @ gate_weights[e], xe @ up_weights[e])
+        if intermediate_transform is not None:
+            inner = intermediate_transform(inner, e)
+        total = total + (inner @ down_weights[e]).to(total.dtype) * tw.unsqueeze(-1)
+    return total
+
+
+def _quantize_e4m3(weight: torch.Tensor):
+    """Per-output-channel e4m3: scale = amax/448 over dim 1 (the reduction axis)."""
+    w = weight.detach().float()
+    amax = w.abs().amax(dim=1, keepdim=True)
+    scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+    q = (w / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return q, scale.squeeze(1).contiguous()
+
+
+class TRHashEngine(nn.Module):
+    """Shared SwiGLU plus deterministic top-k token-ID experts."""
+
+    def __init__(self, config: TRHashEngineConfig):
+        super().__init__()
+        self.config = config
+        self.register_buffer("route_table", build_route_table(config))
+        self.register_buffer(
+            "_route_weights", torch.tensor(config.route_weights, dtype=torch.float32), persistent=False
+        )
+        codes, pairs = self._compile_fused_metadata(self.route_table)
+        self.register_buffer("fused_route_codes", codes)
+        self.register_buffer("fused_expert_pairs", pairs)
+
+        E, H, W = config.num_experts, config.hidden_size, config.expert_width
+        self.expert_gate = nn.Parameter(torch.empty(E, H, W))
+        self.expert_up = nn.Parameter(torch.empty(E, H, W))
+        self.expert_down = nn.Parameter(torch.empty(E, W, H))
+        if config.shared_width:
+            self.shared_gate = nn.Linear(H, config.shared_width, bias=False)
+            self.shared_up = nn.Linear(H, config.shared_width, bias=False)
+            self.shared_down = nn.Linear(config.shared_width, H, bias=False)
+        else:
+            self.shared_gate = None
+            self.shared_up = None
+            self.shared_down = None
+        self.reset_parameters()
+
+        self.last_backend: Optional[BackendDecision] = None
+        self._graph_pool: Dict[GraphBucket, "_CapturedTRHashGraph"] = {}
+        self._bucket_planner = GraphBucketPlanner(config.graph_buckets) if config.graph_buckets else None
+        self._active_num_experts = config.num_experts
+        self._active_expert_width = config.expert_width
+        self._active_route_table = self.route_table
+        self._fused_shared_gate_up_weight: Optional[torch.Tensor] = None
+        self._packed_key = None
+        self._packed: Optional[ops.PackedLayer] = None
+        self._fp8 = False
+        if config.precision is TRHashPrecision.FP8:
+            self.quantize_fp8_()
+
+    # ------------------------------------------------------------------ plumbing
+    def _apply(self, fn, recurse: bool = True):
+        # _active_route_table is a plain attribute (an alias of route_table or
+        # a rebuilt reduced table), so move it with the module explicitly.
+        aliased = self._active_route_table is self.route_table
+        super()._apply(fn, recurse=recurse)
+        self._active_route_table = self.route_table if aliased else fn(self._active_route_table)
+        if self._fused_shared_gate_up_weight is not None:
+            self._fused_shared_gate_up_weight = fn(self._fused_shared_gate_up_weight)
+        self._packed_key = None
+        self._packed = None
+        return self
+
+    @property
+    def active_num_experts(self) -> int:
+        return self._active_num_experts
+
+    @property
+    def active_expert_width(self) -> int:
+        return self._active_expert_width
+
+    def set_active_capacity(self, *, num_experts: Optional[int] = None, expert_width: Optional[int] = None) -> None:
+        """Use a prefix sub-network (engine.py:214-261); routing is rebuilt for it."""
+        if num_experts is not None:
+            if num_experts not in SUPPORTED_EXPERT_COUNTS:
+                raise ValueError(f"num_experts must be one of {SUPPORTED_EXPERT_COUNTS}, got {num_experts}")
+            if num_experts > self.config.num_experts:
+                raise ValueError(
+                    f"active num_experts ({num_experts}) cannot exceed the allocated capacity "
+                    f"({self.config.num_experts})"
+                )
+            if num_experts == self.config.num_experts:
+                self._active_route_table = self.route_table
+            else:
+                reduced = replace(self.config, num_experts=num_experts)
+                self._active_route_table = build_route_table(reduced).to(device=self.route_table.device)
+            self._active_num_experts = num_experts
+        if expert_width is not None:
+            if not 0 < expert_width <= self.config.expert_width:
+                raise ValueError(
+                    f"active expert_width must be in (0, {self.config.expert_width}], got {expert_width}"
+                )
+            self._active_expert_width = expert_width
+        if num_experts is not None or expert_width is not None:
+            self._graph_pool.clear()
+            self._packed_key = None
+            self._packed = None
+
+    def _compile_fused_metadata(self, route_table: torch.Tensor):
+        if supports_fused_cuda(self.config):
+            return compile_top2_pair_metadata(route_table, num_experts=self.config.num_experts)
+        return torch.empty(0, dtype=torch.uint8), torch.empty((0, 2), dtype=torch.int32)
+
+    def load_route_table(self, route_table: torch.Tensor) -> None:
+        """Install an external [top_k, vocab] table (engine.py:276-306)."""
+        if tuple(route_table.shape) != tuple(self.route_table.shape):
+            raise ValueError(
+                f"route_table shape {tuple(route_table.shape)} does not match "
+                f"the engine's {tuple(self.route_table.shape)} ([top_k, vocab_size])"
+            )
+        if int(route_table.min()) < 0 or int(route_table.max()) >= self.config.num_experts:
+            raise ValueError("route_table contains an out-of-range expert index")
+        self.route_table.copy_(route_table.to(device=self.route_table.device))
+        codes, pairs = self._compile_fused_metadata(self.route_table)
+        self.fused_route_codes = codes.to(device=self.fused_route_codes.device)
+        self.fused_expert_pairs = pairs.to(device=self.fused_expert_pairs.device)
+        if self._active_num_experts == self.config.num_experts:
+            self._active_route_table = self.route_table
+        else:
+            reduced = replace(self.config, num_experts=self._active_num_experts)
+            self._active_route_table = build_route_table(reduced).to(device=self.route_table.device)
+        self._graph_pool.clear()
+
+    def reset_parameters(self) -> None:
+        std = self.config.initializer_range
+        for p in (self.expert_gate, self.expert_up, self.expert_down):
+            nn.init.normal_(p, mean=0.0, std=std)
+        for m in (self.shared_gate, self.shared_up, self.shared_down):
+            if m is not None:
+                nn.init.normal_(m.weight, mean=0.0, std=std)
+
+    # ------------------------------------------------------------------ fp8
+    def _master(self, name: str) -> Optional[torch.Tensor]:
+        if name.startswith("shared_"):
+            mod = getattr(self, name)
+            return None if mod is None else mod.weight
+        return getattr(self, name)
+
+    def quantize_fp8_(self) -> None:
+        """(Re)build the e4m3 weight copies and per-output-channel scales from
+        the current parameters; forwards then use q * scale."""
+        for name in _FP8_WEIGHTS:
+            w = self._master(name)
+            if w is None:
+                continue
+            q, s = _quantize_e4m3(w)
+            for suffix, t in (("_fp8", q), ("_scale", s)):
+                key = name + suffix
+                if key in self._buffers:
+                    self._buffers[key] = t.to(device=w.device)
+                else:
+                    self.register_buffer(key, t.to(device=w.device))
+        self._fp8 = True
+        self._packed_key = None
+        self._packed = None
+
+    def _dequantized(self, name: str, dtype: torch.dtype) -> torch.Tensor:
+        q = getattr(self, name + "_fp8")
+        s = getattr(self, name + "_scale")
+        return (q.float() * s.unsqueeze(1)).to(dtype)
+
+    # ------------------------------------------------------------------ pytorch backend
+    def _routes(self, token_ids: torch.Tensor) -> torch.Tensor:
+        clamped = token_ids.clamp(0, self.config.vocab_size - 1)
+        return self._active_route_table[:, clamped]
+
+    def _expert_tensors(self, dtype: Optional[torch.dtype] = None):
+        if self._fp8:
+            dt = dtype or torch.bfloat16
+            return tuple(self._dequantized(n, dt) for n in ("expert_gate", "expert_up", "expert_down"))
+        return self.expert_gate, self.expert_up, self.expert_down
+
+    def _active_expert_weights(self, dtype: Optional[torch.dtype] = None):
+        """(gate, up, down) truncated to the active capacity (engine.py:320-331)."""
+        gate, up, down = self._expert_tensors(dtype)
+        E, W = self._active_num_experts, self._active_expert_width
+        if E == self.config.num_experts and W == self.config.expert_width:
+            return gate, up, down
+        return (
+            gate[:E, :, :W].contiguous(),
+            up[:E, :, :W].contiguous(),
+            down[:E, :W, :].contiguous(),
+        )
+
+    def _shared(self, flat_x: torch.Tensor) -> torch.Tensor:
+        if self.shared_gate is None:
+            return torch.zeros_like(flat_x)
+        if self._fp8:
+            dt = flat_x.dtype
+            g = F.linear(flat_x, self._dequantized("shared_gate", dt))
+            u = F.linear(flat_x, self._dequantized("shared_up", dt))
+            return F.linear(_silu_mul(g, u), self._dequantized("shared_down", dt))
+        fused = self._fused_shared_gate_up_weight
+        gate_lora = getattr(self.shared_gate, "is_lora_adapter", False)
+        up_lora = getattr(self.shared_up, "is_lora_adapter", False)
+        if fused is not None and gate_lora and up_lora:
+            width = int(self.shared_gate.base.out_features)
+            base_g, base_u = F.linear(flat_x, fused).split([width, width], dim=-1)
+            gate = base_g + self.shared_gate.lora_residual(flat_x)
+            up = base_u + self.shared_up.lora_residual(flat_x)
+        else:
+            gate = self.shared_gate(flat_x)
+            up = self.shared_up(flat_x)
+        return self.shared_down(_silu_mul(gate, up))
+
+    def refresh_fused_shared_lora_weight(self) -> bool:
+        gate_lora = getattr(self.shared_gate, "is_lora_adapter", False)
+        up_lora = getattr(self.shared_up, "is_lora_adapter", False)
+        if not (gate_lora and up_lora):
+            self._fused_shared_gate_up_weight = None
+            return False
+        self._fused_shared_gate_up_weight = torch.cat(
+            [self.shared_gate.base.weight, self.shared_up.base.weight], dim=0
+        ).detach()
+        return True
+
+    def _reference_routed(self, flat_x: torch.Tensor, routes: torch.Tensor) -> torch.Tensor:
+        rw = self._route_weights.to(dtype=flat_x.dtype)[:, None].expand_as(routes)
+        gate, up, down = self._active_expert_weights(flat_x.dtype)
+        return reference_topk_swiglu(flat_x, routes, gate, up, down, rw)
+
+    # ------------------------------------------------------------------ hip backend
+    def _hip_act_dtype(self) -> torch.dtype:
+        if self._fp8:
+            return torch.bfloat16
+        dt = self.expert_gate.dtype
+        if dt not in (torch.float32, torch.bfloat16):
+            raise NotImplementedError(f"HIP kernels support float32/bfloat16/fp8 weights, got {dt}")
+        return dt
+
+    def _hip_sources(self):
+        if self._fp8:
+            names = [n for n in _FP8_WEIGHTS if hasattr(self, n + "_fp8")]
+            return [getattr(self, n + suffix) for n in names for suffix in ("_fp8", "_scale")]
+        srcs = [self.expert_gate, self.expert_up, self.expert_down]
+        if self.shared_gate is not None:
+            srcs += [self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight]
+        return srcs
+
+    def _hip_packed(self) -> ops.PackedLayer:
+        """Weights in kernel layout, rebuilt when a source tensor or the active
+        capacity changes (keyed on storage pointer and in-place version)."""
+        srcs = self._hip_sources()
+        key = (
+            tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in srcs),
+            self._active_num_experts,
+            self._active_expert_width,
+        )
+        if self._packed is not None and self._packed_key == key:
+            return self._packed
+        E, W = self._active_num_experts, self._active_expert_width
+        with torch.no_grad():
+            if self._fp8:
+                gq, gs = self.expert_gate_fp8[:E, :, :W], self.expert_gate_scale[:E, :W]
+                uq, us = self.expert_up_fp8[:E, :, :W], self.expert_up_scale[:E, :W]
+                dq, ds = self.expert_down_fp8[:E, :W, :], self.expert_down_scale[:E]
+                egu, egu_s = ops.pack_expert_gate_up(gq, uq, gs, us)
+                ed, ed_s = ops.pack_expert_down(dq, ds)
+            else:
+                egu, egu_s = ops.pack_expert_gate_up(self.expert_gate[:E, :, :W], self.expert_up[:E, :, :W])
+                ed, ed_s = ops.pack_expert_down(self.expert_down[:E, :W, :])
+            packed = ops.PackedLayer(
+                act_dtype=self._hip_act_dtype(),
+                expert_gate_up=egu,
+                expert_gate_up_scale=egu_s,
+                expert_down=ed,
+                expert_down_scale=ed_s,
+                num_experts=E,
+                expert_width=W,
+            )
+            if self.shared_gate is not None:
+                packed.shared_width = self.config.shared_width
+                if self._fp8:
+                    sgu, sgu_s = ops.pack_linear_gate_up(
+                        self.shared_gate_fp8, self.shared_up_fp8, self.shared_gate_scale, self.shared_up_scale
+                    )
+                    sd, sd_s = ops.pack_linear_down(self.shared_down_fp8, self.shared_down_scale)
+                else:
+                    sgu, sgu_s = ops.pack_linear_gate_up(self.shared_gate.weight, self.shared_up.weight)
+                    sd, sd_s = ops.pack_linear_down(self.shared_down.weight)
+                packed.shared_gate_up, packed.shared_gate_up_scale = sgu, sgu_s
+                packed.shared_down, packed.shared_down_scale = sd, sd_s
+        self._packed, self._packed_key = packed, key
+        return packed
+
+    def _hip_forward(self, flat_x: torch.Tensor, flat_ids: torch.Tensor, decision: BackendDecision,
+                     residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        packed = self._hip_packed()
+        x = flat_x if flat_x.dtype == packed.act_dtype else flat_x.to(packed.act_dtype)
+        x = x.contiguous()
+        order = ops.ORDER_ASSIGNMENT if decision.partition == PARTITION_ASSIGNMENT else ops.ORDER_TOKEN
+        res = None
+        if residual is not None:
+            res = residual.reshape(-1, residual.size(-1))
+            res = (res if res.dtype == packed.act_dtype else res.to(packed.act_dtype)).contiguous()
+        out = ops.layer_forward(
+            x,
+            flat_ids,
+            self._active_route_table,
+            packed,
+            self.config.route_weights,
+            self.config.shared_output_scale,
+            self.config.routed_output_scale,
+            order=order,
+            residual=res,
+        )
+        return out if out.dtype == flat_x.dtype else out.to(flat_x.dtype)
+
+    # ------------------------------------------------------------------ forward
+    def _forward_eager(self, hidden_states: torch.Tensor, token_ids: torch.Tensor, backend,
+                       decision: Optional[BackendDecision] = None) -> torch.Tensor:
+        if hidden_states.ndim != 3:
+            raise ValueError("hidden_states must be [batch, sequence, hidden]")
+        if token_ids.shape != hidden_states.shape[:2]:
+            raise ValueError("token_ids must match hidden batch/sequence dimensions")
+        if hidden_states.size(-1) != self.config.hidden_size:
+            raise ValueError(f"expected hidden size {self.config.hidden_size}, got {hidden_states.size(-1)}")
+        batch, sequence, hidden = hidden_states.shape
+        reduced = (
+            self._active_num_experts != self.config.num_experts
+            or self._active_expert_width != self.config.expert_width
+        )
+        if reduced and backend is TRHashBackend.FUSED_CUDA:
+            raise RuntimeError(
+                "FUSED_CUDA requires the full allocated capacity: its precompiled pair metadata is tied to "
+                "config.num_experts. Use TRHashBackend.PYTORCH or CGGR while active capacity is reduced "
+                f"(active={self._active_num_experts}/{self.config.num_experts} experts, "
+                f"{self._active_expert_width}/{self.config.expert_width} width)."
+            )
+        flat_x = hidden_states.reshape(-1, hidden)
+        if backend is TRHashBackend.HIP:
+            if decision is None:
+                decision = BackendDecision(TRHashBackend.HIP, TRHashBackend.HIP, (), False, self._fp8)
+            out = self._hip_forward(flat_x, token_ids.reshape(-1), decision)
+            return out.view(batch, sequence, hidden)
+        if backend in (TRHashBackend.FUSED_CUDA, TRHashBackend.CGGR):
+            raise RuntimeError(f"{backend.value} Triton kernels are not part of this build")
+        shared = self._shared(flat_x)
+        routes = self._routes(token_ids).reshape(self.config.top_k, -1)
+        routed = self._reference_routed(flat_x, routes)
+        out = self.config.shared_output_scale * shared + self.config.routed_output_scale * routed
+        return out.view(batch, sequence, hidden)
+
+    def _needs_autograd(self, hidden_states: torch.Tensor) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        return hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())
+
+    def _decide(self, hidden_states: torch.Tensor) -> BackendDecision:
+        return select_backend(
+            self.config,
+            device_type=hidden_states.device.type,
+            autograd=self._needs_autograd(hidden_states),
+        )
+
+    def forward(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
+        decision = self._decide(hidden_states)
+        self.last_backend = decision
+        if decision.selected is TRHashBackend.CUDA_GRAPH:
+            return self._forward_cuda_graph(hidden_states, token_ids)
+        return self._forward_eager(hidden_states, token_ids, decision.selected, decision)
+
+    def forward_with_residual(self, hidden_states: torch.Tensor, token_ids: torch.Tensor,
+                              residual: torch.Tensor) -> torch.Tensor:
+        """``residual + forward(hidden_states, token_ids)``; on the HIP backend
+        the add runs in the down-projection epilogue (block.py:270-278)."""
+        decision = self._decide(hidden_states)
+        self.last_backend = decision
+        if decision.selected is TRHashBackend.HIP and hidden_states.ndim == 3:
+            b, t, h = hidden_states.shape
+            if token_ids.shape != hidden_states.shape[:2]:
+                raise ValueError("token_ids must match hidden batch/sequence dimensions")
+            out = self._hip_forward(hidden_states.reshape(-1, h), token_ids.reshape(-1), decision, residual)
+            return out.view(b, t, h)
+        return residual + self.forward(hidden_states, token_ids)
+
+    def _forward_cuda_graph(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
+        if self.training or torch.is_grad_enabled():
+            raise RuntimeError("CUDA Graph TR-Hash requires eval mode and torch.no_grad()")
+        if hidden_states.device.type != "cuda":
+            raise RuntimeError("CUDA Graph TR-Hash requires CUDA tensors")
+        if self._bucket_planner is None:
+            raise RuntimeError("CUDA Graph backend has no configured buckets")
+        batch, sequence, _ = hidden_states.shape
+        bucket = self._bucket_planner.select(batch, sequence)
+        runner = self._graph_pool.get(bucket)
+        if runner is None:
+            runner = _CapturedTRHashGraph(self, bucket, hidden_states)
+            self._graph_pool[bucket] = runner
+        return runner.replay(hidden_states, token_ids)
+
+    def capability_summary(self, device_type: str = "cpu") -> dict:
+        """Stable, serializable metadata (engine.py:616-655; same 21 keys)."""
+        decision = select_backend(self.config, device_type=device_type)
+        return {
+            "experts": self.config.num_experts,
+            "top_k": self.config.top_k,
+            "shared_width": self.config.shared_width,
+            "expert_width": self.config.expert_width,
+            "stored_width": self.config.stored_mlp_width,
+            "active_width": self.config.active_mlp_width,
+            "active_width_fraction": self.config.active_width_fraction,
+            "active_num_experts": self._active_num_experts,
+            "active_expert_width": self._active_expert_width,
+            "is_reduced_capacity": (
+                self._active_num_experts != self.config.num_experts
+                or self._active_expert_width != self.config.expert_width
+            ),
+            "attention": self.config.attention_backbone.value,
+            "routing": self.config.routing_strategy.value,
+            "phase": self.config.phase.value,
+            "precision": self.config.precision.value,
+            "world_size": self.config.world_size,
+            "parallelism": "replicated_ddp" if self.config.world_size > 1 else "single_device",
+            "requested_backend": decision.requested.value,
+            "selected_backend": decision.selected.value,
+            "backend_reasons": list(decision.reasons),
+            "fused_cuda_eligible": supports_fused_cuda(self.config),
+            "cuda_graph_buckets": [[b.batch_size, b.sequence_length] for b in self.config.graph_buckets],
+        }
+
+
+class _CapturedTRHashGraph:
+    """One lazily captured static-shape inference graph (engine.py:658-716).
+
+    The captured body is the HIP backend when the library is available (the
+    kernels record no memset nodes and allocate nothing outside torch's graph
+    pool), else the PYTORCH definition.
+    """
+
+    def __init__(self, engine: TRHashEngine, bucket: GraphBucket, sample: torch.Tensor):
+        if engine.config.phase is not TRHashPhase.INFERENCE:
+            raise RuntimeError("only inference graphs can be captured")
+        from .. import _native
+
+        self.engine = engine
+        self.bucket = bucket
+        self.inner = TRHashBackend.HIP if _native.available() else TRHashBackend.PYTORCH
+        shape = (bucket.batch_size, bucket.sequence_length, engine.config.hidden_size)
+        self.hidden = torch.zeros(shape, dtype=sample.dtype, device=sample.device)
+        self.token_ids = torch.zeros(bucket.batch_size, bucket.sequence_length, dtype=torch.long,
+                                     device=sample.device)
+        self.graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                self.output = engine._forward_eager(self.hidden, self.token_ids, self.inner)
+        stream.synchronize()
+        with torch.cuda.graph(self.graph):
+            self.output = engine._forward_eager(self.hidden, self.token_ids, self.inner)
+
+    def replay(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
+        batch, sequence, _ = hidden_states.shape
+        self.hidden.zero_()
+        self.token_ids.zero_()
+        self.hidden[:batch, :sequence].copy_(hidden_states)
+        self.token_ids[:batch, :sequence].copy_(token_ids)
+        self.graph.replay()
+        return self.output[:batch, :sequence].clone()

@@ -1,0 +1,298 @@
+// extern "C" entry points of libtrmoe: argument validation on the host, then
+// one launch (or two for the multi-block partition) on the caller's stream.
+// Every shape a kernel's grid and indexing assume is checked here first.
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "trmoe_common.h"
+#include "trmoe_gemm.h"
+#include "trmoe_internal.h"
+
+namespace trmoe {
+
+static thread_local std::string g_last_error;
+
+int set_error(int status, const char* msg) {
+    g_last_error = msg ? msg : "";
+    return status;
+}
+
+int check_launch(const char* what) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        std::string m = std::string(what) + ": " + hipGetErrorString(err);
+        return set_error(TRMOE_ERR_HIP, m.c_str());
+    }
+    return TRMOE_OK;
+}
+
+static inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int elem_bytes(int dtype) {
+    switch (dtype) {
+        case TRMOE_F32: return 4;
+        case TRMOE_BF16: return 2;
+        case TRMOE_FP8_E4M3: return 1;
+        default: return 0;
+    }
+}
+
+static bool valid_pair(int act, int wdt) {
+    return (act == TRMOE_F32 && wdt == TRMOE_F32) || (act == TRMOE_BF16 && wdt == TRMOE_BF16) ||
+           (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3);
+}
+
+#define TRMOE_REQUIRE(cond, msg)                                  \
+    do {                                                          \
+        if (!(cond)) return set_error(TRMOE_ERR_INVALID, (msg));  \
+    } while (0)
+
+}  // namespace trmoe
+
+using namespace trmoe;
+
+extern "C" {
+
+int trmoe_abi_version(void) { return TRMOE_ABI_VERSION; }
+
+const char* trmoe_last_error(void) { return g_last_error.c_str(); }
+
+int trmoe_device_supported(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int trmoe_pack_dims(int kind, int64_t out_features, int64_t in_features, int64_t row_align,
+                    int64_t* rows, int64_t* cols) {
+    TRMOE_REQUIRE(kind == TRMOE_PACK_GATE_UP || kind == TRMOE_PACK_PLAIN, "pack_dims: bad kind");
+    TRMOE_REQUIRE(out_features > 0 && in_features > 0, "pack_dims: dimensions must be positive");
+    TRMOE_REQUIRE(row_align > 0 && row_align % 64 == 0, "pack_dims: row_align must be a positive multiple of 64");
+    TRMOE_REQUIRE(rows != nullptr && cols != nullptr, "pack_dims: null output");
+    *rows = (kind == TRMOE_PACK_GATE_UP) ? 2 * round_up(out_features, row_align / 2)
+                                         : round_up(out_features, row_align);
+    *cols = round_up(in_features, 8);
+    return TRMOE_OK;
+}
+
+int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b, int64_t groups,
+                      int64_t out_features, int64_t in_features, int64_t s_group, int64_t s_out,
+                      int64_t s_in, const float* scale_a, const float* scale_b,
+                      int64_t scale_group_stride, int64_t row_align, void* dst, float* dst_scale,
+                      void* stream) {
+    int64_t rows = 0, cols = 0;
+    int st = trmoe_pack_dims(kind, out_features, in_features, row_align, &rows, &cols);
+    if (st) return st;
+    TRMOE_REQUIRE(elem_bytes(dtype) > 0, "pack_weight: bad dtype");
+    TRMOE_REQUIRE(groups > 0, "pack_weight: groups must be positive");
+    TRMOE_REQUIRE(src_a != nullptr && dst != nullptr, "pack_weight: null pointer");
+    TRMOE_REQUIRE(kind == TRMOE_PACK_PLAIN || src_b != nullptr, "pack_weight: GATE_UP needs src_b");
+    if (dtype == TRMOE_FP8_E4M3) {
+        TRMOE_REQUIRE(scale_a != nullptr && dst_scale != nullptr, "pack_weight: fp8 needs scales");
+        TRMOE_REQUIRE(kind == TRMOE_PACK_PLAIN || scale_b != nullptr, "pack_weight: fp8 GATE_UP needs scale_b");
+    } else {
+        TRMOE_REQUIRE(scale_a == nullptr && scale_b == nullptr && dst_scale == nullptr,
+                      "pack_weight: scales are only for fp8 weights");
+    }
+    PackArgs p;
+    p.a = src_a;
+    p.b = (kind == TRMOE_PACK_GATE_UP) ? src_b : src_a;
+    p.sa = scale_a;
+    p.sb = (kind == TRMOE_PACK_GATE_UP) ? scale_b : scale_a;
+    p.groups = groups;
+    p.out_features = out_features;
+    p.in_features = in_features;
+    p.s_group = s_group;
+    p.s_out = s_out;
+    p.s_in = s_in;
+    p.scale_group_stride = scale_group_stride;
+    p.dst = dst;
+    p.dst_scale = dst_scale;
+    p.dst_rows = rows;
+    p.dst_cols = cols;
+    p.interleave = (kind == TRMOE_PACK_GATE_UP);
+    p.elem_bytes = elem_bytes(dtype);
+    return launch_pack(p, as_stream(stream));
+}
+
+size_t trmoe_route_sort_workspace_bytes(int64_t n_tokens, int top_k, int num_experts, int order) {
+    if (n_tokens < 0 || top_k < 1 || num_experts < 1) return 0;
+    int64_t nb = route_sort_blocks(n_tokens, top_k, order);
+    return nb <= 1 ? 0 : (size_t)nb * (size_t)num_experts * sizeof(int32_t);
+}
+
+int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* route_table,
+                     int64_t vocab_size, int top_k, int num_experts, int order, int64_t* routes,
+                     int64_t* sorted_indices, int64_t* inverse, int32_t* expert_offsets,
+                     int32_t* expert_counts, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0, "route_sort: n_tokens must be non-negative");
+    TRMOE_REQUIRE(top_k == 1 || top_k == 2 || top_k == 4, "route_sort: top_k must be 1, 2 or 4");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "route_sort: num_experts must be in [1, 16]");
+    TRMOE_REQUIRE(top_k <= num_experts, "route_sort: top_k cannot exceed num_experts");
+    TRMOE_REQUIRE(vocab_size > 0, "route_sort: vocab_size must be positive");
+    TRMOE_REQUIRE(order == TRMOE_ORDER_TOKEN || order == TRMOE_ORDER_ASSIGNMENT, "route_sort: bad order");
+    TRMOE_REQUIRE(route_table != nullptr && expert_offsets != nullptr && expert_counts != nullptr,
+                  "route_sort: null pointer");
+    TRMOE_REQUIRE(n_tokens == 0 || (token_ids != nullptr && sorted_indices != nullptr && inverse != nullptr),
+                  "route_sort: null pointer");
+    TRMOE_REQUIRE(n_tokens * top_k < (int64_t)1 << 31, "route_sort: too many assignments");
+    return launch_route_sort(token_ids, n_tokens, route_table, vocab_size, top_k, num_experts, order,
+                             routes, sorted_indices, inverse, expert_offsets, expert_counts, workspace,
+                             workspace_bytes, as_stream(stream));
+}
+
+int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
+                         int64_t hidden, int64_t ldx, const void* w_packed, const float* w_scale,
+                         int64_t shared_width, void* h, int64_t ldh, void* stream) {
+    TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_gate_up: unsupported dtype pair");
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_gate_up: bad dimensions");
+    TRMOE_REQUIRE(ldx >= hidden, "shared_gate_up: ldx < hidden");
+    TRMOE_REQUIRE(ldh >= round_up(shared_width, 128), "shared_gate_up: ldh < round_up(shared_width, 128)");
+    TRMOE_REQUIRE(hidden < (int64_t)1 << 30, "shared_gate_up: hidden too large");
+    TRMOE_REQUIRE((w_dtype == TRMOE_FP8_E4M3) == (w_scale != nullptr), "shared_gate_up: w_scale iff fp8");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x && w_packed && h, "shared_gate_up: null pointer");
+    TRMOE_REQUIRE(aligned16(w_packed), "shared_gate_up: packed weights must be 16-byte aligned");
+    const int epc = (act_dtype == TRMOE_F32) ? 4 : 8;
+    GateUpArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = n_tokens;
+    a.K = (int)hidden;
+    a.w = w_packed;
+    a.ldw = round_up(hidden, 8);
+    a.w_scale = w_scale;
+    a.h = h;
+    a.ldh = ldh;
+    a.x_vec_ok = aligned16(x) && (ldx % epc == 0);
+    return launch_gate_up(act_dtype, w_dtype, a, 2 * round_up(shared_width, 128), as_stream(stream));
+}
+
+int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
+                         int64_t hidden, int64_t ldx, const int64_t* sorted_indices,
+                         const int32_t* expert_offsets, int num_experts, int top_k,
+                         const void* w_gate_up, const float* s_gate_up, const void* w_down,
+                         const float* s_down, int64_t expert_width, void* y, int64_t ldy,
+                         void* stream) {
+    TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "routed_experts: unsupported dtype pair");
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && expert_width > 0, "routed_experts: bad dimensions");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "routed_experts: num_experts must be in [1, 16]");
+    TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= num_experts, "routed_experts: bad top_k");
+    TRMOE_REQUIRE(ldx >= hidden && ldy >= hidden, "routed_experts: bad leading dimension");
+    TRMOE_REQUIRE(hidden < (int64_t)1 << 30, "routed_experts: hidden too large");
+    TRMOE_REQUIRE((w_dtype == TRMOE_FP8_E4M3) == (s_gate_up != nullptr && s_down != nullptr),
+                  "routed_experts: scales iff fp8");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x && sorted_indices && expert_offsets && w_gate_up && w_down && y, "routed_experts: null pointer");
+    TRMOE_REQUIRE(aligned16(w_gate_up) && aligned16(w_down), "routed_experts: packed weights must be 16-byte aligned");
+    const int64_t f_pad = round_up(expert_width, 64);
+    if (routed_lds_bytes(act_dtype, f_pad) > 160 * 1024)
+        return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: expert_width too large for the LDS-resident tile");
+    const int epc = (act_dtype == TRMOE_F32) ? 4 : 8;
+    RoutedArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.n_tokens = n_tokens;
+    a.K = (int)hidden;
+    a.sorted = sorted_indices;
+    a.offsets = expert_offsets;
+    a.E = num_experts;
+    a.wgu = w_gate_up;
+    a.wgu_ld = round_up(hidden, 8);
+    a.sgu = s_gate_up;
+    a.wd = w_down;
+    a.wd_ld = round_up(expert_width, 8);
+    a.sd = s_down;
+    a.w_elem_bytes = elem_bytes(w_dtype);
+    a.F_pad = (int)f_pad;
+    a.W = (int)expert_width;
+    a.H = (int)hidden;
+    a.H_pad = (int)round_up(hidden, 128);
+    a.y = y;
+    a.ldy = ldy;
+    a.x_vec_ok = aligned16(x) && (ldx % epc == 0);
+    const int64_t max_tiles = (n_tokens * top_k + 127) / 128 + num_experts;
+    return launch_routed(act_dtype, w_dtype, a, max_tiles, as_stream(stream));
+}
+
+int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
+                              int64_t shared_width, int64_t ldh, const void* w_down,
+                              const float* w_scale, int64_t hidden, const void* y, int64_t ldy,
+                              const int64_t* inverse, int top_k, const float* route_weights,
+                              float shared_scale, float routed_scale, const void* residual,
+                              int64_t ldr, void* out, int64_t ldo, void* stream) {
+    TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_down_combine: unsupported dtype pair");
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_down_combine: bad dimensions");
+    TRMOE_REQUIRE(ldh >= shared_width && ldo >= hidden, "shared_down_combine: bad leading dimension");
+    TRMOE_REQUIRE(shared_width < (int64_t)1 << 30, "shared_down_combine: shared_width too large");
+    TRMOE_REQUIRE((w_dtype == TRMOE_FP8_E4M3) == (w_scale != nullptr), "shared_down_combine: w_scale iff fp8");
+    TRMOE_REQUIRE((y == nullptr) == (inverse == nullptr), "shared_down_combine: y and inverse go together");
+    if (y != nullptr) {
+        TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, "shared_down_combine: bad top_k");
+        TRMOE_REQUIRE(route_weights != nullptr, "shared_down_combine: null route_weights");
+        TRMOE_REQUIRE(ldy >= hidden, "shared_down_combine: ldy < hidden");
+    }
+    TRMOE_REQUIRE(residual == nullptr || ldr >= hidden, "shared_down_combine: ldr < hidden");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(h && w_down && out, "shared_down_combine: null pointer");
+    TRMOE_REQUIRE(aligned16(w_down), "shared_down_combine: packed weights must be 16-byte aligned");
+    const int epc = (act_dtype == TRMOE_F32) ? 4 : 8;
+    DownArgs a;
+    a.h = h;
+    a.ldh = ldh;
+    a.M = n_tokens;
+    a.K = (int)shared_width;
+    a.w = w_down;
+    a.ldw = round_up(shared_width, 8);
+    a.w_scale = w_scale;
+    a.N = (int)hidden;
+    a.y = y;
+    a.ldy = ldy;
+    a.inverse = inverse;
+    a.top_k = (y != nullptr) ? top_k : 0;
+    for (int j = 0; j < 4; ++j) a.rw[j] = (y != nullptr && j < top_k) ? route_weights[j] : 0.f;
+    a.shared_scale = shared_scale;
+    a.routed_scale = routed_scale;
+    a.residual = residual;
+    a.ldr = ldr;
+    a.out = out;
+    a.ldo = ldo;
+    a.h_vec_ok = aligned16(h) && (ldh % epc == 0);
+    return launch_down_combine(act_dtype, w_dtype, a, round_up(hidden, 128), as_stream(stream));
+}
+
+int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y, int64_t ldy,
+                  const int64_t* inverse, int top_k, const float* route_weights,
+                  float routed_scale, const void* residual, int64_t ldr, void* out, int64_t ldo,
+                  void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "combine: bad dtype");
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0, "combine: bad dimensions");
+    TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, "combine: bad top_k");
+    TRMOE_REQUIRE(ldy >= hidden && ldo >= hidden && (residual == nullptr || ldr >= hidden),
+                  "combine: bad leading dimension");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(y && inverse && route_weights && out, "combine: null pointer");
+    CombineArgs a;
+    a.M = n_tokens;
+    a.N = hidden;
+    a.y = y;
+    a.ldy = ldy;
+    a.inverse = inverse;
+    a.top_k = top_k;
+    for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? route_weights[j] : 0.f;
+    a.routed_scale = routed_scale;
+    a.residual = residual;
+    a.ldr = ldr;
+    a.out = out;
+    a.ldo = ldo;
+    return launch_combine(act_dtype, a, as_stream(stream));
+}
+
+}  // extern "C"

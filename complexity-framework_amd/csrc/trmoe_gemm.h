@@ -1,0 +1,105 @@
+// Kernel argument blocks and launchers of the TR-MoE tile kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace trmoe {
+
+struct PackArgs {
+    const void* a;
+    const void* b;
+    const float* sa;
+    const float* sb;
+    int64_t groups, out_features, in_features;
+    int64_t s_group, s_out, s_in;
+    int64_t scale_group_stride;
+    void* dst;
+    float* dst_scale;
+    int64_t dst_rows, dst_cols;
+    int interleave;
+    int elem_bytes;
+};
+
+struct GateUpArgs {
+    const void* x;
+    int64_t ldx;
+    int64_t M;
+    int K;
+    const void* w;
+    int64_t ldw;
+    const float* w_scale;
+    void* h;
+    int64_t ldh;
+    int x_vec_ok;
+};
+
+struct DownArgs {
+    const void* h;
+    int64_t ldh;
+    int64_t M;
+    int K;
+    const void* w;
+    int64_t ldw;
+    const float* w_scale;
+    int N;
+    const void* y;
+    int64_t ldy;
+    const int64_t* inverse;
+    int top_k;
+    float rw[4];
+    float shared_scale;
+    float routed_scale;
+    const void* residual;
+    int64_t ldr;
+    void* out;
+    int64_t ldo;
+    int h_vec_ok;
+};
+
+struct RoutedArgs {
+    const void* x;
+    int64_t ldx;
+    int64_t n_tokens;
+    int K;                 // hidden
+    const int64_t* sorted;
+    const int32_t* offsets;
+    int E;
+    const void* wgu;       // [E, 2*F_pad, wgu_ld]
+    int64_t wgu_ld;
+    const float* sgu;      // [E, 2*F_pad] or null
+    const void* wd;        // [E, H_pad, wd_ld]
+    int64_t wd_ld;
+    const float* sd;       // [E, H_pad] or null
+    int w_elem_bytes;
+    int F_pad;             // expert width rounded up to 64
+    int W;                 // expert width (down K)
+    int H;                 // output columns
+    int H_pad;             // rounded up to 128
+    void* y;
+    int64_t ldy;
+    int x_vec_ok;
+};
+
+struct CombineArgs {
+    int64_t M, N;
+    const void* y;
+    int64_t ldy;
+    const int64_t* inverse;
+    int top_k;
+    float rw[4];
+    float routed_scale;
+    const void* residual;
+    int64_t ldr;
+    void* out;
+    int64_t ldo;
+};
+
+int launch_pack(const PackArgs& p, hipStream_t stream);
+int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
+int launch_down_combine(int act, int wdt, const DownArgs& a, int64_t packed_rows, hipStream_t stream);
+int routed_lds_bytes(int act, int64_t f_pad);
+int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t max_tiles, hipStream_t stream);
+int launch_combine(int act, const CombineArgs& a, hipStream_t stream);
+
+}  // namespace trmoe

@@ -1,0 +1,445 @@
+// K2/K3/K4: MFMA tile kernels of the TR-MoE layer, plus weight packing.
+//
+//   k_gate_up_swiglu   shared SwiGLU gate|up GEMM with the SwiGLU epilogue
+//                      (engine.py:333-349, first half)
+//   k_routed_experts   per-expert gate|up -> SwiGLU -> down over the K1
+//                      partition, one workgroup per (expert, 128-row) tile
+//                      (triton_token_routed.py:1033-1342)
+//   k_down_combine     shared down GEMM; the epilogue gathers each token's k
+//                      expert rows through `inverse` and applies the route
+//                      weights and branch scales (engine.py:509-531, 578)
+//   k_combine          the epilogue alone, for shared_width == 0
+//   k_pack             weight re-layout into the K-contiguous packed form
+#include "trmoe_common.h"
+#include "trmoe_internal.h"
+#include "trmoe_gemm.h"
+
+#include <type_traits>
+
+namespace trmoe {
+
+// ---------------------------------------------------------------------------
+// packing
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pack(PackArgs p) {
+    const int64_t total = p.groups * p.dst_rows * p.dst_cols;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t col = idx % p.dst_cols;
+        const int64_t rowg = idx / p.dst_cols;
+        const int64_t row = rowg % p.dst_rows;
+        const int64_t g = rowg / p.dst_rows;
+        int64_t feat;
+        const char* src;
+        const float* ssrc;
+        if (p.interleave) {
+            const int64_t blk = row >> 6, w = row & 63;
+            feat = blk * 32 + (w & 31);
+            src = (w >= 32) ? (const char*)p.b : (const char*)p.a;
+            ssrc = (w >= 32) ? p.sb : p.sa;
+        } else {
+            feat = row;
+            src = (const char*)p.a;
+            ssrc = p.sa;
+        }
+        const bool valid = feat < p.out_features && col < p.in_features;
+        const int64_t s = g * p.s_group + feat * p.s_out + col * p.s_in;
+        char* d = (char*)p.dst + idx * p.elem_bytes;
+        if (p.elem_bytes == 1) {
+            *(uint8_t*)d = valid ? ((const uint8_t*)src)[s] : 0;
+        } else if (p.elem_bytes == 2) {
+            *(uint16_t*)d = valid ? ((const uint16_t*)src)[s] : 0;
+        } else {
+            *(uint32_t*)d = valid ? ((const uint32_t*)src)[s] : 0;
+        }
+        if (p.dst_scale != nullptr && col == 0) {
+            const bool fv = feat < p.out_features;
+            p.dst_scale[g * p.dst_rows + row] = fv ? ssrc[g * p.scale_group_stride + feat] : 0.0f;
+        }
+    }
+}
+
+int launch_pack(const PackArgs& p, hipStream_t stream) {
+    const int64_t total = p.groups * p.dst_rows * p.dst_cols;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_pack, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    return check_launch("pack_weight");
+}
+
+// ---------------------------------------------------------------------------
+// B operand selection: same kind as A, or e4m3 expanded to bf16
+// ---------------------------------------------------------------------------
+template <class Kind, bool FP8, int ROWS>
+struct BProvSel {
+    using type = PackedRows<Kind, ROWS>;
+};
+template <class Kind, int ROWS>
+struct BProvSel<Kind, true, ROWS> {
+    using type = PackedRowsFP8<ROWS>;
+};
+
+template <class Kind, bool FP8, int ROWS>
+__device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS>::type& bp, const void* base,
+                                           int64_t ld, int64_t row0, int K) {
+    if constexpr (FP8) {
+        bp.base = static_cast<const uint8_t*>(base) + row0 * ld;
+    } else {
+        bp.base = static_cast<const typename Kind::T*>(base) + row0 * ld;
+    }
+    bp.ld = ld;
+    bp.K = K;
+}
+
+using ShapeMain = TileShape<128, 128, 2>;
+
+// ---------------------------------------------------------------------------
+// K2: shared gate|up + SwiGLU
+// ---------------------------------------------------------------------------
+template <class Kind, bool FP8>
+__global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
+    using Shape = ShapeMain;
+    using T = typename Kind::T;
+    extern __shared__ __align__(16) char lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+
+    GlobalRows<Kind, Shape::BM> ap;
+    ap.K = a.K;
+    ap.vec_ok = a.x_vec_ok;
+#pragma unroll
+    for (int j = 0; j < GlobalRows<Kind, Shape::BM>::kChunks; ++j) {
+        const int row = (threadIdx.x + kThreads * j) >> 3;
+        const int64_t m = m0 + row;
+        ap.rowp[j] = (m < a.M) ? static_cast<const T*>(a.x) + m * a.ldx : nullptr;
+    }
+    typename BProvSel<Kind, FP8, Shape::BN>::type bp;
+    init_bprov<Kind, FP8, Shape::BN>(bp, a.w, a.ldw, n0, a.K);
+
+    f32x16 acc[Shape::TM][Shape::TN];
+    zero_acc<Kind>(acc);
+    tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
+
+    const int r = lane & 31;
+#pragma unroll
+    for (int p = 0; p < Shape::TN / 2; ++p) {
+        const int64_t pbase = n0 + wn0 + 64 * p;     // packed row of the gate tile
+        const int64_t feat = (pbase >> 1) + r;
+        const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
+        const float su = a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f;
+#pragma unroll
+        for (int tm = 0; tm < Shape::TM; ++tm) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int64_t row = m0 + wm0 + tm * 32 + acc_row(lane, i);
+                if (row < a.M) {
+                    const float g = acc[tm][2 * p][i] * sg;
+                    const float u = acc[tm][2 * p + 1][i] * su;
+                    static_cast<T*>(a.h)[row * a.ldh + feat] = from_f32<T>(silu_f(g) * u);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K4: shared down + weighted un-permute + combine
+// ---------------------------------------------------------------------------
+template <class Kind, bool FP8>
+__global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
+    using Shape = ShapeMain;
+    using T = typename Kind::T;
+    extern __shared__ __align__(16) char lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+
+    GlobalRows<Kind, Shape::BM> ap;
+    ap.K = a.K;
+    ap.vec_ok = a.h_vec_ok;
+#pragma unroll
+    for (int j = 0; j < GlobalRows<Kind, Shape::BM>::kChunks; ++j) {
+        const int row = (threadIdx.x + kThreads * j) >> 3;
+        const int64_t m = m0 + row;
+        ap.rowp[j] = (m < a.M) ? static_cast<const T*>(a.h) + m * a.ldh : nullptr;
+    }
+    typename BProvSel<Kind, FP8, Shape::BN>::type bp;
+    init_bprov<Kind, FP8, Shape::BN>(bp, a.w, a.ldw, n0, a.K);
+
+    f32x16 acc[Shape::TM][Shape::TN];
+    zero_acc<Kind>(acc);
+    tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
+
+    const int r = lane & 31;
+    float cscale[Shape::TN];
+#pragma unroll
+    for (int tn = 0; tn < Shape::TN; ++tn) {
+        const int64_t col = n0 + wn0 + tn * 32 + r;
+        cscale[tn] = a.shared_scale * ((a.w_scale && col < a.N) ? a.w_scale[col] : 1.0f);
+    }
+    const T* y = static_cast<const T*>(a.y);
+    const T* res = static_cast<const T*>(a.residual);
+    T* out = static_cast<T*>(a.out);
+#pragma unroll
+    for (int tm = 0; tm < Shape::TM; ++tm) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int64_t row = m0 + wm0 + tm * 32 + acc_row(lane, i);
+            if (row >= a.M) continue;
+            int64_t yrow[kMaxTopK];
+            if (y != nullptr) {
+                for (int j = 0; j < a.top_k; ++j) {
+                    // clamp: a malformed route table must not turn into a wild read
+                    int64_t r = a.inverse[(int64_t)j * a.M + row];
+                    r = r < 0 ? 0 : (r >= a.top_k * a.M ? a.top_k * a.M - 1 : r);
+                    yrow[j] = r * a.ldy;
+                }
+            }
+#pragma unroll
+            for (int tn = 0; tn < Shape::TN; ++tn) {
+                const int64_t col = n0 + wn0 + tn * 32 + r;
+                if (col >= a.N) continue;
+                float v = acc[tm][tn][i] * cscale[tn];
+                if (y != nullptr) {
+                    float s = 0.f;
+                    for (int j = 0; j < a.top_k; ++j) s += a.rw[j] * to_f32(y[yrow[j] + col]);
+                    v += a.routed_scale * s;
+                }
+                if (res != nullptr) v += to_f32(res[row * a.ldr + col]);
+                out[row * a.ldo + col] = from_f32<T>(v);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K3: routed experts (gate|up -> SwiGLU -> down) over the partition
+// ---------------------------------------------------------------------------
+// Tile t of the launch maps to expert e and rows [row0, row0 + 128) of its
+// segment; tiles past the last segment exit.  Phase 1 streams the gathered
+// token rows against 64-feature chunks of the expert's packed gate|up rows and
+// leaves h (128 rows x F_pad features) in LDS in the operand layout; phase 2
+// streams the expert's packed down rows in 128-column chunks against it.
+template <class Kind, bool FP8>
+__global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
+    using Shape = ShapeMain;
+    using T = typename Kind::T;
+    constexpr int SE = Kind::kStageElems;
+    constexpr int EPC = Kind::kPerChunk;
+    extern __shared__ __align__(16) char lds[];
+    char* hs = lds + Shape::kLdsBytes;
+    const int hs_stage_bytes = Shape::BM * kRowBytes;
+
+    // tile -> (expert, row range)
+    __shared__ int s_tile[3];
+    if (threadIdx.x == 0) {
+        int acc_tiles = 0, e_sel = -1, row0 = 0, row1 = 0;
+        for (int e = 0; e < a.E; ++e) {
+            const int b = a.offsets[e], c = a.offsets[e + 1] - b;
+            const int nt = (c + Shape::BM - 1) / Shape::BM;
+            if ((int)blockIdx.x < acc_tiles + nt) {
+                e_sel = e;
+                row0 = b + ((int)blockIdx.x - acc_tiles) * Shape::BM;
+                row1 = min(row0 + Shape::BM, b + c);
+                break;
+            }
+            acc_tiles += nt;
+        }
+        s_tile[0] = e_sel;
+        s_tile[1] = row0;
+        s_tile[2] = row1;
+    }
+    __syncthreads();
+    const int e = s_tile[0];
+    if (e < 0) return;
+    const int64_t row0 = s_tile[1];
+    const int rows = s_tile[2] - s_tile[1];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int r = lane & 31;
+
+    const int64_t gu_rows = 2 * (int64_t)a.F_pad;
+    const char* wgu = static_cast<const char*>(a.wgu) + (int64_t)e * gu_rows * a.wgu_ld * a.w_elem_bytes;
+    const float* sgu = a.sgu ? a.sgu + (int64_t)e * gu_rows : nullptr;
+    const char* wd = static_cast<const char*>(a.wd) + (int64_t)e * a.H_pad * a.wd_ld * a.w_elem_bytes;
+    const float* sd = a.sd ? a.sd + (int64_t)e * a.H_pad : nullptr;
+
+    // ---- phase 1: h = silu(x Wg) * (x Wu) into LDS
+    const int nchunks = a.F_pad / 64;
+    for (int fc = 0; fc < nchunks; ++fc) {
+        GlobalRows<Kind, Shape::BM> ap;
+        ap.K = a.K;
+        ap.vec_ok = a.x_vec_ok;
+#pragma unroll
+        for (int j = 0; j < GlobalRows<Kind, Shape::BM>::kChunks; ++j) {
+            const int row = (threadIdx.x + kThreads * j) >> 3;
+            if (row < rows) {
+                const int64_t t = (int64_t)((uint64_t)a.sorted[row0 + row] % (uint64_t)a.n_tokens);
+                ap.rowp[j] = static_cast<const T*>(a.x) + t * a.ldx;
+            } else {
+                ap.rowp[j] = nullptr;
+            }
+        }
+        typename BProvSel<Kind, FP8, Shape::BN>::type bp;
+        init_bprov<Kind, FP8, Shape::BN>(bp, wgu, a.wgu_ld, (int64_t)fc * 128, a.K);
+        f32x16 acc[Shape::TM][Shape::TN];
+        zero_acc<Kind>(acc);
+        tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
+
+        const int prow = fc * 128 + wn0;          // packed row of this wave's gate tile
+        const int feat = (prow >> 1) + r;          // feature index in [0, F_pad)
+        const float sg = sgu ? sgu[prow + r] : 1.0f;
+        const float su = sgu ? sgu[prow + 32 + r] : 1.0f;
+        const int st = feat / SE, el = feat % SE;
+        char* hcol = hs + st * hs_stage_bytes;
+#pragma unroll
+        for (int tm = 0; tm < Shape::TM; ++tm) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = wm0 + tm * 32 + acc_row(lane, i);
+                const float g = acc[tm][0][i] * sg;
+                const float u = acc[tm][1][i] * su;
+                T* dst = reinterpret_cast<T*>(hcol + lds_byte(row, el / EPC)) + (el % EPC);
+                *dst = from_f32<T>(silu_f(g) * u);
+            }
+        }
+    }
+
+    // ---- phase 2: y = h Wd, 128 output columns at a time
+    const int ncol = a.H_pad / Shape::BN;
+    T* y = static_cast<T*>(a.y);
+    for (int oc = 0; oc < ncol; ++oc) {
+        typename BProvSel<Kind, FP8, Shape::BN>::type bp;
+        init_bprov<Kind, FP8, Shape::BN>(bp, wd, a.wd_ld, (int64_t)oc * Shape::BN, a.W);
+        f32x16 acc[Shape::TM][Shape::TN];
+        zero_acc<Kind>(acc);
+        tile_loop_lds_a<Kind, Shape>(hs, hs_stage_bytes, bp, a.W, lds, wm0, wn0, acc);
+#pragma unroll
+        for (int tn = 0; tn < Shape::TN; ++tn) {
+            const int64_t col = (int64_t)oc * Shape::BN + wn0 + tn * 32 + r;
+            if (col >= a.H) continue;
+            const float cs = sd ? sd[col] : 1.0f;
+#pragma unroll
+            for (int tm = 0; tm < Shape::TM; ++tm) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = wm0 + tm * 32 + acc_row(lane, i);
+                    if (row < rows) y[(row0 + row) * a.ldy + col] = from_f32<T>(acc[tm][tn][i] * cs);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_combine: routed un-permute without a shared branch
+// ---------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
+    const int64_t total = a.M * a.N;
+    const T* y = static_cast<const T*>(a.y);
+    const T* res = static_cast<const T*>(a.residual);
+    T* out = static_cast<T*>(a.out);
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = idx / a.N, col = idx - row * a.N;
+        float s = 0.f;
+        for (int j = 0; j < a.top_k; ++j) {
+            int64_t r = a.inverse[(int64_t)j * a.M + row];
+            r = r < 0 ? 0 : (r >= a.top_k * a.M ? a.top_k * a.M - 1 : r);
+            s += a.rw[j] * to_f32(y[r * a.ldy + col]);
+        }
+        float v = a.routed_scale * s;
+        if (res != nullptr) v += to_f32(res[row * a.ldr + col]);
+        out[row * a.ldo + col] = from_f32<T>(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+template <class F>
+static int ensure_lds(F* fn, int bytes) {
+    if (bytes <= 65536) return TRMOE_OK;
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess) return set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
+    return TRMOE_OK;
+}
+
+int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + ShapeMain::BM - 1) / ShapeMain::BM), (unsigned)(packed_rows / ShapeMain::BN));
+    const int lds = ShapeMain::kLdsBytes;
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) {
+        hipLaunchKernelGGL((k_gate_up_swiglu<KindF32, false>), grid, dim3(kThreads), lds, stream, a);
+    } else if (act == TRMOE_BF16 && wdt == TRMOE_BF16) {
+        hipLaunchKernelGGL((k_gate_up_swiglu<KindBF16, false>), grid, dim3(kThreads), lds, stream, a);
+    } else if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) {
+        hipLaunchKernelGGL((k_gate_up_swiglu<KindBF16, true>), grid, dim3(kThreads), lds, stream, a);
+    } else {
+        return set_error(TRMOE_ERR_UNSUPPORTED, "shared_gate_up: unsupported dtype pair");
+    }
+    return check_launch("shared_gate_up");
+}
+
+int launch_down_combine(int act, int wdt, const DownArgs& a, int64_t packed_rows, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + ShapeMain::BM - 1) / ShapeMain::BM), (unsigned)(packed_rows / ShapeMain::BN));
+    const int lds = ShapeMain::kLdsBytes;
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) {
+        hipLaunchKernelGGL((k_down_combine<KindF32, false>), grid, dim3(kThreads), lds, stream, a);
+    } else if (act == TRMOE_BF16 && wdt == TRMOE_BF16) {
+        hipLaunchKernelGGL((k_down_combine<KindBF16, false>), grid, dim3(kThreads), lds, stream, a);
+    } else if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) {
+        hipLaunchKernelGGL((k_down_combine<KindBF16, true>), grid, dim3(kThreads), lds, stream, a);
+    } else {
+        return set_error(TRMOE_ERR_UNSUPPORTED, "shared_down_combine: unsupported dtype pair");
+    }
+    return check_launch("shared_down_combine");
+}
+
+int routed_lds_bytes(int act, int64_t f_pad) {
+    const int64_t per_row = (act == TRMOE_F32) ? 4 * f_pad : 2 * f_pad;
+    return ShapeMain::kLdsBytes + (int)(ShapeMain::BM * per_row);
+}
+
+int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t max_tiles, hipStream_t stream) {
+    const int lds = routed_lds_bytes(act, a.F_pad);
+    dim3 grid((unsigned)max_tiles);
+    int st;
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) {
+        if ((st = ensure_lds(k_routed_experts<KindF32, false>, lds))) return st;
+        hipLaunchKernelGGL((k_routed_experts<KindF32, false>), grid, dim3(kThreads), lds, stream, a);
+    } else if (act == TRMOE_BF16 && wdt == TRMOE_BF16) {
+        if ((st = ensure_lds(k_routed_experts<KindBF16, false>, lds))) return st;
+        hipLaunchKernelGGL((k_routed_experts<KindBF16, false>), grid, dim3(kThreads), lds, stream, a);
+    } else if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) {
+        if ((st = ensure_lds(k_routed_experts<KindBF16, true>, lds))) return st;
+        hipLaunchKernelGGL((k_routed_experts<KindBF16, true>), grid, dim3(kThreads), lds, stream, a);
+    } else {
+        return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: unsupported dtype pair");
+    }
+    return check_launch("routed_experts");
+}
+
+int launch_combine(int act, const CombineArgs& a, hipStream_t stream) {
+    const int64_t total = a.M * a.N;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    if (act == TRMOE_F32) {
+        hipLaunchKernelGGL(k_combine<float>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(k_combine<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    }
+    return check_launch("combine");
+}
+
+}  // namespace trmoe

@@ -1,0 +1,204 @@
+/*
+ * trmoe.h -- C ABI of the MI355X (gfx950) TR-MoE feed-forward kernels.
+ *
+ * One layer of the reference's TRHashEngine forward
+ * (complexity/tr_hash/engine.py:534-579) is
+ *
+ *     out = shared_scale * shared_swiglu(x) + routed_scale * routed(x, ids)
+ *
+ * and this library computes it with four kernel families:
+ *
+ *   K1 trmoe_route_sort          route gather + counting partition
+ *   K2 trmoe_shared_gate_up      shared SwiGLU gate|up GEMM, SwiGLU epilogue
+ *   K3 trmoe_routed_experts      grouped expert MLP over the partition
+ *   K4 trmoe_shared_down_combine shared down GEMM with the weighted
+ *                                un-permute of K3's rows fused in its epilogue
+ *      trmoe_combine             the same un-permute when shared_width == 0
+ *
+ * Conventions (every entry point):
+ *   - device pointers are plain, caller-owned and stay valid until the work
+ *     queued on `stream` (a hipStream_t, NULL = default stream) completes;
+ *   - the library never allocates or frees device memory; scratch is passed
+ *     in (see *_workspace_bytes);
+ *   - work is enqueued asynchronously on `stream`; no call synchronises;
+ *   - the return value is a trmoe_status; on failure trmoe_last_error()
+ *     returns a message that stays valid until the calling thread's next
+ *     call into the library;
+ *   - tensors are row-major with the element strides given (ld*).
+ *
+ * Weights are consumed in a packed layout produced on the device by
+ * trmoe_pack_weight() (see trmoe_pack_dims()).
+ */
+#ifndef TRMOE_H
+#define TRMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRMOE_ABI_VERSION 1
+
+enum trmoe_status {
+    TRMOE_OK = 0,
+    TRMOE_ERR_INVALID = 1,      /* bad argument (shape, pointer, enum)   */
+    TRMOE_ERR_UNSUPPORTED = 2,  /* valid but not implemented here         */
+    TRMOE_ERR_HIP = 3           /* a HIP runtime call or launch failed    */
+};
+
+enum trmoe_dtype {
+    TRMOE_F32 = 0,
+    TRMOE_BF16 = 1,
+    TRMOE_FP8_E4M3 = 2          /* OCP float8_e4m3fn, weights only        */
+};
+
+enum trmoe_order {
+    /* segment order (expert, token): the reference's fused GPU partition,
+     * complexity_cuda/triton_token_routed.py:211-277 */
+    TRMOE_ORDER_TOKEN = 0,
+    /* segment order (expert, slot*N + token): the reference's stable CPU
+     * sort, triton_token_routed.py:2320-2351 (and CGGR, :69-93) */
+    TRMOE_ORDER_ASSIGNMENT = 1
+};
+
+enum trmoe_pack_kind {
+    /* two [out, in] sources interleaved in groups of 32 output rows
+     * (gate rows 0..31, up rows 0..31, gate rows 32..63, ...) so that one
+     * GEMM tile holds gate and up of the same features */
+    TRMOE_PACK_GATE_UP = 0,
+    /* one [out, in] source */
+    TRMOE_PACK_PLAIN = 1
+};
+
+/* Library ABI version (TRMOE_ABI_VERSION it was built with). */
+int trmoe_abi_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* trmoe_last_error(void);
+
+/* 1 if the current HIP device is a gfx950 the kernels were built for. */
+int trmoe_device_supported(void);
+
+/*
+ * Packed weight geometry.  For `kind` GATE_UP, `out_features` is the width of
+ * each of the two sources (shared or expert width) and the packed tensor has
+ * *rows = 2 * round_up(out_features, row_align / 2) rows; for PLAIN,
+ * *rows = round_up(out_features, row_align).  *cols = round_up(in_features, 8).
+ * row_align must be a positive multiple of 64.
+ */
+int trmoe_pack_dims(int kind, int64_t out_features, int64_t in_features, int64_t row_align,
+                    int64_t* rows, int64_t* cols);
+
+/*
+ * Pack `groups` weight matrices (one per expert; 1 for shared weights) into
+ * dst[groups][rows][cols] (dtype `dtype`, rows/cols from trmoe_pack_dims).
+ * Source element (g, o, i) is read at src[g*s_group + o*s_out + i*s_in]
+ * (element strides), which covers nn.Linear weights [out, in]
+ * (s_out=in, s_in=1) and the reference's expert tensors [E, in, out]
+ * (s_out=1, s_in=out) without a host transpose.  src_b is the up source for
+ * GATE_UP (NULL for PLAIN).  For TRMOE_FP8_E4M3, src_* hold e4m3 codes and
+ * scale_a/scale_b hold per-output-channel float scales at
+ * scale[g*scale_group_stride + o]; dst_scale[groups][rows] receives them in
+ * packed row order.  For other dtypes the scale pointers must be NULL.
+ * Reference tensors: engine.py:127-163 (expert_gate/up [E,H,W], expert_down
+ * [E,W,H], shared_* nn.Linear).
+ */
+int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b, int64_t groups,
+                      int64_t out_features, int64_t in_features, int64_t s_group, int64_t s_out,
+                      int64_t s_in, const float* scale_a, const float* scale_b,
+                      int64_t scale_group_stride, int64_t row_align, void* dst, float* dst_scale,
+                      void* stream);
+
+/*
+ * K1 -- replaces sort_pair_hash_by_expert (triton_token_routed.py:2205-2351)
+ * and the route gather TRHashEngine._routes (engine.py:316-318).
+ *
+ * token_ids int64[n] are clamped to [0, vocab-1]; route_table int64[k, vocab]
+ * is the (active) persisted table.  Assignment a = slot*n + t.  Outputs:
+ *   routes         int64[k, n]   (may be NULL) routes[s, t] = table[s, id_t]
+ *   sorted_indices int64[k*n]    assignment at each partition position
+ *   inverse        int64[k*n]    inverse[sorted_indices[r]] = r
+ *   expert_offsets int32[E+1]    segment starts, offsets[E] = k*n
+ *   expert_counts  int32[E]
+ * 1 <= num_experts <= 16, top_k in {1, 2, 4}, top_k <= num_experts, entries of
+ * the table in [0, num_experts) and distinct per token.
+ */
+size_t trmoe_route_sort_workspace_bytes(int64_t n_tokens, int top_k, int num_experts, int order);
+int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* route_table,
+                     int64_t vocab_size, int top_k, int num_experts, int order, int64_t* routes,
+                     int64_t* sorted_indices, int64_t* inverse, int32_t* expert_offsets,
+                     int32_t* expert_counts, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * K2 -- shared SwiGLU first half; replaces the two nn.Linear calls and
+ * _silu_mul of TRHashEngine._shared (engine.py:333-349).
+ *
+ * x[n, hidden] (act_dtype, row stride ldx) times the GATE_UP-packed
+ * [shared_gate; shared_up] weights (w_dtype, pack row_align 256):
+ *     h[t, f] = silu(x_t . Wg_f) * (x_t . Wu_f)      f < round_up(S, 128)
+ * h is act_dtype with row stride ldh >= round_up(S, 128); the padding columns
+ * are written as zero.  (act, w) dtypes: (F32, F32), (BF16, BF16),
+ * (BF16, FP8_E4M3) with w_scale = the packed scales.
+ */
+int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
+                         int64_t hidden, int64_t ldx, const void* w_packed, const float* w_scale,
+                         int64_t shared_width, void* h, int64_t ldh, void* stream);
+
+/*
+ * K3 -- routed experts; replaces hash_cggr_grouped_gemm (gate, up),
+ * fused_swiglu and cggr_grouped_gemm (down) of the reference's fused path
+ * (triton_token_routed.py:1033-1342, engine.py:485-507).
+ *
+ * For every partition position r of expert e (expert_offsets from K1):
+ *     t = sorted_indices[r] mod n_tokens
+ *     y[r, :] = (silu(x_t . Wg_e) * (x_t . Wu_e)) . Wd_e
+ * w_gate_up: GATE_UP-packed expert gate/up, groups = E, row_align 128;
+ * w_down: PLAIN-packed transposed expert down ([E, hidden, width] view of the
+ * reference's [E, width, hidden]), row_align 128.  y is act_dtype [k*n, ldy].
+ * `num_experts` is the active expert count; `expert_width` the active width.
+ */
+int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
+                         int64_t hidden, int64_t ldx, const int64_t* sorted_indices,
+                         const int32_t* expert_offsets, int num_experts, int top_k,
+                         const void* w_gate_up, const float* s_gate_up, const void* w_down,
+                         const float* s_down, int64_t expert_width, void* y, int64_t ldy,
+                         void* stream);
+
+/*
+ * K4 -- shared down GEMM + weighted un-permute + combine; replaces
+ * shared_down, pair_hash_reduce / pair_hash_weighted_reduce
+ * (triton_token_routed.py:280-330, 376-435) and the final
+ * `shared_scale*shared + routed_scale*routed` (engine.py:578).
+ *
+ *     out[t, c] = shared_scale * (h_t . Wd_c)
+ *               + routed_scale * sum_j route_weights[j] * y[inverse[j*n + t], c]
+ *               (+ residual[t, c] when residual != NULL)
+ * h: K2's output (act_dtype, [n, ldh], K = round_up(S, 128));
+ * w_down: PLAIN-packed shared_down.weight [hidden, S] (row_align 128).
+ * y/inverse may be NULL (no routed term).  route_weights: top_k host floats.
+ */
+int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
+                              int64_t shared_width, int64_t ldh, const void* w_down,
+                              const float* w_scale, int64_t hidden, const void* y, int64_t ldy,
+                              const int64_t* inverse, int top_k, const float* route_weights,
+                              float shared_scale, float routed_scale, const void* residual,
+                              int64_t ldr, void* out, int64_t ldo, void* stream);
+
+/*
+ * K4 without a shared branch (shared_width == 0, engine.py:335):
+ *     out[t, c] = routed_scale * sum_j route_weights[j] * y[inverse[j*n+t], c]
+ *                 (+ residual[t, c])
+ */
+int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y, int64_t ldy,
+                  const int64_t* inverse, int top_k, const float* route_weights,
+                  float routed_scale, const void* residual, int64_t ldr, void* out, int64_t ldo,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRMOE_H */

@@ -1,0 +1,207 @@
+"""Each HIP kernel family against a float64 CPU reference of the same op.
+
+Tolerances are normwise (max|got - ref| / max|ref|): 1e-5 for fp32 inputs,
+1e-2 for bf16 inputs (one bf16 rounding of the output), fp8 weights are
+compared against the dequantised weights at the bf16 bound.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import trmoe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
+
+
+def nerr(got, ref):
+    return O.normwise_rel_err(got.double(), ref.double())
+
+
+def _rand(*shape, scale=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def test_fp8_to_bf16_conversion_is_exact_for_all_codes(gpu):
+    """pack + a 1x1 identity GEMM would hide a wrong decode: check the decode
+    itself through the gate/up kernel with x = unit vectors."""
+    from complexity_amd import ops
+
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes[0x7F] = 0
+    codes[0xFF] = 0  # NaN codes are never produced by the quantiser
+    H, S = 256, 128
+    # gate weights: row f holds code f at column f (diagonal), up weights = 1.0 (code 0x38)
+    wg = torch.zeros(S, H, dtype=torch.uint8)
+    wu = torch.full((S, H), 0x38, dtype=torch.uint8)
+    x = torch.zeros(H, H)
+    x[torch.arange(H), torch.arange(H)] = 1.0
+    # two passes cover the 256 codes with S = 128 features
+    for half in range(2):
+        wg.zero_()
+        for f in range(S):
+            wg[f, half * 128 + f] = codes[half * 128 + f]
+        pg, sg = ops.pack_linear_gate_up(wg.view(torch.float8_e4m3fn).to(gpu), wu.view(torch.float8_e4m3fn).to(gpu),
+                                        torch.ones(S, device=gpu), torch.ones(S, device=gpu))
+        h = ops.shared_gate_up(x.to(torch.bfloat16).to(gpu), pg, sg, S).float().cpu()
+        for f in range(S):
+            row = half * 128 + f
+            g = O.e4m3_decode_table()[int(codes[row])]
+            expect = g / (1.0 + np.exp(-g)) * 1.0 if g == g else 0.0
+            got = float(h[row, f])
+            assert abs(got - expect) <= 2 ** -7 * abs(expect) + 1e-30, (row, got, expect)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,H,S", [(1, 64, 64), (200, 96, 160), (513, 896, 384), (64, 40, 100)])
+def test_shared_gate_up(gpu, dtype, N, H, S):
+    from complexity_amd import ops
+
+    x = _rand(N, H, seed=1)
+    wg, wu = _rand(S, H, scale=0.1, seed=2), _rand(S, H, scale=0.1, seed=3)
+    xd = x.to(dtype)
+    pg, _ = ops.pack_linear_gate_up(wg.to(dtype).to(gpu), wu.to(dtype).to(gpu))
+    h = ops.shared_gate_up(xd.to(gpu), pg, None, S).cpu()
+    xr, gr, ur = xd.double(), wg.to(dtype).double(), wu.to(dtype).double()
+    ref = F.silu(xr @ gr.T) * (xr @ ur.T)
+    assert h.shape[1] == (S + 127) // 128 * 128
+    assert nerr(h[:, :S], ref) <= TOL[dtype]
+    assert (h[:, S:] == 0).all()
+
+
+def test_shared_gate_up_unaligned_rows(gpu):
+    """x with a row stride that is not a multiple of 8 takes the scalar loads."""
+    from complexity_amd import ops
+
+    N, H, S = 77, 36, 64
+    base = _rand(N, H + 3, seed=4).to(torch.bfloat16)
+    x = base[:, 1 : H + 1]  # misaligned view
+    wg, wu = _rand(S, H, 0.1, 5).to(torch.bfloat16), _rand(S, H, 0.1, 6).to(torch.bfloat16)
+    pg, _ = ops.pack_linear_gate_up(wg.to(gpu), wu.to(gpu))
+    xg = base.to(gpu)[:, 1 : H + 1]
+    h = ops.shared_gate_up(xg, pg, None, S).cpu()
+    ref = F.silu(x.double() @ wg.double().T) * (x.double() @ wu.double().T)
+    assert nerr(h[:, :S], ref) <= 1e-2
+
+
+def test_shared_gate_up_fp8_weights(gpu):
+    from complexity_amd import ops
+
+    N, H, S = 300, 256, 256
+    x = _rand(N, H, seed=7).to(torch.bfloat16)
+    wg, wu = _rand(S, H, 0.02, 8), _rand(S, H, 0.02, 9)
+    qg, sg = O.quantize_e4m3(wg, 1)
+    qu, su = O.quantize_e4m3(wu, 1)
+    pg, ps = ops.pack_linear_gate_up(qg.to(gpu), qu.to(gpu), sg.to(gpu), su.to(gpu))
+    h = ops.shared_gate_up(x.to(gpu), pg, ps, S).cpu()
+    dg, du = O.dequantize_e4m3(qg, sg, 1).double(), O.dequantize_e4m3(qu, su, 1).double()
+    ref = F.silu(x.double() @ dg.T) * (x.double() @ du.T)
+    assert nerr(h[:, :S], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_y,with_res", [(True, False), (True, True), (False, False)])
+def test_shared_down_combine(gpu, dtype, with_y, with_res):
+    from complexity_amd import ops
+
+    N, S, H, k = 333, 320, 200, 2
+    h = _rand(N, S, seed=10).to(dtype)
+    wd = _rand(H, S, 0.05, 11).to(dtype)
+    pd, _ = ops.pack_linear_down(wd.to(gpu))
+    hpad = torch.zeros(N, (S + 127) // 128 * 128, dtype=dtype)
+    hpad[:, :S] = h
+    y = _rand(k * N, H, seed=12).to(dtype)
+    perm = torch.randperm(k * N, generator=torch.Generator().manual_seed(13))
+    res = _rand(N, H, seed=14).to(dtype)
+    rw = (0.7, 0.3)
+    out = ops.shared_down_combine(hpad.to(gpu), S, pd, None, H, y.to(gpu) if with_y else None,
+                                  perm.to(gpu) if with_y else None, k, rw, 0.5, 2.0,
+                                  res.to(gpu) if with_res else None).cpu()
+    ref = 0.5 * (h.double() @ wd.double().T)
+    if with_y:
+        yr = y.double()
+        ref = ref + 2.0 * (rw[0] * yr[perm[:N]] + rw[1] * yr[perm[N:]])
+    if with_res:
+        ref = ref + res.double()
+    assert nerr(out, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_combine_without_shared(gpu, dtype):
+    from complexity_amd import ops
+
+    N, H, k = 129, 72, 4
+    y = _rand(k * N, H, seed=15).to(dtype)
+    perm = torch.randperm(k * N, generator=torch.Generator().manual_seed(16))
+    rw = (0.4, 0.3, 0.2, 0.1)
+    out = ops.combine(y.to(gpu), perm.to(gpu), N, k, rw, 1.5).cpu()
+    yr = y.double()
+    ref = 1.5 * sum(rw[j] * yr[perm[j * N:(j + 1) * N]] for j in range(k))
+    assert nerr(out, ref) <= TOL[dtype]
+
+
+def _routed_ref(x, table, ids, gate, up, down, order):
+    routes = O.gather_routes(table, ids)
+    k, n = routes.shape
+    s, _, off, _ = O.counting_partition(routes, gate.shape[0], order)
+    y = torch.empty(k * n, x.shape[1], dtype=torch.float64)
+    xr = x.double()
+    for e in range(gate.shape[0]):
+        rows = torch.from_numpy(s[off[e]:off[e + 1]])
+        if rows.numel() == 0:
+            continue
+        xt = xr[rows % n]
+        hh = F.silu(xt @ gate[e].double()) * (xt @ up[e].double())
+        y[off[e]:off[e + 1]] = hh @ down[e].double()
+    return y
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("E,k,H,W,n", [(4, 2, 96, 64, 700), (8, 4, 64, 12, 300), (16, 2, 128, 256, 900),
+                                        (2, 1, 40, 8, 33), (4, 2, 896, 64, 2048)])
+def test_routed_experts(gpu, dtype, E, k, H, W, n):
+    from complexity_amd import ops
+
+    table = O.route_table("token_id_multi_hash", 500, E, k, 0)
+    rng = np.random.default_rng(E + k + W)
+    ids = rng.integers(0, 500, n)
+    x = _rand(n, H, seed=20).to(dtype)
+    gate, up = _rand(E, H, W, scale=0.1, seed=21).to(dtype), _rand(E, H, W, scale=0.1, seed=22).to(dtype)
+    down = _rand(E, W, H, scale=0.1, seed=23).to(dtype)
+    order = O.ORDER_TOKEN
+    s, inv, off, cnt = ops.route_sort(torch.from_numpy(ids).to(gpu), torch.from_numpy(table).to(gpu), E, order)
+    pgu, _ = ops.pack_expert_gate_up(gate.to(gpu), up.to(gpu))
+    pd, _ = ops.pack_expert_down(down.to(gpu))
+    y = ops.routed_experts(x.to(gpu), s, off, E, k, pgu, None, pd, None, W).cpu()
+    ref = _routed_ref(x, table, ids, gate, up, down, order)
+    assert nerr(y, ref) <= TOL[dtype]
+
+
+def test_routed_experts_fp8_and_active_slice(gpu):
+    """fp8 expert weights, packed from an active-capacity prefix view."""
+    from complexity_amd import ops
+
+    E, k, H, W, n = 16, 2, 256, 256, 1500
+    Ea, Wa = 8, 128
+    table = O.route_table("token_id_multi_hash", 32000, Ea, k, 0)
+    ids = np.random.default_rng(3).integers(0, 32000, n)
+    x = _rand(n, H, seed=30).to(torch.bfloat16)
+    gate, up, down = _rand(E, H, W, scale=0.02, seed=31), _rand(E, H, W, scale=0.02, seed=32), \
+        _rand(E, W, H, scale=0.02, seed=33)
+    qg, sg = O.quantize_e4m3(gate, 1)
+    qu, su = O.quantize_e4m3(up, 1)
+    qd, sd = O.quantize_e4m3(down, 1)
+    s, inv, off, cnt = ops.route_sort(torch.from_numpy(ids).to(gpu), torch.from_numpy(table).to(gpu), Ea)
+    pgu, pgus = ops.pack_expert_gate_up(qg.to(gpu)[:Ea, :, :Wa], qu.to(gpu)[:Ea, :, :Wa],
+                                        sg.to(gpu)[:Ea, :Wa], su.to(gpu)[:Ea, :Wa])
+    pd, pds = ops.pack_expert_down(qd.to(gpu)[:Ea, :Wa, :], sd.to(gpu)[:Ea])
+    y = ops.routed_experts(x.to(gpu), s, off, Ea, k, pgu, pgus, pd, pds, Wa).cpu()
+    dg = O.dequantize_e4m3(qg, sg, 1)[:Ea, :, :Wa]
+    du = O.dequantize_e4m3(qu, su, 1)[:Ea, :, :Wa]
+    dd = O.dequantize_e4m3(qd, sd, 1)[:Ea, :Wa, :]
+    ref = _routed_ref(x, table, ids, dg, du, dd, O.ORDER_TOKEN)
+    assert nerr(y, ref) <= 1e-2

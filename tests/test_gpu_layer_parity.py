@@ -1,0 +1,246 @@
+"""TRHashEngine on the HIP backend vs the CPU oracle of the universal dispatch.
+
+Bounds (normwise max|got - ref| / max|ref|, the north-star metric): 1e-4 for
+fp32, 2e-2 for bf16, 5e-2 for fp8 (against the oracle run on the engine's own
+dequantised e4m3 weights).  The bf16 cases are compared with an fp32 oracle
+fed the same bf16-rounded inputs and weights.
+"""
+
+import pytest
+import torch
+
+from oracle import trmoe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BOUND = {"fp32": 1e-4, "bf16": 2e-2, "fp8": 5e-2}
+
+
+def _oracle_params(engine, dequant_fp8=False):
+    p = {}
+    names = ["expert_gate", "expert_up", "expert_down"]
+    for n in names:
+        if dequant_fp8:
+            p[n] = O.dequantize_e4m3(getattr(engine, n + "_fp8").cpu(), getattr(engine, n + "_scale").cpu(), 1)
+        else:
+            p[n] = getattr(engine, n).detach().float().cpu()
+    if engine.shared_gate is not None:
+        for n in ("shared_gate", "shared_up", "shared_down"):
+            if dequant_fp8:
+                p[n] = O.dequantize_e4m3(getattr(engine, n + "_fp8").cpu(), getattr(engine, n + "_scale").cpu(), 1)
+            else:
+                p[n] = getattr(engine, n).weight.detach().float().cpu()
+    return p
+
+
+def _oracle(engine, x, ids, rows=None, dequant_fp8=False):
+    cfg = engine.config
+    table = engine._active_route_table.cpu().numpy()
+    p = _oracle_params(engine, dequant_fp8)
+    xr = x.float().cpu()
+    idr = ids.cpu()
+    if rows is not None:
+        xr = xr.reshape(-1, xr.shape[-1])[rows].unsqueeze(0)
+        idr = idr.reshape(-1)[rows].unsqueeze(0)
+    return O.engine_forward(
+        xr, idr, torch.from_numpy(table), p, route_weights=cfg.route_weights,
+        shared_scale=cfg.shared_output_scale, routed_scale=cfg.routed_output_scale,
+        active_experts=engine.active_num_experts, active_width=engine.active_expert_width)
+
+
+def _run(engine, x, ids):
+    from complexity_amd.tr_hash import TRHashBackend
+
+    with torch.no_grad():
+        out = engine(x, ids)
+    torch.cuda.synchronize()
+    assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
+    return out
+
+
+@pytest.mark.parametrize("E", [4, 8])
+def test_reference_fused_shape_fp32(gpu, E):
+    """The reference's own fused-vs-pytorch shape (test_tr_hash_engine.py:328-398)."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(29)
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=16, vocab_size=257, num_experts=E, top_k=2,
+                                             shared_width=24, expert_width=8, precision="fp32",
+                                             backend="hip")).to(gpu)
+    ids = torch.randint(0, 257, (2, 11), device=gpu)
+    x = torch.randn(2, 11, 16, device=gpu)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["fp32"]
+
+
+def test_fp32_residual_with_bf16_expert_weights(gpu):
+    """test_tr_hash_engine.py:401-433: x stays fp32, experts run in bf16."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(31)
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=16, vocab_size=257, num_experts=4, top_k=2,
+                                             shared_width=0, expert_width=8, precision="bf16",
+                                             backend="hip")).to(gpu).to(torch.bfloat16).eval()
+    ids = torch.randint(0, 257, (1, 19), device=gpu)
+    x = torch.randn(1, 19, 16, device=gpu)
+    out = _run(engine, x, ids)
+    assert out.dtype is torch.float32
+    ref = _oracle(engine, x.to(torch.bfloat16), ids)
+    assert O.normwise_rel_err(out, ref) <= BOUND["bf16"]
+
+
+@pytest.mark.parametrize("E,k,weights,S,H,W", [
+    (2, 1, None, 48, 64, 32),
+    (8, 4, None, 40, 24, 12),
+    (16, 4, (0.4, 0.2, 0.2, 0.2), 64, 128, 64),
+    (4, 2, (0.7, 0.3), 0, 96, 64),
+    (16, 2, None, 200, 136, 128),
+])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_engine_shapes(gpu, E, k, weights, S, H, W, dtype):
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(E * 100 + k)
+    cfg = TRHashEngineConfig(hidden_size=H, vocab_size=3001, num_experts=E, top_k=k, shared_width=S,
+                             expert_width=W, routing_strategy="token_id_multi_hash",
+                             route_weights=weights or (), routed_output_scale=2.0, shared_output_scale=0.5,
+                             precision=dtype, backend="hip")
+    engine = TRHashEngine(cfg).to(gpu)
+    if dtype == "bf16":
+        engine = engine.to(torch.bfloat16)
+    ids = torch.randint(-5, 3010, (3, 171), device=gpu)
+    x = torch.randn(3, 171, H, device=gpu)
+    if dtype == "bf16":
+        x = x.to(torch.bfloat16)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND[dtype]
+
+
+def test_c1_fp32_full_size(gpu):
+    from complexity_amd import workloads as Wl
+
+    w = Wl.C1
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x, ids = Wl.make_hidden(w).to(gpu), Wl.make_token_ids(w).to(gpu)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["fp32"]
+
+
+@pytest.mark.parametrize("name", ["c2_bf16_prefill_16384", "c3_bf16_decode_64"])
+def test_bf16_layer_full_size(gpu, name):
+    from complexity_amd import workloads as Wl
+
+    w = Wl.WORKLOADS[name]
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x, ids = Wl.make_hidden(w).to(gpu).to(torch.bfloat16), Wl.make_token_ids(w).to(gpu)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["bf16"]
+
+
+@pytest.mark.parametrize("name", ["c5_fp8_32768", "c5_fp8_32768_active_8x128"])
+def test_fp8_layer_full_size(gpu, name):
+    """Whole layer at N=32768; the oracle checks a fixed sample of 1024 rows
+    (every token's output depends only on its own row and id)."""
+    from complexity_amd import workloads as Wl
+
+    w = Wl.WORKLOADS[name]
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x, ids = Wl.make_hidden(w).to(gpu).to(torch.bfloat16), Wl.make_token_ids(w).to(gpu)
+    out = _run(engine, x, ids)
+    rows = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(0))[:1024]
+    ref = _oracle(engine, x, ids, rows=rows, dequant_fp8=True)
+    got = out.reshape(-1, w.hidden)[rows.to(gpu)]
+    assert O.normwise_rel_err(got, ref.reshape(-1, w.hidden)) <= BOUND["fp8"]
+
+
+def test_fp8_quantisation_matches_oracle(gpu):
+    from complexity_amd import workloads as Wl
+
+    w = Wl.C5
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    for n in ("expert_gate", "expert_down", "shared_up", "shared_down"):
+        master = getattr(engine, n) if n.startswith("expert") else getattr(engine, n).weight
+        q, s = O.quantize_e4m3(master.detach().float().cpu(), 1)
+        assert torch.equal(getattr(engine, n + "_fp8").cpu().view(torch.uint8), q.view(torch.uint8)), n
+        assert torch.equal(getattr(engine, n + "_scale").cpu(), s), n
+
+
+def test_active_capacity_on_hip_matches_oracle_and_restores(gpu):
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(5)
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=64, vocab_size=997, num_experts=8, top_k=2,
+                                             shared_width=96, expert_width=48,
+                                             routing_strategy="token_id_balanced_hash", precision="fp32",
+                                             backend="hip")).to(gpu)
+    ids = torch.randint(0, 997, (2, 50), device=gpu)
+    x = torch.randn(2, 50, 64, device=gpu)
+    full = _run(engine, x, ids)
+    engine.set_active_capacity(num_experts=4, expert_width=20)
+    reduced = _run(engine, x, ids)
+    assert O.normwise_rel_err(reduced, _oracle(engine, x, ids)) <= BOUND["fp32"]
+    assert not torch.allclose(full, reduced)
+    engine.set_active_capacity(num_experts=8, expert_width=48)
+    assert torch.equal(_run(engine, x, ids), full)
+
+
+def test_partition_orders_give_identical_outputs(gpu):
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(9)
+    common = dict(hidden_size=64, vocab_size=997, num_experts=4, top_k=2, shared_width=64, expert_width=64,
+                  precision="fp32")
+    a = TRHashEngine(TRHashEngineConfig(**common, backend="hip")).to(gpu)
+    b = TRHashEngine(TRHashEngineConfig(**common, backend="cggr")).to(gpu)
+    b.load_state_dict(a.state_dict())
+    ids = torch.randint(0, 997, (4, 33), device=gpu)
+    x = torch.randn(4, 33, 64, device=gpu)
+    with torch.no_grad():
+        ya, yb = a(x, ids), b(x, ids)
+    assert a.last_backend.partition == "token" and b.last_backend.partition == "assignment"
+    assert torch.equal(ya, yb)
+
+
+def test_residual_fused_into_down_epilogue(gpu):
+    from complexity_amd import workloads as Wl
+
+    w = Wl.C3
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x, ids = Wl.make_hidden(w).to(gpu).to(torch.bfloat16), Wl.make_token_ids(w).to(gpu)
+    res = torch.randn_like(x)
+    with torch.no_grad():
+        fused = engine.forward_with_residual(x, ids, res)
+        plain = engine(x, ids)
+    assert O.normwise_rel_err(fused, (plain.float() + res.float())) <= 1e-2
+
+
+def test_empty_batch(gpu):
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=16, vocab_size=97, precision="fp32",
+                                             backend="hip")).to(gpu)
+    with torch.no_grad():
+        out = engine(torch.zeros(0, 5, 16, device=gpu), torch.zeros(0, 5, dtype=torch.long, device=gpu))
+    assert out.shape == (0, 5, 16)
+
+
+def test_graph_backend_replays_hip_kernels(gpu):
+    """Captured HIP path: several replays with eager work between them, each
+    checked against the eager result (no memset nodes are recorded)."""
+    from complexity_amd.tr_hash import GraphBucket, TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(11)
+    common = dict(hidden_size=128, vocab_size=997, num_experts=4, top_k=2, shared_width=256, expert_width=64,
+                  precision="bf16", phase="inference")
+    graph = TRHashEngine(TRHashEngineConfig(**common, backend="cuda_graph",
+                                            graph_buckets=(GraphBucket(4, 16),))).to(gpu).to(torch.bfloat16).eval()
+    eager = TRHashEngine(TRHashEngineConfig(**common, backend="hip")).to(gpu).to(torch.bfloat16).eval()
+    eager.load_state_dict(graph.state_dict())
+    with torch.no_grad():
+        for step in range(4):
+            ids = torch.randint(0, 997, (3, 10), device=gpu)
+            x = torch.randn(3, 10, 128, device=gpu, dtype=torch.bfloat16)
+            got = graph(x, ids)
+            _ = torch.randn(1000, device=gpu).sum()  # unrelated eager work
+            torch.cuda.synchronize()
+            assert torch.equal(got, eager(x, ids)), step

@@ -1,0 +1,259 @@
+"""Pin the CPU oracle: golden vectors from the reference, closed forms, brute force.
+
+These run without a GPU.  The oracle is the checker of every GPU parity test,
+so each of its functions is checked here by something other than a retyped
+copy of itself.
+"""
+
+import ctypes
+import hashlib
+import json
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import trmoe_oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def _digest(table):
+    return hashlib.sha256(np.ascontiguousarray(table, dtype=np.int64).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def coracle():
+    lib_path = ROOT / "oracle" / "lib" / "liboracle_route.so"
+    if not lib_path.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "-s"], check=True)
+    lib = ctypes.CDLL(str(lib_path))
+    lib.oracle_mix32.restype = ctypes.c_uint32
+    lib.oracle_mix32.argtypes = [ctypes.c_uint32]
+    lib.oracle_multi_hash_table.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                            ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]
+    lib.oracle_partition.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
+def c_partition(lib, routes, E, order):
+    k, n = routes.shape
+    r = np.ascontiguousarray(routes, dtype=np.int64)
+    s = np.empty(k * n, np.int64)
+    inv = np.empty(k * n, np.int64)
+    off = np.empty(E + 1, np.int32)
+    cnt = np.empty(E, np.int32)
+    st = lib.oracle_partition(r.ctypes.data, n, k, E, order, s.ctypes.data, inv.ctypes.data, off.ctypes.data,
+                              cnt.ctypes.data)
+    assert st == 0
+    return s, inv, off, cnt
+
+
+# ---------------------------------------------------------------------------
+# mix32 / route tables
+# ---------------------------------------------------------------------------
+
+def test_mix32_inverts_through_published_lowbias32_inverse():
+    rng = np.random.default_rng(0)
+    v = np.concatenate([rng.integers(0, 2**32, 100000, dtype=np.uint64),
+                        np.array([0, 1, 2**31, 2**32 - 1], dtype=np.uint64)])
+    assert np.array_equal(O.mix32_inverse(O.mix32(v)), v)
+    assert int(O.mix32(np.array([0], dtype=np.uint64))[0]) == 0
+
+
+def test_c_and_numpy_mix32_agree(coracle):
+    rng = np.random.default_rng(1)
+    for v in rng.integers(0, 2**32, 2000, dtype=np.uint64):
+        assert coracle.oracle_mix32(int(v)) == int(O.mix32(np.array([v]))[0])
+
+
+def test_every_reference_route_digest():
+    data = json.loads((GOLDEN / "route_digests.json").read_text())
+    assert data["route_seed"] == O.DEFAULT_ROUTE_SEED
+    for case in data["cases"]:
+        table = O.route_table(case["strategy"], case["vocab_size"], case["num_experts"], case["top_k"],
+                              case["layer_index"], hash_count=case["hash_count"])
+        assert table[:, :32].tolist() == case["head"], case
+        assert _digest(table) == case["sha256"], case
+
+
+@pytest.mark.parametrize("experts", [4, 8, 16])
+def test_full_v32000_tables_match_reference_and_c_oracle(coracle, experts):
+    golden = np.load(GOLDEN / "route_tables_v32000.npz")[f"multi_e{experts}_l0"].astype(np.int64)
+    numpy_table = O.multi_hash_table(32000, experts, 2, 0)
+    c_table = np.empty((2, 32000), np.int64)
+    assert coracle.oracle_multi_hash_table(32000, experts, 2, 0, O.DEFAULT_ROUTE_SEED, 2,
+                                           c_table.ctypes.data) == 0
+    assert np.array_equal(numpy_table, golden)
+    assert np.array_equal(c_table, golden)
+
+
+def test_multi_hash_has_no_score_ties_at_measured_shapes():
+    """top-k order then never depends on a tie-break rule."""
+    for experts in (4, 8, 16):
+        for layer in (0, 7, 15):
+            s = np.sort(O.multi_hash_scores(32000, experts, layer), axis=1)
+            assert not (s[:, 1:] == s[:, :-1]).any()
+
+
+def test_route_table_invariants_from_reference_tests():
+    """tests/test_tr_hash_engine.py:51-90 on the oracle: distinct and balanced."""
+    for strategy, tol in (("modulo_cyclic", 1), ("token_id_balanced_hash", 1),
+                          ("token_id_affine_hash", 80), ("token_id_multi_hash", 80)):
+        for experts, k in ((2, 1), (4, 2), (8, 4), (16, 4)):
+            t = O.route_table(strategy, 997, experts, k, 3)
+            assert all(len(set(col)) == k for col in t.T.tolist())
+            for row in t:
+                c = np.bincount(row, minlength=experts)
+                assert c.max() - c.min() <= tol
+
+
+def test_pair_metadata_matches_reference_and_round_trips():
+    z = np.load(GOLDEN / "pair_codes_v997.npz")
+    for key in [k for k in z.files if k.endswith("_codes")]:
+        stem = key[: -len("_codes")]
+        routes = z[stem + "_routes"].astype(np.int64)
+        experts = int(stem.rsplit("_e", 1)[1])
+        codes, pairs = O.pair_metadata(routes, experts)
+        assert np.array_equal(codes, z[key])
+        assert np.array_equal(pairs, z[stem + "_pairs"])
+        # decode by the definition: pair index + swap bit
+        swap_bit = 0x8 if len(pairs) <= 8 else 0x20
+        idx = codes & (swap_bit - 1)
+        sw = (codes & swap_bit) != 0
+        dec0 = np.where(sw, pairs[idx, 1], pairs[idx, 0])
+        dec1 = np.where(sw, pairs[idx, 0], pairs[idx, 1])
+        assert np.array_equal(np.stack([dec0, dec1]), routes)
+
+
+# ---------------------------------------------------------------------------
+# counting partition
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("order", [O.ORDER_TOKEN, O.ORDER_ASSIGNMENT])
+@pytest.mark.parametrize("experts,k", [(1, 1), (2, 1), (4, 2), (8, 2), (8, 4), (16, 4), (16, 2)])
+def test_partition_brute_force_numpy_and_c(coracle, order, experts, k):
+    rng = np.random.default_rng(experts * 10 + k + 100 * order)
+    table = O.route_table("token_id_multi_hash" if experts > 1 else "modulo_cyclic", 257, experts, k, 1)
+    for n in (0, 1, 7, 64, 300):
+        ids = rng.integers(-5, 270, n)  # includes out-of-range ids: clamped
+        routes = O.gather_routes(table, ids)
+        s, inv, off, cnt = O.counting_partition(routes, experts, order)
+        assert np.array_equal(s, O.brute_force_partition(routes, experts, order))
+        cs, cinv, coff, ccnt = c_partition(coracle, routes, experts, order)
+        assert np.array_equal(s, cs) and np.array_equal(inv, cinv)
+        assert np.array_equal(off, coff) and np.array_equal(cnt, ccnt)
+        # invariants: permutation, inverse, histogram, segment membership, order
+        assert np.array_equal(np.sort(s), np.arange(k * n))
+        assert np.array_equal(inv[s], np.arange(k * n))
+        flat = routes.reshape(-1)
+        assert np.array_equal(cnt, np.bincount(flat, minlength=experts))
+        for e in range(experts):
+            seg = s[off[e]:off[e + 1]]
+            assert (flat[seg] == e).all()
+            key = seg % max(n, 1) if order == O.ORDER_TOKEN else seg
+            assert (np.diff(key) > 0).all()
+
+
+def test_token_and_assignment_orders_differ_but_share_offsets():
+    table = O.route_table("token_id_multi_hash", 1000, 4, 2, 0)
+    ids = np.arange(0, 1000, 3)
+    routes = O.gather_routes(table, ids)
+    a = O.counting_partition(routes, 4, O.ORDER_TOKEN)
+    b = O.counting_partition(routes, 4, O.ORDER_ASSIGNMENT)
+    assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])
+    assert not np.array_equal(a[0], b[0])
+
+
+# ---------------------------------------------------------------------------
+# floating-point layer
+# ---------------------------------------------------------------------------
+
+def _params(E, H, W, S, seed=0, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    p = {
+        "expert_gate": torch.randn(E, H, W, generator=g, dtype=dtype) * 0.3,
+        "expert_up": torch.randn(E, H, W, generator=g, dtype=dtype) * 0.3,
+        "expert_down": torch.randn(E, W, H, generator=g, dtype=dtype) * 0.3,
+    }
+    if S:
+        p["shared_gate"] = torch.randn(S, H, generator=g, dtype=dtype) * 0.3
+        p["shared_up"] = torch.randn(S, H, generator=g, dtype=dtype) * 0.3
+        p["shared_down"] = torch.randn(H, S, generator=g, dtype=dtype) * 0.3
+    return p
+
+
+@pytest.mark.parametrize("E,k,S,weights,scales", [
+    (2, 1, 12, (1.0,), (1.0, 1.0)),
+    (4, 2, 12, (0.5, 0.5), (1.0, 2.0)),
+    (4, 2, 0, (0.7, 0.3), (0.5, 1.0)),
+    (8, 4, 12, (0.4, 0.2, 0.2, 0.2), (1.0, 1.0)),
+    (16, 4, 12, (0.25,) * 4, (1.0, 1.0)),
+])
+def test_masked_dense_matches_token_loop(E, k, S, weights, scales):
+    """engine.py:66-104 vs the reference test's token-by-token loop."""
+    H, W, V = 8, 4, 101
+    p = _params(E, H, W, S)
+    table = torch.from_numpy(O.route_table("token_id_multi_hash", V, E, k, 0))
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 5, H, generator=g, dtype=torch.float64)
+    ids = torch.randint(-3, V + 3, (2, 5), generator=g)
+    a = O.engine_forward(x, ids, table, p, route_weights=weights, shared_scale=scales[0],
+                         routed_scale=scales[1])
+    b = O.naive_engine_output(x, ids, table, p, route_weights=weights, shared_scale=scales[0],
+                              routed_scale=scales[1])
+    assert torch.allclose(a, b, atol=1e-12, rtol=1e-12)
+
+
+def test_shared_swiglu_matches_explicit_formula():
+    H, S = 6, 10
+    p = _params(1, H, 4, S)
+    x = torch.randn(7, H, dtype=torch.float64)
+    got = O.shared_swiglu(x, p["shared_gate"], p["shared_up"], p["shared_down"])
+    for t in range(7):
+        g = sum(p["shared_gate"][:, i] * x[t, i] for i in range(H))
+        u = sum(p["shared_up"][:, i] * x[t, i] for i in range(H))
+        h = g / (1 + torch.exp(-g)) * u
+        ref = torch.stack([sum(p["shared_down"][c, j] * h[j] for j in range(S)) for c in range(H)])
+        assert torch.allclose(got[t], ref, atol=1e-12)
+
+
+def test_active_capacity_slices_prefix():
+    H, W, S, V = 8, 6, 0, 97
+    p = _params(8, H, W, S)
+    table4 = torch.from_numpy(O.route_table("token_id_multi_hash", V, 4, 2, 0))
+    x = torch.randn(1, 9, H, dtype=torch.float64)
+    ids = torch.arange(9).view(1, 9)
+    full = {k2: v for k2, v in p.items()}
+    got = O.engine_forward(x, ids, table4, full, route_weights=(0.5, 0.5), active_experts=4, active_width=3)
+    sliced = {"expert_gate": p["expert_gate"][:4, :, :3], "expert_up": p["expert_up"][:4, :, :3],
+              "expert_down": p["expert_down"][:4, :3, :]}
+    ref = O.naive_engine_output(x, ids, table4, sliced, route_weights=(0.5, 0.5))
+    assert torch.allclose(got, ref, atol=1e-12)
+
+
+def test_e4m3_decode_table_matches_torch_float8():
+    codes = torch.arange(256, dtype=torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    mine = O.e4m3_decode_table()
+    nan = np.isnan(mine)
+    assert np.array_equal(nan, np.isnan(ref))
+    assert np.array_equal(mine[~nan], ref[~nan])
+    assert mine[0x7E] == 448.0 and mine[0x01] == 2.0 ** -9
+
+
+def test_quantize_e4m3_scale_and_error_bound():
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(3, 64, 16, generator=g) * 0.02
+    q, s = O.quantize_e4m3(w, 1)
+    assert s.shape == (3, 16)
+    deq = O.dequantize_e4m3(q, s, 1)
+    assert torch.allclose(w.abs().amax(dim=1), deq.abs().amax(dim=1), rtol=1e-6, atol=0)
+    # e4m3 has a 3-bit mantissa: relative rounding error <= 2^-4 for normal values
+    rel = ((deq - w).abs() / w.abs().clamp_min(1e-30))
+    normal = w.abs() >= s.unsqueeze(1) * 2.0 ** -6
+    assert rel[normal].max() <= 2.0 ** -4 + 1e-6

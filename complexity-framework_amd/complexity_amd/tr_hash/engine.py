@@ -93,8 +93,12 @@ def reference_topk_swiglu(
 
 
 def _quantize_e4m3(weight: torch.Tensor):
-    """Per-output-channel e4m3: scale = amax/448 over dim 1 (the reduction axis)."""
-    w = weight.detach().float()
+    """Per-output-channel e4m3: scale = amax/448 over dim 1 (the reduction axis).
+
+    Computed on the host so the stored codes do not depend on the device's
+    division and conversion rounding (checkpoints are reproducible).
+    """
+    w = weight.detach().float().cpu()
     amax = w.abs().amax(dim=1, keepdim=True)
     scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
     q = (w / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)

@@ -218,8 +218,7 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     a.y = y;
     a.ldy = ldy;
     a.x_vec_ok = aligned16(x) && (ldx % epc == 0);
-    const int64_t max_tiles = (n_tokens * top_k + 127) / 128 + num_experts;
-    return launch_routed(act_dtype, w_dtype, a, max_tiles, as_stream(stream));
+    return launch_routed(act_dtype, w_dtype, a, n_tokens * top_k, as_stream(stream));
 }
 
 int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,

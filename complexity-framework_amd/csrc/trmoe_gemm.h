@@ -99,7 +99,7 @@ int launch_pack(const PackArgs& p, hipStream_t stream);
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
 int launch_down_combine(int act, int wdt, const DownArgs& a, int64_t packed_rows, hipStream_t stream);
 int routed_lds_bytes(int act, int64_t f_pad);
-int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t max_tiles, hipStream_t stream);
+int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t assignments, hipStream_t stream);
 int launch_combine(int act, const CombineArgs& a, hipStream_t stream);
 
 }  // namespace trmoe

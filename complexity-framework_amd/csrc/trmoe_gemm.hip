@@ -226,9 +226,8 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
 // token rows against 64-feature chunks of the expert's packed gate|up rows and
 // leaves h (128 rows x F_pad features) in LDS in the operand layout; phase 2
 // streams the expert's packed down rows in 128-column chunks against it.
-template <class Kind, bool FP8>
+template <class Kind, bool FP8, class Shape>
 __global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
-    using Shape = ShapeMain;
     using T = typename Kind::T;
     constexpr int SE = Kind::kStageElems;
     constexpr int EPC = Kind::kPerChunk;
@@ -405,28 +404,47 @@ int launch_down_combine(int act, int wdt, const DownArgs& a, int64_t packed_rows
     return check_launch("shared_down_combine");
 }
 
-int routed_lds_bytes(int act, int64_t f_pad) {
+// 64-row tiles halve the LDS-resident h for wide fp32 experts.
+using ShapeRoutedSmall = TileShape<64, 128, 2>;
+
+template <class Shape>
+static int routed_lds_bytes_for(int act, int64_t f_pad) {
     const int64_t per_row = (act == TRMOE_F32) ? 4 * f_pad : 2 * f_pad;
-    return ShapeMain::kLdsBytes + (int)(ShapeMain::BM * per_row);
+    return Shape::kLdsBytes + (int)(Shape::BM * per_row);
 }
 
-int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t max_tiles, hipStream_t stream) {
-    const int lds = routed_lds_bytes(act, a.F_pad);
-    dim3 grid((unsigned)max_tiles);
-    int st;
-    if (act == TRMOE_F32 && wdt == TRMOE_F32) {
-        if ((st = ensure_lds(k_routed_experts<KindF32, false>, lds))) return st;
-        hipLaunchKernelGGL((k_routed_experts<KindF32, false>), grid, dim3(kThreads), lds, stream, a);
-    } else if (act == TRMOE_BF16 && wdt == TRMOE_BF16) {
-        if ((st = ensure_lds(k_routed_experts<KindBF16, false>, lds))) return st;
-        hipLaunchKernelGGL((k_routed_experts<KindBF16, false>), grid, dim3(kThreads), lds, stream, a);
-    } else if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) {
-        if ((st = ensure_lds(k_routed_experts<KindBF16, true>, lds))) return st;
-        hipLaunchKernelGGL((k_routed_experts<KindBF16, true>), grid, dim3(kThreads), lds, stream, a);
-    } else {
-        return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: unsupported dtype pair");
-    }
+constexpr int kMaxLdsBytes = 160 * 1024;
+
+int routed_lds_bytes(int act, int64_t f_pad) {
+    const int big = routed_lds_bytes_for<ShapeMain>(act, f_pad);
+    return big <= kMaxLdsBytes ? big : routed_lds_bytes_for<ShapeRoutedSmall>(act, f_pad);
+}
+
+template <class Kind, bool FP8, class Shape>
+static int launch_routed_shape(int act, const RoutedArgs& a, int64_t assignments, hipStream_t stream) {
+    const int lds = routed_lds_bytes_for<Shape>(act, a.F_pad);
+    // tiles of all segments <= ceil(assignments / BM) + one partial tile per expert
+    const int64_t max_tiles = (assignments + Shape::BM - 1) / Shape::BM + a.E;
+    int st = ensure_lds(k_routed_experts<Kind, FP8, Shape>, lds);
+    if (st) return st;
+    hipLaunchKernelGGL((k_routed_experts<Kind, FP8, Shape>), dim3((unsigned)max_tiles), dim3(kThreads), lds,
+                       stream, a);
     return check_launch("routed_experts");
+}
+
+template <class Kind, bool FP8>
+static int launch_routed_kind(int act, const RoutedArgs& a, int64_t assignments, hipStream_t stream) {
+    if (routed_lds_bytes_for<ShapeMain>(act, a.F_pad) <= kMaxLdsBytes)
+        return launch_routed_shape<Kind, FP8, ShapeMain>(act, a, assignments, stream);
+    return launch_routed_shape<Kind, FP8, ShapeRoutedSmall>(act, a, assignments, stream);
+}
+
+int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t assignments, hipStream_t stream) {
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) return launch_routed_kind<KindF32, false>(act, a, assignments, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return launch_routed_kind<KindBF16, false>(act, a, assignments, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3)
+        return launch_routed_kind<KindBF16, true>(act, a, assignments, stream);
+    return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: unsupported dtype pair");
 }
 
 int launch_combine(int act, const CombineArgs& a, hipStream_t stream) {

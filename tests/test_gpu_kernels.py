@@ -80,7 +80,7 @@ def test_shared_gate_up_unaligned_rows(gpu):
     N, H, S = 77, 36, 64
     base = _rand(N, H + 3, seed=4).to(torch.bfloat16)
     x = base[:, 1 : H + 1]  # misaligned view
-    wg, wu = _rand(S, H, 0.1, 5).to(torch.bfloat16), _rand(S, H, 0.1, 6).to(torch.bfloat16)
+    wg, wu = _rand(S, H, scale=0.1, seed=5).to(torch.bfloat16), _rand(S, H, scale=0.1, seed=6).to(torch.bfloat16)
     pg, _ = ops.pack_linear_gate_up(wg.to(gpu), wu.to(gpu))
     xg = base.to(gpu)[:, 1 : H + 1]
     h = ops.shared_gate_up(xg, pg, None, S).cpu()
@@ -93,7 +93,7 @@ def test_shared_gate_up_fp8_weights(gpu):
 
     N, H, S = 300, 256, 256
     x = _rand(N, H, seed=7).to(torch.bfloat16)
-    wg, wu = _rand(S, H, 0.02, 8), _rand(S, H, 0.02, 9)
+    wg, wu = _rand(S, H, scale=0.02, seed=8), _rand(S, H, scale=0.02, seed=9)
     qg, sg = O.quantize_e4m3(wg, 1)
     qu, su = O.quantize_e4m3(wu, 1)
     pg, ps = ops.pack_linear_gate_up(qg.to(gpu), qu.to(gpu), sg.to(gpu), su.to(gpu))
@@ -110,7 +110,7 @@ def test_shared_down_combine(gpu, dtype, with_y, with_res):
 
     N, S, H, k = 333, 320, 200, 2
     h = _rand(N, S, seed=10).to(dtype)
-    wd = _rand(H, S, 0.05, 11).to(dtype)
+    wd = _rand(H, S, scale=0.05, seed=11).to(dtype)
     pd, _ = ops.pack_linear_down(wd.to(gpu))
     hpad = torch.zeros(N, (S + 127) // 128 * 128, dtype=dtype)
     hpad[:, :S] = h

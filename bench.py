@@ -36,15 +36,17 @@ PEAK = {"bf16": 2500.0, "fp8": 2500.0, "fp32": 157.3}   # dense TFLOP/s (fp8 wei
 HBM_PEAK = 8000.0                                         # GB/s
 
 
-def _kernel_work(w, n_tokens):
-    """Algorithmic FLOPs and bytes per launch of each kernel (intermediates excluded
-    from the layer total, included per kernel since each kernel must move them)."""
+def _kernel_work(w, n_tokens, strategy):
+    """Algorithmic FLOPs and bytes per launch of each kernel.  FLOPs count only
+    the useful work of the layer (6 N H (S + k W) in total, split by kernel);
+    the dense-routed kernels also execute the masked experts, which is not
+    credited.  Bytes count each kernel's operands and outputs once."""
     H, S, E, k = w.hidden, w.shared, w.active_experts or w.experts, w.top_k
     Wd = w.active_width or w.width
     act = 4 if w.dtype == "fp32" else 2
     wb = {"fp32": 4, "bf16": 2, "fp8": 1}[w.dtype]
     N = n_tokens
-    return {
+    work = {
         "route_sort": dict(flops=0.0, bytes=8 * N + 8 * k * N * 2 + 8 * k * N),
         "routed_experts": dict(flops=6.0 * N * H * k * Wd,
                                bytes=act * k * N * H + wb * 3 * E * H * Wd + act * k * N * H),
@@ -52,12 +54,20 @@ def _kernel_work(w, n_tokens):
         "shared_down_combine": dict(flops=2.0 * N * S * H,
                                     bytes=act * N * S + wb * S * H + act * k * N * H + act * N * H),
     }
+    if strategy == "dense":
+        F = S + E * Wd
+        work["dense_routed_gate_up"] = dict(flops=4.0 * N * H * (S + k * Wd),
+                                            bytes=act * N * H + wb * 2 * F * H + act * N * F)
+        work["shared_down_combine"] = dict(flops=2.0 * N * H * (S + k * Wd),
+                                           bytes=act * N * F + wb * F * H + act * N * H)
+    return work
 
 
 class KernelTimer:
     """Wraps the ops entry points so every launch is bracketed by events."""
 
-    NAMES = ("route_sort", "routed_experts", "shared_gate_up", "shared_down_combine", "combine")
+    NAMES = ("route_sort", "routed_experts", "shared_gate_up", "shared_down_combine", "combine",
+             "dense_routed_gate_up")
 
     def __init__(self, ops, torch):
         self.ops, self.torch = ops, torch
@@ -173,6 +183,55 @@ def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 30, warmup:
     }
 
 
+def time_engine(torch, engine, x, ids, steps, warmup, timer):
+    """K timed forwards after W warm-ups; per-kernel averages from the events."""
+    from complexity_amd.tr_hash import TRHashBackend
+
+    timer.events = {n: [] for n in timer.NAMES}
+    with torch.no_grad():
+        for _ in range(warmup):
+            engine(x, ids)
+        assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
+        torch.cuda.synchronize()
+        timer.enabled = True
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            engine(x, ids)
+        stop.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        timer.enabled = False
+    return start.elapsed_time(stop) / steps, timer.averages_ms(), wall, engine._packed.strategy
+
+
+def kernel_report(w, kernel_ms, strategy):
+    work = _kernel_work(w, w.tokens, strategy)
+    kernels = {}
+    for name, ms in kernel_ms.items():
+        wk = work.get(name, dict(flops=0.0, bytes=0.0))
+        kernels[name] = {
+            "avg_us": ms * 1e3,
+            "tflops": wk["flops"] / (ms * 1e-3) / 1e12 if wk["flops"] else 0.0,
+            "gbps": wk["bytes"] / (ms * 1e-3) / 1e9,
+        }
+    dominant = max(kernel_ms, key=kernel_ms.get)
+    dwk = work[dominant]
+    dms = kernel_ms[dominant]
+    if dwk["flops"]:
+        achieved = dwk["flops"] / (dms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK[w.dtype], "unit": "TFLOP/s",
+                "frac": achieved / PEAK[w.dtype], "traffic": None, "kernel": dominant,
+                "algorithmic_flops_per_launch": dwk["flops"], "avg_us": dms * 1e3}
+    else:
+        achieved = dwk["bytes"] / (dms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK, "traffic": None, "kernel": dominant,
+                "algorithmic_bytes_per_launch": dwk["bytes"], "avg_us": dms * 1e3}
+    return kernels, dominant, roof
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,48 +263,19 @@ def main():
     ids = workloads.make_token_ids(w).to(dev)
 
     timer = KernelTimer(ops, torch)
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            engine(x, ids)
-        assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
-        torch.cuda.synchronize()
-        timer.enabled = True
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        start.record()
-        for _ in range(args.steps):
-            engine(x, ids)
-        stop.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        timer.enabled = False
-    ms_per_step = start.elapsed_time(stop) / args.steps
-    kernel_ms = timer.averages_ms()
+    ms_per_step, kernel_ms, wall, strategy = time_engine(torch, engine, x, ids, args.steps, args.warmup, timer)
+    kernels, dominant, roof = kernel_report(w, kernel_ms, strategy)
+    secondary = {}
+    other = "grouped" if strategy == "dense" else None
+    if other is not None:
+        engine.routed_strategy = other
+        ms2, kms2, _, _ = time_engine(torch, engine, x, ids, args.steps, args.warmup, timer)
+        k2, _, _ = kernel_report(w, kms2, other)
+        secondary = {"strategy": other, "ms_per_step": ms2, "tokens_per_s": w.tokens / (ms2 * 1e-3),
+                     "kernels": k2}
+        engine.routed_strategy = "auto"
     timer.restore()
-
     tokens = w.tokens
-    work = _kernel_work(w, tokens)
-    kernels = {}
-    for name, ms in kernel_ms.items():
-        wk = work.get(name, dict(flops=0.0, bytes=0.0))
-        kernels[name] = {
-            "avg_us": ms * 1e3,
-            "tflops": wk["flops"] / (ms * 1e-3) / 1e12 if wk["flops"] else 0.0,
-            "gbps": wk["bytes"] / (ms * 1e-3) / 1e9,
-        }
-    dominant = max(kernel_ms, key=kernel_ms.get)
-    dwk = work[dominant]
-    dms = kernel_ms[dominant]
-    if dwk["flops"]:
-        achieved = dwk["flops"] / (dms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK[w.dtype], "unit": "TFLOP/s",
-                "frac": achieved / PEAK[w.dtype], "traffic": None, "kernel": dominant,
-                "algorithmic_flops_per_launch": dwk["flops"], "avg_us": dms * 1e3}
-    else:
-        achieved = dwk["bytes"] / (dms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK, "traffic": None, "kernel": dominant,
-                "algorithmic_bytes_per_launch": dwk["bytes"], "avg_us": dms * 1e3}
 
     layer_tflops = w.flops() / (ms_per_step * 1e-3) / 1e12
     result = {
@@ -267,8 +297,10 @@ def main():
         "layer_tflops": layer_tflops,
         "layer_mfma_frac": layer_tflops / PEAK[w.dtype],
         "wall_s_timed": wall,
+        "strategy": strategy,
         "kernels": kernels,
         "roofline": roof,
+        "other_strategy": secondary,
         "backend": engine.last_backend.selected.value,
         "device": torch.cuda.get_device_name(0),
     }

@@ -38,7 +38,13 @@ SIGNATURES = {
     "trmoe_pack_weight": (
         _c_int,
         [_c_int, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-         _c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp],
+         _c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp],
+    ),
+    "trmoe_dense_routed_features": (_c_i64, [_c_i64, _c_int, _c_i64]),
+    "trmoe_dense_routed_gate_up": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_i64, _c_vp,
+         _c_vp, _c_i64, _c_int, _c_vp, _c_float, _c_float, _c_vp, _c_i64, _c_vp],
     ),
     "trmoe_route_sort_workspace_bytes": (_c_size, [_c_i64, _c_int, _c_int, _c_int]),
     "trmoe_route_sort": (

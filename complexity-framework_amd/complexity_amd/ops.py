@@ -22,7 +22,7 @@ ORDER_ASSIGNMENT = N.ORDER_ASSIGNMENT
 # Padding the packed layouts use (must match the kernel tiles).
 SHARED_GATE_UP_ALIGN = 256   # rows = 2 * round_up(S, 128)
 EXPERT_GATE_UP_ALIGN = 128   # rows = 2 * round_up(W, 64)
-DOWN_ALIGN = 128             # rows = round_up(H, 128)
+DOWN_ALIGN = 256             # rows = round_up(H, 256)
 
 _DTYPES = {torch.float32: N.F32, torch.bfloat16: N.BF16, torch.float8_e4m3fn: N.FP8_E4M3}
 
@@ -48,6 +48,22 @@ def _stream(t: torch.Tensor):
 
 def _lib():
     return N.load()
+
+
+def rows16(x: torch.Tensor) -> torch.Tensor:
+    """x[n, k] laid out as the kernels read activations: 16-byte-aligned rows,
+    a row stride that is a multiple of 16 bytes, and zeros between k and the
+    next multiple of 16 bytes (the kernels load whole 16-byte chunks).
+    Returns x itself when it already qualifies, else a zero-padded copy."""
+    elem = x.element_size()
+    n, k = x.shape
+    if (x.stride(1) == 1 and x.data_ptr() % 16 == 0 and (x.stride(0) * elem) % 16 == 0
+            and (k * elem) % 16 == 0):
+        return x
+    ld = _round_up(k * elem, 16) // elem
+    padded = torch.zeros(n, ld, dtype=x.dtype, device=x.device)
+    padded[:, :k] = x
+    return padded[:, :k]
 
 
 def _require_cuda(*tensors):
@@ -104,12 +120,16 @@ def pack_dims(kind: int, out_features: int, in_features: int, row_align: int) ->
 
 
 def _pack(kind: int, a: torch.Tensor, b: Optional[torch.Tensor], groups: int, out_f: int, in_f: int,
-          strides: Tuple[int, int, int], row_align: int, scale_a=None, scale_b=None):
-    """Scales are [groups, out_f] (or [out_f] for one group); made contiguous here."""
+          strides: Tuple[int, int, int], row_align: int, scale_a=None, scale_b=None,
+          into: Optional[torch.Tensor] = None, dst_ld: int = 0, dst_group_stride: int = 0):
+    """Scales are [groups, out_f] (or [out_f] for one group); made contiguous here.
+
+    ``into`` (a view whose data pointer is the first packed element) writes
+    the groups into a larger packed tensor with the given element strides."""
     lib = _lib()
     _require_cuda(a, b)
     rows, cols = pack_dims(kind, out_f, in_f, row_align)
-    dst = torch.empty(groups, rows, cols, dtype=a.dtype, device=a.device)
+    dst = torch.empty(groups, rows, cols, dtype=a.dtype, device=a.device) if into is None else into
     dst_scale = None
     scale_stride = 0
     if scale_a is not None:
@@ -119,7 +139,8 @@ def _pack(kind: int, a: torch.Tensor, b: Optional[torch.Tensor], groups: int, ou
         scale_stride = out_f
     st = lib.trmoe_pack_weight(kind, dtype_code(a.dtype), _p(a), _p(b), groups, out_f, in_f,
                                strides[0], strides[1], strides[2], _p(scale_a), _p(scale_b),
-                               scale_stride, row_align, _p(dst), _p(dst_scale), _stream(a))
+                               scale_stride, row_align, _p(dst), dst_ld, dst_group_stride, _p(dst_scale), 0,
+                               _stream(a))
     N.check(st, "trmoe_pack_weight")
     return dst, dst_scale
 
@@ -135,7 +156,7 @@ def pack_linear_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor, scale_gate=Non
 
 
 def pack_linear_down(w_down: torch.Tensor, scale=None):
-    """nn.Linear weight [H, S] -> packed [round_up(H,128), round_up(S,8)]."""
+    """nn.Linear weight [H, S] -> packed [round_up(H,256), round_up(S,8)]."""
     H, S = w_down.shape
     dst, sc = _pack(N.PACK_PLAIN, w_down, None, 1, H, S, (0, w_down.stride(0), w_down.stride(1)),
                     DOWN_ALIGN, scale, None)
@@ -153,10 +174,69 @@ def pack_expert_gate_up(gate: torch.Tensor, up: torch.Tensor, scale_gate=None, s
 
 
 def pack_expert_down(down: torch.Tensor, scale=None):
-    """Expert down [E, W, H] -> packed [E, round_up(H,128), round_up(W,8)]; scale [E, H]."""
+    """Expert down [E, W, H] -> packed [E, round_up(H,256), round_up(W,8)]; scale [E, H]."""
     E, W, H = down.shape
     return _pack(N.PACK_PLAIN, down, None, E, H, W, (down.stride(0), down.stride(2), down.stride(1)),
                  DOWN_ALIGN, scale, None)
+
+
+def dense_routed_features(shared_width: int, num_experts: int, expert_width: int) -> int:
+    return int(_lib().trmoe_dense_routed_features(shared_width, num_experts, expert_width))
+
+
+def pack_dense_routed(shared_gate, shared_up, shared_down, gate, up, down):
+    """Fused weights of the dense-routed strategy (bf16 / f32 only).
+
+    gate|up: shared features then each expert's, GATE_UP-interleaved,
+    [2F, round_up(H, 8)]; down: [round_up(H, 256), F] with shared_down.weight
+    in columns [0, S) and expert e's down^T at column round_up(S,128) +
+    e*round_up(W,64).  F = dense_routed_features(S, E, W); gaps are zero.
+    Expert tensors may be active-capacity slices [E', H, W'] / [E', W', H]."""
+    E, H, W = gate.shape
+    S = 0 if shared_gate is None else shared_gate.shape[0]
+    F = dense_routed_features(S, E, W)
+    s_pad, w_pad = _round_up(S, 128), _round_up(W, 64)
+    cols = _round_up(H, 8)
+    dev, dt = gate.device, gate.dtype
+    gu = torch.zeros(2 * F, cols, dtype=dt, device=dev)
+    dd = torch.zeros(_round_up(H, DOWN_ALIGN), F, dtype=dt, device=dev)
+    if S:
+        if shared_up.stride() != shared_gate.stride():
+            raise ValueError("shared gate and up weights must have the same strides")
+        _pack(N.PACK_GATE_UP, shared_gate, shared_up, 1, S, H, (0, shared_gate.stride(0), shared_gate.stride(1)),
+              SHARED_GATE_UP_ALIGN, into=gu, dst_ld=cols)
+        _pack(N.PACK_PLAIN, shared_down, None, 1, H, S, (0, shared_down.stride(0), shared_down.stride(1)),
+              DOWN_ALIGN, into=dd, dst_ld=F)
+    if up.stride() != gate.stride():
+        raise ValueError("gate and up expert weights must have the same strides")
+    _pack(N.PACK_GATE_UP, gate, up, E, W, H, (gate.stride(0), gate.stride(2), gate.stride(1)),
+          EXPERT_GATE_UP_ALIGN, into=gu[2 * s_pad:], dst_ld=cols, dst_group_stride=2 * w_pad * cols)
+    _pack(N.PACK_PLAIN, down, None, E, H, W, (down.stride(0), down.stride(2), down.stride(1)),
+          DOWN_ALIGN, into=dd[:, s_pad:], dst_ld=F, dst_group_stride=w_pad)
+    return gu, dd, F
+
+
+def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: int, num_experts: int,
+                         expert_width: int, token_ids: torch.Tensor, route_table: torch.Tensor,
+                         route_weights: Sequence[float], shared_scale: float, routed_scale: float) -> torch.Tensor:
+    """h_ext[N, F]: shared SwiGLU features and route-weighted expert features."""
+    lib = _lib()
+    _require_cuda(x, w_packed, token_ids, route_table)
+    x = rows16(x)
+    n, hidden = x.shape
+    F = dense_routed_features(shared_width, num_experts, expert_width)
+    ids = token_ids.reshape(-1)
+    ids = (ids if ids.dtype == torch.int64 else ids.to(torch.int64)).contiguous()
+    table = route_table.contiguous()
+    h = torch.empty(n, F, dtype=x.dtype, device=x.device)
+    rw = _weights_arg(route_weights)
+    st = lib.trmoe_dense_routed_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
+                                        x.stride(0), _p(w_packed), None, shared_width, num_experts, expert_width,
+                                        _p(ids), _p(table), table.shape[1], table.shape[0],
+                                        ctypes.cast(rw, ctypes.c_void_p), float(shared_scale),
+                                        float(routed_scale), _p(h), F, _stream(x))
+    N.check(st, "trmoe_dense_routed_gate_up")
+    return h
 
 
 # ---------------------------------------------------------------------------
@@ -168,6 +248,7 @@ def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[to
     """h[N, round_up(S,128)] = silu(x Wg^T) * (x Wu^T)."""
     lib = _lib()
     _require_cuda(x, w_packed)
+    x = rows16(x)
     n, hidden = x.shape
     ldh = _round_up(shared_width, 128)
     h = torch.empty(n, ldh, dtype=x.dtype, device=x.device)
@@ -184,6 +265,7 @@ def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Ten
     """y[k*N, H] in partition order."""
     lib = _lib()
     _require_cuda(x, sorted_idx, offsets, w_gate_up, w_down)
+    x = rows16(x)
     n, hidden = x.shape
     y = torch.empty(top_k * n, hidden, dtype=x.dtype, device=x.device)
     st = lib.trmoe_routed_experts(dtype_code(x.dtype), dtype_code(w_gate_up.dtype), _p(x), n, hidden,
@@ -236,32 +318,62 @@ def combine(y: torch.Tensor, inverse: torch.Tensor, n_tokens: int, top_k: int,
 # whole layer
 # ---------------------------------------------------------------------------
 
+STRATEGY_GROUPED = "grouped"
+STRATEGY_DENSE = "dense"
+
+
+def choose_strategy(shared_width: int, num_experts: int, expert_width: int, top_k: int, fp8: bool) -> str:
+    """Dense-routed when computing every expert for every token costs at most
+    8% more MFMA work than the routed experts' own share (and the weights are
+    not e4m3: the fused down rows would mix per-block scales)."""
+    if fp8:
+        return STRATEGY_GROUPED
+    extra = (num_experts - top_k) * expert_width
+    useful = shared_width + top_k * expert_width
+    return STRATEGY_DENSE if extra <= 0.08 * useful else STRATEGY_GROUPED
+
+
 @dataclass
 class PackedLayer:
     """Weights of one layer in kernel layout (built by TRHashEngine)."""
 
     act_dtype: torch.dtype
-    expert_gate_up: torch.Tensor
-    expert_gate_up_scale: Optional[torch.Tensor]
-    expert_down: torch.Tensor
-    expert_down_scale: Optional[torch.Tensor]
     num_experts: int
     expert_width: int
+    strategy: str = STRATEGY_GROUPED
+    expert_gate_up: Optional[torch.Tensor] = None
+    expert_gate_up_scale: Optional[torch.Tensor] = None
+    expert_down: Optional[torch.Tensor] = None
+    expert_down_scale: Optional[torch.Tensor] = None
     shared_width: int = 0
     shared_gate_up: Optional[torch.Tensor] = None
     shared_gate_up_scale: Optional[torch.Tensor] = None
     shared_down: Optional[torch.Tensor] = None
     shared_down_scale: Optional[torch.Tensor] = None
+    dense_gate_up: Optional[torch.Tensor] = None     # dense-routed fused weights
+    dense_down: Optional[torch.Tensor] = None
+    dense_features: int = 0
 
 
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
                   route_weights: Sequence[float], shared_scale: float, routed_scale: float,
                   order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual) -- K1..K4."""
+    """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual).
+
+    grouped: K1 partition, K3 grouped experts, K2 shared gate|up, K4 down with
+    the un-permute in its epilogue.  dense: fused gate|up over shared and
+    expert features with route-weighted expert outputs, then one down GEMM."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
     if n == 0:
         return torch.empty(0, hidden, dtype=x.dtype, device=x.device)
+    x = rows16(x)
+    if packed.strategy == STRATEGY_DENSE:
+        h = dense_routed_gate_up(x, packed.dense_gate_up, packed.shared_width, packed.num_experts,
+                                 packed.expert_width, token_ids, route_table, route_weights, shared_scale,
+                                 routed_scale)
+        return shared_down_combine(h, packed.dense_features, packed.dense_down, None, hidden, None, None,
+                                   top_k, route_weights, 1.0, 1.0, residual)
     sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, packed.num_experts, order)
     y = routed_experts(x, sorted_idx, offsets, packed.num_experts, top_k, packed.expert_gate_up,
                        packed.expert_gate_up_scale, packed.expert_down, packed.expert_down_scale,

@@ -143,6 +143,11 @@ class TRHashEngine(nn.Module):
         self._packed_key = None
         self._packed: Optional[ops.PackedLayer] = None
         self._fp8 = False
+        # HIP routed-expert strategy: "grouped" (route partition + grouped
+        # expert GEMMs + un-permute in the down epilogue), "dense" (every
+        # expert folded into the shared GEMMs, masked by route weights) or
+        # "auto" (dense when it adds at most 8% MFMA work).
+        self.routed_strategy = "auto"
         if config.precision is TRHashPrecision.FP8:
             self.quantize_fp8_()
 
@@ -339,15 +344,40 @@ class TRHashEngine(nn.Module):
         """Weights in kernel layout, rebuilt when a source tensor or the active
         capacity changes (keyed on storage pointer and in-place version)."""
         srcs = self._hip_sources()
+        E, W = self._active_num_experts, self._active_expert_width
+        strategy = self.routed_strategy
+        if strategy == "auto":
+            strategy = ops.choose_strategy(self.config.shared_width, E, W, self.config.top_k, self._fp8)
+        if strategy == ops.STRATEGY_DENSE and self._fp8:
+            raise NotImplementedError("the dense-routed strategy needs bf16/f32 weights")
         key = (
             tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in srcs),
-            self._active_num_experts,
-            self._active_expert_width,
+            E,
+            W,
+            strategy,
         )
         if self._packed is not None and self._packed_key == key:
             return self._packed
-        E, W = self._active_num_experts, self._active_expert_width
         with torch.no_grad():
+            if strategy == ops.STRATEGY_DENSE:
+                shared = (None, None, None)
+                if self.shared_gate is not None:
+                    shared = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight)
+                gu, dd, feats = ops.pack_dense_routed(
+                    *shared, self.expert_gate[:E, :, :W], self.expert_up[:E, :, :W], self.expert_down[:E, :W, :]
+                )
+                packed = ops.PackedLayer(
+                    act_dtype=self._hip_act_dtype(),
+                    num_experts=E,
+                    expert_width=W,
+                    strategy=strategy,
+                    shared_width=self.config.shared_width,
+                    dense_gate_up=gu,
+                    dense_down=dd,
+                    dense_features=feats,
+                )
+                self._packed, self._packed_key = packed, key
+                return packed
             if self._fp8:
                 gq, gs = self.expert_gate_fp8[:E, :, :W], self.expert_gate_scale[:E, :W]
                 uq, us = self.expert_up_fp8[:E, :, :W], self.expert_up_scale[:E, :W]
@@ -359,12 +389,13 @@ class TRHashEngine(nn.Module):
                 ed, ed_s = ops.pack_expert_down(self.expert_down[:E, :W, :])
             packed = ops.PackedLayer(
                 act_dtype=self._hip_act_dtype(),
+                num_experts=E,
+                expert_width=W,
+                strategy=ops.STRATEGY_GROUPED,
                 expert_gate_up=egu,
                 expert_gate_up_scale=egu_s,
                 expert_down=ed,
                 expert_down_scale=ed_s,
-                num_experts=E,
-                expert_width=W,
             )
             if self.shared_gate is not None:
                 packed.shared_width = self.config.shared_width

@@ -41,6 +41,12 @@ static int elem_bytes(int dtype) {
     }
 }
 
+// Activation rows are read as whole 16-byte chunks through buffer loads whose
+// ranges stay below 2^31 bytes.
+static bool rows_ok(const void* p, int64_t ld, int elem) {
+    return aligned16(p) && (ld * elem) % 16 == 0 && ld * elem < ((int64_t)1 << 23);
+}
+
 static bool valid_pair(int act, int wdt) {
     return (act == TRMOE_F32 && wdt == TRMOE_F32) || (act == TRMOE_BF16 && wdt == TRMOE_BF16) ||
            (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3);
@@ -84,7 +90,8 @@ int trmoe_pack_dims(int kind, int64_t out_features, int64_t in_features, int64_t
 int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b, int64_t groups,
                       int64_t out_features, int64_t in_features, int64_t s_group, int64_t s_out,
                       int64_t s_in, const float* scale_a, const float* scale_b,
-                      int64_t scale_group_stride, int64_t row_align, void* dst, float* dst_scale,
+                      int64_t scale_group_stride, int64_t row_align, void* dst, int64_t dst_ld,
+                      int64_t dst_group_stride, float* dst_scale, int64_t dst_scale_group_stride,
                       void* stream) {
     int64_t rows = 0, cols = 0;
     int st = trmoe_pack_dims(kind, out_features, in_features, row_align, &rows, &cols);
@@ -116,6 +123,10 @@ int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b,
     p.dst_scale = dst_scale;
     p.dst_rows = rows;
     p.dst_cols = cols;
+    p.dst_ld = dst_ld ? dst_ld : cols;
+    p.dst_group_stride = dst_group_stride ? dst_group_stride : rows * p.dst_ld;
+    p.dst_scale_group_stride = dst_scale_group_stride ? dst_scale_group_stride : rows;
+    TRMOE_REQUIRE(p.dst_ld >= cols, "pack_weight: dst_ld smaller than the packed columns");
     p.interleave = (kind == TRMOE_PACK_GATE_UP);
     p.elem_bytes = elem_bytes(dtype);
     return launch_pack(p, as_stream(stream));
@@ -160,7 +171,8 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
     if (n_tokens == 0) return TRMOE_OK;
     TRMOE_REQUIRE(x && w_packed && h, "shared_gate_up: null pointer");
     TRMOE_REQUIRE(aligned16(w_packed), "shared_gate_up: packed weights must be 16-byte aligned");
-    const int epc = (act_dtype == TRMOE_F32) ? 4 : 8;
+    TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)),
+                  "shared_gate_up: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     GateUpArgs a;
     a.x = x;
     a.ldx = ldx;
@@ -171,8 +183,64 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
     a.w_scale = w_scale;
     a.h = h;
     a.ldh = ldh;
-    a.x_vec_ok = aligned16(x) && (ldx % epc == 0);
+    a.shared_mult = 1.0f;
+    a.shared_feats = 0;
+    a.expert_feats = 1;
+    a.ids = nullptr;
+    a.table = nullptr;
+    a.vocab = 1;
+    a.top_k = 0;
+    for (int j = 0; j < 4; ++j) a.rw[j] = 0.f;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * round_up(shared_width, 128), as_stream(stream));
+}
+
+int64_t trmoe_dense_routed_features(int64_t shared_width, int num_experts, int64_t expert_width) {
+    if (shared_width < 0 || num_experts < 1 || expert_width < 1) return -1;
+    return round_up(round_up(shared_width, 128) + num_experts * round_up(expert_width, 64), 128);
+}
+
+int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                               int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                               int num_experts, int64_t expert_width, const int64_t* token_ids,
+                               const int64_t* route_table, int64_t vocab_size, int top_k,
+                               const float* route_weights, float shared_scale, float routed_scale, void* h,
+                               int64_t ldh, void* stream) {
+    TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "dense_routed_gate_up: unsupported dtype pair");
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width >= 0 && expert_width > 0,
+                  "dense_routed_gate_up: bad dimensions");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "dense_routed_gate_up: num_experts must be in [1, 16]");
+    TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= num_experts, "dense_routed_gate_up: bad top_k");
+    TRMOE_REQUIRE(vocab_size > 0, "dense_routed_gate_up: vocab_size must be positive");
+    const int64_t feats = trmoe_dense_routed_features(shared_width, num_experts, expert_width);
+    TRMOE_REQUIRE(ldx >= hidden, "dense_routed_gate_up: ldx < hidden");
+    TRMOE_REQUIRE(ldh >= feats, "dense_routed_gate_up: ldh < trmoe_dense_routed_features()");
+    TRMOE_REQUIRE(hidden < (int64_t)1 << 30, "dense_routed_gate_up: hidden too large");
+    TRMOE_REQUIRE((w_dtype == TRMOE_FP8_E4M3) == (w_scale != nullptr), "dense_routed_gate_up: w_scale iff fp8");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x && w_packed && h && token_ids && route_table && route_weights,
+                  "dense_routed_gate_up: null pointer");
+    TRMOE_REQUIRE(aligned16(w_packed), "dense_routed_gate_up: packed weights must be 16-byte aligned");
+    TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)),
+                  "dense_routed_gate_up: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    GateUpArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = n_tokens;
+    a.K = (int)hidden;
+    a.w = w_packed;
+    a.ldw = round_up(hidden, 8);
+    a.w_scale = w_scale;
+    a.h = h;
+    a.ldh = ldh;
+    a.shared_mult = shared_scale;
+    a.shared_feats = round_up(shared_width, 128);
+    a.expert_feats = round_up(expert_width, 64);
+    a.ids = token_ids;
+    a.table = route_table;
+    a.vocab = vocab_size;
+    a.top_k = top_k;
+    for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? routed_scale * route_weights[j] : 0.f;
+    return launch_gate_up(act_dtype, w_dtype, a, 2 * feats, as_stream(stream));
 }
 
 int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
@@ -195,7 +263,10 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     const int64_t f_pad = round_up(expert_width, 64);
     if (routed_lds_bytes(act_dtype, f_pad) > 160 * 1024)
         return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: expert_width too large for the LDS-resident tile");
-    const int epc = (act_dtype == TRMOE_F32) ? 4 : 8;
+    TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)),
+                  "routed_experts: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    if (n_tokens * ldx * elem_bytes(act_dtype) >= ((int64_t)1 << 31))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: x must be smaller than 2 GiB");
     RoutedArgs a;
     a.x = x;
     a.ldx = ldx;
@@ -214,10 +285,9 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     a.F_pad = (int)f_pad;
     a.W = (int)expert_width;
     a.H = (int)hidden;
-    a.H_pad = (int)round_up(hidden, 128);
+    a.H_pad = (int)round_up(hidden, 256);  // packed down rows per expert
     a.y = y;
     a.ldy = ldy;
-    a.x_vec_ok = aligned16(x) && (ldx % epc == 0);
     return launch_routed(act_dtype, w_dtype, a, n_tokens * top_k, as_stream(stream));
 }
 
@@ -242,7 +312,8 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
     if (n_tokens == 0) return TRMOE_OK;
     TRMOE_REQUIRE(h && w_down && out, "shared_down_combine: null pointer");
     TRMOE_REQUIRE(aligned16(w_down), "shared_down_combine: packed weights must be 16-byte aligned");
-    const int epc = (act_dtype == TRMOE_F32) ? 4 : 8;
+    TRMOE_REQUIRE(rows_ok(h, ldh, elem_bytes(act_dtype)),
+                  "shared_down_combine: h rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     DownArgs a;
     a.h = h;
     a.ldh = ldh;
@@ -263,8 +334,7 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
     a.ldr = ldr;
     a.out = out;
     a.ldo = ldo;
-    a.h_vec_ok = aligned16(h) && (ldh % epc == 0);
-    return launch_down_combine(act_dtype, w_dtype, a, round_up(hidden, 128), as_stream(stream));
+    return launch_down_combine(act_dtype, w_dtype, a, as_stream(stream));
 }
 
 int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y, int64_t ldy,

@@ -77,22 +77,25 @@ __device__ __forceinline__ int acc_row(int lane, int i) {
 __device__ __forceinline__ int acc_col(int lane) { return lane & 31; }
 
 // ---------------------------------------------------------------------------
-// global chunk loads
+// buffer loads
 // ---------------------------------------------------------------------------
-// 16 bytes of K elements [k, k + kPerChunk) of one row; zero beyond K.
-template <class Kind>
-__device__ __forceinline__ u32x4 load_chunk(const typename Kind::T* row, int k, int K, bool vec_ok) {
-    using T = typename Kind::T;
-    if (row == nullptr || k >= K) return u32x4{0, 0, 0, 0};
-    if (vec_ok && k + Kind::kPerChunk <= K) {
-        return *reinterpret_cast<const u32x4*>(row + k);
-    }
-    union { u32x4 v; T e[Kind::kPerChunk]; } u;
-    u.v = u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < Kind::kPerChunk; ++i)
-        if (k + i < K) u.e[i] = row[k + i];
-    return u.v;
+// Operands are read with raw buffer loads: a load whose byte offset is at or
+// past the descriptor's range returns zero, so absent rows and the K tail
+// need no branches.  kOutOfRange is an offset no range reaches (ranges are
+// kept below 2^31 bytes by the host).
+constexpr int kOutOfRange = (int)0x80000000u;
+constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer, 32-bit dword data
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+__device__ __forceinline__ u32x2 buffer_load8(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, offset, 0, 0));
 }
 
 // 8 OCP e4m3 weights -> 8 bf16 (exact: every e4m3 value is a bf16 value).
@@ -108,90 +111,80 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 q) {
 // ---------------------------------------------------------------------------
 // operand providers for the tile main loop
 // ---------------------------------------------------------------------------
-// Each provider owns ROWS rows of one operand tile.  A thread handles
-// ROWS*8/256 chunks: chunk q = tid + 256*j sits at row q/8, chunk q%8.
+// A provider owns ROWS rows of one operand tile.  Thread t handles the
+// ROWS*8/256 chunks q = t + 256*j: row q/8, 16-byte chunk t%8 of the row's
+// 128-byte K stage.  prefetch(kt) issues the buffer loads of stage kt into
+// registers, commit() writes them to an LDS stage in the swizzled layout.
+//
+// Row requirements (checked by the host): rows start 16-byte aligned and the
+// elements between K and the next multiple of 8 are zero (or K % 8 == 0), so
+// whole 16-byte chunks can be loaded.
 
-// Activation rows from global memory (dense or gathered), staged through LDS.
-template <class Kind, int ROWS>
-struct GlobalRows {
-    using T = typename Kind::T;
-    static constexpr int kChunks = ROWS * 8 / kThreads;
-    const T* rowp[kChunks];
-    u32x4 reg[kChunks];
-    int K;
-    bool vec_ok;
-
-    __device__ void prefetch(int kt) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            int q = threadIdx.x + kThreads * j;
-            int c = q & 7;
-            reg[j] = load_chunk<Kind>(rowp[j], kt * Kind::kStageElems + c * Kind::kPerChunk, K, vec_ok);
-        }
-    }
-    __device__ void commit(char* stage) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            int q = threadIdx.x + kThreads * j;
-            *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = reg[j];
-        }
-    }
-};
-
-// Packed weight rows [rows, ld] (bf16 or f32), no row guard (rows are padded).
-template <class Kind, int ROWS>
-struct PackedRows {
-    using T = typename Kind::T;
-    static constexpr int kChunks = ROWS * 8 / kThreads;
-    const T* base;     // first row of the tile
-    int64_t ld;        // elements per packed row
-    u32x4 reg[kChunks];
-    int K;
-
-    __device__ void prefetch(int kt) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            int q = threadIdx.x + kThreads * j;
-            int r = q >> 3, c = q & 7;
-            int k = kt * Kind::kStageElems + c * Kind::kPerChunk;
-            reg[j] = (k < K) ? *reinterpret_cast<const u32x4*>(base + r * ld + k) : u32x4{0, 0, 0, 0};
-        }
-    }
-    __device__ void commit(char* stage) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            int q = threadIdx.x + kThreads * j;
-            *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = reg[j];
-        }
-    }
-};
-
-// Packed e4m3 weight rows [rows, ld bytes]; expanded to bf16 on the way to LDS.
+// 16-byte-chunk operand (bf16 or f32 elements in memory and in LDS).
 template <int ROWS>
-struct PackedRowsFP8 {
+struct BufRows {
     static constexpr int kChunks = ROWS * 8 / kThreads;
-    const uint8_t* base;
-    int64_t ld;
-    u32x2 reg[kChunks];
-    int K;
+    using Reg = u32x4;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int row_off[kChunks];   // byte offset of the row, kOutOfRange when absent
+    int kbytes;             // bytes of K per row; chunks at or past it load zero
 
-    __device__ void prefetch(int kt) {
+    __device__ void prefetch(int kt, Reg (&reg)[kChunks]) const {
+        const int kb = kt * kRowBytes + (threadIdx.x & 7) * 16;
+        const bool in_k = kb < kbytes;
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) reg[j] = buffer_load16(rsrc, in_k ? row_off[j] + kb : kOutOfRange);
+    }
+    __device__ void commit(char* stage, const Reg (&reg)[kChunks]) const {
 #pragma unroll
         for (int j = 0; j < kChunks; ++j) {
-            int q = threadIdx.x + kThreads * j;
-            int r = q >> 3, c = q & 7;
-            int k = kt * 64 + c * 8;
-            reg[j] = (k < K) ? *reinterpret_cast<const u32x2*>(base + r * ld + k) : u32x2{0, 0};
+            const int q = threadIdx.x + kThreads * j;
+            *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = reg[j];
         }
     }
-    __device__ void commit(char* stage) {
+};
+
+// e4m3 operand: 8-byte chunks in memory (64 K values per stage), expanded to
+// 16-byte bf16 chunks in LDS.
+template <int ROWS>
+struct BufRowsFP8 {
+    static constexpr int kChunks = ROWS * 8 / kThreads;
+    using Reg = u32x2;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int row_off[kChunks];
+    int kbytes;
+
+    __device__ void prefetch(int kt, Reg (&reg)[kChunks]) const {
+        const int kb = kt * 64 + (threadIdx.x & 7) * 8;
+        const bool in_k = kb < kbytes;
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) reg[j] = buffer_load8(rsrc, in_k ? row_off[j] + kb : kOutOfRange);
+    }
+    __device__ void commit(char* stage, const Reg (&reg)[kChunks]) const {
 #pragma unroll
         for (int j = 0; j < kChunks; ++j) {
-            int q = threadIdx.x + kThreads * j;
+            const int q = threadIdx.x + kThreads * j;
             *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = fp8x8_to_bf16x8(reg[j]);
         }
     }
 };
+
+// Dense rows [row0, row0 + ROWS) of a row-major matrix with `rows_total`
+// rows of `ld_bytes` bytes; rows past the end load zero.
+template <class Prov>
+__device__ __forceinline__ void init_dense_rows(Prov& p, const void* base, int64_t row0, int64_t rows_total,
+                                                int64_t ld_bytes, int kbytes) {
+    constexpr int ROWS = Prov::kChunks * kThreads / 8;
+    const int64_t avail = rows_total - row0;
+    const int64_t nrows = avail < ROWS ? avail : ROWS;
+    p.rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
+    p.kbytes = kbytes;
+#pragma unroll
+    for (int j = 0; j < Prov::kChunks; ++j) {
+        const int r = (threadIdx.x >> 3) + 32 * j;
+        p.row_off[j] = (r < nrows) ? (int)(r * ld_bytes) : kOutOfRange;
+    }
+}
 
 // ---------------------------------------------------------------------------
 // the tile main loop
@@ -245,32 +238,52 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[TM][TN]) {
             for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.f;
 }
 
-// A and B both streamed from global through the two LDS stages.
+// A and B both streamed from global.  Two LDS stages and two register sets:
+// the loads of stage kt+2 are issued before the MFMAs of stage kt, so every
+// load has two stages of MFMA work to land before its commit to LDS.
 template <class Kind, class Shape, class AProv, class BProv>
-__device__ __forceinline__ void tile_loop(AProv& ap, BProv& bp, int K, char* lds, int wm0, int wn0,
+__device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int K, char* lds, int wm0, int wn0,
                                           f32x16 (&acc)[Shape::TM][Shape::TN]) {
     const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
-    char* stage0 = lds;
-    char* stage1 = lds + Shape::kStageBytes;
     constexpr int kABytes = Shape::BM * kRowBytes;
-    ap.prefetch(0);
-    bp.prefetch(0);
-    ap.commit(stage0);
-    bp.commit(stage0 + kABytes);
+    char* st0 = lds;
+    char* st1 = lds + Shape::kStageBytes;
+    typename AProv::Reg ra0[AProv::kChunks], ra1[AProv::kChunks];
+    typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
+    ap.prefetch(0, ra0);
+    bp.prefetch(0, rb0);
+    if (nk > 1) {
+        ap.prefetch(1, ra1);
+        bp.prefetch(1, rb1);
+    }
+    ap.commit(st0, ra0);
+    bp.commit(st0 + kABytes, rb0);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        char* cur = (kt & 1) ? stage1 : stage0;
-        char* nxt = (kt & 1) ? stage0 : stage1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            ap.prefetch(kt + 1);
-            bp.prefetch(kt + 1);
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        // st0 holds stage kt; ra1/rb1 carry stage kt+1
+        if (kt + 2 < nk) {
+            ap.prefetch(kt + 2, ra0);
+            bp.prefetch(kt + 2, rb0);
         }
-        mma_stage<Kind, Shape::TM, Shape::TN>(cur, cur + kABytes, wm0, wn0, acc);
-        if (more) {
-            ap.commit(nxt);
-            bp.commit(nxt + kABytes);
+        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
+        ap.commit(st1, ra1);
+        bp.commit(st1 + kABytes, rb1);
+        __syncthreads();
+        // st1 holds stage kt+1; ra0/rb0 carry stage kt+2
+        if (kt + 3 < nk) {
+            ap.prefetch(kt + 3, ra1);
+            bp.prefetch(kt + 3, rb1);
         }
+        mma_stage<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc);
+        if (kt + 2 < nk) {
+            ap.commit(st0, ra0);
+            bp.commit(st0 + kABytes, rb0);
+        }
+        __syncthreads();
+    }
+    if (kt < nk) {  // odd stage count: the last stage sits in st0
+        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
         __syncthreads();
     }
 }
@@ -278,25 +291,32 @@ __device__ __forceinline__ void tile_loop(AProv& ap, BProv& bp, int K, char* lds
 // A resident in LDS (one 128-byte-row stage per K stage, BM rows each), B
 // streamed.  `bstage` holds 2 * BN * 128 bytes.
 template <class Kind, class Shape, class BProv>
-__device__ __forceinline__ void tile_loop_lds_a(const char* a_lds, int a_stage_bytes, BProv& bp, int K,
+__device__ __forceinline__ void tile_loop_lds_a(const char* a_lds, int a_stage_bytes, const BProv& bp, int K,
                                                 char* bstage, int wm0, int wn0,
                                                 f32x16 (&acc)[Shape::TM][Shape::TN]) {
     const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
     constexpr int kBBytes = Shape::BN * kRowBytes;
-    bp.prefetch(0);
-    bp.commit(bstage);
+    typename BProv::Reg rb[BProv::kChunks];
+    bp.prefetch(0, rb);
+    bp.commit(bstage, rb);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         char* cur = bstage + (kt & 1) * kBBytes;
         char* nxt = bstage + ((kt + 1) & 1) * kBBytes;
         const bool more = kt + 1 < nk;
-        if (more) bp.prefetch(kt + 1);
+        if (more) bp.prefetch(kt + 1, rb);
         mma_stage<Kind, Shape::TM, Shape::TN>(a_lds + kt * a_stage_bytes, cur, wm0, wn0, acc);
-        if (more) bp.commit(nxt);
+        if (more) bp.commit(nxt, rb);
         __syncthreads();
     }
 }
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) with the hardware exp2 and reciprocal (about
+// 1 ulp each); for g < -126/log2(e) the exponential overflows to +inf and
+// the reciprocal returns 0, the correct limit.
+__device__ __forceinline__ float silu_f(float g) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 }  // namespace trmoe

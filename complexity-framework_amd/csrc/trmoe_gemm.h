@@ -16,7 +16,10 @@ struct PackArgs {
     int64_t scale_group_stride;
     void* dst;
     float* dst_scale;
-    int64_t dst_rows, dst_cols;
+    int64_t dst_rows, dst_cols;      // packed rows / cols written per group
+    int64_t dst_ld;                  // elements between packed rows
+    int64_t dst_group_stride;        // elements between groups
+    int64_t dst_scale_group_stride;  // floats between groups of dst_scale
     int interleave;
     int elem_bytes;
 };
@@ -31,7 +34,18 @@ struct GateUpArgs {
     const float* w_scale;
     void* h;
     int64_t ldh;
-    int x_vec_ok;
+    // Dense-routed epilogue: packed features at or past `shared_feats` belong
+    // to expert (f - shared_feats) / expert_feats and are scaled by the
+    // token's route weight for that expert (0 when not routed); shared
+    // features are scaled by shared_mult.  ids == nullptr: no routed block.
+    float shared_mult;
+    int64_t shared_feats;
+    int64_t expert_feats;
+    const int64_t* ids;
+    const int64_t* table;   // [top_k, vocab]
+    int64_t vocab;
+    int top_k;
+    float rw[4];            // per-slot route weight times the routed scale
 };
 
 struct DownArgs {
@@ -54,7 +68,6 @@ struct DownArgs {
     int64_t ldr;
     void* out;
     int64_t ldo;
-    int h_vec_ok;
 };
 
 struct RoutedArgs {
@@ -75,10 +88,9 @@ struct RoutedArgs {
     int F_pad;             // expert width rounded up to 64
     int W;                 // expert width (down K)
     int H;                 // output columns
-    int H_pad;             // rounded up to 128
+    int H_pad;             // packed down rows per expert: H rounded up to 256
     void* y;
     int64_t ldy;
-    int x_vec_ok;
 };
 
 struct CombineArgs {
@@ -97,7 +109,7 @@ struct CombineArgs {
 
 int launch_pack(const PackArgs& p, hipStream_t stream);
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
-int launch_down_combine(int act, int wdt, const DownArgs& a, int64_t packed_rows, hipStream_t stream);
+int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream);
 int routed_lds_bytes(int act, int64_t f_pad);
 int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t assignments, hipStream_t stream);
 int launch_combine(int act, const CombineArgs& a, hipStream_t stream);

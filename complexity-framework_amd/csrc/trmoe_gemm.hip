@@ -14,6 +14,9 @@
 #include "trmoe_internal.h"
 #include "trmoe_gemm.h"
 
+#include <stdlib.h>
+#include <string.h>
+
 #include <type_traits>
 
 namespace trmoe {
@@ -44,7 +47,7 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs p) {
         }
         const bool valid = feat < p.out_features && col < p.in_features;
         const int64_t s = g * p.s_group + feat * p.s_out + col * p.s_in;
-        char* d = (char*)p.dst + idx * p.elem_bytes;
+        char* d = (char*)p.dst + (g * p.dst_group_stride + row * p.dst_ld + col) * p.elem_bytes;
         if (p.elem_bytes == 1) {
             *(uint8_t*)d = valid ? ((const uint8_t*)src)[s] : 0;
         } else if (p.elem_bytes == 2) {
@@ -54,7 +57,7 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs p) {
         }
         if (p.dst_scale != nullptr && col == 0) {
             const bool fv = feat < p.out_features;
-            p.dst_scale[g * p.dst_rows + row] = fv ? ssrc[g * p.scale_group_stride + feat] : 0.0f;
+            p.dst_scale[g * p.dst_scale_group_stride + row] = fv ? ssrc[g * p.scale_group_stride + feat] : 0.0f;
         }
     }
 }
@@ -73,33 +76,31 @@ int launch_pack(const PackArgs& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 template <class Kind, bool FP8, int ROWS>
 struct BProvSel {
-    using type = PackedRows<Kind, ROWS>;
+    using type = BufRows<ROWS>;
 };
 template <class Kind, int ROWS>
 struct BProvSel<Kind, true, ROWS> {
-    using type = PackedRowsFP8<ROWS>;
+    using type = BufRowsFP8<ROWS>;
 };
 
+// Packed weight rows [row0, row0 + ROWS) of a [rows, ld] packed tensor
+// (every such row exists: packing pads rows to the tile multiple).
 template <class Kind, bool FP8, int ROWS>
 __device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS>::type& bp, const void* base,
                                            int64_t ld, int64_t row0, int K) {
-    if constexpr (FP8) {
-        bp.base = static_cast<const uint8_t*>(base) + row0 * ld;
-    } else {
-        bp.base = static_cast<const typename Kind::T*>(base) + row0 * ld;
-    }
-    bp.ld = ld;
-    bp.K = K;
+    const int64_t elem = FP8 ? 1 : (int64_t)sizeof(typename Kind::T);
+    init_dense_rows(bp, base, row0, row0 + ROWS, ld * elem, (int)(K * elem));
 }
 
 using ShapeMain = TileShape<128, 128, 2>;
+using ShapeBig = TileShape<256, 256, 2>;
+using ShapeDown224 = TileShape<256, 224, 4>;
 
 // ---------------------------------------------------------------------------
 // K2: shared gate|up + SwiGLU
 // ---------------------------------------------------------------------------
-template <class Kind, bool FP8>
+template <class Kind, bool FP8, class Shape>
 __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
-    using Shape = ShapeMain;
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -108,17 +109,23 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
     const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
-    GlobalRows<Kind, Shape::BM> ap;
-    ap.K = a.K;
-    ap.vec_ok = a.x_vec_ok;
-#pragma unroll
-    for (int j = 0; j < GlobalRows<Kind, Shape::BM>::kChunks; ++j) {
-        const int row = (threadIdx.x + kThreads * j) >> 3;
-        const int64_t m = m0 + row;
-        ap.rowp[j] = (m < a.M) ? static_cast<const T*>(a.x) + m * a.ldx : nullptr;
-    }
+    BufRows<Shape::BM> ap;
+    init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
     typename BProvSel<Kind, FP8, Shape::BN>::type bp;
     init_bprov<Kind, FP8, Shape::BN>(bp, a.w, a.ldw, n0, a.K);
+
+    // Routes of this tile's rows, gathered once while the first stages load
+    // (tiles holding expert features only); read back in the epilogue after
+    // the main loop's barriers.
+    __shared__ int s_route[Shape::BM][kMaxTopK];
+    const bool tile_routed = a.ids != nullptr && ((n0 + Shape::BN) >> 1) > a.shared_feats;
+    if (tile_routed && threadIdx.x < Shape::BM) {
+        const int64_t row = m0 + threadIdx.x;
+        int64_t id = row < a.M ? a.ids[row] : 0;
+        id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
+        for (int j = 0; j < kMaxTopK; ++j)
+            s_route[threadIdx.x][j] = (j < a.top_k && row < a.M) ? (int)a.table[(int64_t)j * a.vocab + id] : -1;
+    }
 
     f32x16 acc[Shape::TM][Shape::TN];
     zero_acc<Kind>(acc);
@@ -128,9 +135,15 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
 #pragma unroll
     for (int p = 0; p < Shape::TN / 2; ++p) {
         const int64_t pbase = n0 + wn0 + 64 * p;     // packed row of the gate tile
-        const int64_t feat = (pbase >> 1) + r;
+        const int64_t fblock = pbase >> 1;            // first feature of this 32-feature block
+        const int64_t feat = fblock + r;
         const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
         const float su = a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f;
+        // expert blocks are multiples of 64 features, so a 32-feature block
+        // is wholly shared or wholly one expert's
+        const bool routed = a.ids != nullptr && fblock >= a.shared_feats;
+        const int64_t expert = routed ? (fblock - a.shared_feats) / a.expert_feats : -1;
+        const float mult = routed ? 1.0f : a.shared_mult;
 #pragma unroll
         for (int tm = 0; tm < Shape::TM; ++tm) {
 #pragma unroll
@@ -139,7 +152,15 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
                 if (row < a.M) {
                     const float g = acc[tm][2 * p][i] * sg;
                     const float u = acc[tm][2 * p + 1][i] * su;
-                    static_cast<T*>(a.h)[row * a.ldh + feat] = from_f32<T>(silu_f(g) * u);
+                    float hv = silu_f(g) * u * mult;
+                    if (routed) {
+                        const int* rr = s_route[wm0 + tm * 32 + acc_row(lane, i)];
+                        float tw = 0.f;
+#pragma unroll
+                        for (int j = 0; j < kMaxTopK; ++j) tw += (rr[j] == expert) ? a.rw[j] : 0.f;
+                        hv *= tw;
+                    }
+                    static_cast<T*>(a.h)[row * a.ldh + feat] = from_f32<T>(hv);
                 }
             }
         }
@@ -149,9 +170,8 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
 // ---------------------------------------------------------------------------
 // K4: shared down + weighted un-permute + combine
 // ---------------------------------------------------------------------------
-template <class Kind, bool FP8>
+template <class Kind, bool FP8, class Shape>
 __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
-    using Shape = ShapeMain;
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -160,17 +180,22 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
-    GlobalRows<Kind, Shape::BM> ap;
-    ap.K = a.K;
-    ap.vec_ok = a.h_vec_ok;
-#pragma unroll
-    for (int j = 0; j < GlobalRows<Kind, Shape::BM>::kChunks; ++j) {
-        const int row = (threadIdx.x + kThreads * j) >> 3;
-        const int64_t m = m0 + row;
-        ap.rowp[j] = (m < a.M) ? static_cast<const T*>(a.h) + m * a.ldh : nullptr;
-    }
+    BufRows<Shape::BM> ap;
+    init_dense_rows(ap, a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), a.K * (int)sizeof(T));
     typename BProvSel<Kind, FP8, Shape::BN>::type bp;
     init_bprov<Kind, FP8, Shape::BN>(bp, a.w, a.ldw, n0, a.K);
+
+    // y row of each (tile row, slot), clamped so that a malformed route table
+    // cannot become a wild read; gathered while the first stages load.
+    __shared__ int s_yrow[Shape::BM][kMaxTopK];
+    if (a.y != nullptr && threadIdx.x < Shape::BM) {
+        const int64_t row = m0 + threadIdx.x;
+        const int64_t last = (int64_t)a.top_k * a.M - 1;
+        for (int j = 0; j < kMaxTopK; ++j) {
+            int64_t v = (j < a.top_k && row < a.M) ? a.inverse[(int64_t)j * a.M + row] : 0;
+            s_yrow[threadIdx.x][j] = (int)(v < 0 ? 0 : (v > last ? last : v));
+        }
+    }
 
     f32x16 acc[Shape::TM][Shape::TN];
     zero_acc<Kind>(acc);
@@ -194,12 +219,8 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
             if (row >= a.M) continue;
             int64_t yrow[kMaxTopK];
             if (y != nullptr) {
-                for (int j = 0; j < a.top_k; ++j) {
-                    // clamp: a malformed route table must not turn into a wild read
-                    int64_t r = a.inverse[(int64_t)j * a.M + row];
-                    r = r < 0 ? 0 : (r >= a.top_k * a.M ? a.top_k * a.M - 1 : r);
-                    yrow[j] = r * a.ldy;
-                }
+                const int* yr = s_yrow[wm0 + tm * 32 + acc_row(lane, i)];
+                for (int j = 0; j < a.top_k; ++j) yrow[j] = (int64_t)yr[j] * a.ldy;
             }
 #pragma unroll
             for (int tn = 0; tn < Shape::TN; ++tn) {
@@ -274,17 +295,17 @@ __global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
     // ---- phase 1: h = silu(x Wg) * (x Wu) into LDS
     const int nchunks = a.F_pad / 64;
     for (int fc = 0; fc < nchunks; ++fc) {
-        GlobalRows<Kind, Shape::BM> ap;
-        ap.K = a.K;
-        ap.vec_ok = a.x_vec_ok;
+        BufRows<Shape::BM> ap;
+        ap.rsrc = make_rsrc(a.x, (uint32_t)(a.n_tokens * a.ldx * (int64_t)sizeof(T)));
+        ap.kbytes = a.K * (int)sizeof(T);
 #pragma unroll
-        for (int j = 0; j < GlobalRows<Kind, Shape::BM>::kChunks; ++j) {
-            const int row = (threadIdx.x + kThreads * j) >> 3;
+        for (int j = 0; j < BufRows<Shape::BM>::kChunks; ++j) {
+            const int row = (threadIdx.x >> 3) + 32 * j;
             if (row < rows) {
                 const int64_t t = (int64_t)((uint64_t)a.sorted[row0 + row] % (uint64_t)a.n_tokens);
-                ap.rowp[j] = static_cast<const T*>(a.x) + t * a.ldx;
+                ap.row_off[j] = (int)(t * a.ldx * (int64_t)sizeof(T));
             } else {
-                ap.rowp[j] = nullptr;
+                ap.row_off[j] = kOutOfRange;
             }
         }
         typename BProvSel<Kind, FP8, Shape::BN>::type bp;
@@ -313,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
     }
 
     // ---- phase 2: y = h Wd, 128 output columns at a time
-    const int ncol = a.H_pad / Shape::BN;
+    const int ncol = (a.H + Shape::BN - 1) / Shape::BN;
     T* y = static_cast<T*>(a.y);
     for (int oc = 0; oc < ncol; ++oc) {
         typename BProvSel<Kind, FP8, Shape::BN>::type bp;
@@ -374,34 +395,77 @@ static int ensure_lds(F* fn, int bytes) {
     return TRMOE_OK;
 }
 
-int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    dim3 grid((unsigned)((a.M + ShapeMain::BM - 1) / ShapeMain::BM), (unsigned)(packed_rows / ShapeMain::BN));
-    const int lds = ShapeMain::kLdsBytes;
-    if (act == TRMOE_F32 && wdt == TRMOE_F32) {
-        hipLaunchKernelGGL((k_gate_up_swiglu<KindF32, false>), grid, dim3(kThreads), lds, stream, a);
-    } else if (act == TRMOE_BF16 && wdt == TRMOE_BF16) {
-        hipLaunchKernelGGL((k_gate_up_swiglu<KindBF16, false>), grid, dim3(kThreads), lds, stream, a);
-    } else if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) {
-        hipLaunchKernelGGL((k_gate_up_swiglu<KindBF16, true>), grid, dim3(kThreads), lds, stream, a);
-    } else {
-        return set_error(TRMOE_ERR_UNSUPPORTED, "shared_gate_up: unsupported dtype pair");
-    }
+// Tile choice: 256x256 workgroup tiles (128x128 per wave) halve the L2->CU
+// traffic per MFMA relative to 128x128 and are used whenever they still give
+// at least two workgroups per CU; the down GEMM uses 256x224 when the hidden
+// size is a multiple of 224 (896 = 4 x 224: one full wave of 256 tiles with
+// no padded columns).
+constexpr int64_t kBigTileMinBlocks = 512;
+
+// TRMOE_GEMM_TILE=small|big forces one tile family (tuning sweeps); unset = auto.
+static int tile_override() {
+    static int v = [] {
+        const char* e = getenv("TRMOE_GEMM_TILE");
+        if (e == nullptr) return 0;
+        if (strcmp(e, "small") == 0) return 1;
+        if (strcmp(e, "big") == 0) return 2;
+        return 0;
+    }();
+    return v;
+}
+
+template <class Kind, bool FP8, class Shape>
+static int launch_gate_up_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)(packed_rows / Shape::BN));
+    int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape>, Shape::kLdsBytes);
+    if (st) return st;
+    hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape>), grid, dim3(kThreads), Shape::kLdsBytes, stream, a);
     return check_launch("shared_gate_up");
 }
 
-int launch_down_combine(int act, int wdt, const DownArgs& a, int64_t packed_rows, hipStream_t stream) {
-    dim3 grid((unsigned)((a.M + ShapeMain::BM - 1) / ShapeMain::BM), (unsigned)(packed_rows / ShapeMain::BN));
-    const int lds = ShapeMain::kLdsBytes;
-    if (act == TRMOE_F32 && wdt == TRMOE_F32) {
-        hipLaunchKernelGGL((k_down_combine<KindF32, false>), grid, dim3(kThreads), lds, stream, a);
-    } else if (act == TRMOE_BF16 && wdt == TRMOE_BF16) {
-        hipLaunchKernelGGL((k_down_combine<KindBF16, false>), grid, dim3(kThreads), lds, stream, a);
-    } else if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) {
-        hipLaunchKernelGGL((k_down_combine<KindBF16, true>), grid, dim3(kThreads), lds, stream, a);
-    } else {
-        return set_error(TRMOE_ERR_UNSUPPORTED, "shared_down_combine: unsupported dtype pair");
-    }
+template <class Kind, bool FP8>
+static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int64_t big_blocks = ((a.M + ShapeBig::BM - 1) / ShapeBig::BM) * (packed_rows / ShapeBig::BN);
+    const int ov = tile_override();
+    if (packed_rows % ShapeBig::BN == 0 && (ov == 2 || (ov == 0 && big_blocks >= kBigTileMinBlocks)))
+        return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+    return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
+}
+
+int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) return launch_gate_up_kind<KindF32, false>(a, packed_rows, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return launch_gate_up_kind<KindBF16, false>(a, packed_rows, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) return launch_gate_up_kind<KindBF16, true>(a, packed_rows, stream);
+    return set_error(TRMOE_ERR_UNSUPPORTED, "shared_gate_up: unsupported dtype pair");
+}
+
+template <class Kind, bool FP8, class Shape>
+static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)((a.N + Shape::BN - 1) / Shape::BN));
+    int st = ensure_lds(k_down_combine<Kind, FP8, Shape>, Shape::kLdsBytes);
+    if (st) return st;
+    hipLaunchKernelGGL((k_down_combine<Kind, FP8, Shape>), grid, dim3(kThreads), Shape::kLdsBytes, stream, a);
     return check_launch("shared_down_combine");
+}
+
+// The packed down weights have round_up(N, 256) rows, so every tile choice
+// below reads only packed rows.
+template <class Kind, bool FP8>
+static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
+    const int64_t mt = (a.M + 255) / 256;
+    const int ov = tile_override();
+    if (ov == 1) return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
+    if (a.N % ShapeDown224::BN == 0 && (ov == 2 || mt * (a.N / ShapeDown224::BN) >= 256))
+        return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
+    if (ov == 2 || mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
+    return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
+}
+
+int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream) {
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) return launch_down_kind<KindF32, false>(a, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return launch_down_kind<KindBF16, false>(a, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) return launch_down_kind<KindBF16, true>(a, stream);
+    return set_error(TRMOE_ERR_UNSUPPORTED, "shared_down_combine: unsupported dtype pair");
 }
 
 // 64-row tiles halve the LDS-resident h for wide fp32 experts.

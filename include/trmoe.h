@@ -24,7 +24,11 @@
  *   - the return value is a trmoe_status; on failure trmoe_last_error()
  *     returns a message that stays valid until the calling thread's next
  *     call into the library;
- *   - tensors are row-major with the element strides given (ld*).
+ *   - tensors are row-major with the element strides given (ld*);
+ *   - activation rows (x, h) start 16-byte aligned, their stride is a multiple
+ *     of 16 bytes, and when hidden*elem is not a multiple of 16 the elements
+ *     up to the next multiple of 16 bytes are zero: the kernels read whole
+ *     16-byte chunks through buffer loads (out-of-range chunks read as zero).
  *
  * Weights are consumed in a packed layout produced on the device by
  * trmoe_pack_weight() (see trmoe_pack_dims()).
@@ -102,13 +106,17 @@ int trmoe_pack_dims(int kind, int64_t out_features, int64_t in_features, int64_t
  * scale_a/scale_b hold per-output-channel float scales at
  * scale[g*scale_group_stride + o]; dst_scale[groups][rows] receives them in
  * packed row order.  For other dtypes the scale pointers must be NULL.
+ * dst_ld / dst_group_stride / dst_scale_group_stride (elements; 0 = dense
+ * defaults cols / rows*dst_ld / rows) let a group land inside a larger
+ * packed tensor, as the dense-routed layout below requires.
  * Reference tensors: engine.py:127-163 (expert_gate/up [E,H,W], expert_down
  * [E,W,H], shared_* nn.Linear).
  */
 int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b, int64_t groups,
                       int64_t out_features, int64_t in_features, int64_t s_group, int64_t s_out,
                       int64_t s_in, const float* scale_a, const float* scale_b,
-                      int64_t scale_group_stride, int64_t row_align, void* dst, float* dst_scale,
+                      int64_t scale_group_stride, int64_t row_align, void* dst, int64_t dst_ld,
+                      int64_t dst_group_stride, float* dst_scale, int64_t dst_scale_group_stride,
                       void* stream);
 
 /*
@@ -148,6 +156,28 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
                          int64_t shared_width, void* h, int64_t ldh, void* stream);
 
 /*
+ * K2+K3 fused, "dense-routed" strategy (for expert widths small against the
+ * shared width).  The packed gate|up weights hold the shared features
+ * (round_up(S, 128)) followed by every expert's features (round_up(W, 64)
+ * each), all GATE_UP-interleaved over round_up(hidden, 8) columns, with
+ * 2 * trmoe_dense_routed_features() rows.  For token t and feature f:
+ *     shared f:           h[t, f] = shared_scale * silu(g) * u
+ *     expert e, slot j:   h[t, f] = routed_scale * sum_j w_j [route_j(t) == e] * silu(g) * u
+ * so that one trmoe_shared_down_combine() over h with the matching packed
+ * down weights (shared_down.weight columns, then each expert's down^T) and
+ * shared_scale = 1, no y, is the whole layer: the masked dense expert loop
+ * of the reference's universal path (engine.py:66-104) inside the shared
+ * GEMMs.  Routes are gathered from route_table[k, vocab] with clamped ids.
+ */
+int64_t trmoe_dense_routed_features(int64_t shared_width, int num_experts, int64_t expert_width);
+int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                               int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                               int num_experts, int64_t expert_width, const int64_t* token_ids,
+                               const int64_t* route_table, int64_t vocab_size, int top_k,
+                               const float* route_weights, float shared_scale, float routed_scale, void* h,
+                               int64_t ldh, void* stream);
+
+/*
  * K3 -- routed experts; replaces hash_cggr_grouped_gemm (gate, up),
  * fused_swiglu and cggr_grouped_gemm (down) of the reference's fused path
  * (triton_token_routed.py:1033-1342, engine.py:485-507).
@@ -157,7 +187,7 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
  *     y[r, :] = (silu(x_t . Wg_e) * (x_t . Wu_e)) . Wd_e
  * w_gate_up: GATE_UP-packed expert gate/up, groups = E, row_align 128;
  * w_down: PLAIN-packed transposed expert down ([E, hidden, width] view of the
- * reference's [E, width, hidden]), row_align 128.  y is act_dtype [k*n, ldy].
+ * reference's [E, width, hidden]), row_align 256.  y is act_dtype [k*n, ldy].
  * `num_experts` is the active expert count; `expert_width` the active width.
  */
 int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
@@ -177,7 +207,7 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
  *               + routed_scale * sum_j route_weights[j] * y[inverse[j*n + t], c]
  *               (+ residual[t, c] when residual != NULL)
  * h: K2's output (act_dtype, [n, ldh], K = round_up(S, 128));
- * w_down: PLAIN-packed shared_down.weight [hidden, S] (row_align 128).
+ * w_down: PLAIN-packed shared_down.weight [hidden, S] (row_align 256).
  * y/inverse may be NULL (no routed term).  route_weights: top_k host floats.
  */
 int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,

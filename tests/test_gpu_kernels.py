@@ -205,3 +205,42 @@ def test_routed_experts_fp8_and_active_slice(gpu):
     dd = O.dequantize_e4m3(qd, sd, 1)[:Ea, :Wa, :]
     ref = _routed_ref(x, table, ids, dg, du, dd, O.ORDER_TOKEN)
     assert nerr(y, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,H,S", [(4100, 256, 3072), (16384, 896, 3072)])
+def test_shared_gate_up_big_tiles(gpu, dtype, N, H, S):
+    """Shapes that select the 256x256 workgroup tile (with an M tail)."""
+    from complexity_amd import ops
+
+    x = _rand(N, H, seed=40).to(dtype)
+    wg, wu = _rand(S, H, scale=0.05, seed=41).to(dtype), _rand(S, H, scale=0.05, seed=42).to(dtype)
+    pg, _ = ops.pack_linear_gate_up(wg.to(gpu), wu.to(gpu))
+    h = ops.shared_gate_up(x.to(gpu), pg, None, S).cpu()
+    rows = torch.randperm(N, generator=torch.Generator().manual_seed(1))[:512]
+    rows = torch.cat([rows, torch.arange(N - 40, N)])
+    xr = x[rows].double()
+    ref = F.silu(xr @ wg.double().T) * (xr @ wu.double().T)
+    assert nerr(h[rows, :S], ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,S,H", [(16384, 3072, 896), (9000, 1024, 2048), (4096, 512, 896)])
+def test_shared_down_combine_big_tiles(gpu, dtype, N, S, H):
+    """256x224 (H = 896) and 256x256 (H = 2048) down tiles, with M tails."""
+    from complexity_amd import ops
+
+    k = 2
+    h = _rand(N, S, scale=0.5, seed=43).to(dtype)
+    wd = _rand(H, S, scale=0.05, seed=44).to(dtype)
+    pd, _ = ops.pack_linear_down(wd.to(gpu))
+    y = _rand(k * N, H, seed=45).to(dtype)
+    perm = torch.randperm(k * N, generator=torch.Generator().manual_seed(46))
+    hp = torch.zeros(N, (S + 127) // 128 * 128, dtype=dtype)
+    hp[:, :S] = h
+    out = ops.shared_down_combine(hp.to(gpu), S, pd, None, H, y.to(gpu), perm.to(gpu), k, (0.5, 0.5), 1.0,
+                                  1.0).cpu()
+    rows = torch.cat([torch.randperm(N, generator=torch.Generator().manual_seed(2))[:512], torch.arange(N - 40, N)])
+    yr = y.double()
+    ref = h[rows].double() @ wd.double().T + 0.5 * (yr[perm[rows]] + yr[perm[N + rows]])
+    assert nerr(out[rows], ref) <= TOL[dtype]

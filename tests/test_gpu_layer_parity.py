@@ -244,3 +244,47 @@ def test_graph_backend_replays_hip_kernels(gpu):
             _ = torch.randn(1000, device=gpu).sum()  # unrelated eager work
             torch.cuda.synchronize()
             assert torch.equal(got, eager(x, ids)), step
+
+
+def test_fp32_layer_at_prefill_size(gpu):
+    """C1's fp32 layer at C2's 16384 tokens: the large-tile fp32 kernels."""
+    from dataclasses import replace
+
+    from complexity_amd import workloads as Wl
+
+    w = replace(Wl.C1, name="fp32_16384", batch=8, seq=2048, ids="zipf")
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x, ids = Wl.make_hidden(w).to(gpu), Wl.make_token_ids(w).to(gpu)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["fp32"]
+
+
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("E,k,S,W,dtype,weights", [
+    (4, 2, 3072, 64, "bf16", None),
+    (4, 2, 256, 64, "fp32", (0.7, 0.3)),
+    (8, 4, 96, 12, "fp32", None),
+    (2, 1, 0, 40, "bf16", None),
+    (16, 2, 512, 32, "bf16", None),
+])
+def test_routed_strategies_agree_with_oracle(gpu, strategy, E, k, S, W, dtype, weights):
+    """Both HIP strategies (dense-routed and grouped) on the same engine."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(E + k + S + W)
+    H = 128
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=H, vocab_size=5000, num_experts=E, top_k=k,
+                                             shared_width=S, expert_width=W, routing_strategy="token_id_multi_hash",
+                                             route_weights=weights or (), routed_output_scale=2.0,
+                                             shared_output_scale=0.5, precision=dtype, backend="hip")).to(gpu)
+    if dtype == "bf16":
+        engine = engine.to(torch.bfloat16)
+    engine.routed_strategy = strategy
+    ids = torch.randint(0, 5000, (2, 300), device=gpu)
+    x = torch.randn(2, 300, H, device=gpu, dtype=torch.bfloat16 if dtype == "bf16" else torch.float32)
+    out = _run(engine, x, ids)
+    assert engine._packed.strategy == strategy
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND[dtype]
+    engine.set_active_capacity(num_experts=max(k, E // 2), expert_width=max(1, W // 2))
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND[dtype]

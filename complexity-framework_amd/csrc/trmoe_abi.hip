@@ -173,6 +173,8 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
     TRMOE_REQUIRE(aligned16(w_packed), "shared_gate_up: packed weights must be 16-byte aligned");
     TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)),
                   "shared_gate_up: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    TRMOE_REQUIRE(aligned16(h) && (ldh * elem_bytes(act_dtype)) % 16 == 0,
+                  "shared_gate_up: h must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     GateUpArgs a;
     a.x = x;
     a.ldx = ldx;
@@ -222,6 +224,8 @@ int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_
     TRMOE_REQUIRE(aligned16(w_packed), "dense_routed_gate_up: packed weights must be 16-byte aligned");
     TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)),
                   "dense_routed_gate_up: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    TRMOE_REQUIRE(aligned16(h) && (ldh * elem_bytes(act_dtype)) % 16 == 0,
+                  "dense_routed_gate_up: h must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     GateUpArgs a;
     a.x = x;
     a.ldx = ldx;
@@ -334,6 +338,11 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
     a.ldr = ldr;
     a.out = out;
     a.ldo = ldo;
+    {
+        const int eb = elem_bytes(act_dtype);
+        a.vec_ok = aligned16(out) && (ldo * eb) % 16 == 0 && (y == nullptr || (aligned16(y) && (ldy * eb) % 16 == 0)) &&
+                   (residual == nullptr || (aligned16(residual) && (ldr * eb) % 16 == 0));
+    }
     return launch_down_combine(act_dtype, w_dtype, a, as_stream(stream));
 }
 

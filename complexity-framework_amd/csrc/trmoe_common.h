@@ -121,9 +121,10 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 q) {
 // whole 16-byte chunks can be loaded.
 
 // 16-byte-chunk operand (bf16 or f32 elements in memory and in LDS).
-template <int ROWS>
+template <int ROWS, int NT>
 struct BufRows {
-    static constexpr int kChunks = ROWS * 8 / kThreads;
+    static constexpr int kChunks = ROWS * 8 / NT;
+    static constexpr int kThreadsPerBlock = NT;
     using Reg = u32x4;
     __amdgpu_buffer_rsrc_t rsrc;
     int row_off[kChunks];   // byte offset of the row, kOutOfRange when absent
@@ -137,18 +138,20 @@ struct BufRows {
     }
     __device__ void commit(char* stage, const Reg (&reg)[kChunks]) const {
 #pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            const int q = threadIdx.x + kThreads * j;
-            *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = reg[j];
-        }
+        for (int j = 0; j < kChunks; ++j) commit_one(stage, reg, j);
+    }
+    __device__ __forceinline__ void commit_one(char* stage, const Reg (&reg)[kChunks], int j) const {
+        const int q = threadIdx.x + NT * j;
+        *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = reg[j];
     }
 };
 
 // e4m3 operand: 8-byte chunks in memory (64 K values per stage), expanded to
 // 16-byte bf16 chunks in LDS.
-template <int ROWS>
+template <int ROWS, int NT>
 struct BufRowsFP8 {
-    static constexpr int kChunks = ROWS * 8 / kThreads;
+    static constexpr int kChunks = ROWS * 8 / NT;
+    static constexpr int kThreadsPerBlock = NT;
     using Reg = u32x2;
     __amdgpu_buffer_rsrc_t rsrc;
     int row_off[kChunks];
@@ -162,10 +165,11 @@ struct BufRowsFP8 {
     }
     __device__ void commit(char* stage, const Reg (&reg)[kChunks]) const {
 #pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            const int q = threadIdx.x + kThreads * j;
-            *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = fp8x8_to_bf16x8(reg[j]);
-        }
+        for (int j = 0; j < kChunks; ++j) commit_one(stage, reg, j);
+    }
+    __device__ __forceinline__ void commit_one(char* stage, const Reg (&reg)[kChunks], int j) const {
+        const int q = threadIdx.x + NT * j;
+        *reinterpret_cast<u32x4*>(stage + lds_byte(q >> 3, q & 7)) = fp8x8_to_bf16x8(reg[j]);
     }
 };
 
@@ -174,14 +178,15 @@ struct BufRowsFP8 {
 template <class Prov>
 __device__ __forceinline__ void init_dense_rows(Prov& p, const void* base, int64_t row0, int64_t rows_total,
                                                 int64_t ld_bytes, int kbytes) {
-    constexpr int ROWS = Prov::kChunks * kThreads / 8;
+    constexpr int NT = Prov::kThreadsPerBlock;
+    constexpr int ROWS = Prov::kChunks * NT / 8;
     const int64_t avail = rows_total - row0;
     const int64_t nrows = avail < ROWS ? avail : ROWS;
     p.rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
     p.kbytes = kbytes;
 #pragma unroll
     for (int j = 0; j < Prov::kChunks; ++j) {
-        const int r = (threadIdx.x >> 3) + 32 * j;
+        const int r = (threadIdx.x >> 3) + (NT / 8) * j;
         p.row_off[j] = (r < nrows) ? (int)(r * ld_bytes) : kOutOfRange;
     }
 }
@@ -192,12 +197,14 @@ __device__ __forceinline__ void init_dense_rows(Prov& p, const void* base, int64
 // Block tile BM x BN, 4 waves as WAVES_M x WAVES_N, each wave TM x TN MFMA
 // tiles of 32x32.  Two LDS stages; one barrier per K stage.  `lds` holds
 // 2 * (BM + BN) * 128 bytes.
-template <int BM_, int BN_, int WAVES_M_>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int PGR_ = 1>
 struct TileShape {
+    static constexpr int PGR = PGR_;   // 1, 2: global prefetch depth; 3: full pipeline (see tile_loop_pipe)
     static constexpr int BM = BM_;
     static constexpr int BN = BN_;
     static constexpr int WAVES_M = WAVES_M_;
-    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int WAVES_N = WAVES_N_;
+    static constexpr int NT = 64 * WAVES_M * WAVES_N;   // threads per workgroup
     static constexpr int WM = BM / WAVES_M;
     static constexpr int WN = BN / WAVES_N;
     static constexpr int TM = WM / 32;
@@ -205,6 +212,7 @@ struct TileShape {
     static constexpr int kStageBytes = (BM + BN) * kRowBytes;
     static constexpr int kLdsBytes = 2 * kStageBytes;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+    static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "tile rows must split evenly over threads");
 };
 
 template <class Kind, int TM, int TN>
@@ -228,6 +236,41 @@ __device__ __forceinline__ void mma_stage(const char* As, const char* Bs, int wm
     }
 }
 
+// One K stage of MFMAs with the LDS writes of the next stage (already in
+// registers) spread over its four K groups, so the writes drain while the
+// matrix pipe is busy instead of after it.
+template <class Kind, int TM, int TN, class AProv, class BProv>
+__device__ __forceinline__ void mma_stage_commit(const char* As, const char* Bs, int wm0, int wn0,
+                                                 f32x16 (&acc)[TM][TN], const AProv& ap,
+                                                 const typename AProv::Reg (&ra)[AProv::kChunks],
+                                                 const BProv& bp, const typename BProv::Reg (&rb)[BProv::kChunks],
+                                                 char* nxt_a, char* nxt_b) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+    constexpr int kAPer = (AProv::kChunks + 3) / 4;
+    constexpr int kBPer = (BProv::kChunks + 3) / 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        u32x4 a[TM], b[TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+            a[tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+            b[tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) mfma_group(Kind{}, a[tm], b[tn], acc[tm][tn]);
+#pragma unroll
+        for (int j = g * kAPer; j < (g + 1) * kAPer; ++j)
+            if (j < AProv::kChunks) ap.commit_one(nxt_a, ra, j);
+#pragma unroll
+        for (int j = g * kBPer; j < (g + 1) * kBPer; ++j)
+            if (j < BProv::kChunks) bp.commit_one(nxt_b, rb, j);
+    }
+}
+
 template <class Kind, int TM, int TN>
 __device__ __forceinline__ void zero_acc(f32x16 (&acc)[TM][TN]) {
 #pragma unroll
@@ -238,12 +281,45 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[TM][TN]) {
             for (int i = 0; i < 16; ++i) acc[tm][tn][i] = 0.f;
 }
 
-// A and B both streamed from global.  Two LDS stages and two register sets:
-// the loads of stage kt+2 are issued before the MFMAs of stage kt, so every
-// load has two stages of MFMA work to land before its commit to LDS.
+// A and B both streamed from global through two LDS stages.  Each K stage
+// is one basic block: the loads of stage kt+1 are issued before the MFMAs of
+// stage kt and written to the other LDS stage after them (past the last
+// stage they read zeros and land in a stage nobody reads), then one barrier.
 template <class Kind, class Shape, class AProv, class BProv>
-__device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int K, char* lds, int wm0, int wn0,
-                                          f32x16 (&acc)[Shape::TM][Shape::TN]) {
+__device__ __forceinline__ void tile_loop_pgr1(const AProv& ap, const BProv& bp, int K, char* lds, int wm0,
+                                               int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
+    constexpr int kABytes = Shape::BM * kRowBytes;
+    typename AProv::Reg ra[AProv::kChunks];
+    typename BProv::Reg rb[BProv::kChunks];
+    ap.prefetch(0, ra);
+    bp.prefetch(0, rb);
+    ap.commit(lds, ra);
+    bp.commit(lds + kABytes, rb);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        char* cur = lds + (kt & 1) * Shape::kStageBytes;
+        char* nxt = lds + ((kt + 1) & 1) * Shape::kStageBytes;
+        ap.prefetch(kt + 1, ra);
+        bp.prefetch(kt + 1, rb);
+        // keep the loads at the top of the stage: left alone, the scheduler
+        // sinks them next to the LDS writes and exposes their whole latency
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage<Kind, Shape::TM, Shape::TN>(cur, cur + kABytes, wm0, wn0, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        ap.commit(nxt, ra);
+        bp.commit(nxt + kABytes, rb);
+        __syncthreads();
+    }
+}
+
+// Same contract as tile_loop with two register sets: the loads of stage
+// kt+2 are issued before the MFMAs of stage kt, so a load has two stages of
+// MFMA work to land before its commit.  Unrolled by two with the odd tail
+// after the loop (a mid-loop exit would duplicate the accumulators).
+template <class Kind, class Shape, class AProv, class BProv>
+__device__ __forceinline__ void tile_loop_pgr2(const AProv& ap, const BProv& bp, int K, char* lds, int wm0,
+                                               int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
     const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
     constexpr int kABytes = Shape::BM * kRowBytes;
     char* st0 = lds;
@@ -252,40 +328,136 @@ __device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int 
     typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
     ap.prefetch(0, ra0);
     bp.prefetch(0, rb0);
-    if (nk > 1) {
-        ap.prefetch(1, ra1);
-        bp.prefetch(1, rb1);
-    }
+    ap.prefetch(1, ra1);
+    bp.prefetch(1, rb1);
     ap.commit(st0, ra0);
     bp.commit(st0 + kABytes, rb0);
     __syncthreads();
     int kt = 0;
     for (; kt + 1 < nk; kt += 2) {
         // st0 holds stage kt; ra1/rb1 carry stage kt+1
-        if (kt + 2 < nk) {
-            ap.prefetch(kt + 2, ra0);
-            bp.prefetch(kt + 2, rb0);
-        }
+        ap.prefetch(kt + 2, ra0);
+        bp.prefetch(kt + 2, rb0);
+        __builtin_amdgcn_sched_barrier(0);
         mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
+        __builtin_amdgcn_sched_barrier(0);
         ap.commit(st1, ra1);
         bp.commit(st1 + kABytes, rb1);
         __syncthreads();
         // st1 holds stage kt+1; ra0/rb0 carry stage kt+2
-        if (kt + 3 < nk) {
-            ap.prefetch(kt + 3, ra1);
-            bp.prefetch(kt + 3, rb1);
-        }
+        ap.prefetch(kt + 3, ra1);
+        bp.prefetch(kt + 3, rb1);
+        __builtin_amdgcn_sched_barrier(0);
         mma_stage<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc);
-        if (kt + 2 < nk) {
-            ap.commit(st0, ra0);
-            bp.commit(st0 + kABytes, rb0);
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        ap.commit(st0, ra0);
+        bp.commit(st0 + kABytes, rb0);
         __syncthreads();
     }
     if (kt < nk) {  // odd stage count: the last stage sits in st0
         mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
         __syncthreads();
     }
+}
+
+// Full software pipeline: loads of stage kt+2 are issued at the top of stage
+// kt (two register sets), and stage kt+1 (already in registers) is written
+// to the other LDS stage between the MFMA groups of stage kt; one barrier per
+// stage.  Loads past the last stage read zeros into a stage nobody reads.
+template <class Kind, class Shape, class AProv, class BProv>
+__device__ __forceinline__ void tile_loop_pipe(const AProv& ap, const BProv& bp, int K, char* lds, int wm0,
+                                               int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
+    constexpr int kABytes = Shape::BM * kRowBytes;
+    char* st0 = lds;
+    char* st1 = lds + Shape::kStageBytes;
+    typename AProv::Reg ra0[AProv::kChunks], ra1[AProv::kChunks];
+    typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
+    ap.prefetch(0, ra0);
+    bp.prefetch(0, rb0);
+    ap.prefetch(1, ra1);
+    bp.prefetch(1, rb1);
+    ap.commit(st0, ra0);
+    bp.commit(st0 + kABytes, rb0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        ap.prefetch(kt + 2, ra0);
+        bp.prefetch(kt + 2, rb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc, ap, ra1, bp, rb1, st1,
+                                                      st1 + kABytes);
+        __syncthreads();
+        ap.prefetch(kt + 3, ra1);
+        bp.prefetch(kt + 3, rb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc, ap, ra0, bp, rb0, st0,
+                                                      st0 + kABytes);
+        __syncthreads();
+    }
+    if (kt < nk) {  // odd stage count: the last stage sits in st0
+        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
+        __syncthreads();
+    }
+}
+
+// The same pipeline split in two so that a persistent kernel can start the
+// next tile's loads (pipe_start) before the current tile's epilogue and run
+// its K loop later (pipe_body).
+template <class AProv, class BProv>
+struct PipeRegs {
+    typename AProv::Reg ra0[AProv::kChunks], ra1[AProv::kChunks];
+    typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
+};
+
+template <class AProv, class BProv>
+__device__ __forceinline__ void pipe_start(const AProv& ap, const BProv& bp, PipeRegs<AProv, BProv>& rg) {
+    ap.prefetch(0, rg.ra0);
+    bp.prefetch(0, rg.rb0);
+    ap.prefetch(1, rg.ra1);
+    bp.prefetch(1, rg.rb1);
+}
+
+template <class Kind, class Shape, class AProv, class BProv>
+__device__ __forceinline__ void pipe_body(const AProv& ap, const BProv& bp, PipeRegs<AProv, BProv>& rg, int K,
+                                          char* lds, int wm0, int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
+    constexpr int kABytes = Shape::BM * kRowBytes;
+    char* st0 = lds;
+    char* st1 = lds + Shape::kStageBytes;
+    ap.commit(st0, rg.ra0);
+    bp.commit(st0 + kABytes, rg.rb0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        ap.prefetch(kt + 2, rg.ra0);
+        bp.prefetch(kt + 2, rg.rb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc, ap, rg.ra1, bp, rg.rb1,
+                                                      st1, st1 + kABytes);
+        __syncthreads();
+        ap.prefetch(kt + 3, rg.ra1);
+        bp.prefetch(kt + 3, rg.rb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc, ap, rg.ra0, bp, rg.rb0,
+                                                      st0, st0 + kABytes);
+        __syncthreads();
+    }
+    if (kt < nk) {  // odd stage count: the last stage sits in st0
+        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
+        __syncthreads();
+    }
+}
+
+template <class Kind, class Shape, class AProv, class BProv>
+__device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int K, char* lds, int wm0, int wn0,
+                                          f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    if constexpr (Shape::PGR == 3)
+        tile_loop_pipe<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
+    else if constexpr (Shape::PGR == 2)
+        tile_loop_pgr2<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
+    else
+        tile_loop_pgr1<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
 }
 
 // A resident in LDS (one 128-byte-row stage per K stage, BM rows each), B
@@ -305,7 +477,9 @@ __device__ __forceinline__ void tile_loop_lds_a(const char* a_lds, int a_stage_b
         char* nxt = bstage + ((kt + 1) & 1) * kBBytes;
         const bool more = kt + 1 < nk;
         if (more) bp.prefetch(kt + 1, rb);
+        __builtin_amdgcn_sched_barrier(0);
         mma_stage<Kind, Shape::TM, Shape::TN>(a_lds + kt * a_stage_bytes, cur, wm0, wn0, acc);
+        __builtin_amdgcn_sched_barrier(0);
         if (more) bp.commit(nxt, rb);
         __syncthreads();
     }

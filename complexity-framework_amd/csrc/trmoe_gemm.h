@@ -68,6 +68,7 @@ struct DownArgs {
     int64_t ldr;
     void* out;
     int64_t ldo;
+    int vec_ok;             // y / residual / out rows 16-byte aligned (vector epilogue)
 };
 
 struct RoutedArgs {

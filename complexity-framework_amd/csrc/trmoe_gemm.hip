@@ -74,50 +74,42 @@ int launch_pack(const PackArgs& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 // B operand selection: same kind as A, or e4m3 expanded to bf16
 // ---------------------------------------------------------------------------
-template <class Kind, bool FP8, int ROWS>
+template <class Kind, bool FP8, int ROWS, int NT>
 struct BProvSel {
-    using type = BufRows<ROWS>;
+    using type = BufRows<ROWS, NT>;
 };
-template <class Kind, int ROWS>
-struct BProvSel<Kind, true, ROWS> {
-    using type = BufRowsFP8<ROWS>;
+template <class Kind, int ROWS, int NT>
+struct BProvSel<Kind, true, ROWS, NT> {
+    using type = BufRowsFP8<ROWS, NT>;
 };
 
 // Packed weight rows [row0, row0 + ROWS) of a [rows, ld] packed tensor
 // (every such row exists: packing pads rows to the tile multiple).
-template <class Kind, bool FP8, int ROWS>
-__device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS>::type& bp, const void* base,
+template <class Kind, bool FP8, int ROWS, int NT>
+__device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS, NT>::type& bp, const void* base,
                                            int64_t ld, int64_t row0, int K) {
     const int64_t elem = FP8 ? 1 : (int64_t)sizeof(typename Kind::T);
     init_dense_rows(bp, base, row0, row0 + ROWS, ld * elem, (int)(K * elem));
 }
 
-using ShapeMain = TileShape<128, 128, 2>;
-using ShapeBig = TileShape<256, 256, 2>;
-using ShapeDown224 = TileShape<256, 224, 4>;
+using ShapeMain = TileShape<128, 128, 2, 2>;
+using ShapeBig = TileShape<256, 256, 2, 4>;        // 8 waves of 128x64, 2 waves per SIMD
+using ShapeBig8P2 = TileShape<256, 256, 2, 4, 2>;  // same, two stages of global prefetch
+using ShapeBig4P2 = TileShape<256, 256, 2, 2, 2>;  // 4 waves of 128x128, two stages of prefetch
+using ShapeDown224 = TileShape<256, 224, 4, 1>;
+using ShapeDown224P2 = TileShape<256, 224, 4, 1, 2>;
+using ShapeBig8Pipe = TileShape<256, 256, 2, 4, 3>;
+using ShapeBig4Pipe = TileShape<256, 256, 2, 2, 3>;
+using ShapeDown224Pipe = TileShape<256, 224, 4, 1, 3>;
 
 // ---------------------------------------------------------------------------
 // K2: shared gate|up + SwiGLU
 // ---------------------------------------------------------------------------
-template <class Kind, bool FP8, class Shape>
-__global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
-    using T = typename Kind::T;
-    extern __shared__ __align__(16) char lds[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
-    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
-    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
-    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
-
-    BufRows<Shape::BM> ap;
-    init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
-    typename BProvSel<Kind, FP8, Shape::BN>::type bp;
-    init_bprov<Kind, FP8, Shape::BN>(bp, a.w, a.ldw, n0, a.K);
-
-    // Routes of this tile's rows, gathered once while the first stages load
-    // (tiles holding expert features only); read back in the epilogue after
-    // the main loop's barriers.
-    __shared__ int s_route[Shape::BM][kMaxTopK];
+// Gathers the routes of rows [m0, m0 + BM) into s_route for tiles that hold
+// expert features (dense-routed strategy).
+template <class Shape>
+__device__ __forceinline__ void gate_up_routes(const GateUpArgs& a, int64_t m0, int64_t n0,
+                                               int (*s_route)[kMaxTopK]) {
     const bool tile_routed = a.ids != nullptr && ((n0 + Shape::BN) >> 1) > a.shared_feats;
     if (tile_routed && threadIdx.x < Shape::BM) {
         const int64_t row = m0 + threadIdx.x;
@@ -126,17 +118,28 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
         for (int j = 0; j < kMaxTopK; ++j)
             s_route[threadIdx.x][j] = (j < a.top_k && row < a.M) ? (int)a.table[(int64_t)j * a.vocab + id] : -1;
     }
+}
 
-    f32x16 acc[Shape::TM][Shape::TN];
-    zero_acc<Kind>(acc);
-    tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
-
+// SwiGLU epilogue: h values are written to LDS (free after the main loop's
+// last barrier) as a [BM][BN/2] tile with rows padded by 16 bytes, then
+// copied out with coalesced 16-byte stores.  Ends with LDS still in use by
+// the copy; callers that reuse LDS must barrier first.
+template <class Kind, class Shape>
+__device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
+                                                 int64_t m0, int64_t n0, char* lds,
+                                                 const int (*s_route)[kMaxTopK]) {
+    using T = typename Kind::T;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    constexpr int kHRowBytes = Shape::BN / 2 * (int)sizeof(T) + 16;
+    static_assert(Shape::BM * kHRowBytes <= 160 * 1024, "h tile must fit in LDS");
     const int r = lane & 31;
 #pragma unroll
     for (int p = 0; p < Shape::TN / 2; ++p) {
         const int64_t pbase = n0 + wn0 + 64 * p;     // packed row of the gate tile
         const int64_t fblock = pbase >> 1;            // first feature of this 32-feature block
-        const int64_t feat = fblock + r;
+        const int fl = wn0 / 2 + 32 * p + r;          // feature within the tile
         const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
         const float su = a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f;
         // expert blocks are multiples of 64 features, so a 32-feature block
@@ -148,22 +151,103 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
         for (int tm = 0; tm < Shape::TM; ++tm) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int64_t row = m0 + wm0 + tm * 32 + acc_row(lane, i);
-                if (row < a.M) {
-                    const float g = acc[tm][2 * p][i] * sg;
-                    const float u = acc[tm][2 * p + 1][i] * su;
-                    float hv = silu_f(g) * u * mult;
-                    if (routed) {
-                        const int* rr = s_route[wm0 + tm * 32 + acc_row(lane, i)];
-                        float tw = 0.f;
+                const int rl = wm0 + tm * 32 + acc_row(lane, i);
+                const float g = acc[tm][2 * p][i] * sg;
+                const float u = acc[tm][2 * p + 1][i] * su;
+                float hv = silu_f(g) * u * mult;
+                if (routed) {
+                    const int* rr = s_route[rl];
+                    float tw = 0.f;
 #pragma unroll
-                        for (int j = 0; j < kMaxTopK; ++j) tw += (rr[j] == expert) ? a.rw[j] : 0.f;
-                        hv *= tw;
-                    }
-                    static_cast<T*>(a.h)[row * a.ldh + feat] = from_f32<T>(hv);
+                    for (int j = 0; j < kMaxTopK; ++j) tw += (rr[j] == expert) ? a.rw[j] : 0.f;
+                    hv *= tw;
                 }
+                *reinterpret_cast<T*>(lds + rl * kHRowBytes + fl * (int)sizeof(T)) = from_f32<T>(hv);
             }
         }
+    }
+    __syncthreads();
+    constexpr int kChunksPerRow = Shape::BN / 2 * (int)sizeof(T) / 16;
+    constexpr int kChunks = Shape::BM * kChunksPerRow;
+    char* hbase = static_cast<char*>(a.h) + (n0 >> 1) * (int64_t)sizeof(T);
+#pragma unroll 4
+    for (int q = threadIdx.x; q < kChunks; q += Shape::NT) {
+        const int rl = q / kChunksPerRow, c = q % kChunksPerRow;
+        const int64_t row = m0 + rl;
+        if (row < a.M)
+            *reinterpret_cast<u32x4*>(hbase + row * a.ldh * (int64_t)sizeof(T) + c * 16) =
+                *reinterpret_cast<const u32x4*>(lds + rl * kHRowBytes + c * 16);
+    }
+}
+
+template <class Kind, bool FP8, class Shape>
+__global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
+    using T = typename Kind::T;
+    extern __shared__ __align__(16) char lds[];
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+
+    BufRows<Shape::BM, Shape::NT> ap;
+    init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type bp;
+    init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
+
+    // Routes of this tile's rows, gathered once while the first stages load;
+    // read back in the epilogue after the main loop's barriers.
+    __shared__ int s_route[Shape::BM][kMaxTopK];
+    gate_up_routes<Shape>(a, m0, n0, s_route);
+
+    f32x16 acc[Shape::TM][Shape::TN];
+    zero_acc<Kind>(acc);
+    tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
+    gate_up_epilogue<Kind, Shape>(a, acc, m0, n0, lds, s_route);
+}
+
+// Persistent form: gridDim.x workgroups walk the tiles (M fastest).  The
+// next tile's first two K stages are loaded into registers before the
+// current tile's epilogue, so the SwiGLU math and stores overlap those loads.
+template <class Kind, bool FP8, class Shape>
+__global__ __launch_bounds__(Shape::NT) void k_gate_up_persistent(GateUpArgs a, int tiles_m, int total) {
+    using T = typename Kind::T;
+    using AProv = BufRows<Shape::BM, Shape::NT>;
+    using BProv = typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type;
+    extern __shared__ __align__(16) char lds[];
+    __shared__ int s_route[Shape::BM][kMaxTopK];
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    int tile = blockIdx.x;
+    if (tile >= total) return;
+
+    AProv ap;
+    BProv bp;
+    PipeRegs<AProv, BProv> rg;
+    int64_t m0 = (int64_t)(tile % tiles_m) * Shape::BM;
+    int64_t n0 = (int64_t)(tile / tiles_m) * Shape::BN;
+    init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
+    pipe_start(ap, bp, rg);
+    while (true) {
+        gate_up_routes<Shape>(a, m0, n0, s_route);
+        f32x16 acc[Shape::TM][Shape::TN];
+        zero_acc<Kind>(acc);
+        pipe_body<Kind, Shape>(ap, bp, rg, a.K, lds, wm0, wn0, acc);
+        const int next = tile + (int)gridDim.x;
+        const int64_t cm0 = m0, cn0 = n0;
+        if (next < total) {
+            m0 = (int64_t)(next % tiles_m) * Shape::BM;
+            n0 = (int64_t)(next / tiles_m) * Shape::BN;
+            init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+            init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
+            pipe_start(ap, bp, rg);
+        }
+        gate_up_epilogue<Kind, Shape>(a, acc, cm0, cn0, lds, s_route);
+        __syncthreads();  // LDS and s_route are reused by the next tile
+        if (next >= total) break;
+        tile = next;
     }
 }
 
@@ -171,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void k_gate_up_swiglu(GateUpArgs a) {
 // K4: shared down + weighted un-permute + combine
 // ---------------------------------------------------------------------------
 template <class Kind, bool FP8, class Shape>
-__global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
+__global__ __launch_bounds__(Shape::NT) void k_down_combine(DownArgs a) {
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -180,10 +264,10 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
-    BufRows<Shape::BM> ap;
+    BufRows<Shape::BM, Shape::NT> ap;
     init_dense_rows(ap, a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), a.K * (int)sizeof(T));
-    typename BProvSel<Kind, FP8, Shape::BN>::type bp;
-    init_bprov<Kind, FP8, Shape::BN>(bp, a.w, a.ldw, n0, a.K);
+    typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type bp;
+    init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
 
     // y row of each (tile row, slot), clamped so that a malformed route table
     // cannot become a wild read; gathered while the first stages load.
@@ -211,29 +295,91 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     const T* y = static_cast<const T*>(a.y);
     const T* res = static_cast<const T*>(a.residual);
     T* out = static_cast<T*>(a.out);
+    if constexpr (sizeof(T) == 2) {
+        // bf16: the scaled shared term goes to LDS as a [BM][BN] tile (rows
+        // padded by 16 bytes); the routed gather, residual and store then run
+        // over 16-byte chunks of 8 columns.
+        constexpr int kORowBytes = Shape::BN * 2 + 16;
 #pragma unroll
-    for (int tm = 0; tm < Shape::TM; ++tm) {
+        for (int tm = 0; tm < Shape::TM; ++tm)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int64_t row = m0 + wm0 + tm * 32 + acc_row(lane, i);
-            if (row >= a.M) continue;
-            int64_t yrow[kMaxTopK];
-            if (y != nullptr) {
-                const int* yr = s_yrow[wm0 + tm * 32 + acc_row(lane, i)];
-                for (int j = 0; j < a.top_k; ++j) yrow[j] = (int64_t)yr[j] * a.ldy;
+            for (int i = 0; i < 16; ++i) {
+                const int rl = wm0 + tm * 32 + acc_row(lane, i);
+#pragma unroll
+                for (int tn = 0; tn < Shape::TN; ++tn)
+                    *reinterpret_cast<T*>(lds + rl * kORowBytes + (wn0 + tn * 32 + r) * 2) =
+                        from_f32<T>(acc[tm][tn][i] * cscale[tn]);
             }
+        __syncthreads();
+        constexpr int kChunksPerRow = Shape::BN / 8;
+        for (int q = threadIdx.x; q < Shape::BM * kChunksPerRow; q += Shape::NT) {
+            const int rl = q / kChunksPerRow, c = q % kChunksPerRow;
+            const int64_t row = m0 + rl;
+            const int64_t col = n0 + c * 8;
+            if (row >= a.M || col >= a.N) continue;
+            const u32x4 sv = *reinterpret_cast<const u32x4*>(lds + rl * kORowBytes + c * 16);
+            const bf16x8 sb = __builtin_bit_cast(bf16x8, sv);
+            float v[8];
 #pragma unroll
-            for (int tn = 0; tn < Shape::TN; ++tn) {
-                const int64_t col = n0 + wn0 + tn * 32 + r;
-                if (col >= a.N) continue;
-                float v = acc[tm][tn][i] * cscale[tn];
+            for (int e = 0; e < 8; ++e) v[e] = (float)sb[e];
+            if (a.vec_ok && col + 8 <= a.N) {
                 if (y != nullptr) {
-                    float s = 0.f;
-                    for (int j = 0; j < a.top_k; ++j) s += a.rw[j] * to_f32(y[yrow[j] + col]);
-                    v += a.routed_scale * s;
+                    float acc_r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                    for (int j = 0; j < a.top_k; ++j) {
+                        const bf16x8 yv = __builtin_bit_cast(
+                            bf16x8, *reinterpret_cast<const u32x4*>(y + (int64_t)s_yrow[rl][j] * a.ldy + col));
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc_r[e] += a.rw[j] * (float)yv[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] += a.routed_scale * acc_r[e];
                 }
-                if (res != nullptr) v += to_f32(res[row * a.ldr + col]);
-                out[row * a.ldo + col] = from_f32<T>(v);
+                if (res != nullptr) {
+                    const bf16x8 rv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(res + row * a.ldr + col));
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] += (float)rv[e];
+                }
+                bf16x8 ov;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ov[e] = (bf16_t)v[e];
+                *reinterpret_cast<u32x4*>(out + row * a.ldo + col) = __builtin_bit_cast(u32x4, ov);
+            } else {
+                for (int e = 0; e < 8 && col + e < a.N; ++e) {
+                    float x = v[e];
+                    if (y != nullptr) {
+                        float sacc = 0.f;
+                        for (int j = 0; j < a.top_k; ++j)
+                            sacc += a.rw[j] * to_f32(y[(int64_t)s_yrow[rl][j] * a.ldy + col + e]);
+                        x += a.routed_scale * sacc;
+                    }
+                    if (res != nullptr) x += to_f32(res[row * a.ldr + col + e]);
+                    out[row * a.ldo + col + e] = from_f32<T>(x);
+                }
+            }
+        }
+    } else {
+        // f32: the tile would not fit in LDS; combine straight from registers
+#pragma unroll
+        for (int tm = 0; tm < Shape::TM; ++tm) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int rl = wm0 + tm * 32 + acc_row(lane, i);
+                const int64_t row = m0 + rl;
+                if (row >= a.M) continue;
+#pragma unroll
+                for (int tn = 0; tn < Shape::TN; ++tn) {
+                    const int64_t col = n0 + wn0 + tn * 32 + r;
+                    if (col >= a.N) continue;
+                    float v = acc[tm][tn][i] * cscale[tn];
+                    if (y != nullptr) {
+                        float sacc = 0.f;
+                        for (int j = 0; j < a.top_k; ++j)
+                            sacc += a.rw[j] * to_f32(y[(int64_t)s_yrow[rl][j] * a.ldy + col]);
+                        v += a.routed_scale * sacc;
+                    }
+                    if (res != nullptr) v += to_f32(res[row * a.ldr + col]);
+                    out[row * a.ldo + col] = from_f32<T>(v);
+                }
             }
         }
     }
@@ -248,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
 // leaves h (128 rows x F_pad features) in LDS in the operand layout; phase 2
 // streams the expert's packed down rows in 128-column chunks against it.
 template <class Kind, bool FP8, class Shape>
-__global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
+__global__ __launch_bounds__(Shape::NT) void k_routed_experts(RoutedArgs a) {
     using T = typename Kind::T;
     constexpr int SE = Kind::kStageElems;
     constexpr int EPC = Kind::kPerChunk;
@@ -295,12 +441,12 @@ __global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
     // ---- phase 1: h = silu(x Wg) * (x Wu) into LDS
     const int nchunks = a.F_pad / 64;
     for (int fc = 0; fc < nchunks; ++fc) {
-        BufRows<Shape::BM> ap;
+        BufRows<Shape::BM, Shape::NT> ap;
         ap.rsrc = make_rsrc(a.x, (uint32_t)(a.n_tokens * a.ldx * (int64_t)sizeof(T)));
         ap.kbytes = a.K * (int)sizeof(T);
 #pragma unroll
-        for (int j = 0; j < BufRows<Shape::BM>::kChunks; ++j) {
-            const int row = (threadIdx.x >> 3) + 32 * j;
+        for (int j = 0; j < BufRows<Shape::BM, Shape::NT>::kChunks; ++j) {
+            const int row = (threadIdx.x >> 3) + (Shape::NT / 8) * j;
             if (row < rows) {
                 const int64_t t = (int64_t)((uint64_t)a.sorted[row0 + row] % (uint64_t)a.n_tokens);
                 ap.row_off[j] = (int)(t * a.ldx * (int64_t)sizeof(T));
@@ -308,8 +454,8 @@ __global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
                 ap.row_off[j] = kOutOfRange;
             }
         }
-        typename BProvSel<Kind, FP8, Shape::BN>::type bp;
-        init_bprov<Kind, FP8, Shape::BN>(bp, wgu, a.wgu_ld, (int64_t)fc * 128, a.K);
+        typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type bp;
+        init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, wgu, a.wgu_ld, (int64_t)fc * 128, a.K);
         f32x16 acc[Shape::TM][Shape::TN];
         zero_acc<Kind>(acc);
         tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
@@ -337,8 +483,8 @@ __global__ __launch_bounds__(kThreads) void k_routed_experts(RoutedArgs a) {
     const int ncol = (a.H + Shape::BN - 1) / Shape::BN;
     T* y = static_cast<T*>(a.y);
     for (int oc = 0; oc < ncol; ++oc) {
-        typename BProvSel<Kind, FP8, Shape::BN>::type bp;
-        init_bprov<Kind, FP8, Shape::BN>(bp, wd, a.wd_ld, (int64_t)oc * Shape::BN, a.W);
+        typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type bp;
+        init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, wd, a.wd_ld, (int64_t)oc * Shape::BN, a.W);
         f32x16 acc[Shape::TM][Shape::TN];
         zero_acc<Kind>(acc);
         tile_loop_lds_a<Kind, Shape>(hs, hs_stage_bytes, bp, a.W, lds, wm0, wn0, acc);
@@ -402,34 +548,84 @@ static int ensure_lds(F* fn, int bytes) {
 // no padded columns).
 constexpr int64_t kBigTileMinBlocks = 512;
 
-// TRMOE_GEMM_TILE=small|big forces one tile family (tuning sweeps); unset = auto.
+// TRMOE_GEMM_TILE forces one tile family for tuning sweeps: small (128x128),
+// big (256x256, 8 waves), big8p2, big4p2 (two-stage prefetch); unset = auto.
+enum TileChoice {
+    kTileAuto = 0, kTileSmall, kTileBig, kTileBig8P2, kTileBig4P2, kTileBig8Pipe, kTileBig4Pipe,
+    kTilePersist8, kTilePersist4
+};
 static int tile_override() {
     static int v = [] {
         const char* e = getenv("TRMOE_GEMM_TILE");
-        if (e == nullptr) return 0;
-        if (strcmp(e, "small") == 0) return 1;
-        if (strcmp(e, "big") == 0) return 2;
-        return 0;
+        if (e == nullptr) return (int)kTileAuto;
+        if (strcmp(e, "small") == 0) return (int)kTileSmall;
+        if (strcmp(e, "big") == 0) return (int)kTileBig;
+        if (strcmp(e, "big8p2") == 0) return (int)kTileBig8P2;
+        if (strcmp(e, "big4p2") == 0) return (int)kTileBig4P2;
+        if (strcmp(e, "big8pipe") == 0) return (int)kTileBig8Pipe;
+        if (strcmp(e, "big4pipe") == 0) return (int)kTileBig4Pipe;
+        if (strcmp(e, "persist8") == 0) return (int)kTilePersist8;
+        if (strcmp(e, "persist4") == 0) return (int)kTilePersist4;
+        return (int)kTileAuto;
     }();
     return v;
+}
+
+static int device_cus() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        return n;
+    }();
+    return cus;
+}
+
+template <class Kind, bool FP8, class Shape>
+static int launch_gate_up_persistent(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int tiles_m = (int)((a.M + Shape::BM - 1) / Shape::BM);
+    const int total = tiles_m * (int)(packed_rows / Shape::BN);
+    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    auto kern = k_gate_up_persistent<Kind, FP8, Shape>;
+    int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    int per_cu = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, Shape::NT, kLds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    int grid = device_cus() * per_cu;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Shape::NT), kLds, stream, a, tiles_m, total);
+    return check_launch("shared_gate_up");
 }
 
 template <class Kind, bool FP8, class Shape>
 static int launch_gate_up_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)(packed_rows / Shape::BN));
-    int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape>, Shape::kLdsBytes);
+    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape>, kLds);
     if (st) return st;
-    hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape>), grid, dim3(kThreads), Shape::kLdsBytes, stream, a);
+    hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
     return check_launch("shared_gate_up");
 }
 
 template <class Kind, bool FP8>
 static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    const int64_t big_blocks = ((a.M + ShapeBig::BM - 1) / ShapeBig::BM) * (packed_rows / ShapeBig::BN);
-    const int ov = tile_override();
-    if (packed_rows % ShapeBig::BN == 0 && (ov == 2 || (ov == 0 && big_blocks >= kBigTileMinBlocks)))
-        return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-    return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
+    const int64_t big_blocks = ((a.M + 255) / 256) * (packed_rows / 256);
+    int ov = tile_override();
+    if (ov == kTileAuto) ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? kTileBig : kTileSmall;
+    if (packed_rows % 256 != 0) ov = kTileSmall;
+    switch (ov) {
+        case kTileBig: return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+        case kTileBig8P2: return launch_gate_up_shape<Kind, FP8, ShapeBig8P2>(a, packed_rows, stream);
+        case kTileBig4P2: return launch_gate_up_shape<Kind, FP8, ShapeBig4P2>(a, packed_rows, stream);
+        case kTileBig8Pipe: return launch_gate_up_shape<Kind, FP8, ShapeBig8Pipe>(a, packed_rows, stream);
+        case kTileBig4Pipe: return launch_gate_up_shape<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
+        case kTilePersist8: return launch_gate_up_persistent<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+        case kTilePersist4: return launch_gate_up_persistent<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
+        default: return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
+    }
 }
 
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
@@ -442,9 +638,11 @@ int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, h
 template <class Kind, bool FP8, class Shape>
 static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
     dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)((a.N + Shape::BN - 1) / Shape::BN));
-    int st = ensure_lds(k_down_combine<Kind, FP8, Shape>, Shape::kLdsBytes);
+    constexpr int kEpi = sizeof(typename Kind::T) == 2 ? Shape::BM * (Shape::BN * 2 + 16) : 0;
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    int st = ensure_lds(k_down_combine<Kind, FP8, Shape>, kLds);
     if (st) return st;
-    hipLaunchKernelGGL((k_down_combine<Kind, FP8, Shape>), grid, dim3(kThreads), Shape::kLdsBytes, stream, a);
+    hipLaunchKernelGGL((k_down_combine<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
     return check_launch("shared_down_combine");
 }
 
@@ -453,12 +651,26 @@ static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
 template <class Kind, bool FP8>
 static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
     const int64_t mt = (a.M + 255) / 256;
-    const int ov = tile_override();
-    if (ov == 1) return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
-    if (a.N % ShapeDown224::BN == 0 && (ov == 2 || mt * (a.N / ShapeDown224::BN) >= 256))
-        return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
-    if (ov == 2 || mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
-    return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
+    const bool fits224 = a.N % ShapeDown224::BN == 0;
+    int ov = tile_override();
+    if (ov == kTileAuto) {
+        if (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
+        ov = (mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) ? kTileBig : kTileSmall;
+    }
+    switch (ov) {
+        case kTileBig:
+            if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
+            return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
+        case kTileBig8P2: return launch_down_shape<Kind, FP8, ShapeBig8P2>(a, stream);
+        case kTileBig4P2:
+            if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224P2>(a, stream);
+            return launch_down_shape<Kind, FP8, ShapeBig4P2>(a, stream);
+        case kTileBig8Pipe: return launch_down_shape<Kind, FP8, ShapeBig8Pipe>(a, stream);
+        case kTileBig4Pipe:
+            if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Pipe>(a, stream);
+            return launch_down_shape<Kind, FP8, ShapeBig4Pipe>(a, stream);
+        default: return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
+    }
 }
 
 int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream) {
@@ -469,7 +681,7 @@ int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream)
 }
 
 // 64-row tiles halve the LDS-resident h for wide fp32 experts.
-using ShapeRoutedSmall = TileShape<64, 128, 2>;
+using ShapeRoutedSmall = TileShape<64, 128, 2, 2>;
 
 template <class Shape>
 static int routed_lds_bytes_for(int act, int64_t f_pad) {
@@ -491,7 +703,7 @@ static int launch_routed_shape(int act, const RoutedArgs& a, int64_t assignments
     const int64_t max_tiles = (assignments + Shape::BM - 1) / Shape::BM + a.E;
     int st = ensure_lds(k_routed_experts<Kind, FP8, Shape>, lds);
     if (st) return st;
-    hipLaunchKernelGGL((k_routed_experts<Kind, FP8, Shape>), dim3((unsigned)max_tiles), dim3(kThreads), lds,
+    hipLaunchKernelGGL((k_routed_experts<Kind, FP8, Shape>), dim3((unsigned)max_tiles), dim3(Shape::NT), lds,
                        stream, a);
     return check_launch("routed_experts");
 }

@@ -19,6 +19,7 @@ of the same workload.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -161,6 +162,8 @@ def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 30, warmup:
             for e in engines:
                 e(x, ids)
         torch.cuda.synchronize()
+        gc.collect()
+        gc.disable()
         s, t = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for _ in range(steps):
@@ -168,6 +171,7 @@ def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 30, warmup:
                 e(x, ids)
         t.record()
         torch.cuda.synchronize()
+        gc.enable()
     per_layer_ms = s.elapsed_time(t) / (steps * layers)
     H, S, E, Wd = w.hidden, w.shared, w.experts, w.width
     weight_bytes = 2 * (3 * H * S + 3 * E * H * Wd)
@@ -193,6 +197,11 @@ def time_engine(torch, engine, x, ids, steps, warmup, timer):
             engine(x, ids)
         assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
         torch.cuda.synchronize()
+        # a full collection of the interpreter's heap (torch's import leaves
+        # millions of objects) stalls the host for ~40 ms; keep it out of the
+        # timed region, as timeit does
+        gc.collect()
+        gc.disable()
         timer.enabled = True
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
@@ -203,7 +212,26 @@ def time_engine(torch, engine, x, ids, steps, warmup, timer):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         timer.enabled = False
+        gc.enable()
     return start.elapsed_time(stop) / steps, timer.averages_ms(), wall, engine._packed.strategy
+
+
+def measured_traffic(workload: str, op: str):
+    """HBM bytes per launch of `op` on `workload`, as recorded from rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs in profiles/traffic_*.txt (each counter scaled
+    by what it reads for a copy kernel of known size); None when absent."""
+    for path in sorted((ROOT / "profiles").glob("traffic_*.txt")):
+        fields = {}
+        for line in path.read_text().splitlines():
+            if " = " in line and not line.startswith("#"):
+                key, val = line.split(" = ", 1)
+                fields[key.strip()] = val.strip()
+        if fields.get("workload") == workload and fields.get("op") == op:
+            try:
+                return float(fields["traffic_bytes_per_launch"])
+            except (KeyError, ValueError):
+                return None
+    return None
 
 
 def kernel_report(w, kernel_ms, strategy):
@@ -219,15 +247,17 @@ def kernel_report(w, kernel_ms, strategy):
     dominant = max(kernel_ms, key=kernel_ms.get)
     dwk = work[dominant]
     dms = kernel_ms[dominant]
+    traffic = measured_traffic(w.name, dominant)
     if dwk["flops"]:
         achieved = dwk["flops"] / (dms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK[w.dtype], "unit": "TFLOP/s",
-                "frac": achieved / PEAK[w.dtype], "traffic": None, "kernel": dominant,
-                "algorithmic_flops_per_launch": dwk["flops"], "avg_us": dms * 1e3}
+                "frac": achieved / PEAK[w.dtype], "traffic": traffic, "kernel": dominant,
+                "algorithmic_flops_per_launch": dwk["flops"], "algorithmic_bytes_per_launch": dwk["bytes"],
+                "avg_us": dms * 1e3}
     else:
         achieved = dwk["bytes"] / (dms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK, "traffic": None, "kernel": dominant,
+                "frac": achieved / HBM_PEAK, "traffic": traffic, "kernel": dominant,
                 "algorithmic_bytes_per_launch": dwk["bytes"], "avg_us": dms * 1e3}
     return kernels, dominant, roof
 
@@ -241,6 +271,8 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="end with three elementwise copies of MIB MiB (reference kernel for HBM counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -308,6 +340,14 @@ def main():
         result["decode"] = decode_hbm(torch, workloads, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(w, min(args.cpu_sample, tokens))
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.ones(n // 2, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = n
     print(json.dumps(result))
 
 

@@ -24,6 +24,7 @@ backends then compute with the dequantised values q * scale.
 from __future__ import annotations
 
 import logging
+import os
 from dataclasses import replace
 from typing import Callable, Dict, Optional
 
@@ -552,9 +553,10 @@ class TRHashEngine(nn.Module):
 class _CapturedTRHashGraph:
     """One lazily captured static-shape inference graph (engine.py:658-716).
 
-    The captured body is the HIP backend when the library is available (the
-    kernels record no memset nodes and allocate nothing outside torch's graph
-    pool), else the PYTORCH definition.
+    The captured body is the HIP backend (its kernels record no memset nodes
+    and allocate nothing outside torch's graph pool).  Without the library
+    the capture raises, unless TRMOE_ALLOW_PYTORCH_FALLBACK=1 asks for the
+    PYTORCH definition explicitly.
     """
 
     def __init__(self, engine: TRHashEngine, bucket: GraphBucket, sample: torch.Tensor):
@@ -564,7 +566,12 @@ class _CapturedTRHashGraph:
 
         self.engine = engine
         self.bucket = bucket
-        self.inner = TRHashBackend.HIP if _native.available() else TRHashBackend.PYTORCH
+        if _native.available():
+            self.inner = TRHashBackend.HIP
+        elif capabilities_allow_fallback():
+            self.inner = TRHashBackend.PYTORCH
+        else:
+            raise RuntimeError(f"CUDA_GRAPH needs the HIP library: {_native.load_error()}")
         shape = (bucket.batch_size, bucket.sequence_length, engine.config.hidden_size)
         self.hidden = torch.zeros(shape, dtype=sample.dtype, device=sample.device)
         self.token_ids = torch.zeros(bucket.batch_size, bucket.sequence_length, dtype=torch.long,

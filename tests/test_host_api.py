@@ -1,0 +1,340 @@
+"""CPU tests of the host package: the mirror of the reference's TR-Hash API.
+
+They follow the behaviours the reference's own tests pin
+(tests/test_tr_hash_engine.py, tests/test_tr_hash_dynamic_moe.py,
+tests/test_tr_hash_fused_kernel_parity.py) on the product modules, with the
+routing checked against the golden vectors written from the reference, and
+the PYTORCH (universal) backend checked against the CPU oracle.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from complexity_amd.core.mlp import MLPConfig, TRHashEngineMLP
+from complexity_amd.core.registry import MLP_REGISTRY
+from complexity_amd.tr_hash import (
+    GraphBucket,
+    TRHashBackend,
+    TRHashEngine,
+    TRHashEngineConfig,
+    TRHashPhase,
+    TRHashPrecision,
+    TRHashStrategy,
+)
+from complexity_amd.tr_hash.buckets import GraphBucketPlanner
+from complexity_amd.tr_hash.capabilities import select_backend, supports_fused_cuda
+from complexity_amd.tr_hash.routing import (
+    build_route_table,
+    compile_top2_pair_metadata,
+    decode_top2_pair_metadata,
+    mix32,
+)
+from oracle import trmoe_oracle as O
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _digest(table) -> str:
+    return hashlib.sha256(np.ascontiguousarray(np.asarray(table), dtype=np.int64).tobytes()).hexdigest()
+
+
+def _config(**kw) -> TRHashEngineConfig:
+    base = dict(hidden_size=32, vocab_size=257, num_experts=4, top_k=2, shared_width=48, expert_width=16,
+                routing_strategy=TRHashStrategy.MULTI_HASH)
+    base.update(kw)
+    return TRHashEngineConfig(**base)
+
+
+# --------------------------------------------------------------------------- config
+
+
+@pytest.mark.parametrize("num_experts", [1, 2, 3, 4, 5, 8, 16, 32])
+@pytest.mark.parametrize("top_k", [1, 2, 3, 4])
+def test_supported_expert_and_topk_matrix(num_experts, top_k):
+    ok = num_experts in (1, 2, 4, 8, 16) and top_k in (1, 2, 4) and top_k <= num_experts
+    if ok:
+        cfg = _config(num_experts=num_experts, top_k=top_k)
+        assert len(cfg.route_weights) == top_k
+        assert abs(sum(cfg.route_weights) - 1.0) < 1e-6
+    else:
+        with pytest.raises(ValueError):
+            _config(num_experts=num_experts, top_k=top_k)
+
+
+@pytest.mark.parametrize("kw", [dict(route_hash_count=1), dict(route_hash_count=9), dict(route_weights=(0.7, 0.7)),
+                                dict(route_weights=(1.5, -0.5)), dict(route_weights=(1.0,)),
+                                dict(shared_width=-1), dict(expert_width=0)])
+def test_config_rejects_invalid_values(kw):
+    with pytest.raises(ValueError):
+        _config(**kw)
+
+
+def test_cuda_graph_config_is_inference_only_and_requires_buckets():
+    with pytest.raises(ValueError):
+        _config(backend=TRHashBackend.CUDA_GRAPH, phase=TRHashPhase.INFERENCE)
+    with pytest.raises(ValueError):
+        _config(backend=TRHashBackend.CUDA_GRAPH, graph_buckets=(GraphBucket(1, 8),))
+    cfg = _config(backend=TRHashBackend.CUDA_GRAPH, phase=TRHashPhase.INFERENCE,
+                  graph_buckets=(GraphBucket(4, 64), GraphBucket(1, 8)))
+    assert [b.token_capacity for b in cfg.graph_buckets] == [8, 256]
+
+
+def test_cuda_graph_bucket_selection_is_smallest_containing_shape():
+    planner = GraphBucketPlanner([GraphBucket(8, 128), GraphBucket(1, 64), GraphBucket(2, 32), GraphBucket(4, 16)])
+    # (1, 64) and (4, 16) hold 64 tokens each: ties go to the smaller batch
+    assert planner.select(1, 16) == GraphBucket(1, 64)
+    assert planner.select(3, 16) == GraphBucket(4, 16)
+    assert planner.select(2, 20) == GraphBucket(2, 32)
+    assert planner.select(1, 40) == GraphBucket(1, 64)
+    assert planner.select(3, 100) == GraphBucket(8, 128)
+    with pytest.raises(ValueError):
+        planner.select(9, 1)
+    with pytest.raises(ValueError):
+        planner.select(0, 1)
+
+
+# --------------------------------------------------------------------------- routing
+
+
+def test_mix32_matches_oracle_on_edge_values():
+    vals = np.array([0, 1, 2, 0x7FFFFFFF, 0x80000000, 0xFFFFFFFF, 0x9E3779B1, 12345678], dtype=np.uint64)
+    got = mix32(torch.from_numpy(vals.astype(np.int64))).numpy().astype(np.uint64)
+    assert np.array_equal(got, O.mix32(vals))
+
+
+def test_product_route_tables_match_every_reference_digest():
+    data = json.loads((GOLDEN / "route_digests.json").read_text())
+    assert data["route_seed"] == 0x71D5A17
+    for case in data["cases"]:
+        cfg = TRHashEngineConfig(hidden_size=8, vocab_size=case["vocab_size"], num_experts=case["num_experts"],
+                                 top_k=case["top_k"], shared_width=8, expert_width=8,
+                                 routing_strategy=TRHashStrategy(case["strategy"]),
+                                 layer_index=case["layer_index"], route_hash_count=case["hash_count"])
+        table = build_route_table(cfg)
+        assert table.dtype == torch.int64 and tuple(table.shape) == (case["top_k"], case["vocab_size"])
+        assert table[:, :32].tolist() == case["head"], case
+        assert _digest(table.numpy()) == case["sha256"], case
+
+
+@pytest.mark.parametrize("experts", [4, 8, 16])
+def test_product_full_table_matches_reference_vectors(experts):
+    golden = np.load(GOLDEN / "route_tables_v32000.npz")[f"multi_e{experts}_l0"].astype(np.int64)
+    cfg = TRHashEngineConfig(hidden_size=8, vocab_size=32000, num_experts=experts, top_k=2, shared_width=8,
+                             expert_width=8, routing_strategy=TRHashStrategy.MULTI_HASH)
+    assert np.array_equal(build_route_table(cfg).numpy(), golden)
+
+
+def test_route_tables_are_deterministic_distinct_and_use_every_expert():
+    for strategy in TRHashStrategy:
+        for experts, k in ((4, 2), (8, 4), (16, 2)):
+            cfg = _config(vocab_size=4096, num_experts=experts, top_k=k, routing_strategy=strategy)
+            a, b = build_route_table(cfg), build_route_table(cfg)
+            assert torch.equal(a, b)
+            assert int(a.min()) >= 0 and int(a.max()) < experts
+            srt = a.sort(dim=0).values
+            assert bool((srt[1:] != srt[:-1]).all()), strategy
+            assert set(a[0].tolist()) == set(range(experts)), strategy
+
+
+def test_multi_hash_routes_depend_on_every_hash_channel_and_layer():
+    base = build_route_table(_config(vocab_size=4096, route_hash_count=2))
+    assert not torch.equal(base, build_route_table(_config(vocab_size=4096, route_hash_count=3)))
+    assert not torch.equal(base, build_route_table(_config(vocab_size=4096, layer_index=1)))
+    assert not torch.equal(base, build_route_table(_config(vocab_size=4096, route_seed=7)))
+
+
+@pytest.mark.parametrize("strategy", ["modulo_cyclic", "token_id_balanced_hash", "token_id_affine_hash",
+                                      "token_id_multi_hash"])
+@pytest.mark.parametrize("experts", [2, 4, 8])
+def test_compact_top2_pair_metadata_matches_reference_and_round_trips(strategy, experts):
+    gold = np.load(GOLDEN / "pair_codes_v997.npz")
+    routes = torch.from_numpy(gold[f"{strategy}_e{experts}_routes"].astype(np.int64))
+    codes, pairs = compile_top2_pair_metadata(routes, num_experts=experts)
+    assert np.array_equal(codes.numpy(), gold[f"{strategy}_e{experts}_codes"])
+    assert np.array_equal(pairs.numpy(), gold[f"{strategy}_e{experts}_pairs"])
+    assert torch.equal(decode_top2_pair_metadata(codes, pairs), routes)
+
+
+def test_compact_pair_metadata_rejects_unsupported_shape():
+    with pytest.raises(ValueError):
+        compile_top2_pair_metadata(torch.zeros(3, 10, dtype=torch.long), num_experts=4)
+    with pytest.raises(ValueError):
+        compile_top2_pair_metadata(torch.zeros(2, 10, dtype=torch.long), num_experts=16)
+
+
+# --------------------------------------------------------------------------- backend policy
+
+
+def test_auto_backend_on_cpu_is_pytorch_with_reason():
+    d = select_backend(_config(), device_type="cpu")
+    assert d.requested is TRHashBackend.AUTO and d.selected is TRHashBackend.PYTORCH
+    assert d.reasons
+
+
+def test_auto_backend_on_gpu_selects_hip_and_pytorch_under_autograd():
+    cfg = _config()
+    d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False, fused_cuda_available=False)
+    assert d.selected is TRHashBackend.HIP
+    d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False,
+                       fused_cuda_available=False, autograd=True)
+    assert d.selected is TRHashBackend.PYTORCH and d.reasons
+
+
+def test_missing_library_on_gpu_fails_loudly(monkeypatch):
+    monkeypatch.delenv("TRMOE_ALLOW_PYTORCH_FALLBACK", raising=False)
+    with pytest.raises(RuntimeError):
+        select_backend(_config(), device_type="cuda", hip_available=False, cggr_available=False,
+                       fused_cuda_available=False)
+    monkeypatch.setenv("TRMOE_ALLOW_PYTORCH_FALLBACK", "1")
+    d = select_backend(_config(), device_type="cuda", hip_available=False, cggr_available=False,
+                       fused_cuda_available=False)
+    assert d.selected is TRHashBackend.PYTORCH and any("unavailable" in r for r in d.reasons)
+
+
+def test_explicit_backends_resolve_with_reasons():
+    fused = _config(backend=TRHashBackend.FUSED_CUDA)
+    d = select_backend(fused, device_type="cuda", hip_available=True, cggr_available=False, fused_cuda_available=False)
+    assert d.selected is TRHashBackend.HIP and d.reasons
+    with pytest.raises(RuntimeError):
+        select_backend(_config(backend=TRHashBackend.FUSED_CUDA, num_experts=16), device_type="cuda",
+                       hip_available=True, cggr_available=False, fused_cuda_available=False)
+    cggr = _config(backend=TRHashBackend.CGGR, num_experts=16)
+    d = select_backend(cggr, device_type="cuda", hip_available=True, cggr_available=False, fused_cuda_available=False)
+    assert d.selected is TRHashBackend.HIP and d.partition == "assignment"
+    with pytest.raises(RuntimeError):
+        select_backend(_config(backend=TRHashBackend.HIP), device_type="cpu")
+    with pytest.raises(RuntimeError):
+        select_backend(_config(backend=TRHashBackend.HIP), device_type="cuda", hip_available=True, autograd=True)
+
+
+def test_fused_eligibility_is_the_reference_pair_shape():
+    assert supports_fused_cuda(_config(num_experts=4, top_k=2))
+    assert supports_fused_cuda(_config(num_experts=8, top_k=2))
+    assert not supports_fused_cuda(_config(num_experts=16, top_k=2))
+    assert not supports_fused_cuda(_config(num_experts=4, top_k=1))
+
+
+@pytest.mark.parametrize("precision", [TRHashPrecision.INT8])
+def test_int8_fails_explicitly(precision):
+    with pytest.raises(NotImplementedError):
+        select_backend(_config(precision=precision), device_type="cpu")
+
+
+# --------------------------------------------------------------------------- engine (PYTORCH backend, CPU)
+
+
+def _engine(seed=0, **kw):
+    torch.manual_seed(seed)
+    cfg = _config(precision=TRHashPrecision.FP32, **kw)
+    eng = TRHashEngine(cfg).eval()
+    with torch.no_grad():
+        for p in eng.parameters():
+            p.normal_(0.0, 0.2)
+    return eng
+
+
+def test_pytorch_backend_matches_token_by_token_definition():
+    eng = _engine()
+    x = torch.randn(2, 9, 32)
+    ids = torch.randint(0, 257, (2, 9))
+    with torch.no_grad():
+        out = eng(x, ids)
+    assert eng.last_backend.selected is TRHashBackend.PYTORCH
+    params = {"expert_gate": eng.expert_gate, "expert_up": eng.expert_up, "expert_down": eng.expert_down,
+              "shared_gate": eng.shared_gate.weight, "shared_up": eng.shared_up.weight,
+              "shared_down": eng.shared_down.weight}
+    want = O.naive_engine_output(x.double(), ids, eng.route_table, {k: v.double() for k, v in params.items()},
+                                 route_weights=eng.config.route_weights)
+    assert torch.allclose(out.double(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_capability_summary_contract_is_stable_across_shapes():
+    keys = None
+    for experts, k in ((4, 2), (16, 2), (8, 4), (1, 1)):
+        summary = _engine(num_experts=experts, top_k=k).capability_summary()
+        json.dumps(summary)
+        assert len(summary) == 21
+        keys = keys or set(summary)
+        assert set(summary) == keys
+        assert summary["selected_backend"] == "pytorch"
+
+
+def test_default_active_capacity_equals_allocation_and_restriction_routes_to_active_pool():
+    eng = _engine(num_experts=8, top_k=2)
+    assert (eng.active_num_experts, eng.active_expert_width) == (8, 16)
+    eng.set_active_capacity(num_experts=4)
+    assert int(eng._active_route_table.max()) < 4
+
+
+def test_reduced_capacity_changes_output_and_restoring_reproduces_it():
+    eng = _engine(num_experts=8, top_k=2)
+    x = torch.randn(1, 12, 32)
+    ids = torch.randint(0, 257, (1, 12))
+    with torch.no_grad():
+        full = eng(x, ids)
+        eng.set_active_capacity(num_experts=4, expert_width=8)
+        reduced = eng(x, ids)
+        eng.set_active_capacity(num_experts=8, expert_width=16)
+        restored = eng(x, ids)
+    assert reduced.shape == full.shape
+    assert not torch.allclose(reduced, full)
+    assert torch.equal(restored, full)
+
+
+@pytest.mark.parametrize("kw", [dict(num_experts=3), dict(num_experts=16), dict(expert_width=17),
+                                dict(expert_width=0), dict(num_experts=1)])
+def test_set_active_capacity_rejects_invalid_requests(kw):
+    eng = _engine(num_experts=8, top_k=2)
+    with pytest.raises(ValueError):
+        eng.set_active_capacity(**kw)
+
+
+def test_fp8_quantization_matches_oracle_e4m3():
+    eng = _engine()
+    eng.quantize_fp8_()
+    for name, w in (("expert_gate", eng.expert_gate), ("expert_down", eng.expert_down),
+                    ("shared_up", eng.shared_up.weight), ("shared_down", eng.shared_down.weight)):
+        q, s = O.quantize_e4m3(w.detach().float(), reduce_dim=1)  # the K axis of every weight
+        assert torch.equal(getattr(eng, name + "_fp8").view(torch.uint8), q.view(torch.uint8)), name
+        assert torch.equal(getattr(eng, name + "_scale"), s), name
+
+
+# --------------------------------------------------------------------------- MLP adapter
+
+
+def _mlp_config(**kw):
+    base = dict(hidden_size=32, intermediate_size=64, vocab_size=257, num_experts=4, top_k=2,
+                routing_strategy="token_id_multi_hash")
+    base.update(kw)
+    return MLPConfig(**base)
+
+
+def test_mlp_registry_builds_the_engine_and_requires_token_ids():
+    for name in ("tr_hash_engine", "tr_hash_moe"):
+        mlp = MLP_REGISTRY.build(name, _mlp_config())
+        assert isinstance(mlp, TRHashEngineMLP)
+    mlp = MLP_REGISTRY.build("tr_hash_engine", _mlp_config())
+    with pytest.raises(ValueError):
+        mlp(torch.randn(1, 4, 32))
+    out = mlp(torch.randn(1, 4, 32), token_ids=torch.randint(0, 257, (1, 4)))
+    assert out.shape == (1, 4, 32)
+
+
+@pytest.mark.parametrize("switch,expected", [(False, TRHashBackend.PYTORCH), ("hip", TRHashBackend.HIP)])
+def test_use_custom_kernels_switch_maps_to_backends(switch, expected):
+    mlp = TRHashEngineMLP(_mlp_config(use_custom_kernels=switch))
+    assert mlp.engine.config.backend is expected
+
+
+def test_mlp_adapter_exposes_dynamic_capacity_controls():
+    mlp = TRHashEngineMLP(_mlp_config(num_experts=8))
+    mlp.set_active_experts(4)
+    mlp.set_active_expert_width(4)
+    assert (mlp.engine.active_num_experts, mlp.engine.active_expert_width) == (4, 4)

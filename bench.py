@@ -150,36 +150,61 @@ def cpu_baseline(w, sample_tokens: int, reps: int = 5):
     }
 
 
-def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 30, warmup: int = 5):
+def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 50, warmup: int = 5):
     """C3 decode: 64 tokens through `layers` distinct weight sets per step (286 MB
-    of bf16 weights > the 256 MB Infinity Cache), per-layer time and HBM GB/s."""
+    of bf16 weights > the 256 MB Infinity Cache), per-layer time and HBM GB/s.
+
+    A decode step of the stack is captured once as a HIP graph (the serving
+    form of the reference's CUDA_GRAPH backend, engine.py:597-716) and
+    replayed; the eager per-layer time is reported beside it."""
     w = workloads.C3
     engines = [workloads.build_engine(w, dev, backend="hip", seed=i) for i in range(layers)]
     x = workloads.make_hidden(w).to(dev).to(torch.bfloat16)
     ids = workloads.make_token_ids(w).to(dev)
-    with torch.no_grad():
-        for _ in range(warmup):
-            for e in engines:
-                e(x, ids)
+
+    def stack():
+        out = None
+        for e in engines:
+            out = e(x, ids)
+        return out
+
+    def timed(fn, n):
         torch.cuda.synchronize()
         gc.collect()
         gc.disable()
         s, t = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        for _ in range(steps):
-            for e in engines:
-                e(x, ids)
+        for _ in range(n):
+            fn()
         t.record()
         torch.cuda.synchronize()
         gc.enable()
-    per_layer_ms = s.elapsed_time(t) / (steps * layers)
+        return s.elapsed_time(t) / (n * layers)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            stack()
+        eager_ms = timed(stack, steps)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            stack()
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            stack()
+        for _ in range(warmup):
+            graph.replay()
+        per_layer_ms = timed(graph.replay, steps)
     H, S, E, Wd = w.hidden, w.shared, w.experts, w.width
     weight_bytes = 2 * (3 * H * S + 3 * E * H * Wd)
     bytes_per_layer = weight_bytes + 2 * 2 * w.tokens * H + 8 * w.tokens + 8 * 2 * w.tokens
     return {
         "workload": w.name,
         "layers_rotated": layers,
+        "mode": "hip_graph_replay",
         "ms_per_layer": per_layer_ms,
+        "eager_ms_per_layer": eager_ms,
         "tokens_per_s": w.tokens / (per_layer_ms * 1e-3),
         "hbm_gbps": bytes_per_layer / (per_layer_ms * 1e-3) / 1e9,
         "hbm_frac": bytes_per_layer / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK,

@@ -290,11 +290,13 @@ def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor
     n = h.shape[0]
     out = torch.empty(n, hidden, dtype=h.dtype, device=h.device)
     rw = _weights_arg(route_weights)
+    ws_bytes = lib.trmoe_shared_down_combine_workspace_bytes(dtype_code(h.dtype), n, shared_width, hidden)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=h.device) if ws_bytes else None
     st = lib.trmoe_shared_down_combine(
         dtype_code(h.dtype), dtype_code(w_down.dtype), _p(h), n, shared_width, h.stride(0), _p(w_down),
         _p(w_scale), hidden, _p(y), hidden, _p(inverse), top_k, ctypes.cast(rw, ctypes.c_void_p),
         float(shared_scale), float(routed_scale), _p(residual),
-        residual.stride(0) if residual is not None else 0, _p(out), hidden, _stream(h))
+        residual.stride(0) if residual is not None else 0, _p(out), hidden, _p(ws), ws_bytes, _stream(h))
     N.check(st, "trmoe_shared_down_combine")
     return out
 

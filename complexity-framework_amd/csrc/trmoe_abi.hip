@@ -300,7 +300,8 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
                               const float* w_scale, int64_t hidden, const void* y, int64_t ldy,
                               const int64_t* inverse, int top_k, const float* route_weights,
                               float shared_scale, float routed_scale, const void* residual,
-                              int64_t ldr, void* out, int64_t ldo, void* stream) {
+                              int64_t ldr, void* out, int64_t ldo, void* workspace,
+                              size_t workspace_bytes, void* stream) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_down_combine: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_down_combine: bad dimensions");
     TRMOE_REQUIRE(ldh >= shared_width && ldo >= hidden, "shared_down_combine: bad leading dimension");
@@ -343,7 +344,19 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
         a.vec_ok = aligned16(out) && (ldo * eb) % 16 == 0 && (y == nullptr || (aligned16(y) && (ldy * eb) % 16 == 0)) &&
                    (residual == nullptr || (aligned16(residual) && (ldr * eb) % 16 == 0));
     }
+    const size_t need = down_skinny_workspace_bytes(n_tokens, hidden, shared_width, act_dtype);
+    if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
+        TRMOE_REQUIRE(aligned16(workspace), "shared_down_combine: workspace must be 16-byte aligned");
+        return launch_down_skinny(act_dtype, w_dtype, a, workspace, as_stream(stream));
+    }
     return launch_down_combine(act_dtype, w_dtype, a, as_stream(stream));
+}
+
+size_t trmoe_shared_down_combine_workspace_bytes(int act_dtype, int64_t n_tokens, int64_t shared_width,
+                                                 int64_t hidden) {
+    if (act_dtype != TRMOE_F32 && act_dtype != TRMOE_BF16) return 0;
+    if (n_tokens < 1 || shared_width < 1 || hidden < 1) return 0;
+    return down_skinny_workspace_bytes(n_tokens, hidden, shared_width, act_dtype);
 }
 
 int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y, int64_t ldy,

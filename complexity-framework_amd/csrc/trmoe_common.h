@@ -199,7 +199,9 @@ __device__ __forceinline__ void init_dense_rows(Prov& p, const void* base, int64
 // 2 * (BM + BN) * 128 bytes.
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int PGR_ = 1>
 struct TileShape {
-    static constexpr int PGR = PGR_;   // 1, 2: global prefetch depth; 3: full pipeline (see tile_loop_pipe)
+    // 1, 2: register prefetch depth; 3: full register pipeline (tile_loop_pipe);
+    // 4: direct buffer->LDS loads (tile_loop_dma, bf16/f32 operands only)
+    static constexpr int PGR = PGR_;
     static constexpr int BM = BM_;
     static constexpr int BN = BN_;
     static constexpr int WAVES_M = WAVES_M_;
@@ -449,10 +451,114 @@ __device__ __forceinline__ void pipe_body(const AProv& ap, const BProv& bp, Pipe
     }
 }
 
+// ---------------------------------------------------------------------------
+// direct buffer -> LDS operand loads
+// ---------------------------------------------------------------------------
+// `buffer_load_dwordx4 ... lds` writes each lane's 16 bytes to LDS at
+// M0 + 16 * lane, without passing through VGPRs (out-of-range offsets write
+// zeros, like ordinary buffer loads).  One wave instruction therefore fills
+// 8 consecutive 128-byte tile rows; the swizzle is applied on the global
+// side: the lane that owns LDS slot s of row r fetches K chunk s ^ swz(r),
+// so the stage ends up in the layout lds_byte() describes.
+//
+// Waits are explicit: vmcnt counts these loads, and a workgroup barrier
+// after the wait makes every wave's rows visible.
+
+#define TRMOE_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt on vmcnt only (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// Workgroup barrier that orders the compiler's memory operations around it
+// without the vmcnt(0) drain of __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int ROWS, int NT>
+struct DmaRows {
+    static constexpr int kInstr = ROWS * 8 / NT;   // wave instructions per thread per stage
+    static constexpr int kWaves = NT / 64;
+    static_assert(ROWS % (8 * kWaves) == 0, "each wave fills whole 8-row groups");
+    __amdgpu_buffer_rsrc_t rsrc;
+    int off[kInstr];    // lane's byte offset in the row for K stage 0, kOutOfRange when absent
+    int koff[kInstr];   // byte offset of the lane's chunk within a K stage
+    int kbytes;
+    int wave;           // wave index, uniform
+
+    // rows [row0, row0 + ROWS) of a matrix with rows_total rows of ld_bytes
+    __device__ __forceinline__ void init(const void* base, int64_t row0, int64_t rows_total, int64_t ld_bytes,
+                                         int kbytes_) {
+        const int64_t avail = rows_total - row0;
+        const int64_t nrows = avail < ROWS ? avail : ROWS;
+        rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
+        kbytes = kbytes_;
+        wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int r = (wave * kInstr + j) * 8 + (lane >> 3);
+            koff[j] = ((lane & 7) ^ lds_swz(r)) * 16;
+            off[j] = r < nrows ? (int)(r * ld_bytes) + koff[j] : kOutOfRange;
+        }
+    }
+    __device__ __forceinline__ void issue(int kt, char* stage) const {
+        const int kb = kt * kRowBytes;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int o = (kb + koff[j] < kbytes) ? off[j] + kb : kOutOfRange;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(stage + (wave * kInstr + j) * 8 * kRowBytes),
+                                                    16, o, 0, 0, 0);
+        }
+    }
+};
+
+// Two LDS stages filled by DmaRows: stage kt+2 is requested as soon as every
+// wave has read stage kt, so each load has one stage of MFMA work to land.
+// Ends with a full barrier (callers reuse LDS in their epilogues).
+template <class Kind, class Shape, class AP, class BP>
+__device__ __forceinline__ void tile_loop_dma(const AP& ap, const BP& bp, int K, char* lds, int wm0, int wn0,
+                                              f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
+    constexpr int kABytes = Shape::BM * kRowBytes;
+    constexpr int kPer = AP::kInstr + BP::kInstr;
+    ap.issue(0, lds);
+    bp.issue(0, lds + kABytes);
+    if (nk > 1) {
+        ap.issue(1, lds + Shape::kStageBytes);
+        bp.issue(1, lds + Shape::kStageBytes + kABytes);
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+        char* st = lds + (kt & 1) * Shape::kStageBytes;
+        if (kt + 1 < nk)
+            wait_vmcnt<kPer>();
+        else
+            wait_vmcnt<0>();
+        lds_barrier();
+        mma_stage<Kind, Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
+        if (kt + 2 < nk) {
+            wait_lgkmcnt0();   // this wave's reads of the stage are complete
+            lds_barrier();     // ... and every other wave's
+            ap.issue(kt + 2, st);
+            bp.issue(kt + 2, st + kABytes);
+        }
+    }
+    __syncthreads();
+}
+
 template <class Kind, class Shape, class AProv, class BProv>
 __device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int K, char* lds, int wm0, int wn0,
                                           f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    if constexpr (Shape::PGR == 3)
+    if constexpr (Shape::PGR == 4)
+        tile_loop_dma<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
+    else if constexpr (Shape::PGR == 3)
         tile_loop_pipe<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
     else if constexpr (Shape::PGR == 2)
         tile_loop_pgr2<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);

@@ -108,7 +108,13 @@ struct CombineArgs {
     int64_t ldo;
 };
 
+// Token counts at or below this run the decode-shape kernels (trmoe_skinny.hip).
+constexpr int64_t kSkinnyMaxTokens = 128;
+
 int launch_pack(const PackArgs& p, hipStream_t stream);
+int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
+size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act);
+int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream);
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
 int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream);
 int routed_lds_bytes(int act, int64_t f_pad);

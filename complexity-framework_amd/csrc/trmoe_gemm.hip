@@ -92,6 +92,38 @@ __device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS, NT
     init_dense_rows(bp, base, row0, row0 + ROWS, ld * elem, (int)(K * elem));
 }
 
+// Operand providers of a tile shape: direct buffer->LDS loads for PGR 4,
+// register-staged loads otherwise (and always for e4m3 weights, which are
+// expanded to bf16 on the way into LDS).
+template <class Shape>
+struct AProvOf {
+    using type = std::conditional_t<Shape::PGR == 4, DmaRows<Shape::BM, Shape::NT>, BufRows<Shape::BM, Shape::NT>>;
+};
+template <class Kind, bool FP8, class Shape>
+struct BProvOf {
+    static_assert(!(FP8 && Shape::PGR == 4), "e4m3 weights need the register path");
+    using type = std::conditional_t<Shape::PGR == 4, DmaRows<Shape::BN, Shape::NT>,
+                                    typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type>;
+};
+template <class Shape>
+__device__ __forceinline__ void init_a(typename AProvOf<Shape>::type& ap, const void* base, int64_t row0,
+                                       int64_t rows_total, int64_t ld_bytes, int kbytes) {
+    if constexpr (Shape::PGR == 4)
+        ap.init(base, row0, rows_total, ld_bytes, kbytes);
+    else
+        init_dense_rows(ap, base, row0, rows_total, ld_bytes, kbytes);
+}
+template <class Kind, bool FP8, class Shape>
+__device__ __forceinline__ void init_b(typename BProvOf<Kind, FP8, Shape>::type& bp, const void* base, int64_t ld,
+                                       int64_t row0, int K) {
+    if constexpr (Shape::PGR == 4) {
+        const int64_t elem = (int64_t)sizeof(typename Kind::T);
+        bp.init(base, row0, row0 + Shape::BN, ld * elem, (int)(K * elem));
+    } else {
+        init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, base, ld, row0, K);
+    }
+}
+
 using ShapeMain = TileShape<128, 128, 2, 2>;
 using ShapeBig = TileShape<256, 256, 2, 4>;        // 8 waves of 128x64, 2 waves per SIMD
 using ShapeBig8P2 = TileShape<256, 256, 2, 4, 2>;  // same, two stages of global prefetch
@@ -101,6 +133,8 @@ using ShapeDown224P2 = TileShape<256, 224, 4, 1, 2>;
 using ShapeBig8Pipe = TileShape<256, 256, 2, 4, 3>;
 using ShapeBig4Pipe = TileShape<256, 256, 2, 2, 3>;
 using ShapeDown224Pipe = TileShape<256, 224, 4, 1, 3>;
+using ShapeBigDma = TileShape<256, 256, 2, 4, 4>;    // 8 waves, direct buffer->LDS operand loads
+using ShapeDown224Dma = TileShape<256, 224, 4, 1, 4>;
 
 // ---------------------------------------------------------------------------
 // K2: shared gate|up + SwiGLU
@@ -190,10 +224,10 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
-    BufRows<Shape::BM, Shape::NT> ap;
-    init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
-    typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type bp;
-    init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
+    typename AProvOf<Shape>::type ap;
+    init_a<Shape>(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    typename BProvOf<Kind, FP8, Shape>::type bp;
+    init_b<Kind, FP8, Shape>(bp, a.w, a.ldw, n0, a.K);
 
     // Routes of this tile's rows, gathered once while the first stages load;
     // read back in the epilogue after the main loop's barriers.
@@ -264,10 +298,10 @@ __global__ __launch_bounds__(Shape::NT) void k_down_combine(DownArgs a) {
     const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
-    BufRows<Shape::BM, Shape::NT> ap;
-    init_dense_rows(ap, a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), a.K * (int)sizeof(T));
-    typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type bp;
-    init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
+    typename AProvOf<Shape>::type ap;
+    init_a<Shape>(ap, a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    typename BProvOf<Kind, FP8, Shape>::type bp;
+    init_b<Kind, FP8, Shape>(bp, a.w, a.ldw, n0, a.K);
 
     // y row of each (tile row, slot), clamped so that a malformed route table
     // cannot become a wild read; gathered while the first stages load.
@@ -541,18 +575,19 @@ static int ensure_lds(F* fn, int bytes) {
     return TRMOE_OK;
 }
 
-// Tile choice: 256x256 workgroup tiles (128x128 per wave) halve the L2->CU
+// Tile choice: 256x256 workgroup tiles (8 waves of 128x64) halve the L2->CU
 // traffic per MFMA relative to 128x128 and are used whenever they still give
 // at least two workgroups per CU; the down GEMM uses 256x224 when the hidden
 // size is a multiple of 224 (896 = 4 x 224: one full wave of 256 tiles with
-// no padded columns).
+// no padded columns).  bf16/f32 operands take the direct buffer->LDS loads
+// (PGR 4); e4m3 weights the register-staged loop that expands them.
 constexpr int64_t kBigTileMinBlocks = 512;
 
 // TRMOE_GEMM_TILE forces one tile family for tuning sweeps: small (128x128),
 // big (256x256, 8 waves), big8p2, big4p2 (two-stage prefetch); unset = auto.
 enum TileChoice {
     kTileAuto = 0, kTileSmall, kTileBig, kTileBig8P2, kTileBig4P2, kTileBig8Pipe, kTileBig4Pipe,
-    kTilePersist8, kTilePersist4
+    kTilePersist8, kTilePersist4, kTileDma
 };
 static int tile_override() {
     static int v = [] {
@@ -566,6 +601,7 @@ static int tile_override() {
         if (strcmp(e, "big4pipe") == 0) return (int)kTileBig4Pipe;
         if (strcmp(e, "persist8") == 0) return (int)kTilePersist8;
         if (strcmp(e, "persist4") == 0) return (int)kTilePersist4;
+        if (strcmp(e, "dma") == 0) return (int)kTileDma;
         return (int)kTileAuto;
     }();
     return v;
@@ -614,7 +650,7 @@ template <class Kind, bool FP8>
 static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int64_t big_blocks = ((a.M + 255) / 256) * (packed_rows / 256);
     int ov = tile_override();
-    if (ov == kTileAuto) ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? kTileBig : kTileSmall;
+    if (ov == kTileAuto) ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? kTileDma : kTileSmall;
     if (packed_rows % 256 != 0) ov = kTileSmall;
     switch (ov) {
         case kTileBig: return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
@@ -624,11 +660,18 @@ static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStre
         case kTileBig4Pipe: return launch_gate_up_shape<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
         case kTilePersist8: return launch_gate_up_persistent<Kind, FP8, ShapeBig>(a, packed_rows, stream);
         case kTilePersist4: return launch_gate_up_persistent<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
+        case kTileDma:
+            if constexpr (FP8)
+                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+            else
+                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
         default: return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
     }
 }
 
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if (a.M <= kSkinnyMaxTokens && tile_override() == kTileAuto && packed_rows % 64 == 0)
+        return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
     if (act == TRMOE_F32 && wdt == TRMOE_F32) return launch_gate_up_kind<KindF32, false>(a, packed_rows, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return launch_gate_up_kind<KindBF16, false>(a, packed_rows, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) return launch_gate_up_kind<KindBF16, true>(a, packed_rows, stream);
@@ -654,8 +697,8 @@ static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     int ov = tile_override();
     if (ov == kTileAuto) {
-        if (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
-        ov = (mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) ? kTileBig : kTileSmall;
+        if (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) ov = kTileDma;
+        else ov = (mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) ? kTileDma : kTileSmall;
     }
     switch (ov) {
         case kTileBig:
@@ -669,6 +712,14 @@ static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
         case kTileBig4Pipe:
             if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Pipe>(a, stream);
             return launch_down_shape<Kind, FP8, ShapeBig4Pipe>(a, stream);
+        case kTileDma:
+            if constexpr (FP8) {
+                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
+                return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
+            } else {
+                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
+                return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
+            }
         default: return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
     }
 }

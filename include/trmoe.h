@@ -209,13 +209,23 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
  * h: K2's output (act_dtype, [n, ldh], K = round_up(S, 128));
  * w_down: PLAIN-packed shared_down.weight [hidden, S] (row_align 256).
  * y/inverse may be NULL (no routed term).  route_weights: top_k host floats.
+ *
+ * workspace: device scratch of trmoe_shared_down_combine_workspace_bytes()
+ * bytes (may be NULL when that is 0).  Decode-sized calls (n_tokens <= 128)
+ * split K across workgroups and reduce fp32 partials there, in a fixed order
+ * (results do not depend on scheduling); with a smaller workspace they run
+ * the tile kernel instead.  Calls that share a workspace must be ordered on
+ * one stream.
  */
+size_t trmoe_shared_down_combine_workspace_bytes(int act_dtype, int64_t n_tokens, int64_t shared_width,
+                                                 int64_t hidden);
 int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
                               int64_t shared_width, int64_t ldh, const void* w_down,
                               const float* w_scale, int64_t hidden, const void* y, int64_t ldy,
                               const int64_t* inverse, int top_k, const float* route_weights,
                               float shared_scale, float routed_scale, const void* residual,
-                              int64_t ldr, void* out, int64_t ldo, void* stream);
+                              int64_t ldr, void* out, int64_t ldo, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /*
  * K4 without a shared branch (shared_width == 0, engine.py:335):

@@ -244,3 +244,111 @@ def test_shared_down_combine_big_tiles(gpu, dtype, N, S, H):
     yr = y.double()
     ref = h[rows].double() @ wd.double().T + 0.5 * (yr[perm[rows]] + yr[perm[N + rows]])
     assert nerr(out[rows], ref) <= TOL[dtype]
+
+
+# --------------------------------------------------------------------------- decode-shape kernels
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N", [1, 8, 31, 33, 64, 65, 127, 128])
+def test_shared_gate_up_decode_shapes(gpu, dtype, N):
+    """M <= 128 runs the split-K-across-waves kernel; K not a multiple of the
+    wave split and ragged M are covered."""
+    from complexity_amd import ops
+
+    H, S = 200, 320
+    x = _rand(N, H, seed=31).to(dtype)
+    wg, wu = _rand(S, H, scale=0.1, seed=32).to(dtype), _rand(S, H, scale=0.1, seed=33).to(dtype)
+    pg, _ = ops.pack_linear_gate_up(wg.to(gpu), wu.to(gpu))
+    h = ops.shared_gate_up(x.to(gpu), pg, None, S).cpu()
+    ref = F.silu(x.double() @ wg.double().T) * (x.double() @ wu.double().T)
+    assert nerr(h[:, :S], ref) <= TOL[dtype]
+    assert (h[:, S:] == 0).all()
+
+
+@pytest.mark.parametrize("N", [1, 64, 128])
+def test_shared_gate_up_decode_fp8(gpu, N):
+    from complexity_amd import ops
+
+    H, S = 2048, 384
+    x = _rand(N, H, seed=34).to(torch.bfloat16)
+    wg, wu = _rand(S, H, scale=0.02, seed=35), _rand(S, H, scale=0.02, seed=36)
+    qg, sg = O.quantize_e4m3(wg, 1)
+    qu, su = O.quantize_e4m3(wu, 1)
+    pg, ps = ops.pack_linear_gate_up(qg.to(gpu), qu.to(gpu), sg.to(gpu), su.to(gpu))
+    h = ops.shared_gate_up(x.to(gpu), pg, ps, S).cpu()
+    dg, du = O.dequantize_e4m3(qg, sg, 1).double(), O.dequantize_e4m3(qu, su, 1).double()
+    ref = F.silu(x.double() @ dg.T) * (x.double() @ du.T)
+    assert nerr(h[:, :S], ref) <= 1e-2
+
+
+def _down_case(N, S, H, k, dtype, seed):
+    h = _rand(N, S, seed=seed).to(dtype)
+    wd = _rand(H, S, scale=0.05, seed=seed + 1).to(dtype)
+    hpad = torch.zeros(N, (S + 127) // 128 * 128, dtype=dtype)
+    hpad[:, :S] = h
+    y = _rand(k * N, H, seed=seed + 2).to(dtype)
+    perm = torch.randperm(k * N, generator=torch.Generator().manual_seed(seed + 3))
+    res = _rand(N, H, seed=seed + 4).to(dtype)
+    return h, wd, hpad, y, perm, res
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N", [1, 8, 64, 100, 128])
+@pytest.mark.parametrize("with_y,with_res", [(True, True), (False, False)])
+def test_shared_down_combine_decode_shapes(gpu, dtype, N, with_y, with_res):
+    from complexity_amd import ops
+
+    S, H, k = 3328, 896, 2
+    h, wd, hpad, y, perm, res = _down_case(N, S, H, k, dtype, 40)
+    pd, _ = ops.pack_linear_down(wd.to(gpu))
+    rw = (0.7, 0.3)
+    out = ops.shared_down_combine(hpad.to(gpu), S, pd, None, H, y.to(gpu) if with_y else None,
+                                  perm.to(gpu) if with_y else None, k, rw, 0.5, 2.0,
+                                  res.to(gpu) if with_res else None).cpu()
+    ref = 0.5 * (h.double() @ wd.double().T)
+    if with_y:
+        yr = y.double()
+        ref = ref + 2.0 * (rw[0] * yr[perm[:N]] + rw[1] * yr[perm[N:]])
+    if with_res:
+        ref = ref + res.double()
+    assert nerr(out, ref) <= TOL[dtype]
+
+
+def test_shared_down_combine_decode_without_workspace_uses_tile_kernel(gpu):
+    """The split-K path and the tile kernel (no workspace) agree, and the
+    split-K result is identical from call to call (fixed reduction order)."""
+    import ctypes
+
+    from complexity_amd import _native, ops
+
+    N, S, H, k = 64, 3328, 896, 2
+    h, wd, hpad, y, perm, res = _down_case(N, S, H, k, torch.bfloat16, 50)
+    pd, _ = ops.pack_linear_down(wd.to(gpu))
+    hg, yg, pg_, rg = hpad.to(gpu), y.to(gpu), perm.to(gpu), res.to(gpu)
+    a = ops.shared_down_combine(hg, S, pd, None, H, yg, pg_, k, (0.5, 0.5), 1.0, 1.0, rg)
+    b = ops.shared_down_combine(hg, S, pd, None, H, yg, pg_, k, (0.5, 0.5), 1.0, 1.0, rg)
+    assert torch.equal(a, b)
+    lib = _native.load()
+    out = torch.empty(N, H, dtype=torch.bfloat16, device=gpu)
+    rw = (ctypes.c_float * 4)(0.5, 0.5, 0.0, 0.0)
+    st = lib.trmoe_shared_down_combine(_native.BF16, _native.BF16, hg.data_ptr(), N, S, hg.stride(0), pd.data_ptr(),
+                                       None, H, yg.data_ptr(), H, pg_.data_ptr(), k,
+                                       ctypes.cast(rw, ctypes.c_void_p), 1.0, 1.0, rg.data_ptr(), H,
+                                       out.data_ptr(), H, None, 0,
+                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _native.check(st, "trmoe_shared_down_combine")
+    assert nerr(a.cpu(), out.cpu()) <= 1e-2
+
+
+def test_shared_down_combine_decode_fp8(gpu):
+    from complexity_amd import ops
+
+    N, S, H = 64, 1024, 2048
+    h = _rand(N, S, seed=60).to(torch.bfloat16)
+    wd = _rand(H, S, scale=0.02, seed=61)
+    q, s = O.quantize_e4m3(wd, 1)
+    pd, ps = ops.pack_linear_down(q.to(gpu), s.to(gpu))
+    out = ops.shared_down_combine(h.to(gpu), S, pd, ps, H, None, None, 2, (0.5, 0.5), 1.0, 1.0).cpu()
+    ref = h.double() @ O.dequantize_e4m3(q, s, 1).double().T
+    assert nerr(out, ref) <= 1e-2

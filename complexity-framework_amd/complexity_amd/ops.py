@@ -281,6 +281,21 @@ def _weights_arg(route_weights: Sequence[float]):
     return arr
 
 
+# Scratch of the decode-sized down GEMM (split-K partials): one cached buffer
+# per (device, stream), so that calls on one stream (which are ordered) share
+# it and no call allocates after the first.
+_DOWN_WS: dict = {}
+
+
+def _down_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _DOWN_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _DOWN_WS[key] = ws
+    return ws
+
+
 def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor, w_scale, hidden: int,
                         y: Optional[torch.Tensor], inverse: Optional[torch.Tensor], top_k: int,
                         route_weights: Sequence[float], shared_scale: float, routed_scale: float,
@@ -291,7 +306,7 @@ def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor
     out = torch.empty(n, hidden, dtype=h.dtype, device=h.device)
     rw = _weights_arg(route_weights)
     ws_bytes = lib.trmoe_shared_down_combine_workspace_bytes(dtype_code(h.dtype), n, shared_width, hidden)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=h.device) if ws_bytes else None
+    ws = _down_workspace(h.device, ws_bytes) if ws_bytes else None
     st = lib.trmoe_shared_down_combine(
         dtype_code(h.dtype), dtype_code(w_down.dtype), _p(h), n, shared_width, h.stride(0), _p(w_down),
         _p(w_scale), hidden, _p(y), hidden, _p(inverse), top_k, ctypes.cast(rw, ctypes.c_void_p),

@@ -200,7 +200,7 @@ __device__ __forceinline__ void init_dense_rows(Prov& p, const void* base, int64
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int PGR_ = 1>
 struct TileShape {
     // 1, 2: register prefetch depth; 3: full register pipeline (tile_loop_pipe);
-    // 4: direct buffer->LDS loads (tile_loop_dma, bf16/f32 operands only)
+    // 4: direct buffer->LDS loads (tile_loop_dma, bf16/f32 operands only);
     static constexpr int PGR = PGR_;
     static constexpr int BM = BM_;
     static constexpr int BN = BN_;
@@ -211,8 +211,11 @@ struct TileShape {
     static constexpr int WN = BN / WAVES_N;
     static constexpr int TM = WM / 32;
     static constexpr int TN = WN / 32;
-    static constexpr int kStageBytes = (BM + BN) * kRowBytes;
-    static constexpr int kLdsBytes = 2 * kStageBytes;
+    // 5: direct loads into four stages of 64-byte rows (tile_loop_dma4, bf16)
+    static constexpr int kStageRowBytes = PGR == 5 ? 64 : kRowBytes;
+    static constexpr int kStages = PGR == 5 ? 4 : 2;
+    static constexpr int kStageBytes = (BM + BN) * kStageRowBytes;
+    static constexpr int kLdsBytes = kStages * kStageBytes;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "tile rows must split evenly over threads");
 };
@@ -520,21 +523,15 @@ struct DmaRows {
     }
 };
 
-// Two LDS stages filled by DmaRows: stage kt+2 is requested as soon as every
-// wave has read stage kt, so each load has one stage of MFMA work to land.
-// Ends with a full barrier (callers reuse LDS in their epilogues).
+// The K loop over two LDS stages filled by DmaRows, stages 0 and 1 already
+// requested (and, of all vector memory operations issued so far, stage 1's
+// are the most recent): stage kt+2 is requested as soon as every wave has
+// read stage kt, so each load has one stage of MFMA work to land.
 template <class Kind, class Shape, class AP, class BP>
-__device__ __forceinline__ void tile_loop_dma(const AP& ap, const BP& bp, int K, char* lds, int wm0, int wn0,
-                                              f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
+__device__ __forceinline__ void dma_mainloop(const AP& ap, const BP& bp, int nk, char* lds, int wm0, int wn0,
+                                             f32x16 (&acc)[Shape::TM][Shape::TN]) {
     constexpr int kABytes = Shape::BM * kRowBytes;
     constexpr int kPer = AP::kInstr + BP::kInstr;
-    ap.issue(0, lds);
-    bp.issue(0, lds + kABytes);
-    if (nk > 1) {
-        ap.issue(1, lds + Shape::kStageBytes);
-        bp.issue(1, lds + Shape::kStageBytes + kABytes);
-    }
     for (int kt = 0; kt < nk; ++kt) {
         char* st = lds + (kt & 1) * Shape::kStageBytes;
         if (kt + 1 < nk)
@@ -550,13 +547,143 @@ __device__ __forceinline__ void tile_loop_dma(const AP& ap, const BP& bp, int K,
             bp.issue(kt + 2, st + kABytes);
         }
     }
+}
+
+// ---- four stages of 64-byte rows ------------------------------------------
+// A K stage of 32 bf16 per row halves the bytes per stage, so four stages fit
+// where two 128-byte stages did and three stages (96 KB for a 256x256 tile)
+// are in flight while one is multiplied: the loop is bound by memory latency
+// (bytes in flight / latency), not by L2 or LDS bandwidth.  Rows hold four
+// 16-byte chunks swizzled by (r >> 1) & 3, which keeps every 8-lane phase of
+// a ds_read_b128 on distinct bank groups.
+constexpr int kRow64 = 64;
+__device__ __forceinline__ int lds_swz64(int r) { return (r >> 1) & 3; }
+__device__ __forceinline__ int lds_byte64(int r, int c) { return r * kRow64 + ((c ^ lds_swz64(r)) << 4); }
+
+template <class Kind, int TM, int TN>
+__device__ __forceinline__ void mma_stage64(const char* As, const char* Bs, int wm0, int wn0,
+                                            f32x16 (&acc)[TM][TN]) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        u32x4 a[TM], b[TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+            a[tm] = *reinterpret_cast<const u32x4*>(As + lds_byte64(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+            b[tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte64(wn0 + tn * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) mfma_group(Kind{}, a[tm], b[tn], acc[tm][tn]);
+    }
+}
+
+template <int ROWS, int NT>
+struct DmaRows64 {
+    static constexpr int kInstr = ROWS * 4 / NT;   // each wave instruction fills 16 rows
+    static constexpr int kWaves = NT / 64;
+    static_assert(ROWS % (16 * kWaves) == 0, "each wave fills whole 16-row groups");
+    __amdgpu_buffer_rsrc_t rsrc;
+    int off[kInstr];
+    int koff[kInstr];
+    int kbytes;
+    int wave;
+
+    __device__ __forceinline__ void init(const void* base, int64_t row0, int64_t rows_total, int64_t ld_bytes,
+                                         int kbytes_) {
+        const int64_t avail = rows_total - row0;
+        const int64_t nrows = avail < ROWS ? avail : ROWS;
+        rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
+        kbytes = kbytes_;
+        wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int r = (wave * kInstr + j) * 16 + (lane >> 2);
+            koff[j] = ((lane & 3) ^ lds_swz64(r)) * 16;
+            off[j] = r < nrows ? (int)(r * ld_bytes) + koff[j] : kOutOfRange;
+        }
+    }
+    __device__ __forceinline__ void issue(int kt, char* stage) const {
+        const int kb = kt * kRow64;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int o = (kb + koff[j] < kbytes) ? off[j] + kb : kOutOfRange;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(stage + (wave * kInstr + j) * 16 * kRow64),
+                                                    16, o, 0, 0, 0);
+        }
+    }
+};
+
+// K loop over four 64-byte-row stages with stages 0..2 already requested
+// (stage 2's the most recent vector memory operations).  One barrier per
+// stage: it both publishes stage kt and retires stage kt-1, whose buffer
+// then receives stage kt+3 before stage kt is multiplied.
+template <class Kind, class Shape, class AP, class BP>
+__device__ __forceinline__ void dma4_mainloop(const AP& ap, const BP& bp, int nk, char* lds, int wm0, int wn0,
+                                              f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    constexpr int kABytes = Shape::BM * kRow64;
+    constexpr int kPer = AP::kInstr + BP::kInstr;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int younger = nk - 1 - kt;   // stages requested after stage kt (at most 2 here)
+        if (younger >= 2)
+            wait_vmcnt<2 * kPer>();
+        else if (younger == 1)
+            wait_vmcnt<kPer>();
+        else
+            wait_vmcnt<0>();
+        lds_barrier();
+        if (kt + 3 < nk) {
+            char* nx = lds + ((kt + 3) & 3) * Shape::kStageBytes;
+            ap.issue(kt + 3, nx);
+            bp.issue(kt + 3, nx + kABytes);
+        }
+        const char* st = lds + (kt & 3) * Shape::kStageBytes;
+        mma_stage64<Kind, Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
+    }
+}
+
+template <class Kind, class Shape, class AP, class BP>
+__device__ __forceinline__ void tile_loop_dma4(const AP& ap, const BP& bp, int K, char* lds, int wm0, int wn0,
+                                               f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    const int nk = (K * (int)sizeof(typename Kind::T) + kRow64 - 1) / kRow64;
+    constexpr int kABytes = Shape::BM * kRow64;
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+        if (s < nk) {
+            ap.issue(s, lds + s * Shape::kStageBytes);
+            bp.issue(s, lds + s * Shape::kStageBytes + kABytes);
+        }
+    dma4_mainloop<Kind, Shape>(ap, bp, nk, lds, wm0, wn0, acc);
+    __syncthreads();
+}
+
+// Whole tile: request stages 0 and 1, run the K loop, end with a full
+// barrier (callers reuse LDS in their epilogues).
+template <class Kind, class Shape, class AP, class BP>
+__device__ __forceinline__ void tile_loop_dma(const AP& ap, const BP& bp, int K, char* lds, int wm0, int wn0,
+                                              f32x16 (&acc)[Shape::TM][Shape::TN]) {
+    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
+    constexpr int kABytes = Shape::BM * kRowBytes;
+    ap.issue(0, lds);
+    bp.issue(0, lds + kABytes);
+    if (nk > 1) {
+        ap.issue(1, lds + Shape::kStageBytes);
+        bp.issue(1, lds + Shape::kStageBytes + kABytes);
+    }
+    dma_mainloop<Kind, Shape>(ap, bp, nk, lds, wm0, wn0, acc);
     __syncthreads();
 }
 
 template <class Kind, class Shape, class AProv, class BProv>
 __device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int K, char* lds, int wm0, int wn0,
                                           f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    if constexpr (Shape::PGR == 4)
+    if constexpr (Shape::PGR == 5)
+        tile_loop_dma4<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
+    else if constexpr (Shape::PGR == 4)
         tile_loop_dma<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
     else if constexpr (Shape::PGR == 3)
         tile_loop_pipe<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);

@@ -95,20 +95,22 @@ __device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS, NT
 // Operand providers of a tile shape: direct buffer->LDS loads for PGR 4,
 // register-staged loads otherwise (and always for e4m3 weights, which are
 // expanded to bf16 on the way into LDS).
+template <class Shape, int ROWS>
+using DmaProv = std::conditional_t<Shape::PGR == 5, DmaRows64<ROWS, Shape::NT>, DmaRows<ROWS, Shape::NT>>;
 template <class Shape>
 struct AProvOf {
-    using type = std::conditional_t<Shape::PGR == 4, DmaRows<Shape::BM, Shape::NT>, BufRows<Shape::BM, Shape::NT>>;
+    using type = std::conditional_t<(Shape::PGR >= 4), DmaProv<Shape, Shape::BM>, BufRows<Shape::BM, Shape::NT>>;
 };
 template <class Kind, bool FP8, class Shape>
 struct BProvOf {
-    static_assert(!(FP8 && Shape::PGR == 4), "e4m3 weights need the register path");
-    using type = std::conditional_t<Shape::PGR == 4, DmaRows<Shape::BN, Shape::NT>,
+    static_assert(!(FP8 && Shape::PGR >= 4), "e4m3 weights need the register path");
+    using type = std::conditional_t<(Shape::PGR >= 4), DmaProv<Shape, Shape::BN>,
                                     typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type>;
 };
 template <class Shape>
 __device__ __forceinline__ void init_a(typename AProvOf<Shape>::type& ap, const void* base, int64_t row0,
                                        int64_t rows_total, int64_t ld_bytes, int kbytes) {
-    if constexpr (Shape::PGR == 4)
+    if constexpr (Shape::PGR >= 4)
         ap.init(base, row0, rows_total, ld_bytes, kbytes);
     else
         init_dense_rows(ap, base, row0, rows_total, ld_bytes, kbytes);
@@ -116,7 +118,7 @@ __device__ __forceinline__ void init_a(typename AProvOf<Shape>::type& ap, const 
 template <class Kind, bool FP8, class Shape>
 __device__ __forceinline__ void init_b(typename BProvOf<Kind, FP8, Shape>::type& bp, const void* base, int64_t ld,
                                        int64_t row0, int K) {
-    if constexpr (Shape::PGR == 4) {
+    if constexpr (Shape::PGR >= 4) {
         const int64_t elem = (int64_t)sizeof(typename Kind::T);
         bp.init(base, row0, row0 + Shape::BN, ld * elem, (int)(K * elem));
     } else {
@@ -135,6 +137,8 @@ using ShapeBig4Pipe = TileShape<256, 256, 2, 2, 3>;
 using ShapeDown224Pipe = TileShape<256, 224, 4, 1, 3>;
 using ShapeBigDma = TileShape<256, 256, 2, 4, 4>;    // 8 waves, direct buffer->LDS operand loads
 using ShapeDown224Dma = TileShape<256, 224, 4, 1, 4>;
+using ShapeBig4Dma = TileShape<256, 256, 2, 2, 4>;   // 4 waves of 128x128: 2/3 of the LDS reads per MFMA
+using ShapeBigDma64 = TileShape<256, 256, 2, 4, 5>;  // four 64-byte-row stages, three in flight
 
 // ---------------------------------------------------------------------------
 // K2: shared gate|up + SwiGLU
@@ -154,14 +158,14 @@ __device__ __forceinline__ void gate_up_routes(const GateUpArgs& a, int64_t m0, 
     }
 }
 
-// SwiGLU epilogue: h values are written to LDS (free after the main loop's
-// last barrier) as a [BM][BN/2] tile with rows padded by 16 bytes, then
-// copied out with coalesced 16-byte stores.  Ends with LDS still in use by
-// the copy; callers that reuse LDS must barrier first.
+// SwiGLU epilogue, in two halves: gate_up_epi_tile writes the h values to
+// LDS (free after the main loop's last barrier) as a [BM][BN/2] tile with
+// rows padded by 16 bytes; after a barrier gate_up_epi_store copies the tile
+// out with coalesced 16-byte stores.  gate_up_epilogue runs both; it ends
+// with LDS still in use by the copy (callers that reuse LDS barrier first).
 template <class Kind, class Shape>
-__device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
-                                                 int64_t m0, int64_t n0, char* lds,
-                                                 const int (*s_route)[kMaxTopK]) {
+__device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
+                                                 int64_t n0, char* lds, const int (*s_route)[kMaxTopK]) {
     using T = typename Kind::T;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
@@ -200,7 +204,12 @@ __device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&a
             }
         }
     }
-    __syncthreads();
+}
+
+template <class Kind, class Shape>
+__device__ __forceinline__ void gate_up_epi_store(const GateUpArgs& a, int64_t m0, int64_t n0, const char* lds) {
+    using T = typename Kind::T;
+    constexpr int kHRowBytes = Shape::BN / 2 * (int)sizeof(T) + 16;
     constexpr int kChunksPerRow = Shape::BN / 2 * (int)sizeof(T) / 16;
     constexpr int kChunks = Shape::BM * kChunksPerRow;
     char* hbase = static_cast<char*>(a.h) + (n0 >> 1) * (int64_t)sizeof(T);
@@ -212,6 +221,16 @@ __device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&a
             *reinterpret_cast<u32x4*>(hbase + row * a.ldh * (int64_t)sizeof(T) + c * 16) =
                 *reinterpret_cast<const u32x4*>(lds + rl * kHRowBytes + c * 16);
     }
+}
+
+template <class Kind, class Shape>
+__device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
+                                                 int64_t m0, int64_t n0, char* lds,
+                                                 const int (*s_route)[kMaxTopK]) {
+    gate_up_epi_tile<Kind, Shape>(a, acc, n0, lds, s_route);
+    wait_lgkmcnt0();   // LDS tile complete; outstanding global loads (a next tile's operands) keep flying
+    lds_barrier();
+    gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
 template <class Kind, bool FP8, class Shape>
@@ -282,6 +301,71 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_persistent(GateUpArgs a, 
         __syncthreads();  // LDS and s_route are reused by the next tile
         if (next >= total) break;
         tile = next;
+    }
+}
+
+// Persistent form over direct buffer->LDS loads (bf16): gridDim.x workgroups
+// walk the tiles (M fastest).  After a tile's last K stage the first K stage
+// of the workgroup's next tile is requested into LDS stage 0 and its second
+// into stage 1 once the epilogue has drained its LDS tile (which overlaps
+// stage 1), so both loads travel while the SwiGLU epilogue runs.
+template <class Kind, class Shape>
+__global__ __launch_bounds__(Shape::NT) void k_gate_up_persist_dma(GateUpArgs a, int tiles_m, int total) {
+    using T = typename Kind::T;
+    static_assert(Shape::PGR == 4, "direct-load shape expected");
+    extern __shared__ __align__(16) char lds[];
+    __shared__ int s_route[Shape::BM][kMaxTopK];
+    constexpr int kABytes = Shape::BM * kRowBytes;
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    int t = blockIdx.x;
+    if (t >= total) return;
+    const int nk = (a.K + Kind::kStageElems - 1) / Kind::kStageElems;
+    const int64_t ldx_b = a.ldx * (int64_t)sizeof(T), ldw_b = a.ldw * (int64_t)sizeof(T);
+    const int kb = a.K * (int)sizeof(T);
+
+    DmaRows<Shape::BM, Shape::NT> ap;
+    DmaRows<Shape::BN, Shape::NT> bp;
+    int64_t m0 = (int64_t)(t % tiles_m) * Shape::BM;
+    int64_t n0 = (int64_t)(t / tiles_m) * Shape::BN;
+    ap.init(a.x, m0, a.M, ldx_b, kb);
+    bp.init(a.w, n0, n0 + Shape::BN, ldw_b, kb);
+    ap.issue(0, lds);
+    bp.issue(0, lds + kABytes);
+    if (nk > 1) {
+        ap.issue(1, lds + Shape::kStageBytes);
+        bp.issue(1, lds + Shape::kStageBytes + kABytes);
+    }
+    while (true) {
+        gate_up_routes<Shape>(a, m0, n0, s_route);
+        f32x16 acc[Shape::TM][Shape::TN];
+        zero_acc<Kind>(acc);
+        dma_mainloop<Kind, Shape>(ap, bp, nk, lds, wm0, wn0, acc);
+        wait_lgkmcnt0();
+        lds_barrier();   // every wave is done with both stages
+        gate_up_epi_tile<Kind, Shape>(a, acc, n0, lds + Shape::kStageBytes, s_route);
+        const int next = t + (int)gridDim.x;
+        const int64_t cm0 = m0, cn0 = n0;
+        if (next < total) {
+            m0 = (int64_t)(next % tiles_m) * Shape::BM;
+            n0 = (int64_t)(next / tiles_m) * Shape::BN;
+            ap.init(a.x, m0, a.M, ldx_b, kb);
+            bp.init(a.w, n0, n0 + Shape::BN, ldw_b, kb);
+            ap.issue(0, lds);
+            bp.issue(0, lds + kABytes);
+        }
+        wait_lgkmcnt0();
+        lds_barrier();   // the LDS tile is complete
+        gate_up_epi_store<Kind, Shape>(a, cm0, cn0, lds + Shape::kStageBytes);
+        wait_lgkmcnt0();
+        lds_barrier();   // ... and has been read out
+        if (next >= total) break;
+        if (nk > 1) {
+            ap.issue(1, lds + Shape::kStageBytes);
+            bp.issue(1, lds + Shape::kStageBytes + kABytes);
+        }
+        t = next;
     }
 }
 
@@ -587,7 +671,7 @@ constexpr int64_t kBigTileMinBlocks = 512;
 // big (256x256, 8 waves), big8p2, big4p2 (two-stage prefetch); unset = auto.
 enum TileChoice {
     kTileAuto = 0, kTileSmall, kTileBig, kTileBig8P2, kTileBig4P2, kTileBig8Pipe, kTileBig4Pipe,
-    kTilePersist8, kTilePersist4, kTileDma
+    kTilePersist8, kTilePersist4, kTileDma, kTilePersistDma, kTileDma4, kTileDma64
 };
 static int tile_override() {
     static int v = [] {
@@ -602,6 +686,9 @@ static int tile_override() {
         if (strcmp(e, "persist8") == 0) return (int)kTilePersist8;
         if (strcmp(e, "persist4") == 0) return (int)kTilePersist4;
         if (strcmp(e, "dma") == 0) return (int)kTileDma;
+        if (strcmp(e, "pdma") == 0) return (int)kTilePersistDma;
+        if (strcmp(e, "dma4") == 0) return (int)kTileDma4;
+        if (strcmp(e, "dma64") == 0) return (int)kTileDma64;
         return (int)kTileAuto;
     }();
     return v;
@@ -630,6 +717,22 @@ static int launch_gate_up_persistent(const GateUpArgs& a, int64_t packed_rows, h
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, Shape::NT, kLds) != hipSuccess || per_cu < 1)
         per_cu = 1;
     int grid = device_cus() * per_cu;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Shape::NT), kLds, stream, a, tiles_m, total);
+    return check_launch("shared_gate_up");
+}
+
+template <class Kind, class Shape>
+static int launch_gate_up_persist_dma(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int tiles_m = (int)((a.M + Shape::BM - 1) / Shape::BM);
+    const int total = tiles_m * (int)(packed_rows / Shape::BN);
+    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
+    constexpr int kLds = Shape::kStageBytes + kEpi > Shape::kLdsBytes ? Shape::kStageBytes + kEpi : Shape::kLdsBytes;
+    static_assert(kLds <= 160 * 1024 - 4096, "stages + epilogue tile must fit in LDS");
+    auto kern = k_gate_up_persist_dma<Kind, Shape>;
+    int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    int grid = device_cus();
     if (grid > total) grid = total;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Shape::NT), kLds, stream, a, tiles_m, total);
     return check_launch("shared_gate_up");
@@ -665,6 +768,25 @@ static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStre
                 return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
             else
                 return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
+        case kTileDma64:
+            if constexpr (FP8)
+                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+            else if constexpr (sizeof(typename Kind::T) == 4)
+                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
+            else
+                return launch_gate_up_shape<Kind, FP8, ShapeBigDma64>(a, packed_rows, stream);
+        case kTileDma4:
+            if constexpr (FP8)
+                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+            else
+                return launch_gate_up_shape<Kind, FP8, ShapeBig4Dma>(a, packed_rows, stream);
+        case kTilePersistDma:
+            if constexpr (FP8)
+                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
+            else if constexpr (sizeof(typename Kind::T) == 4)
+                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
+            else
+                return launch_gate_up_persist_dma<Kind, ShapeBigDma>(a, packed_rows, stream);
         default: return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
     }
 }
@@ -712,7 +834,26 @@ static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
         case kTileBig4Pipe:
             if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Pipe>(a, stream);
             return launch_down_shape<Kind, FP8, ShapeBig4Pipe>(a, stream);
+        case kTileDma64:
+            if constexpr (FP8) {
+                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
+                return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
+            } else if constexpr (sizeof(typename Kind::T) == 4) {
+                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
+                return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
+            } else {
+                // 224 rows do not split into whole 16-row groups per wave
+                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
+                return launch_down_shape<Kind, FP8, ShapeBigDma64>(a, stream);
+            }
+        case kTileDma4:
+            if constexpr (FP8) {
+                return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
+            } else {
+                return launch_down_shape<Kind, FP8, ShapeBig4Dma>(a, stream);
+            }
         case kTileDma:
+        case kTilePersistDma:
             if constexpr (FP8) {
                 if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
                 return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);

@@ -5,17 +5,17 @@
 // so the kernels are organised to keep as many weight loads in flight as the
 // CUs allow and to touch each weight byte once:
 //
-//   k_gate_up_skinny   one workgroup per 64 packed gate|up rows (32 output
-//                      features) and all M tokens; the waves split K, each
-//                      loading its operands straight into MFMA registers
-//                      (no LDS staging), and reduce through LDS before the
-//                      SwiGLU epilogue (same epilogue contract as
+//   k_gate_up_skinny   one workgroup per 16 output features (16 gate + 16 up
+//                      packed rows) and all M tokens; the waves split K, each
+//                      loading its operands straight into 16x16 MFMA
+//                      registers (no LDS staging), and reduce through LDS
+//                      before the SwiGLU epilogue (same epilogue contract as
 //                      k_gate_up_swiglu, including the dense-routed scaling)
-//   k_down_skinny      split-K: workgroup (64 output columns, K chunk)
+//   k_down_skinny      split-K: workgroup (32 output columns, K chunk)
 //                      writes an fp32 partial [split][M][N] to the caller's
 //                      workspace
 //   k_down_reduce      sums the partials in split order (deterministic),
-//                      applies the row scales, the routed un-permute, the
+//                      applies the row scales, the routed un-permute and the
 //                      residual, and stores the output
 #include "trmoe_common.h"
 #include "trmoe_internal.h"
@@ -27,15 +27,29 @@ namespace trmoe {
 
 namespace {
 
-constexpr int kGroupsPerBatch = 8;   // K groups (32 bytes of an A row) per load batch
+// 16x16 MFMA tiles: a K group is 64 bytes of an activation row; lane l
+// supplies row l & 15 and the 16-byte chunk l >> 4 of the group (one
+// instruction touches 16 rows x 64 contiguous bytes of each operand).
+// Output element i of lane l is row 4 * (l >> 4) + i, column l & 15.
+__device__ __forceinline__ void mfma16(KindBF16, u32x4 a, u32x4 b, f32x4& acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                  0, 0, 0);
+}
+__device__ __forceinline__ void mfma16(KindF32, u32x4 a, u32x4 b, f32x4& acc) {
+    const f32x4 fa = __builtin_bit_cast(f32x4, a);
+    const f32x4 fb = __builtin_bit_cast(f32x4, b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[i], acc, 0, 0, 0);
+}
 
-// Weight operand fragment of one K group for the lane's row: 16 bytes of
-// bf16/f32, or 8 bytes of e4m3 expanded to bf16.
+// Weight fragment of one K group for the lane's row: 16 bytes of bf16/f32,
+// or 8 bytes of e4m3 (half as many bytes as the activation group) expanded
+// to bf16.
 template <class Kind, bool FP8>
 struct WFrag {
     using Reg = u32x4;
-    static __device__ __forceinline__ Reg load(__amdgpu_buffer_rsrc_t r, int row_off, int g, int hf, int kb_a) {
-        const int o = 32 * g + 16 * hf;
+    static __device__ __forceinline__ Reg load(__amdgpu_buffer_rsrc_t r, int row_off, int g, int q, int kb_a) {
+        const int o = 64 * g + 16 * q;
         return buffer_load16(r, o < kb_a ? row_off + o : kOutOfRange);
     }
     static __device__ __forceinline__ u32x4 expand(Reg v) { return v; }
@@ -43,91 +57,100 @@ struct WFrag {
 template <class Kind>
 struct WFrag<Kind, true> {
     using Reg = u32x2;
-    static __device__ __forceinline__ Reg load(__amdgpu_buffer_rsrc_t r, int row_off, int g, int hf, int kb_a) {
-        const int o = 16 * g + 8 * hf;   // one e4m3 byte per bf16 element of A
-        return buffer_load8(r, 32 * g + 16 * hf < kb_a ? row_off + o : kOutOfRange);
+    static __device__ __forceinline__ Reg load(__amdgpu_buffer_rsrc_t r, int row_off, int g, int q, int kb_a) {
+        return buffer_load8(r, 64 * g + 16 * q < kb_a ? row_off + 32 * g + 8 * q : kOutOfRange);
     }
     static __device__ __forceinline__ u32x4 expand(Reg v) { return fp8x8_to_bf16x8(v); }
 };
 
-// acc[tm][u] += A(rows tm*32..+31) . W(rows u*32..+31)^T over the K groups
-// [g0, g1) of this wave.  a_off[tm] / w_off[u] are the byte offsets of the
-// lane's row in each operand (kOutOfRange for absent rows); kb_a is the byte
-// length of K in an A row.
-template <class Kind, bool FP8, int MT>
+// acc[tm][u] += A(rows tm*16..+15) . W(rows u*16..+15)^T over the K groups
+// [g0, g1) of this wave, loading GB groups at a time.  a_off[tm] / w_off[u]
+// are the byte offsets of the lane's row in each operand (kOutOfRange for
+// absent rows); kb_a is the byte length of K in an activation row.
+template <class Kind, bool FP8, int MT, int GB>
 __device__ __forceinline__ void skinny_k_loop(__amdgpu_buffer_rsrc_t ar, const int (&a_off)[MT],
                                               __amdgpu_buffer_rsrc_t wr, const int (&w_off)[2], int g0, int g1,
-                                              int kb_a, f32x16 (&acc)[MT][2]) {
+                                              int kb_a, f32x4 (&acc)[MT][2]) {
     using WF = WFrag<Kind, FP8>;
-    const int hf = (threadIdx.x & 63) >> 5;
-    for (int gb = g0; gb < g1; gb += kGroupsPerBatch) {
-        u32x4 av[kGroupsPerBatch][MT];
-        typename WF::Reg wv[kGroupsPerBatch][2];
+    const int q = (threadIdx.x & 63) >> 4;
+    for (int gb = g0; gb < g1; gb += GB) {
+        u32x4 av[GB][MT];
+        typename WF::Reg wv[GB][2];
 #pragma unroll
-        for (int j = 0; j < kGroupsPerBatch; ++j) {
+        for (int j = 0; j < GB; ++j) {
             const int g = gb + j;
             const bool ok = g < g1;
-            const int ao = 32 * g + 16 * hf;
+            const int ao = 64 * g + 16 * q;
 #pragma unroll
             for (int tm = 0; tm < MT; ++tm)
                 av[j][tm] = buffer_load16(ar, (ok && ao < kb_a) ? a_off[tm] + ao : kOutOfRange);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) wv[j][u] = WF::load(wr, ok ? w_off[u] : kOutOfRange, g, hf, kb_a);
+            for (int u = 0; u < 2; ++u) wv[j][u] = WF::load(wr, ok ? w_off[u] : kOutOfRange, g, q, kb_a);
         }
+        // every load of the batch is in flight before the first MFMA waits
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < kGroupsPerBatch; ++j)
+        for (int j = 0; j < GB; ++j)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const u32x4 b = WF::expand(wv[j][u]);
 #pragma unroll
-                for (int tm = 0; tm < MT; ++tm) mfma_group(Kind{}, av[j][tm], b, acc[tm][u]);
+                for (int tm = 0; tm < MT; ++tm) mfma16(Kind{}, av[j][tm], b, acc[tm][u]);
             }
     }
 }
 
-// Writes the wave's accumulators to red[wave][e][lane] (e = (tm*2+u)*16+i).
+// red[wave][e][lane] with e = (tm*2+u)*4+i.
 template <int MT>
-__device__ __forceinline__ void skinny_stash(float* red, const f32x16 (&acc)[MT][2]) {
+__device__ __forceinline__ void skinny_stash(float* red, const f32x4 (&acc)[MT][2]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm)
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                red[((wave * MT * 2 + tm * 2 + u) * 16 + i) * 64 + lane] = acc[tm][u][i];
+            for (int i = 0; i < 4; ++i) red[((wave * MT * 2 + tm * 2 + u) * 4 + i) * 64 + lane] = acc[tm][u][i];
 }
 
 template <int MT, int NW>
 __device__ __forceinline__ float skinny_sum(const float* red, int tm, int u, int i, int lane) {
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) s += red[((w * MT * 2 + tm * 2 + u) * 16 + i) * 64 + lane];
+    for (int w = 0; w < NW; ++w) s += red[((w * MT * 2 + tm * 2 + u) * 4 + i) * 64 + lane];
     return s;
+}
+
+template <int MT>
+__device__ __forceinline__ void zero_acc16(f32x4 (&acc)[MT][2]) {
+#pragma unroll
+    for (int tm = 0; tm < MT; ++tm)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[tm][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 }  // namespace
 
-template <class Kind, bool FP8, int MT, int NW>
+// One workgroup per 16 output features (32 packed rows: 16 gate rows and the
+// matching 16 up rows of a 64-row packed group) and all M tokens.
+template <class Kind, bool FP8, int MT, int NW, int GB>
 __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
     constexpr int kWB = FP8 ? 1 : (int)sizeof(T);
     extern __shared__ __align__(16) float red[];
-    __shared__ int s_route[MT * 32][kMaxTopK];
+    __shared__ int s_route[MT * 16][kMaxTopK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = lane & 31;
-    const int64_t p0 = (int64_t)blockIdx.x * 64;   // first packed row: 32 gate rows, then 32 up rows
-    const int64_t f0 = p0 >> 1;                    // first output feature
-
+    const int r = lane & 15;
+    const int64_t f0 = (int64_t)blockIdx.x * 16;                   // first output feature
+    const int64_t pg = (f0 >> 5) * 64 + (f0 & 31);                 // its gate row in the packed weight
     // descriptors first: built ahead of the divergent route gather they stay
     // in scalar registers
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.x, (uint32_t)(a.M * a.ldx * (int64_t)sizeof(T)));
-    const auto wr = make_rsrc(static_cast<const char*>(a.w) + p0 * a.ldw * kWB, (uint32_t)(64 * a.ldw * kWB));
+    const auto wr = make_rsrc(static_cast<const char*>(a.w) + pg * a.ldw * kWB, (uint32_t)(48 * a.ldw * kWB));
 
     const bool routed = a.ids != nullptr && f0 >= a.shared_feats;
-    if (routed && threadIdx.x < MT * 32) {
+    if (routed && threadIdx.x < MT * 16) {
         const int64_t row = threadIdx.x;
         int64_t id = row < a.M ? a.ids[row] : 0;
         id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
@@ -137,37 +160,32 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     int a_off[MT], w_off[2];
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm) {
-        const int row = tm * 32 + r;
+        const int row = tm * 16 + r;
         a_off[tm] = row < a.M ? (int)(row * a.ldx * (int64_t)sizeof(T)) : kOutOfRange;
     }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) w_off[u] = (int)((u * 32 + r) * a.ldw * kWB);
+    w_off[0] = (int)(r * a.ldw * kWB);          // gate row pg + r
+    w_off[1] = (int)((32 + r) * a.ldw * kWB);   // up row pg + 32 + r
 
-    const int groups = (kb_a + 31) / 32;
+    const int groups = (kb_a + 63) / 64;
     const int per_wave = (groups + NW - 1) / NW;
     const int g0 = wave * per_wave;
     const int g1 = g0 + per_wave < groups ? g0 + per_wave : groups;
-    f32x16 acc[MT][2];
-#pragma unroll
-    for (int tm = 0; tm < MT; ++tm)
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[tm][u][i] = 0.f;
-    skinny_k_loop<Kind, FP8, MT>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
+    f32x4 acc[MT][2];
+    zero_acc16<MT>(acc);
+    skinny_k_loop<Kind, FP8, MT, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
     skinny_stash<MT>(red, acc);
     __syncthreads();
 
     const int64_t expert = routed ? (f0 - a.shared_feats) / a.expert_feats : -1;
     const float mult = routed ? 1.0f : a.shared_mult;
     T* h = static_cast<T*>(a.h);
-    for (int q = threadIdx.x; q < MT * 16 * 64; q += NT) {
-        const int l = q & 63, tm = q >> 10, i = (q >> 6) & 15;
-        const int row = tm * 32 + acc_row(l, i);
+    for (int qi = threadIdx.x; qi < MT * 4 * 64; qi += NT) {
+        const int l = qi & 63, i = (qi >> 6) & 3, tm = qi >> 8;
+        const int row = tm * 16 + 4 * (l >> 4) + i;
         if (row >= a.M) continue;
-        const int fl = l & 31;
-        const float sg = a.w_scale ? a.w_scale[p0 + fl] : 1.0f;
-        const float su = a.w_scale ? a.w_scale[p0 + 32 + fl] : 1.0f;
+        const int fl = l & 15;
+        const float sg = a.w_scale ? a.w_scale[pg + fl] : 1.0f;
+        const float su = a.w_scale ? a.w_scale[pg + 32 + fl] : 1.0f;
         const float g = skinny_sum<MT, NW>(red, tm, 0, i, l) * sg;
         const float u = skinny_sum<MT, NW>(red, tm, 1, i, l) * su;
         float hv = silu_f(g) * u * mult;
@@ -181,58 +199,59 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     }
 }
 
-// Split-K partial of the down GEMM: block (x = 64-column tile, y = K split)
+// Split-K partial of the down GEMM: block (x = 32-column tile, y = K split)
 // writes part[(split * M + row) * N + col] for its rows and columns.
-template <class Kind, bool FP8, int MT, int NW>
+template <class Kind, bool FP8, int MT, int NW, int GB>
 __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int groups_per_split) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
     constexpr int kWB = FP8 ? 1 : (int)sizeof(T);
     extern __shared__ __align__(16) float red[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = lane & 31;
-    const int64_t n0 = (int64_t)blockIdx.x * 64;
+    const int r = lane & 15;
+    const int64_t n0 = (int64_t)blockIdx.x * 32;
     const int split = blockIdx.y;
 
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.h, (uint32_t)(a.M * a.ldh * (int64_t)sizeof(T)));
-    const auto wr = make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(64 * a.ldw * kWB));
+    const auto wr = make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(32 * a.ldw * kWB));
     int a_off[MT], w_off[2];
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm) {
-        const int row = tm * 32 + r;
+        const int row = tm * 16 + r;
         a_off[tm] = row < a.M ? (int)(row * a.ldh * (int64_t)sizeof(T)) : kOutOfRange;
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) w_off[u] = (int)((u * 32 + r) * a.ldw * kWB);
+    for (int u = 0; u < 2; ++u) w_off[u] = (int)((u * 16 + r) * a.ldw * kWB);
 
-    const int groups = (kb_a + 31) / 32;
+    const int groups = (kb_a + 63) / 64;
     const int s0 = split * groups_per_split;
     const int s1 = s0 + groups_per_split < groups ? s0 + groups_per_split : groups;
     const int per_wave = (groups_per_split + NW - 1) / NW;
     const int g0 = s0 + wave * per_wave;
     const int g1 = g0 + per_wave < s1 ? g0 + per_wave : s1;
-    f32x16 acc[MT][2];
-#pragma unroll
-    for (int tm = 0; tm < MT; ++tm)
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[tm][u][i] = 0.f;
-    skinny_k_loop<Kind, FP8, MT>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
+    f32x4 acc[MT][2];
+    zero_acc16<MT>(acc);
+    skinny_k_loop<Kind, FP8, MT, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
     skinny_stash<MT>(red, acc);
     __syncthreads();
 
     float* dst = part + (int64_t)split * a.M * a.N;
-    for (int q = threadIdx.x; q < MT * 2 * 16 * 64; q += NT) {
-        const int l = q & 63, i = (q >> 6) & 15, u = (q >> 10) & 1, tm = q >> 11;
-        const int row = tm * 32 + acc_row(l, i);
-        const int64_t col = n0 + u * 32 + (l & 31);
+    for (int qi = threadIdx.x; qi < MT * 2 * 4 * 64; qi += NT) {
+        const int l = qi & 63, i = (qi >> 6) & 3, u = (qi >> 8) & 1, tm = qi >> 9;
+        const int row = tm * 16 + 4 * (l >> 4) + i;
+        const int64_t col = n0 + u * 16 + (l & 15);
         if (row >= a.M || col >= a.N) continue;
         dst[row * (int64_t)a.N + col] = skinny_sum<MT, NW>(red, tm, u, i, l);
     }
+
 }
 
+// Sums the partials in split order (deterministic), applies the row scales,
+// the routed un-permute and the residual, and stores the output.  A
+// separate launch: the kernel boundary publishes the partials of every XCD
+// (a device-scope release inside k_down_skinny would write back the whole
+// L2 of each XCD per workgroup, which costs far more than the launch).
 template <class T>
 __global__ __launch_bounds__(256) void k_down_reduce(DownArgs a, const float* part, int splits) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -271,30 +290,33 @@ int set_lds(F* fn, int bytes) {
     return err == hipSuccess ? TRMOE_OK : set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
 }
 
-constexpr int red_bytes(int mt, int nw) { return nw * mt * 2 * 16 * 64 * 4; }
+constexpr int red_bytes(int mt, int nw) { return nw * mt * 2 * 4 * 64 * 4; }
 
-template <class Kind, bool FP8, int MT, int NW>
+template <class Kind, bool FP8, int MT, int NW, int GB>
 int gate_up_skinny_mt(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    auto kern = k_gate_up_skinny<Kind, FP8, MT, NW>;
+    auto kern = k_gate_up_skinny<Kind, FP8, MT, NW, GB>;
     constexpr int kLds = red_bytes(MT, NW);
     int st = set_lds(kern, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(packed_rows / 64)), dim3(64 * NW), kLds, stream, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(packed_rows / 32)), dim3(64 * NW), kLds, stream, a);
     return check_launch("shared_gate_up (skinny)");
 }
 
 template <class Kind, bool FP8>
 int gate_up_skinny_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if (a.M <= 32) return gate_up_skinny_mt<Kind, FP8, 1, 8>(a, packed_rows, stream);
-    if (a.M <= 64) return gate_up_skinny_mt<Kind, FP8, 2, 8>(a, packed_rows, stream);
-    return gate_up_skinny_mt<Kind, FP8, 4, 4>(a, packed_rows, stream);
+    if (a.M <= 16) return gate_up_skinny_mt<Kind, FP8, 1, 8, 8>(a, packed_rows, stream);
+    if (a.M <= 32) return gate_up_skinny_mt<Kind, FP8, 2, 8, 8>(a, packed_rows, stream);
+    if (a.M <= 64) return gate_up_skinny_mt<Kind, FP8, 4, 8, 4>(a, packed_rows, stream);
+    return gate_up_skinny_mt<Kind, FP8, 8, 4, 2>(a, packed_rows, stream);
 }
 
-// K groups per split: enough that the fp32 partial (M x 64 x 4 bytes per
-// workgroup) stays at most a quarter of the weight bytes the workgroup
-// streams (64 rows x 32 bytes per group), and at least two groups per wave.
+// K groups (64 activation bytes) per split: enough that the fp32 partial
+// (M x 32 x 4 bytes per workgroup) stays at most a quarter of the weight
+// bytes the workgroup streams (32 rows x 64 bytes per group), and at least
+// two groups per wave (measured: fewer leave the cross-wave reduction
+// dominant).
 int down_groups_per_split(int64_t M, int groups, int nw) {
-    int gps = (int)((M + 1) / 2);
+    int gps = (int)((M + 3) / 4);
     if (gps < 2 * nw) gps = 2 * nw;
     const char* e = getenv("TRMOE_SKINNY_GPS");
     if (e != nullptr && atoi(e) > 0) gps = atoi(e);
@@ -305,13 +327,13 @@ int down_groups_per_split(int64_t M, int groups, int nw) {
 
 int down_nw(int64_t M) { return M <= 64 ? 8 : 4; }
 
-template <class Kind, bool FP8, int MT, int NW>
+template <class Kind, bool FP8, int MT, int NW, int GB>
 int down_skinny_mt(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    auto kern = k_down_skinny<Kind, FP8, MT, NW>;
+    auto kern = k_down_skinny<Kind, FP8, MT, NW, GB>;
     constexpr int kLds = red_bytes(MT, NW);
     int st = set_lds(kern, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64), (unsigned)splits), dim3(64 * NW), kLds, stream, a,
+    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 31) / 32), (unsigned)splits), dim3(64 * NW), kLds, stream, a,
                        part, gps);
     st = check_launch("shared_down_combine (skinny)");
     if (st) return st;
@@ -323,9 +345,10 @@ int down_skinny_mt(const DownArgs& a, float* part, int gps, int splits, hipStrea
 
 template <class Kind, bool FP8>
 int down_skinny_kind(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 1, 8>(a, part, gps, splits, stream);
-    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 2, 8>(a, part, gps, splits, stream);
-    return down_skinny_mt<Kind, FP8, 4, 4>(a, part, gps, splits, stream);
+    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, 8, 8>(a, part, gps, splits, stream);
+    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, 8, 8>(a, part, gps, splits, stream);
+    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, 8, 4>(a, part, gps, splits, stream);
+    return down_skinny_mt<Kind, FP8, 8, 4, 2>(a, part, gps, splits, stream);
 }
 
 }  // namespace
@@ -340,7 +363,7 @@ int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_
 size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act) {
     if (M < 1 || M > kSkinnyMaxTokens) return 0;
     const int eb = act == TRMOE_F32 ? 4 : 2;
-    const int groups = (int)((K * eb + 31) / 32);
+    const int groups = (int)((K * eb + 63) / 64);
     const int gps = down_groups_per_split(M, groups, down_nw(M));
     const int64_t splits = (groups + gps - 1) / gps;
     return (size_t)(splits * M * N * (int64_t)sizeof(float));
@@ -348,7 +371,7 @@ size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act) {
 
 int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream) {
     const int eb = act == TRMOE_F32 ? 4 : 2;
-    const int groups = (int)(((int64_t)a.K * eb + 31) / 32);
+    const int groups = (int)(((int64_t)a.K * eb + 63) / 64);
     const int gps = down_groups_per_split(a.M, groups, down_nw(a.M));
     const int splits = (groups + gps - 1) / gps;
     float* part = static_cast<float*>(workspace);

@@ -212,10 +212,10 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
  *
  * workspace: device scratch of trmoe_shared_down_combine_workspace_bytes()
  * bytes (may be NULL when that is 0).  Decode-sized calls (n_tokens <= 128)
- * split K across workgroups and reduce fp32 partials there, in a fixed order
- * (results do not depend on scheduling); with a smaller workspace they run
- * the tile kernel instead.  Calls that share a workspace must be ordered on
- * one stream.
+ * split K across workgroups, write fp32 partials there and sum them in split
+ * order in a second launch, so results do not depend on scheduling.  With a
+ * smaller workspace the call runs the tile kernel instead.  Calls that share
+ * a workspace must be ordered on one stream.
  */
 size_t trmoe_shared_down_combine_workspace_bytes(int act_dtype, int64_t n_tokens, int64_t shared_width,
                                                  int64_t hidden);

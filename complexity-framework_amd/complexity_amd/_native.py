@@ -56,10 +56,11 @@ SIGNATURES = {
         _c_int,
         [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],
     ),
+    "trmoe_routed_experts_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
     "trmoe_routed_experts": (
         _c_int,
         [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp,
-         _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],
+         _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_size, _c_vp],
     ),
     "trmoe_shared_down_combine_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
     "trmoe_shared_down_combine": (

@@ -261,17 +261,24 @@ def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[to
 
 def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Tensor, num_experts: int,
                    top_k: int, w_gate_up: torch.Tensor, s_gate_up, w_down: torch.Tensor, s_down,
-                   expert_width: int) -> torch.Tensor:
-    """y[k*N, H] in partition order."""
+                   expert_width: int, two_pass: bool = True) -> torch.Tensor:
+    """y[k*N, H] in partition order.  two_pass: grouped gate|up and down
+    GEMMs through a workspace (the default when y rows are 16-byte aligned);
+    False: the fused per-tile kernel."""
     lib = _lib()
     _require_cuda(x, sorted_idx, offsets, w_gate_up, w_down)
     x = rows16(x)
     n, hidden = x.shape
     y = torch.empty(top_k * n, hidden, dtype=x.dtype, device=x.device)
+    ws, ws_bytes = None, 0
+    if two_pass and (hidden * x.element_size()) % 16 == 0:
+        ws_bytes = lib.trmoe_routed_experts_workspace_bytes(dtype_code(x.dtype), top_k * n, expert_width)
+        if ws_bytes:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     st = lib.trmoe_routed_experts(dtype_code(x.dtype), dtype_code(w_gate_up.dtype), _p(x), n, hidden,
                                   x.stride(0), _p(sorted_idx), _p(offsets), num_experts, top_k,
                                   _p(w_gate_up), _p(s_gate_up), _p(w_down), _p(s_down), expert_width,
-                                  _p(y), hidden, _stream(x))
+                                  _p(y), hidden, _p(ws), ws_bytes, _stream(x))
     N.check(st, "trmoe_routed_experts")
     return y
 

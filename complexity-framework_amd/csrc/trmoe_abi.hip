@@ -107,7 +107,7 @@ int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b,
         TRMOE_REQUIRE(scale_a == nullptr && scale_b == nullptr && dst_scale == nullptr,
                       "pack_weight: scales are only for fp8 weights");
     }
-    PackArgs p;
+    PackArgs p{};
     p.a = src_a;
     p.b = (kind == TRMOE_PACK_GATE_UP) ? src_b : src_a;
     p.sa = scale_a;
@@ -175,7 +175,7 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
                   "shared_gate_up: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     TRMOE_REQUIRE(aligned16(h) && (ldh * elem_bytes(act_dtype)) % 16 == 0,
                   "shared_gate_up: h must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
-    GateUpArgs a;
+    GateUpArgs a{};
     a.x = x;
     a.ldx = ldx;
     a.M = n_tokens;
@@ -226,7 +226,7 @@ int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_
                   "dense_routed_gate_up: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     TRMOE_REQUIRE(aligned16(h) && (ldh * elem_bytes(act_dtype)) % 16 == 0,
                   "dense_routed_gate_up: h must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
-    GateUpArgs a;
+    GateUpArgs a{};
     a.x = x;
     a.ldx = ldx;
     a.M = n_tokens;
@@ -252,7 +252,7 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
                          const int32_t* expert_offsets, int num_experts, int top_k,
                          const void* w_gate_up, const float* s_gate_up, const void* w_down,
                          const float* s_down, int64_t expert_width, void* y, int64_t ldy,
-                         void* stream) {
+                         void* workspace, size_t workspace_bytes, void* stream) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "routed_experts: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && expert_width > 0, "routed_experts: bad dimensions");
     TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "routed_experts: num_experts must be in [1, 16]");
@@ -271,7 +271,7 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
                   "routed_experts: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
     if (n_tokens * ldx * elem_bytes(act_dtype) >= ((int64_t)1 << 31))
         return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: x must be smaller than 2 GiB");
-    RoutedArgs a;
+    RoutedArgs a{};
     a.x = x;
     a.ldx = ldx;
     a.n_tokens = n_tokens;
@@ -292,7 +292,60 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     a.H_pad = (int)round_up(hidden, 256);  // packed down rows per expert
     a.y = y;
     a.ldy = ldy;
-    return launch_routed(act_dtype, w_dtype, a, n_tokens * top_k, as_stream(stream));
+    const int64_t assignments = n_tokens * top_k;
+    const size_t need = trmoe_routed_experts_workspace_bytes(act_dtype, assignments, expert_width);
+    if (workspace == nullptr || workspace_bytes < need)
+        return launch_routed(act_dtype, w_dtype, a, assignments, as_stream(stream));
+    TRMOE_REQUIRE(aligned16(workspace), "routed_experts: workspace must be 16-byte aligned");
+    TRMOE_REQUIRE(aligned16(y) && (ldy * elem_bytes(act_dtype)) % 16 == 0,
+                  "routed_experts: y must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    // gate|up + SwiGLU: partition rows gathered from x -> h[assignments, F_pad]
+    GateUpArgs g{};
+    g.x = x;
+    g.ldx = ldx;
+    g.M = assignments;
+    g.K = (int)hidden;
+    g.w = w_gate_up;
+    g.ldw = a.wgu_ld;
+    g.w_scale = s_gate_up;
+    g.h = workspace;
+    g.ldh = f_pad;
+    g.shared_mult = 1.0f;
+    g.shared_feats = 0;
+    g.expert_feats = 1;
+    g.offsets = expert_offsets;
+    g.E = num_experts;
+    g.gather = sorted_indices;
+    g.gather_mod = n_tokens;
+    g.w_expert_stride = 2 * f_pad * a.wgu_ld;
+    g.scale_expert_stride = 2 * f_pad;
+    int st = launch_gate_up_grouped(act_dtype, w_dtype, g, assignments, 2 * f_pad, as_stream(stream));
+    if (st) return st;
+    // down: h rows (partition order) -> y rows
+    DownArgs d{};
+    d.h = workspace;
+    d.ldh = f_pad;
+    d.M = assignments;
+    d.K = (int)expert_width;
+    d.w = w_down;
+    d.ldw = a.wd_ld;
+    d.w_scale = s_down;
+    d.N = (int)hidden;
+    d.shared_scale = 1.0f;
+    d.routed_scale = 0.0f;
+    d.out = y;
+    d.ldo = ldy;
+    d.vec_ok = 1;
+    d.offsets = expert_offsets;
+    d.E = num_experts;
+    d.w_expert_stride = a.H_pad * a.wd_ld;
+    d.scale_expert_stride = a.H_pad;
+    return launch_down_grouped(act_dtype, w_dtype, d, assignments, as_stream(stream));
+}
+
+size_t trmoe_routed_experts_workspace_bytes(int act_dtype, int64_t n_assignments, int64_t expert_width) {
+    if ((act_dtype != TRMOE_F32 && act_dtype != TRMOE_BF16) || n_assignments < 1 || expert_width < 1) return 0;
+    return (size_t)(n_assignments * round_up(expert_width, 64) * elem_bytes(act_dtype));
 }
 
 int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
@@ -319,7 +372,7 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
     TRMOE_REQUIRE(aligned16(w_down), "shared_down_combine: packed weights must be 16-byte aligned");
     TRMOE_REQUIRE(rows_ok(h, ldh, elem_bytes(act_dtype)),
                   "shared_down_combine: h rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
-    DownArgs a;
+    DownArgs a{};
     a.h = h;
     a.ldh = ldh;
     a.M = n_tokens;
@@ -370,7 +423,7 @@ int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y
                   "combine: bad leading dimension");
     if (n_tokens == 0) return TRMOE_OK;
     TRMOE_REQUIRE(y && inverse && route_weights && out, "combine: null pointer");
-    CombineArgs a;
+    CombineArgs a{};
     a.M = n_tokens;
     a.N = hidden;
     a.y = y;

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace trmoe {
 
 typedef __bf16 bf16_t;
@@ -489,6 +491,9 @@ template <int ROWS, int NT>
 struct DmaRows {
     static constexpr int kInstr = ROWS * 8 / NT;   // wave instructions per thread per stage
     static constexpr int kWaves = NT / 64;
+    static constexpr int kRowsPerInstr = 8;
+    // K chunk the lane fetches for LDS row r (its slot is lane & 7)
+    static __device__ __forceinline__ int chunk_of(int lane, int r) { return (lane & 7) ^ lds_swz(r); }
     static_assert(ROWS % (8 * kWaves) == 0, "each wave fills whole 8-row groups");
     __amdgpu_buffer_rsrc_t rsrc;
     int off[kInstr];    // lane's byte offset in the row for K stage 0, kOutOfRange when absent
@@ -508,7 +513,7 @@ struct DmaRows {
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
             const int r = (wave * kInstr + j) * 8 + (lane >> 3);
-            koff[j] = ((lane & 7) ^ lds_swz(r)) * 16;
+            koff[j] = chunk_of(lane, r) * 16;
             off[j] = r < nrows ? (int)(r * ld_bytes) + koff[j] : kOutOfRange;
         }
     }
@@ -585,6 +590,8 @@ template <int ROWS, int NT>
 struct DmaRows64 {
     static constexpr int kInstr = ROWS * 4 / NT;   // each wave instruction fills 16 rows
     static constexpr int kWaves = NT / 64;
+    static constexpr int kRowsPerInstr = 16;
+    static __device__ __forceinline__ int chunk_of(int lane, int r) { return (lane & 3) ^ lds_swz64(r); }
     static_assert(ROWS % (16 * kWaves) == 0, "each wave fills whole 16-row groups");
     __amdgpu_buffer_rsrc_t rsrc;
     int off[kInstr];
@@ -603,7 +610,7 @@ struct DmaRows64 {
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
             const int r = (wave * kInstr + j) * 16 + (lane >> 2);
-            koff[j] = ((lane & 3) ^ lds_swz64(r)) * 16;
+            koff[j] = chunk_of(lane, r) * 16;
             off[j] = r < nrows ? (int)(r * ld_bytes) + koff[j] : kOutOfRange;
         }
     }
@@ -617,6 +624,15 @@ struct DmaRows64 {
         }
     }
 };
+
+// Direct-load providers (a `wave` field and per-lane offsets) versus the
+// register-staged ones (`row_off`).
+template <class P>
+struct requires_wave_field : std::false_type {};
+template <int R, int N>
+struct requires_wave_field<DmaRows<R, N>> : std::true_type {};
+template <int R, int N>
+struct requires_wave_field<DmaRows64<R, N>> : std::true_type {};
 
 // K loop over four 64-byte-row stages with stages 0..2 already requested
 // (stage 2's the most recent vector memory operations).  One barrier per

@@ -45,7 +45,18 @@ struct GateUpArgs {
     const int64_t* table;   // [top_k, vocab]
     int64_t vocab;
     int top_k;
-    float rw[4];            // per-slot route weight times the routed scale
+    float rw[4];            // per-slot route weight times the routed scale    // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
+    // (expert, row tile) pairs of a K1 partition; A rows are
+    // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
+    // null); the weights and their scales advance by w_expert_stride
+    // elements and scale_expert_stride floats per expert; output rows are
+    // partition rows.
+    const int32_t* offsets;
+    int E;
+    const int64_t* gather;
+    int64_t gather_mod;
+    int64_t w_expert_stride;
+    int64_t scale_expert_stride;
 };
 
 struct DownArgs {
@@ -68,7 +79,18 @@ struct DownArgs {
     int64_t ldr;
     void* out;
     int64_t ldo;
-    int vec_ok;             // y / residual / out rows 16-byte aligned (vector epilogue)
+    int vec_ok;             // y / residual / out rows 16-byte aligned (vector epilogue)    // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
+    // (expert, row tile) pairs of a K1 partition; A rows are
+    // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
+    // null); the weights and their scales advance by w_expert_stride
+    // elements and scale_expert_stride floats per expert; output rows are
+    // partition rows.
+    const int32_t* offsets;
+    int E;
+    const int64_t* gather;
+    int64_t gather_mod;
+    int64_t w_expert_stride;
+    int64_t scale_expert_stride;
 };
 
 struct RoutedArgs {
@@ -119,6 +141,11 @@ int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, h
 int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream);
 int routed_lds_bytes(int act, int64_t f_pad);
 int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t assignments, hipStream_t stream);
+// Grouped gate|up (a.offsets set) over `assignments` partition rows.
+int launch_gate_up_grouped(int act, int wdt, const GateUpArgs& a, int64_t assignments, int64_t packed_rows,
+                           hipStream_t stream);
+// Grouped down (a.offsets set): out rows = partition rows, no combine.
+int launch_down_grouped(int act, int wdt, const DownArgs& a, int64_t assignments, hipStream_t stream);
 int launch_combine(int act, const CombineArgs& a, hipStream_t stream);
 
 }  // namespace trmoe

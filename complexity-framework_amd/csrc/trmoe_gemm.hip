@@ -141,6 +141,71 @@ using ShapeBig4Dma = TileShape<256, 256, 2, 2, 4>;   // 4 waves of 128x128: 2/3 
 using ShapeBigDma64 = TileShape<256, 256, 2, 4, 5>;  // four 64-byte-row stages, three in flight
 
 // ---------------------------------------------------------------------------
+// expert-grouped tiles
+// ---------------------------------------------------------------------------
+// Tile `tile` of the partition (row tiles of BM rows, expert by expert) ->
+// (expert, first row, end row); expert -1 past the last tile.  Segments
+// shorter than a tile cost one partial tile, so Zipf-skewed experts only pay
+// for their own rows.
+template <int BM>
+__device__ __forceinline__ void grouped_tile(const int32_t* offsets, int E, int tile, int (&s_tile)[3]) {
+    if (threadIdx.x == 0) {
+        int acc_tiles = 0, e_sel = -1, r0 = 0, r1 = 0;
+        for (int e = 0; e < E; ++e) {
+            const int b = offsets[e], c = offsets[e + 1] - b;
+            const int nt = (c + BM - 1) / BM;
+            if (tile < acc_tiles + nt) {
+                e_sel = e;
+                r0 = b + (tile - acc_tiles) * BM;
+                r1 = r0 + BM < b + c ? r0 + BM : b + c;
+                break;
+            }
+            acc_tiles += nt;
+        }
+        s_tile[0] = e_sel;
+        s_tile[1] = r0;
+        s_tile[2] = r1;
+    }
+    __syncthreads();
+}
+
+// Gathered A rows for the direct-load providers: row r of the tile is
+// a[gather[row0 + r] % mod] (rows at or past nrows load zero).
+template <class Prov>
+__device__ __forceinline__ void init_gather_rows(Prov& p, const void* base, const int64_t* gather, int64_t mod,
+                                                 int64_t row0, int64_t nrows, int64_t ld_bytes, int kbytes) {
+    p.rsrc = make_rsrc(base, (uint32_t)(mod * ld_bytes));
+    p.kbytes = kbytes;
+    if constexpr (requires_wave_field<Prov>::value) {
+        p.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int lane = threadIdx.x & 63;
+        constexpr int kRowsPerInstr = Prov::kRowsPerInstr;
+#pragma unroll
+        for (int j = 0; j < Prov::kInstr; ++j) {
+            const int r = (p.wave * Prov::kInstr + j) * kRowsPerInstr + lane / (64 / kRowsPerInstr);
+            p.koff[j] = Prov::chunk_of(lane, r) * 16;
+            if (r < nrows) {
+                const int64_t t = (int64_t)((uint64_t)gather[row0 + r] % (uint64_t)mod);
+                p.off[j] = (int)(t * ld_bytes) + p.koff[j];
+            } else {
+                p.off[j] = kOutOfRange;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < Prov::kChunks; ++j) {
+            const int r = (threadIdx.x >> 3) + (Prov::kThreadsPerBlock / 8) * j;
+            if (r < nrows) {
+                const int64_t t = (int64_t)((uint64_t)gather[row0 + r] % (uint64_t)mod);
+                p.row_off[j] = (int)(t * ld_bytes);
+            } else {
+                p.row_off[j] = kOutOfRange;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // K2: shared gate|up + SwiGLU
 // ---------------------------------------------------------------------------
 // Gathers the routes of rows [m0, m0 + BM) into s_route for tiles that hold
@@ -240,11 +305,27 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     const int wave = threadIdx.x >> 6;
     const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
     const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
-    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
     typename AProvOf<Shape>::type ap;
-    init_a<Shape>(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    if (a.offsets != nullptr) {
+        __shared__ int s_tile[3];
+        grouped_tile<Shape::BM>(a.offsets, a.E, (int)blockIdx.x, s_tile);
+        if (s_tile[0] < 0) return;
+        const int64_t e = s_tile[0];
+        m0 = s_tile[1];
+        a.M = s_tile[2];   // rows at or past the segment end are not written
+        a.w = static_cast<const char*>(a.w) + e * a.w_expert_stride * (FP8 ? 1 : (int64_t)sizeof(T));
+        if (a.w_scale) a.w_scale += e * a.scale_expert_stride;
+        if (a.gather != nullptr)
+            init_gather_rows(ap, a.x, a.gather, a.gather_mod, m0, a.M - m0, a.ldx * (int64_t)sizeof(T),
+                             a.K * (int)sizeof(T));
+        else
+            init_a<Shape>(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    } else {
+        init_a<Shape>(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
+    }
     typename BProvOf<Kind, FP8, Shape>::type bp;
     init_b<Kind, FP8, Shape>(bp, a.w, a.ldw, n0, a.K);
 
@@ -379,9 +460,19 @@ __global__ __launch_bounds__(Shape::NT) void k_down_combine(DownArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
     const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
-    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
+    if (a.offsets != nullptr) {
+        __shared__ int s_tile[3];
+        grouped_tile<Shape::BM>(a.offsets, a.E, (int)blockIdx.x, s_tile);
+        if (s_tile[0] < 0) return;
+        const int64_t e = s_tile[0];
+        m0 = s_tile[1];
+        a.M = s_tile[2];
+        a.w = static_cast<const char*>(a.w) + e * a.w_expert_stride * (FP8 ? 1 : (int64_t)sizeof(T));
+        if (a.w_scale) a.w_scale += e * a.scale_expert_stride;
+    }
     typename AProvOf<Shape>::type ap;
     init_a<Shape>(ap, a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), a.K * (int)sizeof(T));
     typename BProvOf<Kind, FP8, Shape>::type bp;
@@ -870,6 +961,77 @@ int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream)
     if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return launch_down_kind<KindBF16, false>(a, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) return launch_down_kind<KindBF16, true>(a, stream);
     return set_error(TRMOE_ERR_UNSUPPORTED, "shared_down_combine: unsupported dtype pair");
+}
+
+// ---------------------------------------------------------------------------
+// expert-grouped launches (two-pass routed experts)
+// ---------------------------------------------------------------------------
+using ShapeGroupNarrowDma = TileShape<256, 128, 4, 2, 4>;   // packed gate|up rows not a multiple of 256
+
+template <class Kind, bool FP8, class Shape>
+static int launch_gate_up_grouped_shape(const GateUpArgs& a, int64_t assignments, int64_t packed_rows,
+                                        hipStream_t stream) {
+    const int64_t tiles_m = (assignments + Shape::BM - 1) / Shape::BM + a.E;   // each segment adds <= 1 partial tile
+    dim3 grid((unsigned)tiles_m, (unsigned)(packed_rows / Shape::BN));
+    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape>, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
+    return check_launch("routed_experts (gate|up)");
+}
+
+template <class Kind, bool FP8>
+static int gate_up_grouped_kind(const GateUpArgs& a, int64_t assignments, int64_t packed_rows, hipStream_t stream) {
+    const bool wide = packed_rows % 256 == 0;
+    if constexpr (FP8) {
+        if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBig>(a, assignments, packed_rows, stream);
+        return launch_gate_up_grouped_shape<Kind, FP8, ShapeMain>(a, assignments, packed_rows, stream);
+    } else {
+        if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBigDma>(a, assignments, packed_rows, stream);
+        return launch_gate_up_grouped_shape<Kind, FP8, ShapeGroupNarrowDma>(a, assignments, packed_rows, stream);
+    }
+}
+
+int launch_gate_up_grouped(int act, int wdt, const GateUpArgs& a, int64_t assignments, int64_t packed_rows,
+                           hipStream_t stream) {
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) return gate_up_grouped_kind<KindF32, false>(a, assignments, packed_rows, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_BF16)
+        return gate_up_grouped_kind<KindBF16, false>(a, assignments, packed_rows, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3)
+        return gate_up_grouped_kind<KindBF16, true>(a, assignments, packed_rows, stream);
+    return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: unsupported dtype pair");
+}
+
+template <class Kind, bool FP8, class Shape>
+static int launch_down_grouped_shape(const DownArgs& a, int64_t assignments, hipStream_t stream) {
+    const int64_t tiles_m = (assignments + Shape::BM - 1) / Shape::BM + a.E;
+    dim3 grid((unsigned)tiles_m, (unsigned)((a.N + Shape::BN - 1) / Shape::BN));
+    constexpr int kEpi = sizeof(typename Kind::T) == 2 ? Shape::BM * (Shape::BN * 2 + 16) : 0;
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    int st = ensure_lds(k_down_combine<Kind, FP8, Shape>, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL((k_down_combine<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
+    return check_launch("routed_experts (down)");
+}
+
+template <class Kind, bool FP8>
+static int down_grouped_kind(const DownArgs& a, int64_t assignments, hipStream_t stream) {
+    const bool fits224 = a.N % ShapeDown224::BN == 0;
+    if constexpr (FP8) {
+        if (fits224) return launch_down_grouped_shape<Kind, FP8, ShapeDown224>(a, assignments, stream);
+        return launch_down_grouped_shape<Kind, FP8, ShapeBig>(a, assignments, stream);
+    } else {
+        if (fits224) return launch_down_grouped_shape<Kind, FP8, ShapeDown224Dma>(a, assignments, stream);
+        return launch_down_grouped_shape<Kind, FP8, ShapeBigDma>(a, assignments, stream);
+    }
+}
+
+int launch_down_grouped(int act, int wdt, const DownArgs& a, int64_t assignments, hipStream_t stream) {
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) return down_grouped_kind<KindF32, false>(a, assignments, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return down_grouped_kind<KindBF16, false>(a, assignments, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) return down_grouped_kind<KindBF16, true>(a, assignments, stream);
+    return set_error(TRMOE_ERR_UNSUPPORTED, "routed_experts: unsupported dtype pair");
 }
 
 // 64-row tiles halve the LDS-resident h for wide fp32 experts.

@@ -189,13 +189,20 @@ int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_
  * w_down: PLAIN-packed transposed expert down ([E, hidden, width] view of the
  * reference's [E, width, hidden]), row_align 256.  y is act_dtype [k*n, ldy].
  * `num_experts` is the active expert count; `expert_width` the active width.
+ *
+ * workspace: device scratch of trmoe_routed_experts_workspace_bytes() bytes.
+ * With it the experts run as two grouped GEMMs (gate|up + SwiGLU into the
+ * workspace, then down), each tiled over 256-row tiles of every expert
+ * segment; with NULL (or fewer bytes) one fused kernel keeps each tile's
+ * SwiGLU output in LDS instead.  Both give the same results to rounding.
  */
+size_t trmoe_routed_experts_workspace_bytes(int act_dtype, int64_t n_assignments, int64_t expert_width);
 int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
                          int64_t hidden, int64_t ldx, const int64_t* sorted_indices,
                          const int32_t* expert_offsets, int num_experts, int top_k,
                          const void* w_gate_up, const float* s_gate_up, const void* w_down,
                          const float* s_down, int64_t expert_width, void* y, int64_t ldy,
-                         void* stream);
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * K4 -- shared down GEMM + weighted un-permute + combine; replaces

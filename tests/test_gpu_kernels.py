@@ -162,8 +162,9 @@ def _routed_ref(x, table, ids, gate, up, down, order):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("E,k,H,W,n", [(4, 2, 96, 64, 700), (8, 4, 64, 12, 300), (16, 2, 128, 256, 900),
-                                        (2, 1, 40, 8, 33), (4, 2, 896, 64, 2048)])
-def test_routed_experts(gpu, dtype, E, k, H, W, n):
+                                        (2, 1, 40, 8, 33), (4, 2, 896, 64, 2048), (16, 2, 2048, 256, 1200)])
+@pytest.mark.parametrize("two_pass", [True, False])
+def test_routed_experts(gpu, dtype, E, k, H, W, n, two_pass):
     from complexity_amd import ops
 
     table = O.route_table("token_id_multi_hash", 500, E, k, 0)
@@ -176,12 +177,13 @@ def test_routed_experts(gpu, dtype, E, k, H, W, n):
     s, inv, off, cnt = ops.route_sort(torch.from_numpy(ids).to(gpu), torch.from_numpy(table).to(gpu), E, order)
     pgu, _ = ops.pack_expert_gate_up(gate.to(gpu), up.to(gpu))
     pd, _ = ops.pack_expert_down(down.to(gpu))
-    y = ops.routed_experts(x.to(gpu), s, off, E, k, pgu, None, pd, None, W).cpu()
+    y = ops.routed_experts(x.to(gpu), s, off, E, k, pgu, None, pd, None, W, two_pass=two_pass).cpu()
     ref = _routed_ref(x, table, ids, gate, up, down, order)
     assert nerr(y, ref) <= TOL[dtype]
 
 
-def test_routed_experts_fp8_and_active_slice(gpu):
+@pytest.mark.parametrize("two_pass", [True, False])
+def test_routed_experts_fp8_and_active_slice(gpu, two_pass):
     """fp8 expert weights, packed from an active-capacity prefix view."""
     from complexity_amd import ops
 
@@ -199,7 +201,7 @@ def test_routed_experts_fp8_and_active_slice(gpu):
     pgu, pgus = ops.pack_expert_gate_up(qg.to(gpu)[:Ea, :, :Wa], qu.to(gpu)[:Ea, :, :Wa],
                                         sg.to(gpu)[:Ea, :Wa], su.to(gpu)[:Ea, :Wa])
     pd, pds = ops.pack_expert_down(qd.to(gpu)[:Ea, :Wa, :], sd.to(gpu)[:Ea])
-    y = ops.routed_experts(x.to(gpu), s, off, Ea, k, pgu, pgus, pd, pds, Wa).cpu()
+    y = ops.routed_experts(x.to(gpu), s, off, Ea, k, pgu, pgus, pd, pds, Wa, two_pass=two_pass).cpu()
     dg = O.dequantize_e4m3(qg, sg, 1)[:Ea, :, :Wa]
     du = O.dequantize_e4m3(qu, su, 1)[:Ea, :, :Wa]
     dd = O.dequantize_e4m3(qd, sd, 1)[:Ea, :Wa, :]

@@ -34,6 +34,11 @@ __device__ __forceinline__ int lds_swz(int r) { return (r ^ (r >> 3)) & 7; }
 __device__ __forceinline__ int lds_byte(int r, int c) {
     return r * kRowBytes + ((c ^ lds_swz(r)) << 4);
 }
+// 64-byte rows (four 16-byte chunks, swizzled by (r >> 1) & 3: every 8-lane
+// phase of a ds_read_b128 lands on distinct bank groups).
+constexpr int kRow64 = 64;
+__device__ __forceinline__ int lds_swz64(int r) { return (r >> 1) & 3; }
+__device__ __forceinline__ int lds_byte64(int r, int c) { return r * kRow64 + ((c ^ lds_swz64(r)) << 4); }
 
 // ---------------------------------------------------------------------------
 // element kinds
@@ -214,9 +219,11 @@ struct TileShape {
     static constexpr int TM = WM / 32;
     static constexpr int TN = WN / 32;
     // 5: direct loads into four stages of 64-byte rows (tile_loop_dma4, bf16)
+    // 6: direct loads, bf16 A rows of 128 bytes + e4m3 B rows of 64 bytes per
+    //    64-element K stage, expanded to bf16 at the fragment read
     static constexpr int kStageRowBytes = PGR == 5 ? 64 : kRowBytes;
     static constexpr int kStages = PGR == 5 ? 4 : 2;
-    static constexpr int kStageBytes = (BM + BN) * kStageRowBytes;
+    static constexpr int kStageBytes = PGR == 6 ? BM * kRowBytes + BN * 64 : (BM + BN) * kStageRowBytes;
     static constexpr int kLdsBytes = kStages * kStageBytes;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "tile rows must split evenly over threads");
@@ -240,6 +247,30 @@ __device__ __forceinline__ void mma_stage(const char* As, const char* Bs, int wm
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) mfma_group(Kind{}, a[tm], b[tn], acc[tm][tn]);
+    }
+}
+
+// One 64-element K stage with e4m3 B rows of 64 bytes (lds_byte64 layout):
+// lane (r, h) of group g reads the 8 bytes of K elements 16g + 8h .. +7 and
+// expands them to bf16 (exact) for the MFMA.
+template <int TM, int TN>
+__device__ __forceinline__ void mma_stage_f8(const char* As, const char* Bs, int wm0, int wn0,
+                                             f32x16 (&acc)[TM][TN]) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        u32x4 a[TM], b[TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+            a[tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+            b[tn] = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(Bs + lds_byte64(wn0 + tn * 32 + r, g) + 8 * h));
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) mfma_group(KindBF16{}, a[tm], b[tn], acc[tm][tn]);
     }
 }
 
@@ -544,7 +575,10 @@ __device__ __forceinline__ void dma_mainloop(const AP& ap, const BP& bp, int nk,
         else
             wait_vmcnt<0>();
         lds_barrier();
-        mma_stage<Kind, Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
+        if constexpr (Shape::PGR == 6)
+            mma_stage_f8<Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
+        else
+            mma_stage<Kind, Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
         if (kt + 2 < nk) {
             wait_lgkmcnt0();   // this wave's reads of the stage are complete
             lds_barrier();     // ... and every other wave's
@@ -561,9 +595,6 @@ __device__ __forceinline__ void dma_mainloop(const AP& ap, const BP& bp, int nk,
 // (bytes in flight / latency), not by L2 or LDS bandwidth.  Rows hold four
 // 16-byte chunks swizzled by (r >> 1) & 3, which keeps every 8-lane phase of
 // a ds_read_b128 on distinct bank groups.
-constexpr int kRow64 = 64;
-__device__ __forceinline__ int lds_swz64(int r) { return (r >> 1) & 3; }
-__device__ __forceinline__ int lds_byte64(int r, int c) { return r * kRow64 + ((c ^ lds_swz64(r)) << 4); }
 
 template <class Kind, int TM, int TN>
 __device__ __forceinline__ void mma_stage64(const char* As, const char* Bs, int wm0, int wn0,
@@ -699,7 +730,7 @@ __device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int 
                                           f32x16 (&acc)[Shape::TM][Shape::TN]) {
     if constexpr (Shape::PGR == 5)
         tile_loop_dma4<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
-    else if constexpr (Shape::PGR == 4)
+    else if constexpr (Shape::PGR == 4 || Shape::PGR == 6)
         tile_loop_dma<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
     else if constexpr (Shape::PGR == 3)
         tile_loop_pipe<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);

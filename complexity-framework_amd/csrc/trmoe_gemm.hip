@@ -103,9 +103,13 @@ struct AProvOf {
 };
 template <class Kind, bool FP8, class Shape>
 struct BProvOf {
-    static_assert(!(FP8 && Shape::PGR >= 4), "e4m3 weights need the register path");
-    using type = std::conditional_t<(Shape::PGR >= 4), DmaProv<Shape, Shape::BN>,
-                                    typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type>;
+    static_assert(!(FP8 && (Shape::PGR == 4 || Shape::PGR == 5)), "e4m3 weights: register path or PGR 6");
+    static_assert(!(!FP8 && Shape::PGR == 6), "PGR 6 is the e4m3 weight layout");
+    // PGR 6: e4m3 rows of 64 bytes per K stage, the 64-byte-row DMA layout
+    using type = std::conditional_t<
+        Shape::PGR == 6, DmaRows64<Shape::BN, Shape::NT>,
+        std::conditional_t<(Shape::PGR >= 4), DmaProv<Shape, Shape::BN>,
+                           typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type>>;
 };
 template <class Shape>
 __device__ __forceinline__ void init_a(typename AProvOf<Shape>::type& ap, const void* base, int64_t row0,
@@ -119,7 +123,7 @@ template <class Kind, bool FP8, class Shape>
 __device__ __forceinline__ void init_b(typename BProvOf<Kind, FP8, Shape>::type& bp, const void* base, int64_t ld,
                                        int64_t row0, int K) {
     if constexpr (Shape::PGR >= 4) {
-        const int64_t elem = (int64_t)sizeof(typename Kind::T);
+        const int64_t elem = FP8 ? 1 : (int64_t)sizeof(typename Kind::T);
         bp.init(base, row0, row0 + Shape::BN, ld * elem, (int)(K * elem));
     } else {
         init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, base, ld, row0, K);
@@ -139,6 +143,8 @@ using ShapeBigDma = TileShape<256, 256, 2, 4, 4>;    // 8 waves, direct buffer->
 using ShapeDown224Dma = TileShape<256, 224, 4, 1, 4>;
 using ShapeBig4Dma = TileShape<256, 256, 2, 2, 4>;   // 4 waves of 128x128: 2/3 of the LDS reads per MFMA
 using ShapeBigDma64 = TileShape<256, 256, 2, 4, 5>;  // four 64-byte-row stages, three in flight
+using ShapeBigF8Dma = TileShape<256, 256, 2, 4, 6>;  // e4m3 weights loaded straight into LDS
+using ShapeMainF8Dma = TileShape<128, 128, 2, 2, 6>;
 
 // ---------------------------------------------------------------------------
 // expert-grouped tiles
@@ -762,7 +768,7 @@ constexpr int64_t kBigTileMinBlocks = 512;
 // big (256x256, 8 waves), big8p2, big4p2 (two-stage prefetch); unset = auto.
 enum TileChoice {
     kTileAuto = 0, kTileSmall, kTileBig, kTileBig8P2, kTileBig4P2, kTileBig8Pipe, kTileBig4Pipe,
-    kTilePersist8, kTilePersist4, kTileDma, kTilePersistDma, kTileDma4, kTileDma64
+    kTilePersist8, kTilePersist4, kTileDma, kTilePersistDma, kTileDma4, kTileDma64, kTileF8Dma
 };
 static int tile_override() {
     static int v = [] {
@@ -780,6 +786,7 @@ static int tile_override() {
         if (strcmp(e, "pdma") == 0) return (int)kTilePersistDma;
         if (strcmp(e, "dma4") == 0) return (int)kTileDma4;
         if (strcmp(e, "dma64") == 0) return (int)kTileDma64;
+        if (strcmp(e, "f8dma") == 0) return (int)kTileF8Dma;
         return (int)kTileAuto;
     }();
     return v;
@@ -844,7 +851,8 @@ template <class Kind, bool FP8>
 static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int64_t big_blocks = ((a.M + 255) / 256) * (packed_rows / 256);
     int ov = tile_override();
-    if (ov == kTileAuto) ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? kTileDma : kTileSmall;
+    if (ov == kTileAuto)
+        ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? (FP8 ? kTileF8Dma : kTileDma) : kTileSmall;
     if (packed_rows % 256 != 0) ov = kTileSmall;
     switch (ov) {
         case kTileBig: return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
@@ -854,6 +862,11 @@ static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStre
         case kTileBig4Pipe: return launch_gate_up_shape<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
         case kTilePersist8: return launch_gate_up_persistent<Kind, FP8, ShapeBig>(a, packed_rows, stream);
         case kTilePersist4: return launch_gate_up_persistent<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
+        case kTileF8Dma:
+            if constexpr (FP8)
+                return launch_gate_up_shape<Kind, FP8, ShapeBigF8Dma>(a, packed_rows, stream);
+            else
+                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
         case kTileDma:
             if constexpr (FP8)
                 return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
@@ -910,7 +923,8 @@ static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     int ov = tile_override();
     if (ov == kTileAuto) {
-        if (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) ov = kTileDma;
+        if (FP8 && a.N % 256 == 0 && mt * (a.N / 256) >= 256) ov = kTileF8Dma;
+        else if (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) ov = kTileDma;
         else ov = (mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) ? kTileDma : kTileSmall;
     }
     switch (ov) {
@@ -942,6 +956,13 @@ static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
                 return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
             } else {
                 return launch_down_shape<Kind, FP8, ShapeBig4Dma>(a, stream);
+            }
+        case kTileF8Dma:
+            if constexpr (FP8) {
+                return launch_down_shape<Kind, FP8, ShapeBigF8Dma>(a, stream);
+            } else {
+                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
+                return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
             }
         case kTileDma:
         case kTilePersistDma:
@@ -985,7 +1006,7 @@ template <class Kind, bool FP8>
 static int gate_up_grouped_kind(const GateUpArgs& a, int64_t assignments, int64_t packed_rows, hipStream_t stream) {
     const bool wide = packed_rows % 256 == 0;
     if constexpr (FP8) {
-        if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBig>(a, assignments, packed_rows, stream);
+        if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBigF8Dma>(a, assignments, packed_rows, stream);
         return launch_gate_up_grouped_shape<Kind, FP8, ShapeMain>(a, assignments, packed_rows, stream);
     } else {
         if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBigDma>(a, assignments, packed_rows, stream);
@@ -1019,6 +1040,7 @@ template <class Kind, bool FP8>
 static int down_grouped_kind(const DownArgs& a, int64_t assignments, hipStream_t stream) {
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     if constexpr (FP8) {
+        if (a.N % 256 == 0) return launch_down_grouped_shape<Kind, FP8, ShapeBigF8Dma>(a, assignments, stream);
         if (fits224) return launch_down_grouped_shape<Kind, FP8, ShapeDown224>(a, assignments, stream);
         return launch_down_grouped_shape<Kind, FP8, ShapeBig>(a, assignments, stream);
     } else {

@@ -67,15 +67,15 @@ struct WFrag<Kind, true> {
 // [g0, g1) of this wave, loading GB groups at a time.  a_off[tm] / w_off[u]
 // are the byte offsets of the lane's row in each operand (kOutOfRange for
 // absent rows); kb_a is the byte length of K in an activation row.
-template <class Kind, bool FP8, int MT, int GB>
+template <class Kind, bool FP8, int MT, int NU, int GB>
 __device__ __forceinline__ void skinny_k_loop(__amdgpu_buffer_rsrc_t ar, const int (&a_off)[MT],
-                                              __amdgpu_buffer_rsrc_t wr, const int (&w_off)[2], int g0, int g1,
-                                              int kb_a, f32x4 (&acc)[MT][2]) {
+                                              __amdgpu_buffer_rsrc_t wr, const int (&w_off)[NU], int g0, int g1,
+                                              int kb_a, f32x4 (&acc)[MT][NU]) {
     using WF = WFrag<Kind, FP8>;
     const int q = (threadIdx.x & 63) >> 4;
     for (int gb = g0; gb < g1; gb += GB) {
         u32x4 av[GB][MT];
-        typename WF::Reg wv[GB][2];
+        typename WF::Reg wv[GB][NU];
 #pragma unroll
         for (int j = 0; j < GB; ++j) {
             const int g = gb + j;
@@ -85,14 +85,14 @@ __device__ __forceinline__ void skinny_k_loop(__amdgpu_buffer_rsrc_t ar, const i
             for (int tm = 0; tm < MT; ++tm)
                 av[j][tm] = buffer_load16(ar, (ok && ao < kb_a) ? a_off[tm] + ao : kOutOfRange);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) wv[j][u] = WF::load(wr, ok ? w_off[u] : kOutOfRange, g, q, kb_a);
+            for (int u = 0; u < NU; ++u) wv[j][u] = WF::load(wr, ok ? w_off[u] : kOutOfRange, g, q, kb_a);
         }
         // every load of the batch is in flight before the first MFMA waits
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < GB; ++j)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < NU; ++u) {
                 const u32x4 b = WF::expand(wv[j][u]);
 #pragma unroll
                 for (int tm = 0; tm < MT; ++tm) mfma16(Kind{}, av[j][tm], b, acc[tm][u]);
@@ -100,32 +100,52 @@ __device__ __forceinline__ void skinny_k_loop(__amdgpu_buffer_rsrc_t ar, const i
     }
 }
 
-// red[wave][e][lane] with e = (tm*2+u)*4+i.
-template <int MT>
-__device__ __forceinline__ void skinny_stash(float* red, const f32x4 (&acc)[MT][2]) {
+// red[wave][e][lane] with e = (tm*NU+u)*4+i.
+template <int MT, int NU>
+__device__ __forceinline__ void skinny_stash(float* red, const f32x4 (&acc)[MT][NU]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[((wave * MT * 2 + tm * 2 + u) * 4 + i) * 64 + lane] = acc[tm][u][i];
+            for (int i = 0; i < 4; ++i) red[((wave * MT * NU + tm * NU + u) * 4 + i) * 64 + lane] = acc[tm][u][i];
 }
 
-template <int MT, int NW>
+template <int MT, int NU, int NW>
 __device__ __forceinline__ float skinny_sum(const float* red, int tm, int u, int i, int lane) {
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) s += red[((w * MT * 2 + tm * 2 + u) * 4 + i) * 64 + lane];
+    for (int w = 0; w < NW; ++w) s += red[((w * MT * NU + tm * NU + u) * 4 + i) * 64 + lane];
     return s;
 }
 
-template <int MT>
-__device__ __forceinline__ void zero_acc16(f32x4 (&acc)[MT][2]) {
+template <int MT, int NU>
+__device__ __forceinline__ void zero_acc16(f32x4 (&acc)[MT][NU]) {
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) acc[tm][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < NU; ++u) acc[tm][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// The down epilogue for one output element: row scale, shared scale, the
+// route-weighted y rows of the token, the residual.
+template <class T>
+__device__ __forceinline__ void down_finish(const DownArgs& a, int64_t row, int64_t col, float s) {
+    float v = s * a.shared_scale * (a.w_scale ? a.w_scale[col] : 1.0f);
+    if (a.y != nullptr) {
+        const T* y = static_cast<const T*>(a.y);
+        const int64_t last = (int64_t)a.top_k * a.M - 1;
+        float racc = 0.f;
+        for (int j = 0; j < a.top_k; ++j) {
+            int64_t yr = a.inverse[(int64_t)j * a.M + row];
+            yr = yr < 0 ? 0 : (yr > last ? last : yr);
+            racc += a.rw[j] * to_f32(y[yr * a.ldy + col]);
+        }
+        v += a.routed_scale * racc;
+    }
+    if (a.residual != nullptr) v += to_f32(static_cast<const T*>(a.residual)[row * a.ldr + col]);
+    static_cast<T*>(a.out)[row * a.ldo + col] = from_f32<T>(v);
 }
 
 }  // namespace
@@ -171,9 +191,9 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     const int g0 = wave * per_wave;
     const int g1 = g0 + per_wave < groups ? g0 + per_wave : groups;
     f32x4 acc[MT][2];
-    zero_acc16<MT>(acc);
-    skinny_k_loop<Kind, FP8, MT, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
-    skinny_stash<MT>(red, acc);
+    zero_acc16<MT, 2>(acc);
+    skinny_k_loop<Kind, FP8, MT, 2, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
+    skinny_stash<MT, 2>(red, acc);
     __syncthreads();
 
     const int64_t expert = routed ? (f0 - a.shared_feats) / a.expert_feats : -1;
@@ -186,8 +206,8 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
         const int fl = l & 15;
         const float sg = a.w_scale ? a.w_scale[pg + fl] : 1.0f;
         const float su = a.w_scale ? a.w_scale[pg + 32 + fl] : 1.0f;
-        const float g = skinny_sum<MT, NW>(red, tm, 0, i, l) * sg;
-        const float u = skinny_sum<MT, NW>(red, tm, 1, i, l) * su;
+        const float g = skinny_sum<MT, 2, NW>(red, tm, 0, i, l) * sg;
+        const float u = skinny_sum<MT, 2, NW>(red, tm, 1, i, l) * su;
         float hv = silu_f(g) * u * mult;
         if (routed) {
             float tw = 0.f;
@@ -199,52 +219,58 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     }
 }
 
-// Split-K partial of the down GEMM: block (x = 32-column tile, y = K split)
-// writes part[(split * M + row) * N + col] for its rows and columns.
-template <class Kind, bool FP8, int MT, int NW, int GB>
+// Split-K partial of the down GEMM: block (x = 16*NU-column tile, y = K
+// split) writes part[(split * M + row) * N + col] for its rows and columns;
+// with a single split it finishes the output itself.
+template <class Kind, bool FP8, int MT, int NU, int NW, int GB>
 __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int groups_per_split) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
     constexpr int kWB = FP8 ? 1 : (int)sizeof(T);
+    constexpr int kCols = 16 * NU;
     extern __shared__ __align__(16) float red[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15;
-    const int64_t n0 = (int64_t)blockIdx.x * 32;
+    const int64_t n0 = (int64_t)blockIdx.x * kCols;
     const int split = blockIdx.y;
 
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.h, (uint32_t)(a.M * a.ldh * (int64_t)sizeof(T)));
-    const auto wr = make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(32 * a.ldw * kWB));
-    int a_off[MT], w_off[2];
+    const auto wr = make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(kCols * a.ldw * kWB));
+    int a_off[MT], w_off[NU];
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm) {
         const int row = tm * 16 + r;
         a_off[tm] = row < a.M ? (int)(row * a.ldh * (int64_t)sizeof(T)) : kOutOfRange;
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) w_off[u] = (int)((u * 16 + r) * a.ldw * kWB);
+    for (int u = 0; u < NU; ++u) w_off[u] = (int)((u * 16 + r) * a.ldw * kWB);
 
     const int groups = (kb_a + 63) / 64;
     const int s0 = split * groups_per_split;
     const int s1 = s0 + groups_per_split < groups ? s0 + groups_per_split : groups;
-    const int per_wave = (groups_per_split + NW - 1) / NW;
+    const int per_wave = (s1 - s0 + NW - 1) / NW;
     const int g0 = s0 + wave * per_wave;
     const int g1 = g0 + per_wave < s1 ? g0 + per_wave : s1;
-    f32x4 acc[MT][2];
-    zero_acc16<MT>(acc);
-    skinny_k_loop<Kind, FP8, MT, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
-    skinny_stash<MT>(red, acc);
+    f32x4 acc[MT][NU];
+    zero_acc16<MT, NU>(acc);
+    skinny_k_loop<Kind, FP8, MT, NU, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
+    skinny_stash<MT, NU>(red, acc);
     __syncthreads();
 
+    const bool single = gridDim.y == 1;
     float* dst = part + (int64_t)split * a.M * a.N;
-    for (int qi = threadIdx.x; qi < MT * 2 * 4 * 64; qi += NT) {
-        const int l = qi & 63, i = (qi >> 6) & 3, u = (qi >> 8) & 1, tm = qi >> 9;
+    for (int qi = threadIdx.x; qi < MT * NU * 4 * 64; qi += NT) {
+        const int l = qi & 63, i = (qi >> 6) & 3, u = (qi >> 8) % NU, tm = (qi >> 8) / NU;
         const int row = tm * 16 + 4 * (l >> 4) + i;
         const int64_t col = n0 + u * 16 + (l & 15);
         if (row >= a.M || col >= a.N) continue;
-        dst[row * (int64_t)a.N + col] = skinny_sum<MT, NW>(red, tm, u, i, l);
+        const float v = skinny_sum<MT, NU, NW>(red, tm, u, i, l);
+        if (single)
+            down_finish<T>(a, row, col, v);
+        else
+            dst[row * (int64_t)a.N + col] = v;
     }
-
 }
 
 // Sums the partials in split order (deterministic), applies the row scales,
@@ -260,20 +286,7 @@ __global__ __launch_bounds__(256) void k_down_reduce(DownArgs a, const float* pa
     const int64_t plane = a.M * (int64_t)a.N;
     float s = 0.f;
     for (int sp = 0; sp < splits; ++sp) s += part[sp * plane + idx];
-    float v = s * a.shared_scale * (a.w_scale ? a.w_scale[col] : 1.0f);
-    if (a.y != nullptr) {
-        const T* y = static_cast<const T*>(a.y);
-        const int64_t last = (int64_t)a.top_k * a.M - 1;
-        float racc = 0.f;
-        for (int j = 0; j < a.top_k; ++j) {
-            int64_t yr = a.inverse[(int64_t)j * a.M + row];
-            yr = yr < 0 ? 0 : (yr > last ? last : yr);
-            racc += a.rw[j] * to_f32(y[yr * a.ldy + col]);
-        }
-        v += a.routed_scale * racc;
-    }
-    if (a.residual != nullptr) v += to_f32(static_cast<const T*>(a.residual)[row * a.ldr + col]);
-    static_cast<T*>(a.out)[row * a.ldo + col] = from_f32<T>(v);
+    down_finish<T>(a, row, col, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -290,12 +303,12 @@ int set_lds(F* fn, int bytes) {
     return err == hipSuccess ? TRMOE_OK : set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
 }
 
-constexpr int red_bytes(int mt, int nw) { return nw * mt * 2 * 4 * 64 * 4; }
+constexpr int red_bytes(int mt, int nu, int nw) { return nw * mt * nu * 4 * 64 * 4; }
 
 template <class Kind, bool FP8, int MT, int NW, int GB>
 int gate_up_skinny_mt(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     auto kern = k_gate_up_skinny<Kind, FP8, MT, NW, GB>;
-    constexpr int kLds = red_bytes(MT, NW);
+    constexpr int kLds = red_bytes(MT, 2, NW);
     int st = set_lds(kern, kLds);
     if (st) return st;
     hipLaunchKernelGGL(kern, dim3((unsigned)(packed_rows / 32)), dim3(64 * NW), kLds, stream, a);
@@ -310,13 +323,13 @@ int gate_up_skinny_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t st
     return gate_up_skinny_mt<Kind, FP8, 8, 4, 2>(a, packed_rows, stream);
 }
 
-// K groups (64 activation bytes) per split: enough that the fp32 partial
-// (M x 32 x 4 bytes per workgroup) stays at most a quarter of the weight
-// bytes the workgroup streams (32 rows x 64 bytes per group), and at least
-// two groups per wave (measured: fewer leave the cross-wave reduction
-// dominant).
+// K groups (64 activation bytes) per split.  Up to 16 tokens one split (the
+// whole K per workgroup, 16-column tiles, no reduction launch) measured
+// fastest; above, enough groups that the fp32 partial (M x 32 x 4 bytes per
+// workgroup) stays at most a quarter of the weight bytes the workgroup
+// streams (32 rows x 64 bytes per group), and at least two per wave.
 int down_groups_per_split(int64_t M, int groups, int nw) {
-    int gps = (int)((M + 3) / 4);
+    int gps = M <= 16 ? groups : (int)((M + 3) / 4);
     if (gps < 2 * nw) gps = 2 * nw;
     const char* e = getenv("TRMOE_SKINNY_GPS");
     if (e != nullptr && atoi(e) > 0) gps = atoi(e);
@@ -327,28 +340,42 @@ int down_groups_per_split(int64_t M, int groups, int nw) {
 
 int down_nw(int64_t M) { return M <= 64 ? 8 : 4; }
 
-template <class Kind, bool FP8, int MT, int NW, int GB>
+template <class Kind, bool FP8, int MT, int NU, int NW, int GB>
 int down_skinny_mt(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    auto kern = k_down_skinny<Kind, FP8, MT, NW, GB>;
-    constexpr int kLds = red_bytes(MT, NW);
+    auto kern = k_down_skinny<Kind, FP8, MT, NU, NW, GB>;
+    constexpr int kLds = red_bytes(MT, NU, NW);
     int st = set_lds(kern, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 31) / 32), (unsigned)splits), dim3(64 * NW), kLds, stream, a,
-                       part, gps);
+    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * NU - 1) / (16 * NU)), (unsigned)splits), dim3(64 * NW), kLds,
+                       stream, a, part, gps);
     st = check_launch("shared_down_combine (skinny)");
-    if (st) return st;
+    if (st || splits == 1) return st;
     const int64_t total = a.M * (int64_t)a.N;
     hipLaunchKernelGGL(k_down_reduce<typename Kind::T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
                        a, (const float*)part, splits);
     return check_launch("shared_down_combine (skinny reduce)");
 }
 
+// Column tile: 16 columns (twice the workgroups) for up to 16 tokens, 32
+// above (half the re-reads of the activations).  TRMOE_SKINNY_NU=1/2 forces.
+int down_nu(int64_t M) {
+    const char* e = getenv("TRMOE_SKINNY_NU");
+    if (e != nullptr && (atoi(e) == 1 || atoi(e) == 2)) return atoi(e);
+    return M <= 16 ? 1 : 2;
+}
+
+template <class Kind, bool FP8, int NU>
+int down_skinny_nu(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
+    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, NU, 8, 8>(a, part, gps, splits, stream);
+    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, NU, 8, 8>(a, part, gps, splits, stream);
+    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, NU, 8, 4>(a, part, gps, splits, stream);
+    return down_skinny_mt<Kind, FP8, 8, NU, 4, 2>(a, part, gps, splits, stream);
+}
+
 template <class Kind, bool FP8>
 int down_skinny_kind(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, 8, 8>(a, part, gps, splits, stream);
-    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, 8, 8>(a, part, gps, splits, stream);
-    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, 8, 4>(a, part, gps, splits, stream);
-    return down_skinny_mt<Kind, FP8, 8, 4, 2>(a, part, gps, splits, stream);
+    if (down_nu(a.M) == 1) return down_skinny_nu<Kind, FP8, 1>(a, part, gps, splits, stream);
+    return down_skinny_nu<Kind, FP8, 2>(a, part, gps, splits, stream);
 }
 
 }  // namespace

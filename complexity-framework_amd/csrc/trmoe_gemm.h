@@ -45,7 +45,9 @@ struct GateUpArgs {
     const int64_t* table;   // [top_k, vocab]
     int64_t vocab;
     int top_k;
-    float rw[4];            // per-slot route weight times the routed scale    // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
+    float rw[4];            // per-slot route weight times the routed scale
+    int64_t n_base;         // first packed row of blockIdx.y == 0 (tail launches)
+    // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
     // (expert, row tile) pairs of a K1 partition; A rows are
     // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
     // null); the weights and their scales advance by w_expert_stride
@@ -79,7 +81,8 @@ struct DownArgs {
     int64_t ldr;
     void* out;
     int64_t ldo;
-    int vec_ok;             // y / residual / out rows 16-byte aligned (vector epilogue)    // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
+    int vec_ok;             // y / residual / out rows 16-byte aligned (vector epilogue)
+    // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
     // (expert, row tile) pairs of a K1 partition; A rows are
     // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
     // null); the weights and their scales advance by w_expert_stride

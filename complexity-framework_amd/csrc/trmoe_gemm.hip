@@ -144,6 +144,7 @@ using ShapeDown224Dma = TileShape<256, 224, 4, 1, 4>;
 using ShapeBig4Dma = TileShape<256, 256, 2, 2, 4>;   // 4 waves of 128x128: 2/3 of the LDS reads per MFMA
 using ShapeBigDma64 = TileShape<256, 256, 2, 4, 5>;  // four 64-byte-row stages, three in flight
 using ShapeBigF8Dma = TileShape<256, 256, 2, 4, 6>;  // e4m3 weights loaded straight into LDS
+using ShapeGroupNarrowDma = TileShape<256, 128, 4, 2, 4>;   // 256x128 direct-load tiles
 using ShapeMainF8Dma = TileShape<128, 128, 2, 2, 6>;
 
 // ---------------------------------------------------------------------------
@@ -304,7 +305,7 @@ __device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&a
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
-template <class Kind, bool FP8, class Shape>
+template <class Kind, bool FP8, class Shape, bool GROUPED = false>
 __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
@@ -312,10 +313,10 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
     const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
     int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
-    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+    const int64_t n0 = a.n_base + (int64_t)blockIdx.y * Shape::BN;
 
     typename AProvOf<Shape>::type ap;
-    if (a.offsets != nullptr) {
+    if constexpr (GROUPED) {
         __shared__ int s_tile[3];
         grouped_tile<Shape::BM>(a.offsets, a.E, (int)blockIdx.x, s_tile);
         if (s_tile[0] < 0) return;
@@ -459,7 +460,7 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_persist_dma(GateUpArgs a,
 // ---------------------------------------------------------------------------
 // K4: shared down + weighted un-permute + combine
 // ---------------------------------------------------------------------------
-template <class Kind, bool FP8, class Shape>
+template <class Kind, bool FP8, class Shape, bool GROUPED = false>
 __global__ __launch_bounds__(Shape::NT) void k_down_combine(DownArgs a) {
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(Shape::NT) void k_down_combine(DownArgs a) {
     int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
     const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
 
-    if (a.offsets != nullptr) {
+    if constexpr (GROUPED) {
         __shared__ int s_tile[3];
         grouped_tile<Shape::BM>(a.offsets, a.E, (int)blockIdx.x, s_tile);
         if (s_tile[0] < 0) return;
@@ -838,13 +839,40 @@ static int launch_gate_up_persist_dma(const GateUpArgs& a, int64_t packed_rows, 
 
 template <class Kind, bool FP8, class Shape>
 static int launch_gate_up_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)(packed_rows / Shape::BN));
+    dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)((packed_rows - a.n_base) / Shape::BN));
     constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
     constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
     int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape>, kLds);
     if (st) return st;
     hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
     return check_launch("shared_gate_up");
+}
+
+// 256x256 tiles, but when the last round of tiles would leave at least half
+// of the CUs idle, the trailing column tiles run as a second launch of
+// 256x128 tiles: twice the workgroups for the same work (at C2, 1664 tiles =
+// 6 full rounds + 128 tiles becomes 1536 + 256 half-width tiles).
+template <class Kind>
+static int launch_gate_up_dma_balanced(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int64_t tiles_m = (a.M + 255) / 256;
+    const int64_t cols = (packed_rows - a.n_base) / 256;
+    const int64_t cus = device_cus();
+    int64_t tail_cols = 0;
+    if (getenv("TRMOE_NO_TAIL_SPLIT") == nullptr) {
+        // smallest number of trailing columns whose removal leaves whole rounds
+        for (int64_t k = 1; k < cols; ++k)
+            if ((tiles_m * (cols - k)) % cus == 0 && tiles_m * k * 2 <= cus) {
+                tail_cols = k;
+                break;
+            }
+    }
+    if (tail_cols == 0) return launch_gate_up_shape<Kind, false, ShapeBigDma>(a, packed_rows, stream);
+    const int64_t split = a.n_base + (cols - tail_cols) * 256;
+    int st = launch_gate_up_shape<Kind, false, ShapeBigDma>(a, split, stream);
+    if (st) return st;
+    GateUpArgs t = a;
+    t.n_base = split;
+    return launch_gate_up_shape<Kind, false, ShapeGroupNarrowDma>(t, packed_rows, stream);
 }
 
 template <class Kind, bool FP8>
@@ -871,7 +899,7 @@ static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStre
             if constexpr (FP8)
                 return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
             else
-                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
+                return launch_gate_up_dma_balanced<Kind>(a, packed_rows, stream);
         case kTileDma64:
             if constexpr (FP8)
                 return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
@@ -987,7 +1015,6 @@ int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream)
 // ---------------------------------------------------------------------------
 // expert-grouped launches (two-pass routed experts)
 // ---------------------------------------------------------------------------
-using ShapeGroupNarrowDma = TileShape<256, 128, 4, 2, 4>;   // packed gate|up rows not a multiple of 256
 
 template <class Kind, bool FP8, class Shape>
 static int launch_gate_up_grouped_shape(const GateUpArgs& a, int64_t assignments, int64_t packed_rows,
@@ -996,9 +1023,9 @@ static int launch_gate_up_grouped_shape(const GateUpArgs& a, int64_t assignments
     dim3 grid((unsigned)tiles_m, (unsigned)(packed_rows / Shape::BN));
     constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
     constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
-    int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape>, kLds);
+    int st = ensure_lds(k_gate_up_swiglu<Kind, FP8, Shape, true>, kLds);
     if (st) return st;
-    hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
+    hipLaunchKernelGGL((k_gate_up_swiglu<Kind, FP8, Shape, true>), grid, dim3(Shape::NT), kLds, stream, a);
     return check_launch("routed_experts (gate|up)");
 }
 
@@ -1030,9 +1057,9 @@ static int launch_down_grouped_shape(const DownArgs& a, int64_t assignments, hip
     dim3 grid((unsigned)tiles_m, (unsigned)((a.N + Shape::BN - 1) / Shape::BN));
     constexpr int kEpi = sizeof(typename Kind::T) == 2 ? Shape::BM * (Shape::BN * 2 + 16) : 0;
     constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
-    int st = ensure_lds(k_down_combine<Kind, FP8, Shape>, kLds);
+    int st = ensure_lds(k_down_combine<Kind, FP8, Shape, true>, kLds);
     if (st) return st;
-    hipLaunchKernelGGL((k_down_combine<Kind, FP8, Shape>), grid, dim3(Shape::NT), kLds, stream, a);
+    hipLaunchKernelGGL((k_down_combine<Kind, FP8, Shape, true>), grid, dim3(Shape::NT), kLds, stream, a);
     return check_launch("routed_experts (down)");
 }
 

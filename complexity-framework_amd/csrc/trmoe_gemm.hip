@@ -145,6 +145,7 @@ using ShapeBig4Dma = TileShape<256, 256, 2, 2, 4>;   // 4 waves of 128x128: 2/3 
 using ShapeBigDma64 = TileShape<256, 256, 2, 4, 5>;  // four 64-byte-row stages, three in flight
 using ShapeBigF8Dma = TileShape<256, 256, 2, 4, 6>;  // e4m3 weights loaded straight into LDS
 using ShapeGroupNarrowDma = TileShape<256, 128, 4, 2, 4>;   // 256x128 direct-load tiles
+using ShapeTallDma = TileShape<128, 256, 1, 4, 4>;          // 128x256: 4 waves of 128x64
 using ShapeMainF8Dma = TileShape<128, 128, 2, 2, 6>;
 
 // ---------------------------------------------------------------------------
@@ -217,9 +218,10 @@ __device__ __forceinline__ void init_gather_rows(Prov& p, const void* base, cons
 // ---------------------------------------------------------------------------
 // Gathers the routes of rows [m0, m0 + BM) into s_route for tiles that hold
 // expert features (dense-routed strategy).
-template <class Shape>
+template <class Shape, bool ROUTED = true>
 __device__ __forceinline__ void gate_up_routes(const GateUpArgs& a, int64_t m0, int64_t n0,
                                                int (*s_route)[kMaxTopK]) {
+    if constexpr (!ROUTED) return;
     const bool tile_routed = a.ids != nullptr && ((n0 + Shape::BN) >> 1) > a.shared_feats;
     if (tile_routed && threadIdx.x < Shape::BM) {
         const int64_t row = m0 + threadIdx.x;
@@ -235,7 +237,7 @@ __device__ __forceinline__ void gate_up_routes(const GateUpArgs& a, int64_t m0, 
 // rows padded by 16 bytes; after a barrier gate_up_epi_store copies the tile
 // out with coalesced 16-byte stores.  gate_up_epilogue runs both; it ends
 // with LDS still in use by the copy (callers that reuse LDS barrier first).
-template <class Kind, class Shape>
+template <class Kind, class Shape, bool ROUTED = true>
 __device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
                                                  int64_t n0, char* lds, const int (*s_route)[kMaxTopK]) {
     using T = typename Kind::T;
@@ -254,7 +256,7 @@ __device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&a
         const float su = a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f;
         // expert blocks are multiples of 64 features, so a 32-feature block
         // is wholly shared or wholly one expert's
-        const bool routed = a.ids != nullptr && fblock >= a.shared_feats;
+        const bool routed = ROUTED && a.ids != nullptr && fblock >= a.shared_feats;
         const int64_t expert = routed ? (fblock - a.shared_feats) / a.expert_feats : -1;
         const float mult = routed ? 1.0f : a.shared_mult;
 #pragma unroll
@@ -295,17 +297,20 @@ __device__ __forceinline__ void gate_up_epi_store(const GateUpArgs& a, int64_t m
     }
 }
 
-template <class Kind, class Shape>
+template <class Kind, class Shape, bool ROUTED = true>
 __device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
                                                  int64_t m0, int64_t n0, char* lds,
                                                  const int (*s_route)[kMaxTopK]) {
-    gate_up_epi_tile<Kind, Shape>(a, acc, n0, lds, s_route);
+    gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route);
     wait_lgkmcnt0();   // LDS tile complete; outstanding global loads (a next tile's operands) keep flying
     lds_barrier();
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
-template <class Kind, bool FP8, class Shape, bool GROUPED = false>
+// ROUTED: the tile may hold dense-routed expert features (route gather and
+// per-token expert weights compiled in); the shared-feature launches leave
+// that code out.
+template <class Kind, bool FP8, class Shape, bool GROUPED = false, bool ROUTED = false>
 __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
@@ -338,13 +343,13 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
 
     // Routes of this tile's rows, gathered once while the first stages load;
     // read back in the epilogue after the main loop's barriers.
-    __shared__ int s_route[Shape::BM][kMaxTopK];
-    gate_up_routes<Shape>(a, m0, n0, s_route);
+    __shared__ int s_route[ROUTED ? Shape::BM : 1][kMaxTopK];
+    gate_up_routes<Shape, ROUTED>(a, m0, n0, s_route);
 
     f32x16 acc[Shape::TM][Shape::TN];
     zero_acc<Kind>(acc);
     tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
-    gate_up_epilogue<Kind, Shape>(a, acc, m0, n0, lds, s_route);
+    gate_up_epilogue<Kind, Shape, ROUTED>(a, acc, m0, n0, lds, s_route);
 }
 
 // Persistent form: gridDim.x workgroups walk the tiles (M fastest).  The
@@ -872,7 +877,9 @@ static int launch_gate_up_dma_balanced(const GateUpArgs& a, int64_t packed_rows,
     if (st) return st;
     GateUpArgs t = a;
     t.n_base = split;
-    return launch_gate_up_shape<Kind, false, ShapeGroupNarrowDma>(t, packed_rows, stream);
+    if (getenv("TRMOE_TAIL_NARROW") != nullptr)
+        return launch_gate_up_shape<Kind, false, ShapeGroupNarrowDma>(t, packed_rows, stream);
+    return launch_gate_up_shape<Kind, false, ShapeTallDma>(t, packed_rows, stream);
 }
 
 template <class Kind, bool FP8>
@@ -923,9 +930,51 @@ static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStre
     }
 }
 
+// Expert columns of a dense-routed gate|up, [a.n_base, packed_rows), in
+// 256x128 tiles with the routing code compiled in.
+template <class Kind, bool FP8, class Shape>
+static int launch_gate_up_routed_cols_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)((packed_rows - a.n_base) / Shape::BN));
+    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    auto kern = k_gate_up_swiglu<Kind, FP8, Shape, false, true>;
+    int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL(kern, grid, dim3(Shape::NT), kLds, stream, a);
+    return check_launch("dense_routed_gate_up");
+}
+
+template <class Kind, bool FP8>
+static int launch_gate_up_routed_cols(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if (!FP8 && (packed_rows - a.n_base) % 256 == 0 && getenv("TRMOE_ROUTED_NARROW") == nullptr)
+        return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeTallDma>>(
+            a, packed_rows, stream);
+    return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeGroupNarrowDma>>(
+        a, packed_rows, stream);
+}
+
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     if (a.M <= kSkinnyMaxTokens && tile_override() == kTileAuto && packed_rows % 64 == 0)
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
+    if (a.ids != nullptr) {
+        // dense-routed: the shared columns as a plain gate|up launch, then the
+        // expert columns with the routing epilogue
+        const int64_t shared_rows = 2 * a.shared_feats;
+        if (shared_rows > 0) {
+            GateUpArgs sh = a;
+            sh.ids = nullptr;
+            const int st = launch_gate_up(act, wdt, sh, shared_rows, stream);
+            if (st) return st;
+        }
+        GateUpArgs ex = a;
+        ex.n_base = shared_rows;
+        if (act == TRMOE_F32 && wdt == TRMOE_F32) return launch_gate_up_routed_cols<KindF32, false>(ex, packed_rows, stream);
+        if (act == TRMOE_BF16 && wdt == TRMOE_BF16)
+            return launch_gate_up_routed_cols<KindBF16, false>(ex, packed_rows, stream);
+        if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3)
+            return launch_gate_up_routed_cols<KindBF16, true>(ex, packed_rows, stream);
+        return set_error(TRMOE_ERR_UNSUPPORTED, "dense_routed_gate_up: unsupported dtype pair");
+    }
     if (act == TRMOE_F32 && wdt == TRMOE_F32) return launch_gate_up_kind<KindF32, false>(a, packed_rows, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return launch_gate_up_kind<KindBF16, false>(a, packed_rows, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3) return launch_gate_up_kind<KindBF16, true>(a, packed_rows, stream);

@@ -296,6 +296,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-other", action="store_true", help="skip timing the second routed strategy")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="end with three elementwise copies of MIB MiB (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -323,7 +324,7 @@ def main():
     ms_per_step, kernel_ms, wall, strategy = time_engine(torch, engine, x, ids, args.steps, args.warmup, timer)
     kernels, dominant, roof = kernel_report(w, kernel_ms, strategy)
     secondary = {}
-    other = "grouped" if strategy == "dense" else None
+    other = "grouped" if strategy == "dense" and not args.no_other else None
     if other is not None:
         engine.routed_strategy = other
         ms2, kms2, _, _ = time_engine(torch, engine, x, ids, args.steps, args.warmup, timer)

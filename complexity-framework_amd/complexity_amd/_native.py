@@ -73,6 +73,31 @@ SIGNATURES = {
         [_c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp, _c_float, _c_vp, _c_i64,
          _c_vp, _c_i64, _c_vp],
     ),
+    "trmoe_shared_swiglu_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_float, _c_vp,
+         _c_i64, _c_vp, _c_i64, _c_vp],
+    ),
+    "trmoe_dense_routed_swiglu_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_i64,
+         _c_vp, _c_vp, _c_i64, _c_int, _c_vp, _c_float, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],
+    ),
+    "trmoe_routed_swiglu_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int, _c_vp,
+         _c_vp, _c_i64, _c_vp, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],
+    ),
+    "trmoe_weight_grad_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_int, _c_i64]),
+    "trmoe_weight_grad": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_vp, _c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_size, _c_vp],
+    ),
+    "trmoe_grouped_linear": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],
+    ),
 }
 
 _lib: Optional[ctypes.CDLL] = None

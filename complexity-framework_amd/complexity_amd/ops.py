@@ -408,3 +408,228 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
                                    hidden, y, inverse, top_k, route_weights, shared_scale, routed_scale,
                                    residual)
     return combine(y, inverse, n, top_k, route_weights, routed_scale, residual)
+
+
+# ---------------------------------------------------------------------------
+# backward (bf16 / f32 weights)
+# ---------------------------------------------------------------------------
+
+def pack_linear_down_t(w_down: torch.Tensor) -> torch.Tensor:
+    """shared_down.weight [H, S] -> W_down^T packed [round_up(S,128), round_up(H,8)]."""
+    H, S = w_down.shape
+    dst, _ = _pack(N.PACK_PLAIN, w_down, None, 1, S, H, (0, w_down.stride(1), w_down.stride(0)), 128)
+    return dst[0]
+
+
+def pack_expert_down_t(down: torch.Tensor) -> torch.Tensor:
+    """Expert down [E, W, H] -> [E, round_up(W,64), round_up(H,8)] (rows = features)."""
+    E, W, H = down.shape
+    dst, _ = _pack(N.PACK_PLAIN, down, None, E, W, H, (down.stride(0), down.stride(1), down.stride(2)), 64)
+    return dst
+
+
+def pack_dense_down_t(dense_down: torch.Tensor, features: int, hidden: int) -> torch.Tensor:
+    """The dense-routed packed down [round_up(H,256), F] -> [F, round_up(H,8)]."""
+    dst, _ = _pack(N.PACK_PLAIN, dense_down, None, 1, features, hidden, (0, 1, dense_down.stride(0)), 64)
+    return dst[0]
+
+
+def pack_gate_up_t(gate_up_packed: torch.Tensor, hidden: int) -> torch.Tensor:
+    """A GATE_UP pack [G, 2F, ld] (or [2F, ld]) -> its transpose [G, round_up(H,256), 2F]:
+    the down-style weight of the data gradient [dg|du] . [Wg; Wu]."""
+    single = gate_up_packed.dim() == 2
+    p = gate_up_packed.unsqueeze(0) if single else gate_up_packed
+    G, rows, ld = p.shape
+    dst, _ = _pack(N.PACK_PLAIN, p, None, G, hidden, rows, (p.stride(0), 1, ld), DOWN_ALIGN)
+    return dst[0] if single else dst
+
+
+def shared_swiglu_backward(x: torch.Tensor, dout: torch.Tensor, w_gate_up: torch.Tensor, w_down_t: torch.Tensor,
+                           shared_width: int, shared_scale: float):
+    """(dgu[N, 2F], hm[N, F]) of the shared SwiGLU, F = round_up(S, 128)."""
+    lib = _lib()
+    _require_cuda(x, dout, w_gate_up, w_down_t)
+    n, hidden = x.shape
+    F_ = _round_up(shared_width, 128)
+    dgu = torch.empty(n, 2 * F_, dtype=x.dtype, device=x.device)
+    hm = torch.empty(n, F_, dtype=x.dtype, device=x.device)
+    st = lib.trmoe_shared_swiglu_backward(dtype_code(x.dtype), _p(x), _p(dout), n, hidden, x.stride(0),
+                                          dout.stride(0), _p(w_gate_up), _p(w_down_t), shared_width,
+                                          float(shared_scale), _p(dgu), 2 * F_, _p(hm), F_, _stream(x))
+    N.check(st, "trmoe_shared_swiglu_backward")
+    return dgu, hm
+
+
+def dense_routed_swiglu_backward(x, dout, w_gate_up, w_down_t, shared_width, num_experts, expert_width,
+                                 token_ids, route_table, route_weights, shared_scale, routed_scale):
+    """(dgu[N, 2F], hm[N, F]) over the dense-routed features."""
+    lib = _lib()
+    _require_cuda(x, dout, w_gate_up, w_down_t, token_ids, route_table)
+    n, hidden = x.shape
+    F_ = dense_routed_features(shared_width, num_experts, expert_width)
+    ids = token_ids.reshape(-1)
+    ids = (ids if ids.dtype == torch.int64 else ids.to(torch.int64)).contiguous()
+    table = route_table.contiguous()
+    dgu = torch.empty(n, 2 * F_, dtype=x.dtype, device=x.device)
+    hm = torch.empty(n, F_, dtype=x.dtype, device=x.device)
+    rw = _weights_arg(route_weights)
+    st = lib.trmoe_dense_routed_swiglu_backward(dtype_code(x.dtype), _p(x), _p(dout), n, hidden, x.stride(0),
+                                                dout.stride(0), _p(w_gate_up), _p(w_down_t), shared_width,
+                                                num_experts, expert_width, _p(ids), _p(table), table.shape[1],
+                                                table.shape[0], ctypes.cast(rw, ctypes.c_void_p),
+                                                float(shared_scale), float(routed_scale), _p(dgu), 2 * F_, _p(hm),
+                                                F_, _stream(x))
+    N.check(st, "trmoe_dense_routed_swiglu_backward")
+    return dgu, hm
+
+
+def routed_swiglu_backward(x, dout, sorted_idx, offsets, num_experts, top_k, w_gate_up, w_down_t, expert_width,
+                           route_weights, routed_scale):
+    """(dgu[kN, 2Wp], hm[kN, Wp]) in partition order, Wp = round_up(W, 64)."""
+    lib = _lib()
+    _require_cuda(x, dout, sorted_idx, offsets, w_gate_up, w_down_t)
+    n, hidden = x.shape
+    wp = _round_up(expert_width, 64)
+    rows = top_k * n
+    dgu = torch.empty(rows, 2 * wp, dtype=x.dtype, device=x.device)
+    hm = torch.empty(rows, wp, dtype=x.dtype, device=x.device)
+    rw = _weights_arg(route_weights)
+    st = lib.trmoe_routed_swiglu_backward(dtype_code(x.dtype), _p(x), _p(dout), n, hidden, x.stride(0),
+                                          dout.stride(0), _p(sorted_idx), _p(offsets), num_experts, top_k,
+                                          _p(w_gate_up), _p(w_down_t), expert_width,
+                                          ctypes.cast(rw, ctypes.c_void_p), float(routed_scale), _p(dgu), 2 * wp,
+                                          _p(hm), wp, _stream(x))
+    N.check(st, "trmoe_routed_swiglu_backward")
+    return dgu, hm
+
+
+def weight_grad(a: torch.Tensor, b: torch.Tensor, m: int, n: int, n_rows: int, a_gather=None, b_gather=None,
+                gather_mod: int = 0, offsets=None, segments: int = 1) -> torch.Tensor:
+    """out[e][i, j] = sum over rows t of segment e of a[ra(t), i] * b[rb(t), j] -> [segments, m, n]."""
+    lib = _lib()
+    _require_cuda(a, b)
+    code = dtype_code(a.dtype)
+    out = torch.empty(segments, m, n, dtype=a.dtype, device=a.device)
+    ws_bytes = lib.trmoe_weight_grad_workspace_bytes(code, m, n, segments, n_rows)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    st = lib.trmoe_weight_grad(code, _p(a), a.stride(0), a.shape[0], _p(b), b.stride(0), b.shape[0], _p(a_gather),
+                               _p(b_gather), gather_mod, m, n, n_rows, _p(offsets), segments, _p(out), n, m * n,
+                               _p(ws), ws_bytes, _stream(a))
+    N.check(st, "trmoe_weight_grad")
+    return out
+
+
+def grouped_linear(h: torch.Tensor, k: int, offsets: torch.Tensor, num_experts: int, w_packed: torch.Tensor,
+                   out_features: int) -> torch.Tensor:
+    """y[r] = h[r, :k] . W_e^T over a partition, W PLAIN-packed per expert."""
+    lib = _lib()
+    _require_cuda(h, offsets, w_packed)
+    y = torch.empty(h.shape[0], out_features, dtype=h.dtype, device=h.device)
+    st = lib.trmoe_grouped_linear(dtype_code(h.dtype), _p(h), h.stride(0), h.shape[0], k, _p(offsets), num_experts,
+                                  _p(w_packed), out_features, _p(y), out_features, _stream(h))
+    N.check(st, "trmoe_grouped_linear")
+    return y
+
+
+@dataclass
+class BackwardPacks:
+    """Transposed weight packs the backward reads (built from a PackedLayer)."""
+
+    dense_down_t: Optional[torch.Tensor] = None
+    dense_gate_up_t: Optional[torch.Tensor] = None
+    shared_down_t: Optional[torch.Tensor] = None
+    shared_gate_up_t: Optional[torch.Tensor] = None
+    expert_down_t: Optional[torch.Tensor] = None
+    expert_gate_up_t: Optional[torch.Tensor] = None
+
+
+def backward_packs(packed: PackedLayer, hidden: int, shared_down=None, expert_down=None) -> BackwardPacks:
+    """shared_down: shared_down.weight [H, S]; expert_down: the active [E, W, H] slice."""
+    bp = BackwardPacks()
+    if packed.strategy == STRATEGY_DENSE:
+        bp.dense_down_t = pack_dense_down_t(packed.dense_down, packed.dense_features, hidden)
+        bp.dense_gate_up_t = pack_gate_up_t(packed.dense_gate_up, hidden)
+        return bp
+    if packed.shared_width > 0:
+        bp.shared_down_t = pack_linear_down_t(shared_down)
+        bp.shared_gate_up_t = pack_gate_up_t(packed.shared_gate_up, hidden)
+    bp.expert_down_t = pack_expert_down_t(expert_down)
+    bp.expert_gate_up_t = pack_gate_up_t(packed.expert_gate_up, hidden)
+    return bp
+
+
+def _gate_up_rows(g: torch.Tensor, features: int):
+    """Packed gate|up rows [2F, H] -> (gate rows [F, H], up rows [F, H]) views."""
+    v = g.view(features // 32, 2, 32, g.shape[-1])
+    return v[:, 0].reshape(features, -1), v[:, 1].reshape(features, -1)
+
+
+def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor,
+                   packed: PackedLayer, bwd: BackwardPacks, route_weights: Sequence[float], shared_scale: float,
+                   routed_scale: float, order: int = ORDER_TOKEN, need_dx: bool = True, need_dw: bool = True):
+    """Gradients of layer_forward: (dx[N, H] or None, grads) with grads a dict of
+    shared_gate/shared_up [S, H], shared_down [H, S], expert_gate/expert_up
+    [E, H, W], expert_down [E, W, H] (active sizes; None when not needed)."""
+    n, hidden = x.shape
+    top_k = route_table.shape[0]
+    E, W, S = packed.num_experts, packed.expert_width, packed.shared_width
+    grads = dict.fromkeys(("shared_gate", "shared_up", "shared_down", "expert_gate", "expert_up", "expert_down"))
+    if n == 0:
+        return (torch.zeros_like(x) if need_dx else None), grads
+    x = rows16(x)
+    dout = rows16(dout.contiguous())
+    s_pad, w_pad = _round_up(S, 128), _round_up(W, 64)
+    if packed.strategy == STRATEGY_DENSE:
+        F_ = packed.dense_features
+        dgu, hm = dense_routed_swiglu_backward(x, dout, packed.dense_gate_up, bwd.dense_down_t, S, E, W, token_ids,
+                                               route_table, route_weights, shared_scale, routed_scale)
+        dx = None
+        if need_dx:
+            dx = shared_down_combine(dgu, 2 * F_, bwd.dense_gate_up_t, None, hidden, None, None, top_k,
+                                     (1.0,) * top_k, 1.0, 1.0)
+        if need_dw:
+            dwd = weight_grad(dout, hm, hidden, F_, n)[0]            # [H, F]
+            dwgu = weight_grad(dgu, x, 2 * F_, hidden, n)[0]         # [2F, H]
+            g_rows, u_rows = _gate_up_rows(dwgu, F_)
+            if S:
+                grads["shared_gate"], grads["shared_up"] = g_rows[:S], u_rows[:S]
+                grads["shared_down"] = dwd[:, :S]
+            eg = g_rows[s_pad:].view(E, w_pad, hidden)[:, :W]
+            eu = u_rows[s_pad:].view(E, w_pad, hidden)[:, :W]
+            grads["expert_gate"] = eg.transpose(1, 2)
+            grads["expert_up"] = eu.transpose(1, 2)
+            grads["expert_down"] = dwd[:, s_pad:].reshape(hidden, E, w_pad)[:, :, :W].permute(1, 2, 0)
+        return dx, grads
+
+    sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, E, order)
+    dgu_r, hm_r = routed_swiglu_backward(x, dout, sorted_idx, offsets, E, top_k, packed.expert_gate_up,
+                                         bwd.expert_down_t, W, route_weights, routed_scale)
+    dgu_s = hm_s = None
+    if S > 0:
+        dgu_s, hm_s = shared_swiglu_backward(x, dout, packed.shared_gate_up, bwd.shared_down_t, S, shared_scale)
+    dx = None
+    if need_dx:
+        dxa = grouped_linear(dgu_r, 2 * w_pad, offsets, E, bwd.expert_gate_up_t, hidden)
+        ones = (1.0,) * top_k
+        if S > 0:
+            dx = shared_down_combine(dgu_s, 2 * s_pad, bwd.shared_gate_up_t, None, hidden, dxa, inverse, top_k, ones,
+                                     1.0, 1.0)
+        else:
+            dx = combine(dxa, inverse, n, top_k, ones, 1.0)
+    if need_dw:
+        rows = top_k * n
+        if S > 0:
+            dwd_s = weight_grad(dout, hm_s, hidden, s_pad, n)[0]                 # [H, S_pad]
+            dwgu_s = weight_grad(dgu_s, x, 2 * s_pad, hidden, n)[0]              # [2S_pad, H]
+            g_rows, u_rows = _gate_up_rows(dwgu_s, s_pad)
+            grads["shared_gate"], grads["shared_up"] = g_rows[:S], u_rows[:S]
+            grads["shared_down"] = dwd_s[:, :S]
+        dwd_e = weight_grad(hm_r, dout, w_pad, hidden, rows, b_gather=sorted_idx, gather_mod=n, offsets=offsets,
+                            segments=E)                                           # [E, W_pad, H]
+        dwgu_e = weight_grad(x, dgu_r, hidden, 2 * w_pad, rows, a_gather=sorted_idx, gather_mod=n, offsets=offsets,
+                             segments=E)                                          # [E, H, 2W_pad]
+        v = dwgu_e.view(E, hidden, w_pad // 32, 2, 32)
+        grads["expert_gate"] = v[:, :, :, 0].reshape(E, hidden, w_pad)[:, :, :W]
+        grads["expert_up"] = v[:, :, :, 1].reshape(E, hidden, w_pad)[:, :, :W]
+        grads["expert_down"] = dwd_e[:, :W]
+    return dx, grads

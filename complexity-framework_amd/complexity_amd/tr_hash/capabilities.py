@@ -65,6 +65,16 @@ def supports_hip(config: TRHashEngineConfig) -> bool:
     return config.num_experts <= 16 and config.top_k in (1, 2, 4)
 
 
+_NO_HIP_BACKWARD = "HIP backward needs bf16/f32 weights and hidden_size % 8 == 0"
+
+
+def supports_hip_backward(config: TRHashEngineConfig) -> bool:
+    """Differentiable HIP calls: bf16/f32 weights (e4m3 copies are
+    inference-only) and a hidden size that is a multiple of 8 (the
+    weight-gradient GEMMs read 16-byte column chunks)."""
+    return config.precision is not TRHashPrecision.FP8 and config.hidden_size % 8 == 0
+
+
 def _allow_fallback() -> bool:
     return os.environ.get("TRMOE_ALLOW_PYTORCH_FALLBACK", "0") not in ("", "0", "false", "False")
 
@@ -91,9 +101,10 @@ def select_backend(
 ) -> BackendDecision:
     """Resolve the backend for one forward.
 
-    ``autograd`` is True when the forward must be differentiable; the HIP
-    kernels are forward-only, so such calls resolve to PYTORCH with a reason
-    (or raise when HIP was requested explicitly).
+    ``autograd`` is True when the forward must be differentiable.  The HIP
+    backend has a backward for bf16/f32 weights (``supports_hip_backward``);
+    other differentiable calls resolve to PYTORCH with a reason (or raise when
+    HIP was requested explicitly).
     """
 
     if cggr_available is None:
@@ -128,8 +139,11 @@ def select_backend(
             raise RuntimeError(f"HIP backend requested but the TR-MoE library is unavailable: {_hip_load_error()}")
         if not supports_hip(config):
             raise RuntimeError("HIP backend supports top_k in {1, 2, 4} and at most 16 experts")
-        if autograd:
-            raise RuntimeError("HIP backend is forward-only; run under torch.no_grad() or select pytorch")
+        if autograd and not supports_hip_backward(config):
+            raise RuntimeError(
+                "HIP backward needs bf16/f32 weights and hidden_size % 8 == 0; run under torch.no_grad() "
+                "or select pytorch"
+            )
         return _decision(requested, TRHashBackend.HIP, quantized=quantized, partition=partition)
 
     if requested is TRHashBackend.FUSED_CUDA:
@@ -144,8 +158,8 @@ def select_backend(
                 "fused CUDA backend requested but neither Triton kernels nor the HIP library are available: "
                 + _hip_load_error()
             )
-        if autograd:
-            return _decision(requested, TRHashBackend.PYTORCH, ["HIP kernels are forward-only"], quantized=quantized)
+        if autograd and not supports_hip_backward(config):
+            return _decision(requested, TRHashBackend.PYTORCH, [_NO_HIP_BACKWARD], quantized=quantized)
         return _decision(requested, TRHashBackend.HIP, ["fused_cuda served by HIP kernels"], quantized=quantized)
 
     if requested is TRHashBackend.CGGR:
@@ -155,8 +169,8 @@ def select_backend(
             return _decision(requested, TRHashBackend.CGGR, quantized=quantized, partition=PARTITION_ASSIGNMENT)
         if not hip_available:
             raise RuntimeError("CGGR backend requested but Triton CGGR and the HIP library are unavailable")
-        if autograd:
-            return _decision(requested, TRHashBackend.PYTORCH, ["HIP kernels are forward-only"], quantized=quantized)
+        if autograd and not supports_hip_backward(config):
+            return _decision(requested, TRHashBackend.PYTORCH, [_NO_HIP_BACKWARD], quantized=quantized)
         return _decision(requested, TRHashBackend.HIP, ["cggr served by HIP kernels"], quantized=quantized,
                          partition=PARTITION_ASSIGNMENT)
 
@@ -166,8 +180,8 @@ def select_backend(
         reasons.append("CGGR requires CUDA")
         return _decision(requested, TRHashBackend.PYTORCH, reasons, quantized=quantized)
     if hip_available and supports_hip(config):
-        if autograd:
-            return _decision(requested, TRHashBackend.PYTORCH, ["HIP kernels are forward-only"], quantized=quantized)
+        if autograd and not supports_hip_backward(config):
+            return _decision(requested, TRHashBackend.PYTORCH, [_NO_HIP_BACKWARD], quantized=quantized)
         return _decision(requested, TRHashBackend.HIP, quantized=quantized, partition=partition)
     if fused_cuda_available and supports_fused_cuda(config):
         return _decision(requested, TRHashBackend.FUSED_CUDA, quantized=quantized)

@@ -10,10 +10,11 @@ sites move over unchanged.
 Backends:
 
 * ``PYTORCH`` -- the universal definition (engine.py:66-104, 333-349, 578),
-  used for CPU tensors and for differentiable forwards;
+  used for CPU tensors (and for differentiable fp8 calls);
 * ``HIP`` -- the gfx950 kernels of ``libtrmoe`` (route partition, shared
   SwiGLU GEMM, grouped routed experts, down GEMM with the un-permute and
-  combine in its epilogue), forward-only;
+  combine in its epilogue); differentiable for bf16/f32 weights through one
+  autograd Function whose backward also runs HIP kernels (``hip_autograd``);
 * ``CUDA_GRAPH`` -- HIP (or PYTORCH) captured per static bucket.
 
 ``precision=fp8`` keeps e4m3 copies of every weight with per-output-channel
@@ -34,6 +35,7 @@ import torch.nn.functional as F
 
 from .. import ops
 from .buckets import GraphBucketPlanner
+from .hip_autograd import _LayerPlan, hip_layer_autograd
 from .capabilities import (
     PARTITION_ASSIGNMENT,
     BackendDecision,
@@ -142,6 +144,7 @@ class TRHashEngine(nn.Module):
         self._active_route_table = self.route_table
         self._fused_shared_gate_up_weight: Optional[torch.Tensor] = None
         self._packed_key = None
+        self._bwd_packed = None
         self._packed: Optional[ops.PackedLayer] = None
         self._fp8 = False
         # HIP routed-expert strategy: "grouped" (route partition + grouped
@@ -423,18 +426,59 @@ class TRHashEngine(nn.Module):
         if residual is not None:
             res = residual.reshape(-1, residual.size(-1))
             res = (res if res.dtype == packed.act_dtype else res.to(packed.act_dtype)).contiguous()
-        out = ops.layer_forward(
-            x,
-            flat_ids,
-            self._active_route_table,
-            packed,
-            self.config.route_weights,
-            self.config.shared_output_scale,
-            self.config.routed_output_scale,
-            order=order,
-            residual=res,
-        )
+        params = self._hip_params()
+        if torch.is_grad_enabled() and (
+            x.requires_grad
+            or (res is not None and res.requires_grad)
+            or any(p is not None and p.requires_grad for p in params)
+        ):
+            plan = _LayerPlan(
+                packed,
+                lambda: self._hip_backward_packs(packed),
+                flat_ids,
+                self._active_route_table,
+                self.config.route_weights,
+                self.config.shared_output_scale,
+                self.config.routed_output_scale,
+                order,
+                (self._active_num_experts, self._active_expert_width),
+            )
+            out = hip_layer_autograd(plan, x, res, params)
+        else:
+            out = ops.layer_forward(
+                x,
+                flat_ids,
+                self._active_route_table,
+                packed,
+                self.config.route_weights,
+                self.config.shared_output_scale,
+                self.config.routed_output_scale,
+                order=order,
+                residual=res,
+            )
         return out if out.dtype == flat_x.dtype else out.to(flat_x.dtype)
+
+    def _hip_params(self):
+        """Parameters the differentiable HIP call returns gradients for."""
+        shared = (None, None, None)
+        if self.shared_gate is not None:
+            shared = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight)
+        return (*shared, self.expert_gate, self.expert_up, self.expert_down)
+
+    def _hip_backward_packs(self, packed: ops.PackedLayer) -> ops.BackwardPacks:
+        """Transposed weight packs of the backward, cached with the forward pack."""
+        if self._bwd_packed is not None and self._bwd_packed[0] is packed:
+            return self._bwd_packed[1]
+        E, W = self._active_num_experts, self._active_expert_width
+        with torch.no_grad():
+            bp = ops.backward_packs(
+                packed,
+                self.config.hidden_size,
+                self.shared_down.weight if self.shared_gate is not None else None,
+                self.expert_down[:E, :W, :],
+            )
+        self._bwd_packed = (packed, bp)
+        return bp
 
     # ------------------------------------------------------------------ forward
     def _forward_eager(self, hidden_states: torch.Tensor, token_ids: torch.Tensor, backend,

@@ -439,4 +439,228 @@ int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y
     return launch_combine(act_dtype, a, as_stream(stream));
 }
 
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+static int swiglu_bwd_common(const char* who, int act_dtype, const void* x, const void* dout, int64_t rows,
+                             int64_t hidden, int64_t ldx, int64_t ldd, const void* w_gate_up,
+                             const void* w_down_t, void* dgu, int64_t lddgu, void* hm, int64_t ldhm,
+                             int64_t features, int64_t x_rows) {
+    (void)rows;
+    if (act_dtype != TRMOE_F32 && act_dtype != TRMOE_BF16)
+        return set_error(TRMOE_ERR_UNSUPPORTED, "swiglu_backward: bf16 or f32 only (fp8 weights are inference-only)");
+    if (hidden <= 0 || hidden >= ((int64_t)1 << 30)) return set_error(TRMOE_ERR_INVALID, "swiglu_backward: bad hidden");
+    if (ldx < hidden || ldd < hidden) return set_error(TRMOE_ERR_INVALID, "swiglu_backward: bad leading dimension");
+    if (lddgu < 2 * features || (hm != nullptr && ldhm < features))
+        return set_error(TRMOE_ERR_INVALID, "swiglu_backward: dgu/hm row stride too small");
+    if (!(x && dout && w_gate_up && w_down_t && dgu)) return set_error(TRMOE_ERR_INVALID, "swiglu_backward: null pointer");
+    const int eb = elem_bytes(act_dtype);
+    if (!aligned16(w_gate_up) || !aligned16(w_down_t))
+        return set_error(TRMOE_ERR_INVALID, "swiglu_backward: packed weights must be 16-byte aligned");
+    if (!rows_ok(x, ldx, eb) || !rows_ok(dout, ldd, eb))
+        return set_error(TRMOE_ERR_INVALID,
+                         "swiglu_backward: x/dout rows must be 16-byte aligned with a stride that is a multiple of 16 bytes");
+    if (x_rows * ldx * eb >= ((int64_t)1 << 31) || x_rows * ldd * eb >= ((int64_t)1 << 31))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "swiglu_backward: x and dout must be smaller than 2 GiB");
+    (void)who;
+    return TRMOE_OK;
+}
+
+static void swiglu_bwd_fill(SwigluBwdArgs& a, const void* x, const void* dout, int64_t hidden, int64_t ldx,
+                            int64_t ldd, const void* w_gate_up, const void* w_down_t, int64_t features, void* dgu,
+                            int64_t lddgu, void* hm, int64_t ldhm) {
+    a.x = x;
+    a.ldx = ldx;
+    a.dout = dout;
+    a.ldd = ldd;
+    a.K = (int)hidden;
+    a.wgu = w_gate_up;
+    a.ldwgu = round_up(hidden, 8);
+    a.wdt = w_down_t;
+    a.ldwdt = round_up(hidden, 8);
+    a.F = features;
+    a.dgu = dgu;
+    a.lddgu = lddgu;
+    a.hm = hm;
+    a.ldhm = ldhm;
+    a.expert_feats = 1;
+}
+
+int trmoe_shared_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
+                                 int64_t ldx, int64_t ldd, const void* w_gate_up, const void* w_down_t,
+                                 int64_t shared_width, float shared_scale, void* dgu, int64_t lddgu, void* hm,
+                                 int64_t ldhm, void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0 && shared_width > 0, "shared_swiglu_backward: bad dimensions");
+    if (n_tokens == 0) return TRMOE_OK;
+    const int64_t F = round_up(shared_width, 128);
+    int st = swiglu_bwd_common("shared_swiglu_backward", act_dtype, x, dout, n_tokens, hidden, ldx, ldd, w_gate_up,
+                               w_down_t, dgu, lddgu, hm, ldhm, F, n_tokens);
+    if (st) return st;
+    SwigluBwdArgs a{};
+    swiglu_bwd_fill(a, x, dout, hidden, ldx, ldd, w_gate_up, w_down_t, F, dgu, lddgu, hm, ldhm);
+    a.M = n_tokens;
+    a.x_rows = n_tokens;
+    a.shared_mult = shared_scale;
+    return launch_swiglu_bwd(act_dtype, a, 0, as_stream(stream));
+}
+
+int trmoe_dense_routed_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens,
+                                       int64_t hidden, int64_t ldx, int64_t ldd, const void* w_gate_up,
+                                       const void* w_down_t, int64_t shared_width, int num_experts,
+                                       int64_t expert_width, const int64_t* token_ids, const int64_t* route_table,
+                                       int64_t vocab_size, int top_k, const float* route_weights,
+                                       float shared_scale, float routed_scale, void* dgu, int64_t lddgu, void* hm,
+                                       int64_t ldhm, void* stream) {
+    const int64_t F = trmoe_dense_routed_features(shared_width, num_experts, expert_width);
+    TRMOE_REQUIRE(F > 0 && n_tokens >= 0, "dense_routed_swiglu_backward: bad dimensions");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "dense_routed_swiglu_backward: bad num_experts");
+    TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= num_experts, "dense_routed_swiglu_backward: bad top_k");
+    TRMOE_REQUIRE(vocab_size > 0, "dense_routed_swiglu_backward: bad vocab_size");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(token_ids && route_table && route_weights, "dense_routed_swiglu_backward: null pointer");
+    int st = swiglu_bwd_common("dense_routed_swiglu_backward", act_dtype, x, dout, n_tokens, hidden, ldx, ldd,
+                               w_gate_up, w_down_t, dgu, lddgu, hm, ldhm, F, n_tokens);
+    if (st) return st;
+    SwigluBwdArgs a{};
+    swiglu_bwd_fill(a, x, dout, hidden, ldx, ldd, w_gate_up, w_down_t, F, dgu, lddgu, hm, ldhm);
+    a.M = n_tokens;
+    a.x_rows = n_tokens;
+    a.shared_mult = shared_scale;
+    a.shared_feats = shared_width > 0 ? round_up(shared_width, 128) : 0;
+    a.expert_feats = round_up(expert_width, 64);
+    a.ids = token_ids;
+    a.table = route_table;
+    a.vocab = vocab_size;
+    a.top_k = top_k;
+    for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? route_weights[j] * routed_scale : 0.f;
+    return launch_swiglu_bwd(act_dtype, a, 0, as_stream(stream));
+}
+
+int trmoe_routed_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
+                                 int64_t ldx, int64_t ldd, const int64_t* sorted_indices,
+                                 const int32_t* expert_offsets, int num_experts, int top_k, const void* w_gate_up,
+                                 const void* w_down_t, int64_t expert_width, const float* route_weights,
+                                 float routed_scale, void* dgu, int64_t lddgu, void* hm, int64_t ldhm,
+                                 void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0 && expert_width > 0, "routed_swiglu_backward: bad dimensions");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "routed_swiglu_backward: bad num_experts");
+    TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= num_experts, "routed_swiglu_backward: bad top_k");
+    TRMOE_REQUIRE(n_tokens * top_k < ((int64_t)1 << 31), "routed_swiglu_backward: too many assignments");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(sorted_indices && expert_offsets && route_weights, "routed_swiglu_backward: null pointer");
+    const int64_t F = round_up(expert_width, 64);
+    int st = swiglu_bwd_common("routed_swiglu_backward", act_dtype, x, dout, n_tokens * top_k, hidden, ldx, ldd,
+                               w_gate_up, w_down_t, dgu, lddgu, hm, ldhm, F, n_tokens);
+    if (st) return st;
+    SwigluBwdArgs a{};
+    swiglu_bwd_fill(a, x, dout, hidden, ldx, ldd, w_gate_up, w_down_t, F, dgu, lddgu, hm, ldhm);
+    a.M = n_tokens * top_k;
+    a.x_rows = n_tokens;
+    a.offsets = expert_offsets;
+    a.E = num_experts;
+    a.gather = sorted_indices;
+    a.gather_mod = n_tokens;
+    a.top_k = top_k;
+    for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? route_weights[j] * routed_scale : 0.f;
+    a.wgu_expert_stride = 2 * F * a.ldwgu;
+    a.wdt_expert_stride = F * a.ldwdt;
+    return launch_swiglu_bwd(act_dtype, a, n_tokens * top_k, as_stream(stream));
+}
+
+size_t trmoe_weight_grad_workspace_bytes(int act_dtype, int64_t m, int64_t n, int num_segments, int64_t n_rows) {
+    if ((act_dtype != TRMOE_F32 && act_dtype != TRMOE_BF16) || m <= 0 || n <= 0 || num_segments < 1 || n_rows < 0)
+        return 0;
+    const int splits = wgrad_splits(m, n, num_segments, n_rows / num_segments);
+    return splits > 1 ? (size_t)splits * num_segments * m * n * sizeof(float) : 0;
+}
+
+int trmoe_weight_grad(int act_dtype, const void* a, int64_t lda, int64_t a_rows, const void* b, int64_t ldb,
+                      int64_t b_rows, const int64_t* a_gather, const int64_t* b_gather, int64_t gather_mod,
+                      int64_t m, int64_t n, int64_t n_rows, const int32_t* expert_offsets, int num_segments,
+                      void* out, int64_t ldo, int64_t out_expert_stride, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "weight_grad: bf16 or f32 only");
+    TRMOE_REQUIRE(m > 0 && n > 0 && n_rows >= 0 && num_segments >= 1, "weight_grad: bad dimensions");
+    TRMOE_REQUIRE(m % 8 == 0 && n % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0,
+                  "weight_grad: m, n, lda and ldb must be multiples of 8");
+    TRMOE_REQUIRE(lda >= m && ldb >= n && ldo >= n, "weight_grad: bad leading dimension");
+    TRMOE_REQUIRE(num_segments == 1 || expert_offsets != nullptr, "weight_grad: segments need expert_offsets");
+    TRMOE_REQUIRE(num_segments == 1 || out_expert_stride >= m * ldo, "weight_grad: out_expert_stride too small");
+    TRMOE_REQUIRE((a_gather == nullptr && b_gather == nullptr) || gather_mod > 0, "weight_grad: gather_mod");
+    TRMOE_REQUIRE(a && b && out, "weight_grad: null pointer");
+    const int eb = elem_bytes(act_dtype);
+    TRMOE_REQUIRE(aligned16(a) && aligned16(b), "weight_grad: operands must be 16-byte aligned");
+    if (a_rows * lda * eb >= ((int64_t)1 << 31) || b_rows * ldb * eb >= ((int64_t)1 << 31))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "weight_grad: operands must be smaller than 2 GiB");
+    TRMOE_REQUIRE(a_gather == nullptr || gather_mod <= a_rows, "weight_grad: gather_mod > a_rows");
+    TRMOE_REQUIRE(b_gather == nullptr || gather_mod <= b_rows, "weight_grad: gather_mod > b_rows");
+    TRMOE_REQUIRE(a_gather != nullptr || a_rows >= n_rows, "weight_grad: a_rows < n_rows");
+    TRMOE_REQUIRE(b_gather != nullptr || b_rows >= n_rows, "weight_grad: b_rows < n_rows");
+    TRMOE_REQUIRE(n_rows < ((int64_t)1 << 31), "weight_grad: too many rows");
+    WgradArgs w{};
+    w.a = a;
+    w.lda = lda;
+    w.a_rows = a_rows;
+    w.b = b;
+    w.ldb = ldb;
+    w.b_rows = b_rows;
+    w.a_gather = a_gather;
+    w.b_gather = b_gather;
+    w.gather_mod = gather_mod > 0 ? gather_mod : 1;
+    w.M = m;
+    w.N = n;
+    w.T = n_rows;
+    w.offsets = num_segments > 1 || expert_offsets != nullptr ? expert_offsets : nullptr;
+    w.E = num_segments;
+    w.out = out;
+    w.ldo = ldo;
+    w.out_expert_stride = out_expert_stride;
+    const size_t need = trmoe_weight_grad_workspace_bytes(act_dtype, m, n, num_segments, n_rows);
+    if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
+        TRMOE_REQUIRE(aligned16(workspace), "weight_grad: workspace must be 16-byte aligned");
+        w.splits = wgrad_splits(m, n, num_segments, n_rows / num_segments);
+        w.partial = static_cast<float*>(workspace);
+    } else {
+        w.splits = 1;
+        w.partial = nullptr;
+    }
+    return launch_wgrad(act_dtype, w, as_stream(stream));
+}
+
+int trmoe_grouped_linear(int act_dtype, const void* h, int64_t ldh, int64_t n_rows, int64_t k,
+                         const int32_t* expert_offsets, int num_experts, const void* w, int64_t out_features,
+                         void* y, int64_t ldy, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "grouped_linear: bf16 or f32 only");
+    TRMOE_REQUIRE(n_rows >= 0 && k > 0 && out_features > 0, "grouped_linear: bad dimensions");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_linear: bad num_experts");
+    TRMOE_REQUIRE(ldh >= k && ldy >= out_features, "grouped_linear: bad leading dimension");
+    TRMOE_REQUIRE(k < ((int64_t)1 << 30) && out_features < ((int64_t)1 << 30), "grouped_linear: too large");
+    if (n_rows == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(h && expert_offsets && w && y, "grouped_linear: null pointer");
+    const int eb = elem_bytes(act_dtype);
+    TRMOE_REQUIRE(aligned16(w), "grouped_linear: packed weights must be 16-byte aligned");
+    TRMOE_REQUIRE(rows_ok(h, ldh, eb), "grouped_linear: h rows must be 16-byte aligned");
+    TRMOE_REQUIRE(aligned16(y) && (ldy * eb) % 16 == 0,
+                  "grouped_linear: y must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    if (n_rows * ldh * eb >= ((int64_t)1 << 31))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "grouped_linear: h must be smaller than 2 GiB");
+    DownArgs d{};
+    d.h = h;
+    d.ldh = ldh;
+    d.M = n_rows;
+    d.K = (int)k;
+    d.w = w;
+    d.ldw = round_up(k, 8);
+    d.N = (int)out_features;
+    d.shared_scale = 1.0f;
+    d.routed_scale = 0.0f;
+    d.out = y;
+    d.ldo = ldy;
+    d.vec_ok = 1;
+    d.offsets = expert_offsets;
+    d.E = num_experts;
+    d.w_expert_stride = round_up(out_features, 256) * d.ldw;
+    return launch_down_grouped(act_dtype, act_dtype, d, n_rows, as_stream(stream));
+}
+
 }  // extern "C"

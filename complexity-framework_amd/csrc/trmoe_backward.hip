@@ -1,0 +1,454 @@
+// Backward of the TR-MoE layer (bf16 / f32 weights).
+//
+//   k_swiglu_bwd    per (256-row tile, 128 features): g|u = x Wgu^T
+//                   (recomputed, not saved by the forward), dh = dout W_down,
+//                   then dg, du and hm = m*silu(g)*u in one epilogue.  The
+//                   dense and grouped forms follow the forward's strategies:
+//                   grouped rows are partition rows read through `gather`,
+//                   the way the reference's HashCGGRGroupedGEMM reads tokens
+//                   (triton_token_routed.py:1669-1745).
+//   k_wgrad         weight gradients as token-reduction GEMMs over expert
+//                   segments without padding, split over tokens
+//                   (cggr_grad_w / hash_cggr_grad_w,
+//                   triton_token_routed.py:751-1028); operands are stored
+//                   with the reduction index as rows, so both are transposed
+//                   in registers on their way into the usual LDS layout.
+//   k_wgrad_reduce  sums the split partials in split order (deterministic).
+//
+// The data gradient dx = [dg|du] Wgu (plus, for routed rows, the sum of a
+// token's partition rows through `inverse`) runs on the forward's down/combine
+// kernels with transposed packed weights (trmoe_abi.hip).
+#include "trmoe_common.h"
+#include "trmoe_internal.h"
+#include "trmoe_gemm.h"
+#include "trmoe_tiles.h"
+
+#include <type_traits>
+
+namespace trmoe {
+
+// ---------------------------------------------------------------------------
+// transposing operand provider
+// ---------------------------------------------------------------------------
+// Operand held as a row-major matrix whose ROWS are the reduction index:
+// element (k, m) at row k, column m.  Each thread loads KB rows (KB = K
+// values per 16-byte LDS chunk: 8 bf16, 4 f32) of MB = kChunks consecutive
+// columns, and writes MB chunks, each the KB K values of one column, into
+// the [column][K] swizzled layout the MFMA stage reads.  Rows are
+// [t_base, t_end) of the matrix (direct), or the byte offsets of a table in
+// LDS (gathered rows, kOutOfRange past the segment).
+template <class Kind, int ROWS, int NT, bool GATHER>
+struct BufRowsT {
+    using T = typename Kind::T;
+    static constexpr int KB = Kind::kPerChunk;
+    static constexpr int kChunks = ROWS * 8 / NT;
+    static constexpr int MB = kChunks;
+    static constexpr int kGroups = ROWS / MB;
+    static constexpr int kThreadsPerBlock = NT;
+    static constexpr int kRowLoadBytes = MB * (int)sizeof(T);
+    static_assert(kGroups * 8 == NT, "one (column group, K chunk) pair per thread");
+    static_assert(kRowLoadBytes == 8 || kRowLoadBytes == 16 || kRowLoadBytes == 32, "row loads of 8-32 bytes");
+    static_assert(kRowLoadBytes != 8 || KB == 8, "8-byte row loads are bf16");
+    using Reg = u32x4;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int col_off;        // byte offset of the thread's first column, kOutOfRange past the last
+    int kc;             // K chunk of the stage this thread fills
+    int ld;             // bytes per row (the host keeps the matrix below 2^31 bytes)
+    int base;           // byte offset of the segment's first row (direct rows)
+    int len;            // rows in the segment
+    const int* table;
+
+    __device__ __forceinline__ void init(const void* base_ptr, int64_t rows_total, int64_t ld_bytes, int64_t col0,
+                                         int64_t ncols) {
+        rsrc = make_rsrc(base_ptr, (uint32_t)(rows_total * ld_bytes));
+        const int mg = threadIdx.x % kGroups;
+        kc = threadIdx.x / kGroups;
+        const int64_t c = col0 + (int64_t)mg * MB;
+        col_off = c < ncols ? (int)(c * (int64_t)sizeof(T)) : kOutOfRange;
+        ld = (int)ld_bytes;
+        base = 0;
+        len = 0;
+        table = nullptr;
+    }
+    __device__ __forceinline__ void segment(int64_t t0, int n, const int* tab) {
+        base = (int)(t0 * (int64_t)ld);
+        len = n;
+        table = tab;
+    }
+    __device__ __forceinline__ int offset(int lk) const {
+        int o;
+        if constexpr (GATHER)
+            o = table[lk];
+        else
+            o = lk < len ? base + lk * ld : kOutOfRange;
+        return (o < 0 || col_off < 0) ? kOutOfRange : o + col_off;
+    }
+    __device__ __forceinline__ void prefetch(int kt, Reg (&reg)[kChunks]) const {
+        const int lk0 = kt * Kind::kStageElems + kc * KB;
+        if constexpr (kRowLoadBytes == 8) {
+#pragma unroll
+            for (int k = 0; k < KB; k += 2) {
+                const u32x2 lo = buffer_load8(rsrc, offset(lk0 + k));
+                const u32x2 hi = buffer_load8(rsrc, offset(lk0 + k + 1));
+                reg[k >> 1] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
+        } else if constexpr (kRowLoadBytes == 16) {
+            static_assert(KB == kChunks, "one register per row");
+#pragma unroll
+            for (int k = 0; k < KB; ++k) reg[k] = buffer_load16(rsrc, offset(lk0 + k));
+        } else {
+            static_assert(2 * KB == kChunks, "two registers per row");
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                const int o = offset(lk0 + k);
+                reg[2 * k] = buffer_load16(rsrc, o);
+                reg[2 * k + 1] = buffer_load16(rsrc, o < 0 ? kOutOfRange : o + 16);
+            }
+        }
+    }
+    // the dword of loaded row k that holds column j (bf16: two columns per dword)
+    // (if constexpr: the other layout's subscripts would leave the vector)
+    __device__ __forceinline__ uint32_t row_dword(const Reg (&reg)[kChunks], int k, int j) const {
+        if constexpr (kRowLoadBytes == 8)
+            return reg[k >> 1][(k & 1) * 2 + (j >> 1)];
+        else
+            return reg[k][j >> 1];
+    }
+    // element (row k, column j) of an f32 block
+    __device__ __forceinline__ uint32_t elem(const Reg (&reg)[kChunks], int k, int j) const {
+        if constexpr (kRowLoadBytes == 16)
+            return reg[k][j];
+        else
+            return reg[2 * k + (j >> 2)][j & 3];
+    }
+    __device__ __forceinline__ void commit_one(char* stage, const Reg (&reg)[kChunks], int j) const {
+        u32x4 v;
+        if constexpr (sizeof(T) == 2) {
+            // dword d = (element (2d, j), element (2d+1, j)): one byte permute
+            // of the two rows' dwords holding column j
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+                v[d] = __builtin_amdgcn_perm(row_dword(reg, 2 * d + 1, j), row_dword(reg, 2 * d, j), sel);
+        } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) v[d] = elem(reg, d, j);
+        }
+        const int mg = threadIdx.x % kGroups;
+        *reinterpret_cast<u32x4*>(stage + lds_byte(mg * MB + j, kc)) = v;
+    }
+    __device__ __forceinline__ void commit(char* stage, const Reg (&reg)[kChunks]) const {
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) commit_one(stage, reg, j);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// SwiGLU backward
+// ---------------------------------------------------------------------------
+using ShapeBwdGU = TileShape<256, 256, 2, 4, 4>;   // packed gate|up columns of 128 features
+using ShapeBwdDH = TileShape<256, 128, 2, 4, 4>;   // the same 128 features of dh
+
+template <class Kind, bool GROUPED, bool ROUTED>
+__global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
+    using T = typename Kind::T;
+    using SG = ShapeBwdGU;
+    using SD = ShapeBwdDH;
+    static_assert(SG::BM == SD::BM && SG::WAVES_M == SD::WAVES_M && SG::WAVES_N == SD::WAVES_N &&
+                      SG::WN == 2 * SD::WN && SD::TN == 1 && SG::TN == 2,
+                  "a wave holds gate, up and dh of the same 32 features");
+    extern __shared__ __align__(16) char lds[];
+    constexpr int64_t kElem = (int64_t)sizeof(T);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / SG::WAVES_N) * SG::WM;
+    const int wn0 = (wave % SG::WAVES_N) * SG::WN;   // packed gate|up column within the tile
+    const int wf0 = (wave % SD::WAVES_N) * SD::WN;   // feature within the tile (= wn0 / 2)
+    int64_t m0 = (int64_t)blockIdx.x * SG::BM;
+    int64_t m_end = a.M;
+    const int64_t f0 = (int64_t)blockIdx.y * SD::BN;
+    const char* wgu = static_cast<const char*>(a.wgu);
+    const char* wdt = static_cast<const char*>(a.wdt);
+
+    typename AProvOf<SG>::type ax, ad;
+    if constexpr (GROUPED) {
+        __shared__ int s_tile[3];
+        grouped_tile<SG::BM>(a.offsets, a.E, (int)blockIdx.x, s_tile);
+        if (s_tile[0] < 0) return;
+        const int64_t e = s_tile[0];
+        m0 = s_tile[1];
+        m_end = s_tile[2];
+        wgu += e * a.wgu_expert_stride * kElem;
+        wdt += e * a.wdt_expert_stride * kElem;
+        init_gather_rows(ax, a.x, a.gather, a.gather_mod, m0, m_end - m0, a.ldx * kElem, a.K * (int)kElem);
+        init_gather_rows(ad, a.dout, a.gather, a.gather_mod, m0, m_end - m0, a.ldd * kElem, a.K * (int)kElem);
+    } else {
+        init_a<SG>(ax, a.x, m0, a.M, a.ldx * kElem, a.K * (int)kElem);
+        init_a<SD>(ad, a.dout, m0, a.M, a.ldd * kElem, a.K * (int)kElem);
+    }
+    typename BProvOf<Kind, false, SG>::type bgu;
+    typename BProvOf<Kind, false, SD>::type bdt;
+    bgu.init(wgu, 2 * f0, 2 * a.F, a.ldwgu * kElem, a.K * (int)kElem);
+    bdt.init(wdt, f0, a.F, a.ldwdt * kElem, a.K * (int)kElem);
+
+    __shared__ int s_route[ROUTED ? SG::BM : 1][kMaxTopK];
+    if constexpr (ROUTED) {
+        if (threadIdx.x < SG::BM && f0 + SD::BN > a.shared_feats) {
+            const int64_t row = m0 + threadIdx.x;
+            int64_t id = row < a.M ? a.ids[row] : 0;
+            id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
+            for (int j = 0; j < kMaxTopK; ++j)
+                s_route[threadIdx.x][j] =
+                    (j < a.top_k && row < a.M) ? (int)a.table[(int64_t)j * a.vocab + id] : -1;
+        }
+    }
+
+    f32x16 acc_gu[SG::TM][SG::TN];
+    zero_acc<Kind>(acc_gu);
+    tile_loop<Kind, SG>(ax, bgu, a.K, lds, wm0, wn0, acc_gu);
+    f32x16 acc_dh[SD::TM][SD::TN];
+    zero_acc<Kind>(acc_dh);
+    tile_loop<Kind, SD>(ad, bdt, a.K, lds, wm0, wf0, acc_dh);
+
+    const int64_t f = f0 + wf0 + (lane & 31);
+    if (f >= a.F) return;
+    // expert blocks are multiples of 64 features: a 32-feature wave block is
+    // wholly shared or one expert's
+    const bool routed = ROUTED && f0 + wf0 >= a.shared_feats;
+    const int64_t expert = routed ? (f0 + wf0 - a.shared_feats) / a.expert_feats : -1;
+    const float mult0 = routed ? 1.0f : a.shared_mult;
+    T* dgu = static_cast<T*>(a.dgu);
+    T* hm = static_cast<T*>(a.hm);
+    const int64_t pc = 64 * (f >> 5) + (f & 31);   // packed gate column
+#pragma unroll
+    for (int tm = 0; tm < SG::TM; ++tm) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int rl = wm0 + tm * 32 + acc_row(lane, i);
+            const int64_t row = m0 + rl;
+            if (row >= m_end) continue;
+            const float g = acc_gu[tm][0][i], u = acc_gu[tm][1][i], dh = acc_dh[tm][0][i];
+            float mult = mult0;
+            if constexpr (ROUTED) {
+                if (routed) {
+                    float tw = 0.f;
+#pragma unroll
+                    for (int j = 0; j < kMaxTopK; ++j) tw += (s_route[rl][j] == expert) ? a.rw[j] : 0.f;
+                    mult = tw;
+                }
+            }
+            if constexpr (GROUPED) {
+                const int64_t slot = (int64_t)((uint64_t)a.gather[row] / (uint64_t)a.gather_mod);
+                mult = a.rw[slot < kMaxTopK ? slot : kMaxTopK - 1];
+            }
+            const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+            const float s = __builtin_amdgcn_rcpf(1.0f + e);   // sigmoid(g)
+            const float sl = silu_f(g);
+            const float dm = dh * mult;
+            const float dgv = dm * u * (s + sl * (1.0f - s));   // silu'(g) = s + g s (1 - s)
+            const float duv = dm * sl;
+            dgu[row * a.lddgu + pc] = from_f32<T>(dgv);
+            dgu[row * a.lddgu + pc + 32] = from_f32<T>(duv);
+            if (hm != nullptr) {
+                // same expression order as the forward epilogue, so hm is the
+                // forward's h for the shared and dense-routed forms
+                float hv = sl * u * mult0;
+                if (ROUTED && routed) hv *= mult;
+                if (GROUPED) hv = sl * u * mult;
+                hm[row * a.ldhm + f] = from_f32<T>(hv);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// weight gradients
+// ---------------------------------------------------------------------------
+using ShapeWgrad = TileShape<256, 256, 2, 2, 1>;   // 4 waves of 128x128 (accumulators in AGPRs)
+constexpr int kWgradSeg = 2048;   // most rows of one split when an operand is gathered
+
+// Stores a wave's accumulators through a buffer descriptor: bf16 (BF16) or
+// f32 cells at (r * ld + c); cells outside [0, mlim) x [0, nlim) get an
+// offset with bit 31 set, past any range, and are dropped by the hardware.
+template <class Shape, bool BF16>
+__device__ __forceinline__ void wgrad_store(const f32x16 (&acc)[Shape::TM][Shape::TN], __amdgpu_buffer_rsrc_t rsrc,
+                                            int wm0, int wn0, int col, int lane, int ld, int mlim, int nlim) {
+    constexpr int kEsz = BF16 ? 2 : 4;
+#pragma unroll
+    for (int tm = 0; tm < Shape::TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < Shape::TN; ++tn) {
+            const int c = wn0 + tn * 32 + col;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = wm0 + tm * 32 + acc_row(lane, i);
+                const int off = ((r * ld + c) * kEsz) | ((r < mlim && c < nlim) ? 0 : kOutOfRange);
+                // the element is copied to a scalar first: a bit cast of the
+                // vector element expression itself reads element 0
+                const float v = acc[tm][tn][i];
+                if constexpr (BF16)
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (bf16_t)v), rsrc, off, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rsrc, off, 0, 0);
+            }
+        }
+}
+
+template <class Kind, class Shape, bool GA, bool GB>
+__global__ __launch_bounds__(Shape::NT) void k_wgrad(WgradArgs a) {
+    using T = typename Kind::T;
+    extern __shared__ __align__(16) char lds[];
+    constexpr int kTable = kWgradSeg + Kind::kStageElems;   // the loop prefetches one stage past the end
+    __shared__ int s_ta[GA ? kTable : 1];
+    __shared__ int s_tb[GB ? kTable : 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+    const int e = (int)blockIdx.z / a.splits, sp = (int)blockIdx.z % a.splits;
+    const int64_t seg0 = a.offsets ? a.offsets[e] : 0;
+    const int64_t seg1 = a.offsets ? a.offsets[e + 1] : a.T;
+    const int64_t per = ((seg1 - seg0 + a.splits - 1) / a.splits + Kind::kStageElems - 1) / Kind::kStageElems *
+                        Kind::kStageElems;
+    const int64_t t0 = seg0 + sp * per;
+    const int64_t t1 = t0 + per < seg1 ? t0 + per : seg1;
+
+    BufRowsT<Kind, Shape::BM, Shape::NT, GA> ap;
+    BufRowsT<Kind, Shape::BN, Shape::NT, GB> bp;
+    ap.init(a.a, a.a_rows, a.lda * (int64_t)sizeof(T), m0, a.M);
+    bp.init(a.b, a.b_rows, a.ldb * (int64_t)sizeof(T), n0, a.N);
+
+    // Gathered operands: the byte offsets of the rows are staged in LDS,
+    // kWgradSeg rows at a time.
+    f32x16 acc[Shape::TM][Shape::TN];
+    zero_acc<Kind>(acc);
+    for (int64_t s0 = t0; s0 < t1; s0 += kWgradSeg) {
+        const int len = (int)(t1 - s0 < kWgradSeg ? t1 - s0 : kWgradSeg);
+        if constexpr (GA || GB) {
+            // partition values are below 2^31 (the host checks top_k * tokens)
+            const uint32_t mod = (uint32_t)a.gather_mod;
+            const int lda_b = (int)(a.lda * (int64_t)sizeof(T)), ldb_b = (int)(a.ldb * (int64_t)sizeof(T));
+            for (int i = threadIdx.x; i < kTable; i += Shape::NT) {
+                if constexpr (GA)
+                    s_ta[i] = i < len ? (int)((uint32_t)a.a_gather[s0 + i] % mod) * lda_b : kOutOfRange;
+                if constexpr (GB)
+                    s_tb[i] = i < len ? (int)((uint32_t)a.b_gather[s0 + i] % mod) * ldb_b : kOutOfRange;
+            }
+            __syncthreads();
+        }
+        ap.segment(s0, len, s_ta);
+        bp.segment(s0, len, s_tb);
+        tile_loop_pgr1<Kind, Shape>(ap, bp, len, lds, wm0, wn0, acc);
+        // tile_loop_pgr1 ends on a barrier: the tables may be refilled
+    }
+
+    // Branch-free stores: buffer stores at an offset past the descriptor's
+    // range are dropped, so cells outside the output take kOutOfRange.
+    const bool direct = a.splits == 1;
+    const int64_t obase_el = direct ? (int64_t)e * a.out_expert_stride + m0 * a.ldo + n0
+                                    : ((int64_t)e * a.splits + sp) * a.M * a.N + m0 * a.N + n0;
+    const int ld = (int)(direct ? a.ldo : a.N);
+    const int mlim = (int)(a.M - m0 < Shape::BM ? a.M - m0 : Shape::BM);
+    const int nlim = (int)(a.N - n0 < Shape::BN ? a.N - n0 : Shape::BN);
+    const int esz = direct ? (int)sizeof(T) : 4;
+    void* obase = direct ? static_cast<void*>(static_cast<T*>(a.out) + obase_el)
+                         : static_cast<void*>(a.partial + obase_el);
+    const auto orsrc = make_rsrc(obase, (uint32_t)(((int64_t)(mlim - 1) * ld + nlim) * esz));
+    const int col = lane & 31;
+    if (direct && sizeof(T) == 2)
+        wgrad_store<Shape, true>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
+    else
+        wgrad_store<Shape, false>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
+    const int64_t mn = a.M * a.N;
+    const int64_t total = (int64_t)a.E * mn;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t e = idx / mn, r = idx % mn;
+        const float* p = a.partial + e * a.splits * mn + r;
+        float s = 0.f;
+        for (int sp = 0; sp < a.splits; ++sp) s += p[sp * mn];
+        const int64_t m = r / a.N, n = r % a.N;
+        static_cast<T*>(a.out)[e * a.out_expert_stride + m * a.ldo + n] = from_f32<T>(s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+template <class F>
+static int bwd_lds(F* fn, int bytes) {
+    if (bytes <= 65536) return TRMOE_OK;
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return err == hipSuccess ? TRMOE_OK : set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
+}
+
+template <class Kind, bool GROUPED, bool ROUTED>
+static int swiglu_bwd_kind(const SwigluBwdArgs& a, int64_t assignments, hipStream_t stream) {
+    auto kern = k_swiglu_bwd<Kind, GROUPED, ROUTED>;
+    constexpr int kLds = ShapeBwdGU::kLdsBytes;
+    int st = bwd_lds(kern, kLds);
+    if (st) return st;
+    const int64_t tiles_m =
+        GROUPED ? (assignments + ShapeBwdGU::BM - 1) / ShapeBwdGU::BM + a.E : (a.M + ShapeBwdGU::BM - 1) / ShapeBwdGU::BM;
+    const int64_t tiles_f = (a.F + ShapeBwdDH::BN - 1) / ShapeBwdDH::BN;
+    if (tiles_m <= 0 || tiles_f <= 0) return TRMOE_OK;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles_m, (unsigned)tiles_f), dim3(512), kLds, stream, a);
+    return check_launch("swiglu_backward");
+}
+
+int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipStream_t stream) {
+    const bool grouped = a.offsets != nullptr, routed = a.ids != nullptr;
+    if (act == TRMOE_BF16) {
+        if (grouped) return swiglu_bwd_kind<KindBF16, true, false>(a, assignments, stream);
+        if (routed) return swiglu_bwd_kind<KindBF16, false, true>(a, assignments, stream);
+        return swiglu_bwd_kind<KindBF16, false, false>(a, assignments, stream);
+    }
+    if (grouped) return swiglu_bwd_kind<KindF32, true, false>(a, assignments, stream);
+    if (routed) return swiglu_bwd_kind<KindF32, false, true>(a, assignments, stream);
+    return swiglu_bwd_kind<KindF32, false, false>(a, assignments, stream);
+}
+
+// Splits so that the launch has about two workgroups per CU, each reducing
+// at least 512 rows, at most 32 splits.
+int wgrad_splits(int64_t M, int64_t N, int E, int64_t rows_per_segment) {
+    const int64_t tiles = ((M + ShapeWgrad::BM - 1) / ShapeWgrad::BM) * ((N + ShapeWgrad::BN - 1) / ShapeWgrad::BN) * E;
+    int64_t s = (512 + tiles - 1) / (tiles > 0 ? tiles : 1);
+    const int64_t by_rows = rows_per_segment / 512;
+    if (s > by_rows) s = by_rows;
+    if (s > 32) s = 32;
+    return s < 1 ? 1 : (int)s;
+}
+
+template <class Kind, bool GA, bool GB>
+static int wgrad_kind(const WgradArgs& a, hipStream_t stream) {
+    auto kern = k_wgrad<Kind, ShapeWgrad, GA, GB>;
+    constexpr int kLds = ShapeWgrad::kLdsBytes;
+    int st = bwd_lds(kern, kLds);
+    if (st) return st;
+    const dim3 grid((unsigned)((a.M + ShapeWgrad::BM - 1) / ShapeWgrad::BM),
+                    (unsigned)((a.N + ShapeWgrad::BN - 1) / ShapeWgrad::BN), (unsigned)(a.E * a.splits));
+    hipLaunchKernelGGL(kern, grid, dim3(ShapeWgrad::NT), kLds, stream, a);
+    st = check_launch("weight_grad");
+    if (st || a.splits == 1) return st;
+    int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_wgrad_reduce<typename Kind::T>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    return check_launch("weight_grad (reduce)");
+}
+
+int launch_wgrad(int act, const WgradArgs& a, hipStream_t stream) {
+    const bool ga = a.a_gather != nullptr, gb = a.b_gather != nullptr;
+    if (act == TRMOE_BF16) {
+        if (ga) return gb ? wgrad_kind<KindBF16, true, true>(a, stream) : wgrad_kind<KindBF16, true, false>(a, stream);
+        return gb ? wgrad_kind<KindBF16, false, true>(a, stream) : wgrad_kind<KindBF16, false, false>(a, stream);
+    }
+    if (ga) return gb ? wgrad_kind<KindF32, true, true>(a, stream) : wgrad_kind<KindF32, true, false>(a, stream);
+    return gb ? wgrad_kind<KindF32, false, true>(a, stream) : wgrad_kind<KindF32, false, false>(a, stream);
+}
+
+}  // namespace trmoe

@@ -136,6 +136,73 @@ struct CombineArgs {
 // Token counts at or below this run the decode-shape kernels (trmoe_skinny.hip).
 constexpr int64_t kSkinnyMaxTokens = 128;
 
+// Backward of the SwiGLU block: per (row, feature), with g|u recomputed
+// from x and dh = dout . W_down^T:
+//   dg = dh*m*u*silu'(g), du = dh*m*silu(g), hm = m*silu(g)*u
+// where m is the feature's multiplier (shared_mult for shared features; the
+// token's route weight times the routed scale for dense-routed expert
+// features; rw[slot of the partition row] in grouped mode).  dg|du are
+// written in the packed gate|up column order (32 gate then 32 up columns per
+// 32-feature block), hm in feature order.
+struct SwigluBwdArgs {
+    const void* x;
+    int64_t ldx;
+    const void* dout;
+    int64_t ldd;
+    int64_t M;               // output rows (tokens, or partition rows when grouped)
+    int64_t x_rows;          // rows of x and dout (buffer range)
+    int K;                   // hidden
+    const void* wgu;         // packed gate|up rows [2F, K]
+    int64_t ldwgu;
+    const void* wdt;         // W_down^T rows [F, K]
+    int64_t ldwdt;
+    int64_t F;               // features (per expert when grouped)
+    void* dgu;
+    int64_t lddgu;
+    void* hm;                // may be null
+    int64_t ldhm;
+    float shared_mult;
+    int64_t shared_feats;    // dense-routed: features at or past it are experts'
+    int64_t expert_feats;
+    const int64_t* ids;      // dense-routed routes (null: no routed features)
+    const int64_t* table;
+    int64_t vocab;
+    int top_k;
+    float rw[4];             // per-slot route weight times the routed scale
+    const int32_t* offsets;  // grouped mode
+    int E;
+    const int64_t* gather;
+    int64_t gather_mod;
+    int64_t wgu_expert_stride;   // elements
+    int64_t wdt_expert_stride;
+};
+
+// Token-reduction GEMM: out[e][m][n] = sum over rows t of segment e of
+// A[ra(t)][m] * B[rb(t)][n], ra(t) = a_gather ? a_gather[t] % gather_mod : t
+// (same for B).  Segment e is [offsets[e], offsets[e+1]) or [0, T) without
+// offsets.  Each segment is split over `splits` workgroups whose fp32
+// partials are summed in split order by a second launch.
+struct WgradArgs {
+    const void* a;
+    int64_t lda;
+    int64_t a_rows;
+    const void* b;
+    int64_t ldb;
+    int64_t b_rows;
+    const int64_t* a_gather;
+    const int64_t* b_gather;
+    int64_t gather_mod;
+    int64_t M, N;
+    int64_t T;
+    const int32_t* offsets;
+    int E;
+    int splits;
+    void* out;
+    int64_t ldo;
+    int64_t out_expert_stride;   // elements
+    float* partial;              // [E][splits][M][N] when splits > 1
+};
+
 int launch_pack(const PackArgs& p, hipStream_t stream);
 int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
 size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act);
@@ -149,6 +216,12 @@ int launch_gate_up_grouped(int act, int wdt, const GateUpArgs& a, int64_t assign
                            hipStream_t stream);
 // Grouped down (a.offsets set): out rows = partition rows, no combine.
 int launch_down_grouped(int act, int wdt, const DownArgs& a, int64_t assignments, hipStream_t stream);
+// Backward (trmoe_backward.hip).  Grouped swiglu_bwd walks `assignments`
+// partition rows; wgrad_splits picks the split count for a workspace of
+// `workspace_bytes` (0: as many as the heuristic wants).
+int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipStream_t stream);
+int wgrad_splits(int64_t M, int64_t N, int E, int64_t rows_per_segment);
+int launch_wgrad(int act, const WgradArgs& a, hipStream_t stream);
 int launch_combine(int act, const CombineArgs& a, hipStream_t stream);
 
 }  // namespace trmoe

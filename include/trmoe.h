@@ -244,6 +244,92 @@ int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y
                   float routed_scale, const void* residual, int64_t ldr, void* out, int64_t ldo,
                   void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Backward (bf16 / f32 weights; fp8 weights are inference-only).
+ *
+ * Together these keep the HIP path differentiable: they replace the autograd
+ * of the shared linears and silu*mul (engine.py:333-349) and of the routed
+ * branch -- grad-x of HashCGGRGroupedGEMM / CGGRGroupedGEMM through the
+ * inverse permutation, PairHashReduce's expand and the unpadded grad-W
+ * kernels (triton_token_routed.py:1616-1833, 751-1028).
+ * ------------------------------------------------------------------------- */
+
+/*
+ * SwiGLU backward.  For every row r and feature f (gate|up recomputed from
+ * x, not saved by the forward):
+ *     g, u = x_r . Wg_f, x_r . Wu_f          w_gate_up: the forward's GATE_UP pack
+ *     dh   = dout_r . Wd[:, f]               w_down_t: W_down^T, PLAIN-packed [F, hidden]
+ *     dgu[r, 64*(f/32) + f%32]      = dh * m * u * silu'(g)
+ *     dgu[r, 64*(f/32) + 32 + f%32] = dh * m * silu(g)
+ *     hm[r, f]                      = m * silu(g) * u      (hm may be NULL)
+ * so dgu is the gradient of the gate|up GEMM output in the packed column
+ * order and hm the forward's (scaled) SwiGLU output.  dgu/hm are act_dtype.
+ *
+ * shared:        rows = tokens, F = round_up(shared_width, 128), m = shared_scale;
+ *                w_down_t from shared_down.weight [hidden, S] (out = S rows)
+ * dense-routed:  the layout of trmoe_dense_routed_gate_up, F =
+ *                trmoe_dense_routed_features(); m as in its forward
+ *                (routed_scale * sum_j w_j [route_j(t) == e] on expert e's features);
+ *                w_down_t: the dense packed down weight transposed [F, hidden]
+ * routed:        rows = K1 partition rows r of expert e; x/dout rows are
+ *                sorted_indices[r] mod n_tokens; F = round_up(expert_width, 64)
+ *                per expert: w_gate_up the expert GATE_UP pack (row_align 128),
+ *                w_down_t the expert down [E, W, hidden] PLAIN-packed per expert
+ *                with row_align 64; m = routed_scale * route_weights[sorted_indices[r] / n_tokens]
+ */
+int trmoe_shared_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
+                                 int64_t ldx, int64_t ldd, const void* w_gate_up, const void* w_down_t,
+                                 int64_t shared_width, float shared_scale, void* dgu, int64_t lddgu, void* hm,
+                                 int64_t ldhm, void* stream);
+int trmoe_dense_routed_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens,
+                                       int64_t hidden, int64_t ldx, int64_t ldd, const void* w_gate_up,
+                                       const void* w_down_t, int64_t shared_width, int num_experts,
+                                       int64_t expert_width, const int64_t* token_ids, const int64_t* route_table,
+                                       int64_t vocab_size, int top_k, const float* route_weights,
+                                       float shared_scale, float routed_scale, void* dgu, int64_t lddgu, void* hm,
+                                       int64_t ldhm, void* stream);
+int trmoe_routed_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
+                                 int64_t ldx, int64_t ldd, const int64_t* sorted_indices,
+                                 const int32_t* expert_offsets, int num_experts, int top_k, const void* w_gate_up,
+                                 const void* w_down_t, int64_t expert_width, const float* route_weights,
+                                 float routed_scale, void* dgu, int64_t lddgu, void* hm, int64_t ldhm,
+                                 void* stream);
+
+/*
+ * Weight gradients as token-reduction GEMMs; replaces cggr_grad_w /
+ * hash_cggr_grad_w (triton_token_routed.py:751-1028: per expert, no padding,
+ * split over tokens) and the grad-W of the shared linears.  For segment e
+ * ([expert_offsets[e], expert_offsets[e+1]), or [0, n_rows) when
+ * num_segments == 1 and expert_offsets is NULL):
+ *     out[e][i, j] = sum over rows t of the segment of a[ra(t), i] * b[rb(t), j]
+ * with ra(t) = a_gather ? a_gather[t] mod gather_mod : t (rb likewise), so an
+ * operand is read through K1's sorted_indices without a gathered copy.
+ * m, n, lda, ldb: multiples of 8; out is act_dtype [m, ldo] per segment,
+ * out_expert_stride elements apart.  With a workspace of
+ * trmoe_weight_grad_workspace_bytes() each segment is split over several
+ * workgroups whose fp32 partials are summed in split order (results do not
+ * depend on scheduling); without it one workgroup reduces each tile.
+ */
+size_t trmoe_weight_grad_workspace_bytes(int act_dtype, int64_t m, int64_t n, int num_segments, int64_t n_rows);
+int trmoe_weight_grad(int act_dtype, const void* a, int64_t lda, int64_t a_rows, const void* b, int64_t ldb,
+                      int64_t b_rows, const int64_t* a_gather, const int64_t* b_gather, int64_t gather_mod,
+                      int64_t m, int64_t n, int64_t n_rows, const int32_t* expert_offsets, int num_segments,
+                      void* out, int64_t ldo, int64_t out_expert_stride, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/*
+ * Grouped plain GEMM over a K1 partition: y[r, :] = h[r, :] . W_e^T for the
+ * rows r of expert e, with w PLAIN-packed per expert [E, round_up(out, 256),
+ * round_up(k, 8)].  The backward uses it for the data gradient of the routed
+ * rows, [dg|du]_r . [Wg_e; Wu_e] (the grad-x half of
+ * HashCGGRGroupedGEMM.backward, triton_token_routed.py:1703-1726); the
+ * per-token sum over a token's rows is then trmoe_shared_down_combine's /
+ * trmoe_combine's un-permute with unit weights.
+ */
+int trmoe_grouped_linear(int act_dtype, const void* h, int64_t ldh, int64_t n_rows, int64_t k,
+                         const int32_t* expert_offsets, int num_experts, const void* w, int64_t out_features,
+                         void* y, int64_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

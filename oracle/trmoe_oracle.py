@@ -32,6 +32,9 @@ Pinning (what checks each function beyond retyping it):
 * layer forward -- the masked-dense loop against the token-by-token loop
   (two different formulations, as the reference's own test does), shared
   SwiGLU against an explicit per-token loop, and the f32 path against f64.
+* layer backward -- ``engine_backward`` (autograd of ``engine_forward``)
+  against central finite differences in f64 (``torch.autograd.gradcheck``);
+  the closed-form ``swiglu_backward`` against that autograd.
 """
 
 from __future__ import annotations
@@ -275,7 +278,7 @@ def reference_topk_swiglu(flat_x, routes, gate_w, up_w, down_w, route_weights):
     ``routes`` [k, N] int64, ``route_weights`` [k] (per slot constants,
     engine.py:371) broadcast over tokens; computed in ``flat_x.dtype``.
     """
-    rw = torch.as_tensor(route_weights, dtype=flat_x.dtype).view(-1, 1).expand(routes.shape)
+    rw = torch.as_tensor(route_weights, dtype=flat_x.dtype, device=flat_x.device).view(-1, 1).expand(routes.shape)
     out = torch.zeros_like(flat_x)
     for e in range(gate_w.shape[0]):
         tw = (routes.eq(e).to(flat_x.dtype) * rw).sum(dim=0)
@@ -315,6 +318,47 @@ def engine_forward(x, token_ids, table, params: dict, *, route_weights: Sequence
                            params.get("shared_down"))
     routed = reference_topk_swiglu(flat_x, routes, g, u, d, route_weights)
     return (shared_scale * shared + routed_scale * routed).view(shape)
+
+
+def engine_backward(x, token_ids, table, params: dict, dout, *, route_weights: Sequence[float],
+                    shared_scale: float = 1.0, routed_scale: float = 1.0,
+                    active_experts: Optional[int] = None, active_width: Optional[int] = None):
+    """Gradients of ``engine_forward`` for an output gradient ``dout``:
+    {"x", "shared_gate", "shared_up", "shared_down", "expert_gate",
+    "expert_up", "expert_down"} (full parameter shapes; entries outside the
+    active capacity are zero).  This is what the reference's PYTORCH backend
+    returns through autograd, and what its Triton path's autograd Functions
+    (triton_token_routed.py:1616-1833) compute for the routed branch.
+    """
+    leaves = {"x": x.detach().clone().requires_grad_(True)}
+    for name, t in params.items():
+        if t is not None and t.numel():
+            leaves[name] = t.detach().clone().requires_grad_(True)
+    p = {k: v for k, v in leaves.items() if k != "x"}
+    out = engine_forward(leaves["x"], token_ids, table, p, route_weights=route_weights,
+                         shared_scale=shared_scale, routed_scale=routed_scale,
+                         active_experts=active_experts, active_width=active_width)
+    names = list(leaves)
+    grads = torch.autograd.grad(out, [leaves[n] for n in names], grad_outputs=dout.to(out.dtype),
+                                allow_unused=True)
+    return {n: (torch.zeros_like(leaves[n]) if g is None else g) for n, g in zip(names, grads)}
+
+
+def swiglu_backward(x, dout, gate_w, up_w, down_w, mult=1.0):
+    """Closed-form backward of y = (m * silu(x Wg^T) * (x Wu^T)) Wd^T per row.
+
+    x, dout: [R, H]; gate_w, up_w: [F, H]; down_w: [H, F]; mult: scalar or
+    [R, F] (the route weight of a routed row, the shared scale otherwise).
+    Returns (dg, du, h): the gradients at the gate and up pre-activations and
+    the forward's m * silu(g) * u, each [R, F]; silu'(g) = s + g s (1 - s)
+    with s = sigmoid(g).
+    """
+    g = x @ gate_w.T
+    u = x @ up_w.T
+    dh = dout @ down_w
+    s = torch.sigmoid(g)
+    dm = dh * mult
+    return dm * u * (s + g * s * (1 - s)), dm * g * s, mult * g * s * u
 
 
 def naive_engine_output(x, token_ids, table, params: dict, *, route_weights,

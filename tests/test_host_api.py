@@ -29,7 +29,7 @@ from complexity_amd.tr_hash import (
     TRHashStrategy,
 )
 from complexity_amd.tr_hash.buckets import GraphBucketPlanner
-from complexity_amd.tr_hash.capabilities import select_backend, supports_fused_cuda
+from complexity_amd.tr_hash.capabilities import select_backend, supports_fused_cuda, supports_hip_backward
 from complexity_amd.tr_hash.routing import (
     build_route_table,
     compile_top2_pair_metadata,
@@ -178,13 +178,21 @@ def test_auto_backend_on_cpu_is_pytorch_with_reason():
     assert d.reasons
 
 
-def test_auto_backend_on_gpu_selects_hip_and_pytorch_under_autograd():
+def test_auto_backend_on_gpu_selects_hip_also_under_autograd():
     cfg = _config()
     d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False, fused_cuda_available=False)
     assert d.selected is TRHashBackend.HIP
+    # the HIP backend has a backward for bf16/f32 weights and hidden % 8 == 0
     d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False,
                        fused_cuda_available=False, autograd=True)
-    assert d.selected is TRHashBackend.PYTORCH and d.reasons
+    assert d.selected is TRHashBackend.HIP and not d.reasons
+    assert supports_hip_backward(cfg)
+    # otherwise differentiable calls resolve to PYTORCH with the reason
+    for cfg in (_config(hidden_size=36), _config(precision=TRHashPrecision.FP8)):
+        assert not supports_hip_backward(cfg)
+        d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False,
+                           fused_cuda_available=False, autograd=True)
+        assert d.selected is TRHashBackend.PYTORCH and any("backward" in r for r in d.reasons)
 
 
 def test_missing_library_on_gpu_fails_loudly(monkeypatch):
@@ -210,8 +218,11 @@ def test_explicit_backends_resolve_with_reasons():
     assert d.selected is TRHashBackend.HIP and d.partition == "assignment"
     with pytest.raises(RuntimeError):
         select_backend(_config(backend=TRHashBackend.HIP), device_type="cpu")
+    d = select_backend(_config(backend=TRHashBackend.HIP), device_type="cuda", hip_available=True, autograd=True)
+    assert d.selected is TRHashBackend.HIP
     with pytest.raises(RuntimeError):
-        select_backend(_config(backend=TRHashBackend.HIP), device_type="cuda", hip_available=True, autograd=True)
+        select_backend(_config(backend=TRHashBackend.HIP, hidden_size=36), device_type="cuda", hip_available=True,
+                       autograd=True)
 
 
 def test_fused_eligibility_is_the_reference_pair_shape():

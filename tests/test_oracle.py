@@ -257,3 +257,80 @@ def test_quantize_e4m3_scale_and_error_bound():
     rel = ((deq - w).abs() / w.abs().clamp_min(1e-30))
     normal = w.abs() >= s.unsqueeze(1) * 2.0 ** -6
     assert rel[normal].max() <= 2.0 ** -4 + 1e-6
+
+
+# --------------------------------------------------------------------------- backward
+
+
+def _tiny_layer(seed, E=3, H=6, S=5, W=4, k=2, n=7, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    params = {
+        "expert_gate": torch.randn(E, H, W, generator=g, dtype=dtype) * 0.5,
+        "expert_up": torch.randn(E, H, W, generator=g, dtype=dtype) * 0.5,
+        "expert_down": torch.randn(E, W, H, generator=g, dtype=dtype) * 0.5,
+    }
+    if S:
+        params["shared_gate"] = torch.randn(S, H, generator=g, dtype=dtype) * 0.5
+        params["shared_up"] = torch.randn(S, H, generator=g, dtype=dtype) * 0.5
+        params["shared_down"] = torch.randn(H, S, generator=g, dtype=dtype) * 0.5
+    x = torch.randn(1, n, H, generator=g, dtype=dtype)
+    ids = torch.randint(0, 50, (1, n), generator=g)
+    table = torch.from_numpy(O.multi_hash_table(50, E, k, 0))
+    dout = torch.randn(1, n, H, generator=g, dtype=dtype)
+    return x, ids, table, params, dout
+
+
+@pytest.mark.parametrize("S,active", [(5, None), (0, None), (5, (2, 3))])
+def test_engine_backward_matches_central_differences(S, active):
+    """Directional derivatives of <engine_forward, dout> by central differences
+    in f64 pin every gradient engine_backward returns (names, shapes, scales)."""
+    x, ids, table, params, dout = _tiny_layer(7, S=S)
+    kw = dict(route_weights=(0.7, 0.3), shared_scale=1.5, routed_scale=2.0)
+    if active:
+        kw.update(active_experts=active[0], active_width=active[1])
+        table = torch.from_numpy(O.multi_hash_table(50, active[0], 2, 0))
+    grads = O.engine_backward(x, ids, table, params, dout, **kw)
+
+    def loss(xx, pp):
+        return float((O.engine_forward(xx, ids, table, pp, **kw) * dout).sum())
+
+    g = torch.Generator().manual_seed(11)
+    eps = 1e-6
+    for name in ["x", *params]:
+        base = x if name == "x" else params[name]
+        for _ in range(3):
+            v = torch.randn(base.shape, generator=g, dtype=base.dtype)
+            plus = {**params}
+            minus = {**params}
+            if name == "x":
+                lp, lm = loss(x + eps * v, params), loss(x - eps * v, params)
+            else:
+                plus[name], minus[name] = base + eps * v, base - eps * v
+                lp, lm = loss(x, plus), loss(x, minus)
+            fd = (lp - lm) / (2 * eps)
+            an = float((grads[name] * v).sum())
+            assert abs(fd - an) <= 1e-6 * max(1.0, abs(fd)), (name, fd, an)
+    if active:
+        E, W = active
+        assert grads["expert_gate"][E:].abs().max() == 0 and grads["expert_gate"][:, :, W:].abs().max() == 0
+        assert grads["expert_down"][E:].abs().max() == 0 and grads["expert_down"][:, W:].abs().max() == 0
+
+
+def test_swiglu_backward_closed_form_matches_autograd():
+    g = torch.Generator().manual_seed(5)
+    R, H, F_ = 9, 6, 7
+    x = torch.randn(R, H, generator=g, dtype=torch.float64)
+    dout = torch.randn(R, H, generator=g, dtype=torch.float64)
+    wg = torch.randn(F_, H, generator=g, dtype=torch.float64, requires_grad=True)
+    wu = torch.randn(F_, H, generator=g, dtype=torch.float64)
+    wd = torch.randn(H, F_, generator=g, dtype=torch.float64)
+    mult = torch.rand(R, F_, generator=g, dtype=torch.float64)
+    gate = (x @ wg.T).detach().requires_grad_(True)
+    up = (x @ wu.T).detach().requires_grad_(True)
+    h = mult * torch.nn.functional.silu(gate) * up
+    y = h @ wd.T
+    dg_ref, du_ref = torch.autograd.grad(y, [gate, up], grad_outputs=dout)
+    dg, du, hm = O.swiglu_backward(x, dout, wg.detach(), wu, wd, mult)
+    torch.testing.assert_close(dg, dg_ref, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(du, du_ref, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(hm, h.detach(), rtol=1e-12, atol=1e-12)

@@ -212,6 +212,39 @@ def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 50, warmup:
     }
 
 
+def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
+    """Forward + backward through autograd on the HIP backend (the layer's
+    gradients of x and every weight), timed with HIP events like the forward.
+    Useful backward work is twice the forward's FLOPs; the backward kernel
+    recomputes gate|up, so it executes 1.5x that."""
+    from complexity_amd.tr_hash import TRHashBackend
+
+    xg = x.detach().clone().requires_grad_(True)
+    dout = (torch.randn(x.shape, device=x.device) * 0.1).to(x.dtype)
+
+    def step():
+        out = engine(xg, ids)
+        out.backward(dout)
+
+    for _ in range(warmup):
+        step()
+    assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
+    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    gc.enable()
+    ms = start.elapsed_time(stop) / steps
+    engine.zero_grad(set_to_none=True)
+    return {"workload": w.name, "steps": steps, "ms_per_step_fwd_bwd": ms,
+            "tokens_per_s": w.tokens / (ms * 1e-3), "useful_tflops": 3 * w.flops() / (ms * 1e-3) / 1e12}
+
+
 def time_engine(torch, engine, x, ids, steps, warmup, timer):
     """K timed forwards after W warm-ups; per-kernel averages from the events."""
     from complexity_amd.tr_hash import TRHashBackend
@@ -297,6 +330,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip timing the second routed strategy")
+    ap.add_argument("--no-train", action="store_true", help="skip the forward+backward (autograd) timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="end with three elementwise copies of MIB MiB (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -362,6 +396,10 @@ def main():
         "backend": engine.last_backend.selected.value,
         "device": torch.cuda.get_device_name(0),
     }
+    if not args.no_train and w.dtype != "fp8":
+        train = train_step(torch, engine, w, x, ids)
+        train["backward_ms"] = train["ms_per_step_fwd_bwd"] - ms_per_step
+        result["train"] = train
     if not args.no_decode:
         result["decode"] = decode_hbm(torch, workloads, dev)
     if not args.no_cpu:

@@ -23,6 +23,8 @@
 #include "trmoe_gemm.h"
 #include "trmoe_tiles.h"
 
+#include <stdlib.h>
+
 #include <type_traits>
 
 namespace trmoe {
@@ -142,6 +144,110 @@ struct BufRowsT {
         for (int j = 0; j < kChunks; ++j) commit_one(stage, reg, j);
     }
 };
+
+// bf16 operand with K as rows, loaded straight into LDS: a K stage is 64
+// rows of COLS = 256 columns (512 bytes), 16-byte chunk c of row k stored at
+// chunk c ^ ((k & 3) << 2), so that the transposing fragment reads below hit
+// 64 distinct banks.  One wave instruction fills two rows.
+template <int NT, bool GATHER>
+struct DmaRowsT {
+    static constexpr int kRowB = 512;
+    static constexpr int kInstr = 64 * kRowB / 1024 / (NT / 64);   // per wave per stage
+    static_assert(kInstr >= 1 && kInstr % 2 == 0, "whole row pairs per wave");
+    __amdgpu_buffer_rsrc_t rsrc;
+    int coloff[2];   // lane's source column bytes for rows with (row & 2) == 0 / 2, kOutOfRange past M
+    int h;           // row of the pair this lane fills
+    int wave;
+    int base, len, ld;
+    const int* table;
+
+    __device__ __forceinline__ void init(const void* base_ptr, int64_t rows_total, int64_t ld_bytes, int64_t col0,
+                                         int64_t ncols) {
+        rsrc = make_rsrc(base_ptr, (uint32_t)(rows_total * ld_bytes));
+        const int lane = threadIdx.x & 63;
+        wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        h = lane >> 5;
+        const int pc = lane & 31;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int c = pc ^ ((2 * p + h) << 2);
+            const int64_t col = col0 + 8 * c;
+            coloff[p] = col < ncols ? (int)(col * 2) : kOutOfRange;
+        }
+        ld = (int)ld_bytes;
+        base = 0;
+        len = 0;
+        table = nullptr;
+    }
+    __device__ __forceinline__ void segment(int64_t t0, int n, const int* tab) {
+        base = (int)(t0 * (int64_t)ld);
+        len = n;
+        table = tab;
+    }
+    __device__ __forceinline__ void issue(int kt, char* stage) const {
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int q = wave * kInstr + j;          // row pair of the stage
+            const int lk = kt * 64 + 2 * q + h;
+            int ro;
+            if constexpr (GATHER)
+                ro = table[lk];
+            else
+                ro = lk < len ? base + lk * ld : kOutOfRange;
+            const int co = coloff[j & 1];             // (row & 3) = 2 (j & 1) + h
+            const int o = (ro < 0 || co < 0) ? kOutOfRange : ro + co;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(stage + q * 1024), 16, o, 0, 0, 0);
+        }
+    }
+};
+
+typedef short trmoe_v4s __attribute__((ext_vector_type(4)));
+
+// 8 bytes of a transposing LDS read: lane i of each 16-lane group receives
+// element i of the 4 rows addressed by lanes 4j + i/4 (j = 0..3).
+__device__ __forceinline__ u32x2 ds_read_tr16(const char* p) {
+    const trmoe_v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) trmoe_v4s*)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// One 64-K stage of MFMAs from two DmaRowsT stages ([k][256] each).  For
+// K group g, lane l needs K values 16g + 8(l/32) + 0..7 of column l % 32 of
+// each 32-column block: two transposing reads whose 16 source lanes address
+// rows +((l & 15) >> 2) and 8-byte column blocks (l & 3).
+template <int TM, int TN>
+__device__ __forceinline__ void mma_stage_tr(const char* As, const char* Bs, int wm0, int wn0,
+                                             f32x16 (&acc)[TM][TN]) {
+    const int lane = threadIdx.x & 63;
+    const int j = (lane & 15) >> 2;
+    const int h = lane >> 5;
+    const int cw = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    const int wb = 8 * (lane & 1);
+    const int swz = j << 2;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        u32x4 a[TM], b[TN];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int rowb = (16 * g + 8 * h + 4 * r + j) * 512;
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const u32x2 v = ds_read_tr16(As + rowb + ((((wm0 + 32 * tm) >> 3) + cw) ^ swz) * 16 + wb);
+                a[tm][2 * r] = v[0];
+                a[tm][2 * r + 1] = v[1];
+            }
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const u32x2 v = ds_read_tr16(Bs + rowb + ((((wn0 + 32 * tn) >> 3) + cw) ^ swz) * 16 + wb);
+                b[tn][2 * r] = v[0];
+                b[tn][2 * r + 1] = v[1];
+            }
+        }
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) mfma_group(KindBF16{}, a[tm], b[tn], acc[tm][tn]);
+    }
+}
 
 // ---------------------------------------------------------------------------
 // SwiGLU backward
@@ -361,6 +467,96 @@ __global__ __launch_bounds__(Shape::NT) void k_wgrad(WgradArgs a) {
         wgrad_store<Shape, false>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
 }
 
+// bf16 weight gradients with both operands loaded straight into LDS and
+// transposed at the fragment read (ds_read_b64_tr_b16); same arguments,
+// segments, splits and epilogue as k_wgrad.
+using ShapeWgradTr = TileShape<256, 256, 2, 4, 4>;   // 8 waves of 128x64
+
+template <bool GA, bool GB>
+__global__ __launch_bounds__(ShapeWgradTr::NT) void k_wgrad_tr(WgradArgs a) {
+    using Shape = ShapeWgradTr;
+    using T = bf16_t;
+    extern __shared__ __align__(16) char lds[];
+    constexpr int kTable = kWgradSeg + 128;   // the loop issues up to two stages ahead
+    __shared__ int s_ta[GA ? kTable : 1];
+    __shared__ int s_tb[GB ? kTable : 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+    const int e = (int)blockIdx.z / a.splits, sp = (int)blockIdx.z % a.splits;
+    const int64_t seg0 = a.offsets ? a.offsets[e] : 0;
+    const int64_t seg1 = a.offsets ? a.offsets[e + 1] : a.T;
+    const int64_t per = ((seg1 - seg0 + a.splits - 1) / a.splits + 63) / 64 * 64;
+    const int64_t t0 = seg0 + sp * per;
+    const int64_t t1 = t0 + per < seg1 ? t0 + per : seg1;
+
+    DmaRowsT<Shape::NT, GA> ap;
+    DmaRowsT<Shape::NT, GB> bp;
+    ap.init(a.a, a.a_rows, a.lda * 2, m0, a.M);
+    bp.init(a.b, a.b_rows, a.ldb * 2, n0, a.N);
+    constexpr int kABytes = Shape::BM * kRowBytes;   // 64 rows x 512 bytes
+    constexpr int kPer = 2 * DmaRowsT<Shape::NT, GA>::kInstr;
+
+    f32x16 acc[Shape::TM][Shape::TN];
+    zero_acc<KindBF16>(acc);
+    for (int64_t s0 = t0; s0 < t1; s0 += kWgradSeg) {
+        const int len = (int)(t1 - s0 < kWgradSeg ? t1 - s0 : kWgradSeg);
+        if constexpr (GA || GB) {
+            const uint32_t mod = (uint32_t)a.gather_mod;
+            const int lda_b = (int)(a.lda * 2), ldb_b = (int)(a.ldb * 2);
+            for (int i = threadIdx.x; i < kTable; i += Shape::NT) {
+                if constexpr (GA)
+                    s_ta[i] = i < len ? (int)((uint32_t)a.a_gather[s0 + i] % mod) * lda_b : kOutOfRange;
+                if constexpr (GB)
+                    s_tb[i] = i < len ? (int)((uint32_t)a.b_gather[s0 + i] % mod) * ldb_b : kOutOfRange;
+            }
+            __syncthreads();
+        }
+        ap.segment(s0, len, s_ta);
+        bp.segment(s0, len, s_tb);
+        const int nk = (len + 63) / 64;
+        ap.issue(0, lds);
+        bp.issue(0, lds + kABytes);
+        if (nk > 1) {
+            ap.issue(1, lds + Shape::kStageBytes);
+            bp.issue(1, lds + Shape::kStageBytes + kABytes);
+        }
+        for (int kt = 0; kt < nk; ++kt) {
+            char* st = lds + (kt & 1) * Shape::kStageBytes;
+            if (kt + 1 < nk)
+                wait_vmcnt<kPer>();
+            else
+                wait_vmcnt<0>();
+            lds_barrier();
+            mma_stage_tr<Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
+            if (kt + 2 < nk) {
+                wait_lgkmcnt0();
+                lds_barrier();
+                ap.issue(kt + 2, st);
+                bp.issue(kt + 2, st + kABytes);
+            }
+        }
+        __syncthreads();   // stages and tables free for the next segment
+    }
+
+    const bool direct = a.splits == 1;
+    const int64_t obase_el = direct ? (int64_t)e * a.out_expert_stride + m0 * a.ldo + n0
+                                    : ((int64_t)e * a.splits + sp) * a.M * a.N + m0 * a.N + n0;
+    const int ld = (int)(direct ? a.ldo : a.N);
+    const int mlim = (int)(a.M - m0 < Shape::BM ? a.M - m0 : Shape::BM);
+    const int nlim = (int)(a.N - n0 < Shape::BN ? a.N - n0 : Shape::BN);
+    void* obase = direct ? static_cast<void*>(static_cast<T*>(a.out) + obase_el)
+                         : static_cast<void*>(a.partial + obase_el);
+    const auto orsrc = make_rsrc(obase, (uint32_t)(((int64_t)(mlim - 1) * ld + nlim) * (direct ? 2 : 4)));
+    const int col = lane & 31;
+    if (direct)
+        wgrad_store<Shape, true>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
+    else
+        wgrad_store<Shape, false>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
     const int64_t mn = a.M * a.N;
@@ -413,15 +609,37 @@ int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipS
     return swiglu_bwd_kind<KindF32, false, false>(a, assignments, stream);
 }
 
-// Splits so that the launch has about two workgroups per CU, each reducing
-// at least 512 rows, at most 32 splits.
+static int bwd_device_cus() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+        return n;
+    }();
+    return cus;
+}
+
+// Split count: a workgroup holds a CU (128 KiB of LDS), so the launch runs
+// in ceil(tiles * s / CUs) rounds of rows/s rows each; every split adds an
+// fp32 partial of M*N*E values written and read back by the reduction
+// (about M*N*E * 6e-5 row-steps of a tile at the measured rates).  Picks
+// the s (at most 32, at least 256 rows per split) with the smallest sum.
 int wgrad_splits(int64_t M, int64_t N, int E, int64_t rows_per_segment) {
     const int64_t tiles = ((M + ShapeWgrad::BM - 1) / ShapeWgrad::BM) * ((N + ShapeWgrad::BN - 1) / ShapeWgrad::BN) * E;
-    int64_t s = (512 + tiles - 1) / (tiles > 0 ? tiles : 1);
-    const int64_t by_rows = rows_per_segment / 512;
-    if (s > by_rows) s = by_rows;
-    if (s > 32) s = 32;
-    return s < 1 ? 1 : (int)s;
+    const int64_t cus = bwd_device_cus();
+    const double per_split = (double)M * (double)N * (double)E * 6e-5;
+    int best = 1;
+    double best_cost = 1e300;
+    for (int s = 1; s <= 32; ++s) {
+        if (s > 1 && rows_per_segment / s < 256) break;
+        const int64_t rounds = (tiles * s + cus - 1) / cus;
+        const double cost = (double)rounds * (double)((rows_per_segment + s - 1) / s) + (s > 1 ? s * per_split : 0.0);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
 }
 
 template <class Kind, bool GA, bool GB>
@@ -441,8 +659,36 @@ static int wgrad_kind(const WgradArgs& a, hipStream_t stream) {
     return check_launch("weight_grad (reduce)");
 }
 
+template <bool GA, bool GB>
+static int wgrad_tr(const WgradArgs& a, hipStream_t stream) {
+    auto kern = k_wgrad_tr<GA, GB>;
+    constexpr int kLds = ShapeWgradTr::kLdsBytes;
+    int st = bwd_lds(kern, kLds);
+    if (st) return st;
+    const dim3 grid((unsigned)((a.M + ShapeWgradTr::BM - 1) / ShapeWgradTr::BM),
+                    (unsigned)((a.N + ShapeWgradTr::BN - 1) / ShapeWgradTr::BN), (unsigned)(a.E * a.splits));
+    hipLaunchKernelGGL(kern, grid, dim3(ShapeWgradTr::NT), kLds, stream, a);
+    st = check_launch("weight_grad");
+    if (st || a.splits == 1) return st;
+    int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_wgrad_reduce<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    return check_launch("weight_grad (reduce)");
+}
+
+// bf16: direct loads + transposing fragment reads; TRMOE_WGRAD_REG=1 keeps
+// the register-transposing kernel (the f32 path) for comparison.
+static bool wgrad_use_reg() {
+    static const bool v = getenv("TRMOE_WGRAD_REG") != nullptr;
+    return v;
+}
+
 int launch_wgrad(int act, const WgradArgs& a, hipStream_t stream) {
     const bool ga = a.a_gather != nullptr, gb = a.b_gather != nullptr;
+    if (act == TRMOE_BF16 && !wgrad_use_reg()) {
+        if (ga) return gb ? wgrad_tr<true, true>(a, stream) : wgrad_tr<true, false>(a, stream);
+        return gb ? wgrad_tr<false, true>(a, stream) : wgrad_tr<false, false>(a, stream);
+    }
     if (act == TRMOE_BF16) {
         if (ga) return gb ? wgrad_kind<KindBF16, true, true>(a, stream) : wgrad_kind<KindBF16, true, false>(a, stream);
         return gb ? wgrad_kind<KindBF16, false, true>(a, stream) : wgrad_kind<KindBF16, false, false>(a, stream);

@@ -307,3 +307,33 @@ def test_c2_bf16_layer_backward_full_size(gpu):
     _, got = _hip_grads(engine, x, ids, dout)
     ref = _oracle_grads(engine, x, ids, dout, device=gpu, dtype=torch.float32)
     _check(got, ref, "bf16")
+
+
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("n", [1, 5, 64, 129])
+def test_layer_backward_decode_sizes(gpu, strategy, n):
+    """Few tokens: the data gradient runs on the decode-shape down kernels
+    (K = 2F) and most expert segments are empty."""
+    print(f"layer backward decode sizes {strategy} n={n}", flush=True)
+    torch.manual_seed(n)
+    engine = _engine(gpu, "bf16", 4, 2, 512, 64, 256, None, strategy)
+    ids = torch.randint(0, 5000, (1, n), device=gpu)
+    x = torch.randn(1, n, 256, device=gpu, dtype=torch.bfloat16)
+    dout = torch.randn(1, n, 256, device=gpu, dtype=torch.bfloat16)
+    _, got = _hip_grads(engine, x, ids, dout)
+    _check(got, _oracle_grads(engine, x, ids, dout), "bf16")
+
+
+def test_c1_fp32_layer_backward_full_size(gpu):
+    """C1 (fp32, 2048 tokens, multi-hash, uniform ids) through autograd."""
+    from complexity_amd import workloads as Wl
+
+    print("layer backward C1 full size", flush=True)
+    w = Wl.C1
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x = Wl.make_hidden(w).to(gpu)
+    ids = Wl.make_token_ids(w).to(gpu)
+    dout = torch.randn(x.shape, device=gpu) * 0.1
+    _, got = _hip_grads(engine, x, ids, dout)
+    ref = _oracle_grads(engine, x, ids, dout, device=gpu, dtype=torch.float64)
+    _check(got, ref, "fp32")

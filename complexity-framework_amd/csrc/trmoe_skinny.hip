@@ -323,13 +323,12 @@ int gate_up_skinny_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t st
     return gate_up_skinny_mt<Kind, FP8, 8, 4, 2>(a, packed_rows, stream);
 }
 
-// K groups (64 activation bytes) per split.  Up to 16 tokens one split (the
-// whole K per workgroup, 16-column tiles, no reduction launch) measured
-// fastest; above, enough groups that the fp32 partial (M x 32 x 4 bytes per
-// workgroup) stays at most a quarter of the weight bytes the workgroup
-// streams (32 rows x 64 bytes per group), and at least two per wave.
+// K groups (64 bytes of K) per split: the whole K (no reduction launch) up
+// to 8 tokens; then 32 groups (2 KiB of K: four splits at K = 3328) up to 64
+// tokens and 16 above -- the measured optimum of a sweep over 8..56 groups
+// and 16/32-column tiles at C3's shapes.  At least two groups per wave.
 int down_groups_per_split(int64_t M, int groups, int nw) {
-    int gps = M <= 16 ? groups : (int)((M + 3) / 4);
+    int gps = M <= 8 ? groups : (M <= 64 ? 32 : 16);
     if (gps < 2 * nw) gps = 2 * nw;
     const char* e = getenv("TRMOE_SKINNY_GPS");
     if (e != nullptr && atoi(e) > 0) gps = atoi(e);
@@ -356,12 +355,12 @@ int down_skinny_mt(const DownArgs& a, float* part, int gps, int splits, hipStrea
     return check_launch("shared_down_combine (skinny reduce)");
 }
 
-// Column tile: 16 columns (twice the workgroups) for up to 16 tokens, 32
-// above (half the re-reads of the activations).  TRMOE_SKINNY_NU=1/2 forces.
+// Column tile: 16 columns (twice the workgroups) up to 64 tokens, 32 above
+// (half the re-reads of the activations).  TRMOE_SKINNY_NU=1/2 forces.
 int down_nu(int64_t M) {
     const char* e = getenv("TRMOE_SKINNY_NU");
     if (e != nullptr && (atoi(e) == 1 || atoi(e) == 2)) return atoi(e);
-    return M <= 16 ? 1 : 2;
+    return M <= 64 ? 1 : 2;
 }
 
 template <class Kind, bool FP8, int NU>

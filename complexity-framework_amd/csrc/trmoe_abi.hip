@@ -4,7 +4,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "trmoe_common.h"
 #include "trmoe_gemm.h"
@@ -17,6 +20,21 @@ static thread_local std::string g_last_error;
 int set_error(int status, const char* msg) {
     g_last_error = msg ? msg : "";
     return status;
+}
+
+int set_kernel_lds(const void* kernel, int bytes) {
+    if (bytes <= 65536) return TRMOE_OK;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(kernel, dev);
+    if (done.count(key)) return TRMOE_OK;
+    hipError_t err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess) return set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
+    done.insert(key);
+    return TRMOE_OK;
 }
 
 int check_launch(const char* what) {

@@ -577,10 +577,7 @@ __global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
 // ---------------------------------------------------------------------------
 template <class F>
 static int bwd_lds(F* fn, int bytes) {
-    if (bytes <= 65536) return TRMOE_OK;
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    return err == hipSuccess ? TRMOE_OK : set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
+    return set_kernel_lds(reinterpret_cast<const void*>(fn), bytes);
 }
 
 template <class Kind, bool GROUPED, bool ROUTED>

@@ -614,11 +614,7 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
 // ---------------------------------------------------------------------------
 template <class F>
 static int ensure_lds(F* fn, int bytes) {
-    if (bytes <= 65536) return TRMOE_OK;
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (err != hipSuccess) return set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
-    return TRMOE_OK;
+    return set_kernel_lds(reinterpret_cast<const void*>(fn), bytes);
 }
 
 // Tile choice: 256x256 workgroup tiles (8 waves of 128x64) halve the L2->CU

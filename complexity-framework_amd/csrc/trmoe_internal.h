@@ -16,6 +16,9 @@ constexpr int kMaxTopK = 4;
 int set_error(int status, const char* msg);
 // After a launch: maps a pending HIP error to TRMOE_ERR_HIP.
 int check_launch(const char* what);
+// Raises a kernel's dynamic LDS limit to `bytes` (> 64 KiB) once per
+// (kernel, device): the runtime call is not repeated on every launch.
+int set_kernel_lds(const void* kernel, int bytes);
 
 int64_t route_sort_blocks(int64_t n, int k, int order);
 int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,

@@ -297,10 +297,7 @@ namespace {
 
 template <class F>
 int set_lds(F* fn, int bytes) {
-    if (bytes <= 65536) return TRMOE_OK;
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    return err == hipSuccess ? TRMOE_OK : set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
+    return set_kernel_lds(reinterpret_cast<const void*>(fn), bytes);
 }
 
 constexpr int red_bytes(int mt, int nu, int nw) { return nw * mt * nu * 4 * 64 * 4; }

@@ -520,12 +520,28 @@ class TRHashEngine(nn.Module):
             return False
         return hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())
 
+    def _shared_lora(self) -> bool:
+        return self.shared_gate is not None and (
+            getattr(self.shared_gate, "is_lora_adapter", False) or getattr(self.shared_up, "is_lora_adapter", False)
+            or getattr(self.shared_down, "is_lora_adapter", False)
+        )
+
     def _decide(self, hidden_states: torch.Tensor) -> BackendDecision:
-        return select_backend(
+        decision = select_backend(
             self.config,
             device_type=hidden_states.device.type,
             autograd=self._needs_autograd(hidden_states),
         )
+        if decision.selected is TRHashBackend.HIP and self._shared_lora():
+            # LoRA adapters on the shared linears add a low-rank residual (with
+            # its own dropout) before the SwiGLU (engine.py:337-345); the HIP
+            # kernels compute the shared branch from one weight, so the layer
+            # runs on the universal path.
+            reason = "LoRA adapters on the shared linears run on PYTORCH"
+            if decision.requested is TRHashBackend.HIP:
+                raise RuntimeError("HIP backend: " + reason)
+            decision = replace(decision, selected=TRHashBackend.PYTORCH, reasons=decision.reasons + (reason,))
+        return decision
 
     def forward(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
         decision = self._decide(hidden_states)

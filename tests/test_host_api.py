@@ -349,3 +349,36 @@ def test_mlp_adapter_exposes_dynamic_capacity_controls():
     mlp.set_active_experts(4)
     mlp.set_active_expert_width(4)
     assert (mlp.engine.active_num_experts, mlp.engine.active_expert_width) == (4, 4)
+
+
+def test_shared_lora_adapters_resolve_to_pytorch_with_reason(monkeypatch):
+    """LoRA adapters on the shared linears (reference engine.py:337-345) keep
+    the layer on the universal path; an explicit HIP request raises."""
+    import types
+
+    from complexity_amd.tr_hash import TRHashEngine
+    from complexity_amd.tr_hash import capabilities as caps
+
+    monkeypatch.setattr(caps, "_hip_available", lambda: True)
+
+    class _Adapter(torch.nn.Module):
+        is_lora_adapter = True
+
+        def __init__(self, base):
+            super().__init__()
+            self.base = base
+
+        def forward(self, x):
+            return self.base(x)
+
+    fake_cuda = types.SimpleNamespace(device=types.SimpleNamespace(type="cuda"), requires_grad=False)
+    with torch.no_grad():
+        engine = TRHashEngine(_config())
+        assert engine._decide(fake_cuda).selected is TRHashBackend.HIP
+        engine.shared_gate = _Adapter(engine.shared_gate)
+        d = engine._decide(fake_cuda)
+        assert d.selected is TRHashBackend.PYTORCH and any("LoRA" in r for r in d.reasons)
+        hip = TRHashEngine(_config(backend=TRHashBackend.HIP))
+        hip.shared_up = _Adapter(hip.shared_up)
+        with pytest.raises(RuntimeError, match="LoRA"):
+            hip._decide(fake_cuda)

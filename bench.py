@@ -150,15 +150,20 @@ def cpu_baseline(w, sample_tokens: int, reps: int = 5):
     }
 
 
-def decode_hbm(torch, workloads, dev, layers: int = 16, steps: int = 50, warmup: int = 5):
-    """C3 decode: 64 tokens through `layers` distinct weight sets per step (286 MB
-    of bf16 weights > the 256 MB Infinity Cache), per-layer time and HBM GB/s.
+def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50, warmup: int = 5,
+               per_layer_tables: bool = False):
+    """Decode: w's tokens (C3: 64; C4: 8) through `layers` distinct weight sets
+    per step (286 MB of bf16 weights > the 256 MB Infinity Cache), per-layer
+    time and HBM GB/s.  per_layer_tables: layer i routes with layer_index i
+    (C4's 16-layer model).
 
     A decode step of the stack is captured once as a HIP graph (the serving
     form of the reference's CUDA_GRAPH backend, engine.py:597-716) and
     replayed; the eager per-layer time is reported beside it."""
-    w = workloads.C3
-    engines = [workloads.build_engine(w, dev, backend="hip", seed=i) for i in range(layers)]
+    w = w or workloads.C3
+    engines = [workloads.build_engine(w, dev, backend="hip", seed=i,
+                                      **({"layer_index": i} if per_layer_tables else {}))
+               for i in range(layers)]
     x = workloads.make_hidden(w).to(dev).to(torch.bfloat16)
     ids = workloads.make_token_ids(w).to(dev)
 
@@ -408,6 +413,7 @@ def main():
         result["train"] = train
     if not args.no_decode:
         result["decode"] = decode_hbm(torch, workloads, dev)
+        result["decode_c4"] = decode_hbm(torch, workloads, dev, w=workloads.C4_DECODE, per_layer_tables=True)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(w, min(args.cpu_sample, tokens))
     if args.calibrate_copy:

@@ -3,7 +3,8 @@
 Shapes follow the benchmark configurations of this path: one TR-MoE layer at
 the 200M dimensions (hidden 896, shared SwiGLU 3072, 4 experts x 64, top-2
 multi-hash routing over a 32000 vocab) in fp32 (C1), bf16 prefill (C2) and
-bf16 decode (C3), and the scaled fp8 layer (C5).  Seeds: token ids from
+bf16 decode (C3; C4's 16-layer decode at 8 tokens), and the scaled fp8 layer
+(C5).  Seeds: token ids from
 generator ``seed``, x ~ N(0,1) from ``seed+1``, weights ~ N(0, 0.02) from
 ``seed+2`` drawn in parameter order (expert_gate, expert_up, expert_down,
 shared_gate, shared_up, shared_down), all on the CPU so every device and the
@@ -49,10 +50,13 @@ class LayerWorkload:
 C1 = LayerWorkload("c1_fp32_2048", 4, 512, dtype="fp32", ids="uniform")
 C2 = LayerWorkload("c2_bf16_prefill_16384", 8, 2048)
 C3 = LayerWorkload("c3_bf16_decode_64", 64, 1)
+# C4's MLP layers in greedy decode: 8 sequences, one token each, 16 layers
+# with route tables of layer_index 0..15 (bench.py builds one engine per layer)
+C4_DECODE = LayerWorkload("c4_bf16_decode_8", 8, 1)
 C5 = LayerWorkload("c5_fp8_32768", 16, 2048, hidden=2048, shared=5632, experts=16, width=256, dtype="fp8")
 C5_ACTIVE = replace(C5, name="c5_fp8_32768_active_8x128", active_experts=8, active_width=128)
 
-WORKLOADS = {w.name: w for w in (C1, C2, C3, C5, C5_ACTIVE)}
+WORKLOADS = {w.name: w for w in (C1, C2, C3, C4_DECODE, C5, C5_ACTIVE)}
 
 
 def zipf_ids(n: int, vocab: int, s: float, generator: torch.Generator) -> torch.Tensor:

@@ -137,6 +137,19 @@ def test_bf16_layer_full_size(gpu, name):
     assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["bf16"]
 
 
+@pytest.mark.parametrize("layer", [0, 7, 15])
+def test_c4_decode_layers(gpu, layer):
+    """C4's MLP in greedy decode: 8 tokens, the route table of layer `layer`
+    of the 16-layer model (routing.py:114 layer salt)."""
+    from complexity_amd import workloads as Wl
+
+    w = Wl.C4_DECODE
+    engine = Wl.build_engine(w, gpu, backend="hip", seed=layer, layer_index=layer)
+    x, ids = Wl.make_hidden(w, seed=layer).to(gpu).to(torch.bfloat16), Wl.make_token_ids(w, seed=layer).to(gpu)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["bf16"]
+
+
 @pytest.mark.parametrize("name", ["c5_fp8_32768", "c5_fp8_32768_active_8x128"])
 def test_fp8_layer_full_size(gpu, name):
     """Whole layer at N=32768; the oracle checks a fixed sample of 1024 rows

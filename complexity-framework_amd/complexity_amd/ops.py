@@ -42,7 +42,13 @@ def _p(t: Optional[torch.Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor):
+    """torch's current stream on t's device, as the hipStream_t handle."""
+    if _RAW_STREAM is not None:
+        return ctypes.c_void_p(_RAW_STREAM(t.device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
@@ -295,7 +301,8 @@ _DOWN_WS: dict = {}
 
 
 def _down_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = (device.index, _RAW_STREAM(device.index) if _RAW_STREAM is not None
+           else torch.cuda.current_stream(device).cuda_stream)
     ws = _DOWN_WS.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

@@ -145,6 +145,7 @@ class TRHashEngine(nn.Module):
         self._fused_shared_gate_up_weight: Optional[torch.Tensor] = None
         self._packed_key = None
         self._bwd_packed = None
+        self._decision_cache: Dict[tuple, BackendDecision] = {}
         self._packed: Optional[ops.PackedLayer] = None
         self._fp8 = False
         # HIP routed-expert strategy: "grouped" (route partition + grouped
@@ -521,16 +522,22 @@ class TRHashEngine(nn.Module):
         return hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())
 
     def _shared_lora(self) -> bool:
-        return self.shared_gate is not None and (
-            getattr(self.shared_gate, "is_lora_adapter", False) or getattr(self.shared_up, "is_lora_adapter", False)
-            or getattr(self.shared_down, "is_lora_adapter", False)
-        )
+        mods = self._modules
+        return any(getattr(mods.get(n), "is_lora_adapter", False) for n in ("shared_gate", "shared_up", "shared_down"))
 
     def _decide(self, hidden_states: torch.Tensor) -> BackendDecision:
+        # the decision depends on the frozen config, the device type, whether
+        # the call is differentiable and the shared modules; cached on those
+        mods = self._modules
+        key = (hidden_states.device.type, self._needs_autograd(hidden_states), id(self.config),
+               id(mods.get("shared_gate")), id(mods.get("shared_up")), id(mods.get("shared_down")))
+        cached = self._decision_cache.get(key)
+        if cached is not None:
+            return cached
         decision = select_backend(
             self.config,
             device_type=hidden_states.device.type,
-            autograd=self._needs_autograd(hidden_states),
+            autograd=key[1],
         )
         if decision.selected is TRHashBackend.HIP and self._shared_lora():
             # LoRA adapters on the shared linears add a low-rank residual (with
@@ -541,6 +548,9 @@ class TRHashEngine(nn.Module):
             if decision.requested is TRHashBackend.HIP:
                 raise RuntimeError("HIP backend: " + reason)
             decision = replace(decision, selected=TRHashBackend.PYTORCH, reasons=decision.reasons + (reason,))
+        if len(self._decision_cache) > 16:
+            self._decision_cache.clear()
+        self._decision_cache[key] = decision
         return decision
 
     def forward(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:

@@ -337,3 +337,14 @@ def test_c1_fp32_layer_backward_full_size(gpu):
     _, got = _hip_grads(engine, x, ids, dout)
     ref = _oracle_grads(engine, x, ids, dout, device=gpu, dtype=torch.float64)
     _check(got, ref, "fp32")
+
+
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+def test_layer_backward_out_of_range_ids(gpu, strategy):
+    torch.manual_seed(2)
+    engine = _engine(gpu, "fp32", 4, 2, 128, 64, 128, None, strategy)
+    ids = torch.randint(-30, 5030, (2, 90), device=gpu)
+    x = torch.randn(2, 90, 128, device=gpu)
+    dout = torch.randn(2, 90, 128, device=gpu)
+    _, got = _hip_grads(engine, x, ids, dout)
+    _check(got, _oracle_grads(engine, x, ids, dout), "fp32")

@@ -301,3 +301,23 @@ def test_routed_strategies_agree_with_oracle(gpu, strategy, E, k, S, W, dtype, w
     engine.set_active_capacity(num_experts=max(k, E // 2), expert_width=max(1, W // 2))
     out = _run(engine, x, ids)
     assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND[dtype]
+
+
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("n", [7, 300])
+def test_out_of_range_token_ids_are_clamped(gpu, strategy, n):
+    """engine.py:316-318 clamps ids into [0, V-1] before the gather; the
+    dense-routed kernels (tile and decode shapes) gather routes themselves."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(n)
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=128, vocab_size=1000, num_experts=4, top_k=2,
+                                             shared_width=256, expert_width=64, precision="bf16",
+                                             backend="hip")).to(gpu).to(torch.bfloat16)
+    engine.routed_strategy = strategy
+    ids = torch.randint(-50, 1050, (1, n), device=gpu)
+    x = torch.randn(1, n, 128, device=gpu, dtype=torch.bfloat16)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["bf16"]
+    clamped = _run(engine, x, ids.clamp(0, 999))
+    assert torch.equal(out, clamped)

@@ -9,6 +9,7 @@ is missing or a call fails, an exception is raised.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 from typing import Optional, Sequence, Tuple
 
@@ -565,6 +566,56 @@ def backward_packs(packed: PackedLayer, hidden: int, shared_down=None, expert_do
     return bp
 
 
+# Second stream of the backward: the weight-gradient GEMMs of the gate|up
+# weights run beside the data gradient and the down weights' gradient (they
+# only share read-only inputs), so the launches fill the CUs the others leave
+# idle.  Default priority, one per device.  TRMOE_BWD_STREAMS=0 disables it.
+_SIDE: dict = {}
+
+
+def _side_stream(device: torch.device):
+    if os.environ.get("TRMOE_BWD_STREAMS", "1") in ("0", ""):
+        return None
+    st = _SIDE.get(device.index)
+    if st is None:
+        st = torch.cuda.Stream(device=device)
+        _SIDE[device.index] = st
+    return st
+
+
+class _OnSide:
+    """Runs a block on the side stream after the current stream's work so far;
+    inputs are marked as used there, outputs as used on the current stream."""
+
+    def __init__(self, device, inputs):
+        self.side = _side_stream(device)
+        self.inputs = inputs
+        self.outputs = []
+
+    def __enter__(self):
+        if self.side is None:
+            return self
+        self.cur = torch.cuda.current_stream(self.side.device)
+        self.side.wait_stream(self.cur)
+        for t in self.inputs:
+            t.record_stream(self.side)
+        self.ctx = torch.cuda.stream(self.side)
+        self.ctx.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        if self.side is not None:
+            self.ctx.__exit__(*exc)
+
+    def join(self):
+        """Make the current stream wait for the side stream's block."""
+        if self.side is None:
+            return
+        self.cur.wait_stream(self.side)
+        for t in self.outputs:
+            t.record_stream(self.cur)
+
+
 def _gate_up_rows(g: torch.Tensor, features: int):
     """Packed gate|up rows [2F, H] -> (gate rows [F, H], up rows [F, H]) views."""
     v = g.view(features // 32, 2, 32, g.shape[-1])
@@ -590,13 +641,19 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
         F_ = packed.dense_features
         dgu, hm = dense_routed_swiglu_backward(x, dout, packed.dense_gate_up, bwd.dense_down_t, S, E, W, token_ids,
                                                route_table, route_weights, shared_scale, routed_scale)
+        # the gate|up weight gradient (side stream) overlaps dx and dWd
+        side = _OnSide(x.device, (dgu, x))
+        if need_dw:
+            with side:
+                dwgu = weight_grad(dgu, x, 2 * F_, hidden, n)[0]     # [2F, H]
+                side.outputs.append(dwgu)
         dx = None
         if need_dx:
             dx = shared_down_combine(dgu, 2 * F_, bwd.dense_gate_up_t, None, hidden, None, None, top_k,
                                      (1.0,) * top_k, 1.0, 1.0)
         if need_dw:
             dwd = weight_grad(dout, hm, hidden, F_, n)[0]            # [H, F]
-            dwgu = weight_grad(dgu, x, 2 * F_, hidden, n)[0]         # [2F, H]
+            side.join()
             g_rows, u_rows = _gate_up_rows(dwgu, F_)
             if S:
                 grads["shared_gate"], grads["shared_up"] = g_rows[:S], u_rows[:S]
@@ -614,6 +671,17 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
     dgu_s = hm_s = None
     if S > 0:
         dgu_s, hm_s = shared_swiglu_backward(x, dout, packed.shared_gate_up, bwd.shared_down_t, S, shared_scale)
+    rows = top_k * n
+    # the gate|up weight gradients (side stream) overlap dx and the down ones
+    side = _OnSide(x.device, tuple(t for t in (dgu_s, x, dgu_r, sorted_idx, offsets) if t is not None))
+    if need_dw:
+        with side:
+            if S > 0:
+                dwgu_s = weight_grad(dgu_s, x, 2 * s_pad, hidden, n)[0]          # [2S_pad, H]
+                side.outputs.append(dwgu_s)
+            dwgu_e = weight_grad(x, dgu_r, hidden, 2 * w_pad, rows, a_gather=sorted_idx, gather_mod=n,
+                                 offsets=offsets, segments=E)                     # [E, H, 2W_pad]
+            side.outputs.append(dwgu_e)
     dx = None
     if need_dx:
         dxa = grouped_linear(dgu_r, 2 * w_pad, offsets, E, bwd.expert_gate_up_t, hidden)
@@ -624,17 +692,15 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
         else:
             dx = combine(dxa, inverse, n, top_k, ones, 1.0)
     if need_dw:
-        rows = top_k * n
         if S > 0:
             dwd_s = weight_grad(dout, hm_s, hidden, s_pad, n)[0]                 # [H, S_pad]
-            dwgu_s = weight_grad(dgu_s, x, 2 * s_pad, hidden, n)[0]              # [2S_pad, H]
+        dwd_e = weight_grad(hm_r, dout, w_pad, hidden, rows, b_gather=sorted_idx, gather_mod=n, offsets=offsets,
+                            segments=E)                                           # [E, W_pad, H]
+        side.join()
+        if S > 0:
             g_rows, u_rows = _gate_up_rows(dwgu_s, s_pad)
             grads["shared_gate"], grads["shared_up"] = g_rows[:S], u_rows[:S]
             grads["shared_down"] = dwd_s[:, :S]
-        dwd_e = weight_grad(hm_r, dout, w_pad, hidden, rows, b_gather=sorted_idx, gather_mod=n, offsets=offsets,
-                            segments=E)                                           # [E, W_pad, H]
-        dwgu_e = weight_grad(x, dgu_r, hidden, 2 * w_pad, rows, a_gather=sorted_idx, gather_mod=n, offsets=offsets,
-                             segments=E)                                          # [E, H, 2W_pad]
         v = dwgu_e.view(E, hidden, w_pad // 32, 2, 32)
         grads["expert_gate"] = v[:, :, :, 0].reshape(E, hidden, w_pad)[:, :, :W]
         grads["expert_up"] = v[:, :, :, 1].reshape(E, hidden, w_pad)[:, :, :W]

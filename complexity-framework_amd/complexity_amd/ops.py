@@ -225,8 +225,10 @@ def pack_dense_routed(shared_gate, shared_up, shared_down, gate, up, down):
 
 def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: int, num_experts: int,
                          expert_width: int, token_ids: torch.Tensor, route_table: torch.Tensor,
-                         route_weights: Sequence[float], shared_scale: float, routed_scale: float) -> torch.Tensor:
-    """h_ext[N, F]: shared SwiGLU features and route-weighted expert features."""
+                         route_weights: Sequence[float], shared_scale: float, routed_scale: float,
+                         save: bool = False):
+    """h_ext[N, F]: shared SwiGLU features and route-weighted expert features.
+    save: also return the raw gate|up outputs gu[N, 2F] (packed column order)."""
     lib = _lib()
     _require_cuda(x, w_packed, token_ids, route_table)
     x = rows16(x)
@@ -237,6 +239,15 @@ def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: 
     table = route_table.contiguous()
     h = torch.empty(n, F, dtype=x.dtype, device=x.device)
     rw = _weights_arg(route_weights)
+    if save:
+        gu = torch.empty(n, 2 * F, dtype=x.dtype, device=x.device)
+        st = lib.trmoe_dense_routed_gate_up_save(dtype_code(x.dtype), _p(x), n, hidden, x.stride(0), _p(w_packed),
+                                                 shared_width, num_experts, expert_width, _p(ids), _p(table),
+                                                 table.shape[1], table.shape[0], ctypes.cast(rw, ctypes.c_void_p),
+                                                 float(shared_scale), float(routed_scale), _p(h), F, _p(gu), 2 * F,
+                                                 _stream(x))
+        N.check(st, "trmoe_dense_routed_gate_up_save")
+        return h, gu
     st = lib.trmoe_dense_routed_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
                                         x.stride(0), _p(w_packed), None, shared_width, num_experts, expert_width,
                                         _p(ids), _p(table), table.shape[1], table.shape[0],
@@ -251,14 +262,21 @@ def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: 
 # ---------------------------------------------------------------------------
 
 def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[torch.Tensor],
-                   shared_width: int) -> torch.Tensor:
-    """h[N, round_up(S,128)] = silu(x Wg^T) * (x Wu^T)."""
+                   shared_width: int, save: bool = False):
+    """h[N, round_up(S,128)] = silu(x Wg^T) * (x Wu^T).  save: also return the
+    raw gate|up outputs gu[N, 2 round_up(S,128)] (bf16/f32 weights)."""
     lib = _lib()
     _require_cuda(x, w_packed)
     x = rows16(x)
     n, hidden = x.shape
     ldh = _round_up(shared_width, 128)
     h = torch.empty(n, ldh, dtype=x.dtype, device=x.device)
+    if save:
+        gu = torch.empty(n, 2 * ldh, dtype=x.dtype, device=x.device)
+        st = lib.trmoe_shared_gate_up_save(dtype_code(x.dtype), _p(x), n, hidden, x.stride(0), _p(w_packed),
+                                           shared_width, _p(h), ldh, _p(gu), 2 * ldh, _stream(x))
+        N.check(st, "trmoe_shared_gate_up_save")
+        return h, gu
     st = lib.trmoe_shared_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
                                   x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(h), ldh,
                                   _stream(x))
@@ -389,7 +407,7 @@ class PackedLayer:
 
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
                   route_weights: Sequence[float], shared_scale: float, routed_scale: float,
-                  order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None, save: bool = False):
     """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual).
 
     grouped: K1 partition, K3 grouped experts, K2 shared gate|up, K4 down with
@@ -398,24 +416,33 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
     n, hidden = x.shape
     top_k = route_table.shape[0]
     if n == 0:
-        return torch.empty(0, hidden, dtype=x.dtype, device=x.device)
+        out = torch.empty(0, hidden, dtype=x.dtype, device=x.device)
+        return (out, None) if save else out
     x = rows16(x)
+    gu = None
     if packed.strategy == STRATEGY_DENSE:
         h = dense_routed_gate_up(x, packed.dense_gate_up, packed.shared_width, packed.num_experts,
                                  packed.expert_width, token_ids, route_table, route_weights, shared_scale,
-                                 routed_scale)
-        return shared_down_combine(h, packed.dense_features, packed.dense_down, None, hidden, None, None,
-                                   top_k, route_weights, 1.0, 1.0, residual)
+                                 routed_scale, save=save)
+        if save:
+            h, gu = h
+        out = shared_down_combine(h, packed.dense_features, packed.dense_down, None, hidden, None, None,
+                                  top_k, route_weights, 1.0, 1.0, residual)
+        return (out, gu) if save else out
     sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, packed.num_experts, order)
     y = routed_experts(x, sorted_idx, offsets, packed.num_experts, top_k, packed.expert_gate_up,
                        packed.expert_gate_up_scale, packed.expert_down, packed.expert_down_scale,
                        packed.expert_width)
     if packed.shared_width > 0:
-        h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width)
-        return shared_down_combine(h, packed.shared_width, packed.shared_down, packed.shared_down_scale,
-                                   hidden, y, inverse, top_k, route_weights, shared_scale, routed_scale,
-                                   residual)
-    return combine(y, inverse, n, top_k, route_weights, routed_scale, residual)
+        h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width, save=save)
+        if save:
+            h, gu = h
+        out = shared_down_combine(h, packed.shared_width, packed.shared_down, packed.shared_down_scale,
+                                  hidden, y, inverse, top_k, route_weights, shared_scale, routed_scale,
+                                  residual)
+    else:
+        out = combine(y, inverse, n, top_k, route_weights, routed_scale, residual)
+    return (out, gu) if save else out
 
 
 # ---------------------------------------------------------------------------
@@ -453,8 +480,9 @@ def pack_gate_up_t(gate_up_packed: torch.Tensor, hidden: int) -> torch.Tensor:
 
 
 def shared_swiglu_backward(x: torch.Tensor, dout: torch.Tensor, w_gate_up: torch.Tensor, w_down_t: torch.Tensor,
-                           shared_width: int, shared_scale: float):
-    """(dgu[N, 2F], hm[N, F]) of the shared SwiGLU, F = round_up(S, 128)."""
+                           shared_width: int, shared_scale: float, gu: Optional[torch.Tensor] = None):
+    """(dgu[N, 2F], hm[N, F]) of the shared SwiGLU, F = round_up(S, 128); gu:
+    the forward's saved gate|up outputs (None: recomputed from x)."""
     lib = _lib()
     _require_cuda(x, dout, w_gate_up, w_down_t)
     n, hidden = x.shape
@@ -463,13 +491,14 @@ def shared_swiglu_backward(x: torch.Tensor, dout: torch.Tensor, w_gate_up: torch
     hm = torch.empty(n, F_, dtype=x.dtype, device=x.device)
     st = lib.trmoe_shared_swiglu_backward(dtype_code(x.dtype), _p(x), _p(dout), n, hidden, x.stride(0),
                                           dout.stride(0), _p(w_gate_up), _p(w_down_t), shared_width,
-                                          float(shared_scale), _p(dgu), 2 * F_, _p(hm), F_, _stream(x))
+                                          float(shared_scale), _p(gu), 0 if gu is None else gu.stride(0), _p(dgu),
+                                          2 * F_, _p(hm), F_, _stream(x))
     N.check(st, "trmoe_shared_swiglu_backward")
     return dgu, hm
 
 
 def dense_routed_swiglu_backward(x, dout, w_gate_up, w_down_t, shared_width, num_experts, expert_width,
-                                 token_ids, route_table, route_weights, shared_scale, routed_scale):
+                                 token_ids, route_table, route_weights, shared_scale, routed_scale, gu=None):
     """(dgu[N, 2F], hm[N, F]) over the dense-routed features."""
     lib = _lib()
     _require_cuda(x, dout, w_gate_up, w_down_t, token_ids, route_table)
@@ -485,8 +514,9 @@ def dense_routed_swiglu_backward(x, dout, w_gate_up, w_down_t, shared_width, num
                                                 dout.stride(0), _p(w_gate_up), _p(w_down_t), shared_width,
                                                 num_experts, expert_width, _p(ids), _p(table), table.shape[1],
                                                 table.shape[0], ctypes.cast(rw, ctypes.c_void_p),
-                                                float(shared_scale), float(routed_scale), _p(dgu), 2 * F_, _p(hm),
-                                                F_, _stream(x))
+                                                float(shared_scale), float(routed_scale), _p(gu),
+                                                0 if gu is None else gu.stride(0), _p(dgu), 2 * F_, _p(hm), F_,
+                                                _stream(x))
     N.check(st, "trmoe_dense_routed_swiglu_backward")
     return dgu, hm
 
@@ -624,7 +654,8 @@ def _gate_up_rows(g: torch.Tensor, features: int):
 
 def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor,
                    packed: PackedLayer, bwd: BackwardPacks, route_weights: Sequence[float], shared_scale: float,
-                   routed_scale: float, order: int = ORDER_TOKEN, need_dx: bool = True, need_dw: bool = True):
+                   routed_scale: float, order: int = ORDER_TOKEN, need_dx: bool = True, need_dw: bool = True,
+                   saved_gu: Optional[torch.Tensor] = None):
     """Gradients of layer_forward: (dx[N, H] or None, grads) with grads a dict of
     shared_gate/shared_up [S, H], shared_down [H, S], expert_gate/expert_up
     [E, H, W], expert_down [E, W, H] (active sizes; None when not needed)."""
@@ -640,7 +671,7 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
     if packed.strategy == STRATEGY_DENSE:
         F_ = packed.dense_features
         dgu, hm = dense_routed_swiglu_backward(x, dout, packed.dense_gate_up, bwd.dense_down_t, S, E, W, token_ids,
-                                               route_table, route_weights, shared_scale, routed_scale)
+                                               route_table, route_weights, shared_scale, routed_scale, gu=saved_gu)
         # the gate|up weight gradient (side stream) overlaps dx and dWd
         side = _OnSide(x.device, (dgu, x))
         if need_dw:
@@ -670,7 +701,8 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
                                          bwd.expert_down_t, W, route_weights, routed_scale)
     dgu_s = hm_s = None
     if S > 0:
-        dgu_s, hm_s = shared_swiglu_backward(x, dout, packed.shared_gate_up, bwd.shared_down_t, S, shared_scale)
+        dgu_s, hm_s = shared_swiglu_backward(x, dout, packed.shared_gate_up, bwd.shared_down_t, S, shared_scale,
+                                             gu=saved_gu)
     rows = top_k * n
     # the gate|up weight gradients (side stream) overlap dx and the down ones
     side = _OnSide(x.device, tuple(t for t in (dgu_s, x, dgu_r, sorted_idx, offsets) if t is not None))

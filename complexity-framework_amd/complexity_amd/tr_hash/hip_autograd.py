@@ -5,8 +5,9 @@ Function per kernel (``CGGRGroupedGEMM``, ``HashCGGRGroupedGEMM``,
 ``PairHashReduce``..., complexity_cuda/triton_token_routed.py:1616-1833) and
 nn.Linear autograd for the shared branch (engine.py:333-349).  Here the whole
 layer is one Function: the forward runs the HIP kernels of
-``ops.layer_forward`` and saves only x (the gate|up activations are
-recomputed by the backward kernel); the backward runs
+``ops.layer_forward`` and saves x and, above decode token counts, the raw
+gate|up GEMM outputs (at decode sizes the backward kernel recomputes them);
+the backward runs
 ``ops.layer_backward``: the SwiGLU backward kernel, the data gradient through
 the down/combine kernels (the routed rows summed per token through the
 inverse permutation) and the token-reduction weight-gradient GEMMs.
@@ -24,6 +25,10 @@ from typing import Optional, Sequence
 import torch
 
 from .. import ops
+
+# Token counts up to which the forward runs the decode-shape kernels and the
+# backward recomputes gate|up instead of saving it.
+SAVE_MIN_TOKENS = 128
 
 _PARAM_NAMES = ("shared_gate", "shared_up", "shared_down", "expert_gate", "expert_up", "expert_down")
 
@@ -48,17 +53,25 @@ class _LayerPlan:
 class HIPLayerFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, plan: _LayerPlan, x: torch.Tensor, residual: Optional[torch.Tensor], *params):
+        # Above the decode sizes the forward also keeps the raw gate|up outputs
+        # (as the reference's autograd keeps the gate/up linear outputs), so
+        # the backward runs one GEMM where it would otherwise run three.
+        save = x.shape[0] > SAVE_MIN_TOKENS
         out = ops.layer_forward(x, plan.token_ids, plan.route_table, plan.packed, plan.route_weights,
-                                plan.shared_scale, plan.routed_scale, order=plan.order, residual=residual)
+                                plan.shared_scale, plan.routed_scale, order=plan.order, residual=residual,
+                                save=save)
+        gu = None
+        if save:
+            out, gu = out
         ctx.plan = plan
         ctx.has_residual = residual is not None
         ctx.param_shapes = [None if p is None else (p.shape, p.dtype) for p in params]
-        ctx.save_for_backward(x)
+        ctx.save_for_backward(x, gu)
         return out
 
     @staticmethod
     def backward(ctx, dout: torch.Tensor):
-        (x,) = ctx.saved_tensors
+        x, gu = ctx.saved_tensors
         plan: _LayerPlan = ctx.plan
         need_dx = ctx.needs_input_grad[1]
         need_dres = ctx.has_residual and ctx.needs_input_grad[2]
@@ -66,7 +79,7 @@ class HIPLayerFunction(torch.autograd.Function):
         need_dw = any(need_params)
         dx, grads = ops.layer_backward(dout, x, plan.token_ids, plan.route_table, plan.packed, plan.bwd_packs(),
                                        plan.route_weights, plan.shared_scale, plan.routed_scale, order=plan.order,
-                                       need_dx=need_dx, need_dw=need_dw)
+                                       need_dx=need_dx, need_dw=need_dw, saved_gu=gu)
         E, W = plan.active
         out_params = []
         for name, need, meta in zip(_PARAM_NAMES, need_params, ctx.param_shapes):

@@ -177,9 +177,9 @@ int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* 
                              workspace_bytes, as_stream(stream));
 }
 
-int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
-                         int64_t hidden, int64_t ldx, const void* w_packed, const float* w_scale,
-                         int64_t shared_width, void* h, int64_t ldh, void* stream) {
+static int shared_gate_up_impl(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                               int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                               void* h, int64_t ldh, void* gu, int64_t ldgu, void* stream) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_gate_up: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_gate_up: bad dimensions");
     TRMOE_REQUIRE(ldx >= hidden, "shared_gate_up: ldx < hidden");
@@ -211,7 +211,27 @@ int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_to
     a.vocab = 1;
     a.top_k = 0;
     for (int j = 0; j < 4; ++j) a.rw[j] = 0.f;
+    a.gu = gu;
+    a.ldgu = ldgu;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * round_up(shared_width, 128), as_stream(stream));
+}
+
+int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
+                         int64_t hidden, int64_t ldx, const void* w_packed, const float* w_scale,
+                         int64_t shared_width, void* h, int64_t ldh, void* stream) {
+    return shared_gate_up_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, w_packed, w_scale, shared_width, h,
+                               ldh, nullptr, 0, stream);
+}
+
+int trmoe_shared_gate_up_save(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                              const void* w_packed, int64_t shared_width, void* h, int64_t ldh, void* gu,
+                              int64_t ldgu, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "shared_gate_up_save: bf16 or f32 weights");
+    TRMOE_REQUIRE(n_tokens == 0 || gu != nullptr, "shared_gate_up_save: null gu");
+    TRMOE_REQUIRE(shared_width > 0 && ldgu >= 2 * round_up(shared_width, 128),
+                  "shared_gate_up_save: ldgu < 2 * round_up(shared_width, 128)");
+    return shared_gate_up_impl(act_dtype, act_dtype, x, n_tokens, hidden, ldx, w_packed, nullptr, shared_width, h,
+                               ldh, gu, ldgu, stream);
 }
 
 int64_t trmoe_dense_routed_features(int64_t shared_width, int num_experts, int64_t expert_width) {
@@ -219,12 +239,12 @@ int64_t trmoe_dense_routed_features(int64_t shared_width, int num_experts, int64
     return round_up(round_up(shared_width, 128) + num_experts * round_up(expert_width, 64), 128);
 }
 
-int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
-                               int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
-                               int num_experts, int64_t expert_width, const int64_t* token_ids,
-                               const int64_t* route_table, int64_t vocab_size, int top_k,
-                               const float* route_weights, float shared_scale, float routed_scale, void* h,
-                               int64_t ldh, void* stream) {
+static int dense_routed_gate_up_impl(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                                     int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                                     int num_experts, int64_t expert_width, const int64_t* token_ids,
+                                     const int64_t* route_table, int64_t vocab_size, int top_k,
+                                     const float* route_weights, float shared_scale, float routed_scale, void* h,
+                                     int64_t ldh, void* gu, int64_t ldgu, void* stream) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "dense_routed_gate_up: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width >= 0 && expert_width > 0,
                   "dense_routed_gate_up: bad dimensions");
@@ -262,7 +282,36 @@ int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_
     a.vocab = vocab_size;
     a.top_k = top_k;
     for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? routed_scale * route_weights[j] : 0.f;
+    a.gu = gu;
+    a.ldgu = ldgu;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * feats, as_stream(stream));
+}
+
+int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                               int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                               int num_experts, int64_t expert_width, const int64_t* token_ids,
+                               const int64_t* route_table, int64_t vocab_size, int top_k,
+                               const float* route_weights, float shared_scale, float routed_scale, void* h,
+                               int64_t ldh, void* stream) {
+    return dense_routed_gate_up_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, w_packed, w_scale, shared_width,
+                                     num_experts, expert_width, token_ids, route_table, vocab_size, top_k,
+                                     route_weights, shared_scale, routed_scale, h, ldh, nullptr, 0, stream);
+}
+
+int trmoe_dense_routed_gate_up_save(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                                    const void* w_packed, int64_t shared_width, int num_experts,
+                                    int64_t expert_width, const int64_t* token_ids, const int64_t* route_table,
+                                    int64_t vocab_size, int top_k, const float* route_weights, float shared_scale,
+                                    float routed_scale, void* h, int64_t ldh, void* gu, int64_t ldgu,
+                                    void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16,
+                  "dense_routed_gate_up_save: bf16 or f32 weights");
+    TRMOE_REQUIRE(n_tokens == 0 || gu != nullptr, "dense_routed_gate_up_save: null gu");
+    TRMOE_REQUIRE(ldgu >= 2 * trmoe_dense_routed_features(shared_width, num_experts, expert_width),
+                  "dense_routed_gate_up_save: ldgu < 2 * trmoe_dense_routed_features()");
+    return dense_routed_gate_up_impl(act_dtype, act_dtype, x, n_tokens, hidden, ldx, w_packed, nullptr,
+                                     shared_width, num_experts, expert_width, token_ids, route_table, vocab_size,
+                                     top_k, route_weights, shared_scale, routed_scale, h, ldh, gu, ldgu, stream);
 }
 
 int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
@@ -475,9 +524,10 @@ static int swiglu_bwd_common(const char* who, int act_dtype, const void* x, cons
     const int eb = elem_bytes(act_dtype);
     if (!aligned16(w_gate_up) || !aligned16(w_down_t))
         return set_error(TRMOE_ERR_INVALID, "swiglu_backward: packed weights must be 16-byte aligned");
-    if (!rows_ok(x, ldx, eb) || !rows_ok(dout, ldd, eb))
-        return set_error(TRMOE_ERR_INVALID,
-                         "swiglu_backward: x/dout rows must be 16-byte aligned with a stride that is a multiple of 16 bytes");
+    if (!rows_ok(x, ldx, eb) || !rows_ok(dout, ldd, eb) || !rows_ok(dgu, lddgu, eb) ||
+        (hm != nullptr && !rows_ok(hm, ldhm, eb)))
+        return set_error(TRMOE_ERR_INVALID, "swiglu_backward: x/dout/dgu/hm rows must be 16-byte aligned with a "
+                                            "stride that is a multiple of 16 bytes");
     if (x_rows * ldx * eb >= ((int64_t)1 << 31) || x_rows * ldd * eb >= ((int64_t)1 << 31))
         return set_error(TRMOE_ERR_UNSUPPORTED, "swiglu_backward: x and dout must be smaller than 2 GiB");
     (void)who;
@@ -506,8 +556,8 @@ static void swiglu_bwd_fill(SwigluBwdArgs& a, const void* x, const void* dout, i
 
 int trmoe_shared_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
                                  int64_t ldx, int64_t ldd, const void* w_gate_up, const void* w_down_t,
-                                 int64_t shared_width, float shared_scale, void* dgu, int64_t lddgu, void* hm,
-                                 int64_t ldhm, void* stream) {
+                                 int64_t shared_width, float shared_scale, const void* gu, int64_t ldgu, void* dgu,
+                                 int64_t lddgu, void* hm, int64_t ldhm, void* stream) {
     TRMOE_REQUIRE(n_tokens >= 0 && shared_width > 0, "shared_swiglu_backward: bad dimensions");
     if (n_tokens == 0) return TRMOE_OK;
     const int64_t F = round_up(shared_width, 128);
@@ -519,6 +569,10 @@ int trmoe_shared_swiglu_backward(int act_dtype, const void* x, const void* dout,
     a.M = n_tokens;
     a.x_rows = n_tokens;
     a.shared_mult = shared_scale;
+    TRMOE_REQUIRE(gu == nullptr || ldgu >= 2 * F, "shared_swiglu_backward: ldgu < 2 * round_up(S, 128)");
+    TRMOE_REQUIRE(gu == nullptr || rows_ok(gu, ldgu, elem_bytes(act_dtype)), "shared_swiglu_backward: gu rows must be 16-byte aligned");
+    a.gu = gu;
+    a.ldgu = ldgu;
     return launch_swiglu_bwd(act_dtype, a, 0, as_stream(stream));
 }
 
@@ -527,8 +581,8 @@ int trmoe_dense_routed_swiglu_backward(int act_dtype, const void* x, const void*
                                        const void* w_down_t, int64_t shared_width, int num_experts,
                                        int64_t expert_width, const int64_t* token_ids, const int64_t* route_table,
                                        int64_t vocab_size, int top_k, const float* route_weights,
-                                       float shared_scale, float routed_scale, void* dgu, int64_t lddgu, void* hm,
-                                       int64_t ldhm, void* stream) {
+                                       float shared_scale, float routed_scale, const void* gu, int64_t ldgu,
+                                       void* dgu, int64_t lddgu, void* hm, int64_t ldhm, void* stream) {
     const int64_t F = trmoe_dense_routed_features(shared_width, num_experts, expert_width);
     TRMOE_REQUIRE(F > 0 && n_tokens >= 0, "dense_routed_swiglu_backward: bad dimensions");
     TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "dense_routed_swiglu_backward: bad num_experts");
@@ -551,6 +605,10 @@ int trmoe_dense_routed_swiglu_backward(int act_dtype, const void* x, const void*
     a.vocab = vocab_size;
     a.top_k = top_k;
     for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? route_weights[j] * routed_scale : 0.f;
+    TRMOE_REQUIRE(gu == nullptr || ldgu >= 2 * F, "dense_routed_swiglu_backward: ldgu < 2 * features");
+    TRMOE_REQUIRE(gu == nullptr || rows_ok(gu, ldgu, elem_bytes(act_dtype)), "dense_routed_swiglu_backward: gu rows must be 16-byte aligned");
+    a.gu = gu;
+    a.ldgu = ldgu;
     return launch_swiglu_bwd(act_dtype, a, 0, as_stream(stream));
 }
 

@@ -255,7 +255,9 @@ __device__ __forceinline__ void mma_stage_tr(const char* As, const char* Bs, int
 using ShapeBwdGU = TileShape<256, 256, 2, 4, 4>;   // packed gate|up columns of 128 features
 using ShapeBwdDH = TileShape<256, 128, 2, 4, 4>;   // the same 128 features of dh
 
-template <class Kind, bool GROUPED, bool ROUTED>
+// SAVED: g|u come from a.gu (written by the forward) instead of a
+// recomputing tile loop.
+template <class Kind, bool GROUPED, bool ROUTED, bool SAVED = false>
 __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
     using T = typename Kind::T;
     using SG = ShapeBwdGU;
@@ -308,15 +310,34 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
         }
     }
 
-    f32x16 acc_gu[SG::TM][SG::TN];
-    zero_acc<Kind>(acc_gu);
-    tile_loop<Kind, SG>(ax, bgu, a.K, lds, wm0, wn0, acc_gu);
+    f32x16 acc_gu[SAVED ? 1 : SG::TM][SAVED ? 1 : SG::TN];
+    if constexpr (!SAVED) {
+        zero_acc<Kind>(acc_gu);
+        tile_loop<Kind, SG>(ax, bgu, a.K, lds, wm0, wn0, acc_gu);
+    }
     f32x16 acc_dh[SD::TM][SD::TN];
     zero_acc<Kind>(acc_dh);
     tile_loop<Kind, SD>(ad, bdt, a.K, lds, wm0, wf0, acc_dh);
+    // bf16 saved g|u: the tile's 256 rows x 256 packed columns (128 KiB)
+    // staged in LDS (free after the loop) with direct loads, as four 64-column
+    // stages, then read back in the accumulator layout
+    constexpr bool kStaged = SAVED && sizeof(T) == 2;
+    if constexpr (kStaged) {
+        typename AProvOf<SG>::type gp;
+        const int64_t cols = 2 * (a.F - f0) < 256 ? 2 * (a.F - f0) : 256;
+        gp.init(static_cast<const T*>(a.gu) + 2 * f0, m0, m_end, a.ldgu * kElem, (int)(cols * kElem));
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) gp.issue(kt, lds + kt * SG::BM * kRowBytes);
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
 
     const int64_t f = f0 + wf0 + (lane & 31);
-    if (f >= a.F) return;
+    // bf16: dg|du go through LDS (the staging layout of the saved g|u, in
+    // place) and leave as 16-byte stores; f32 stores them directly
+    constexpr bool kLdsOut = sizeof(T) == 2;
+    if (!kLdsOut && f >= a.F) return;
+    const bool fvalid = f < a.F;
     // expert blocks are multiples of 64 features: a 32-feature wave block is
     // wholly shared or one expert's
     const bool routed = ROUTED && f0 + wf0 >= a.shared_feats;
@@ -324,15 +345,37 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
     const float mult0 = routed ? 1.0f : a.shared_mult;
     T* dgu = static_cast<T*>(a.dgu);
     T* hm = static_cast<T*>(a.hm);
+    // with g|u staged (no recompute accumulators live), hm also waits in
+    // registers and leaves through LDS after dg|du
+    constexpr bool kHmLds = kStaged;
+    T hreg[kHmLds ? SG::TM : 1][kHmLds ? 16 : 1];
     const int64_t pc = 64 * (f >> 5) + (f & 31);   // packed gate column
+    const int pcl = (int)(pc - 2 * f0);             // ... within the tile
+    char* const gst = lds + (pcl >> 6) * SG::BM * kRowBytes;   // its 64-column LDS stage
+    const int cb = (pcl & 63) * 2;                              // byte within a 128-byte stage row
 #pragma unroll
     for (int tm = 0; tm < SG::TM; ++tm) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int rl = wm0 + tm * 32 + acc_row(lane, i);
             const int64_t row = m0 + rl;
-            if (row >= m_end) continue;
-            const float g = acc_gu[tm][0][i], u = acc_gu[tm][1][i], dh = acc_dh[tm][0][i];
+            const bool valid = fvalid && row < m_end;
+            if (!kLdsOut && !valid) continue;
+            float g = 0.f, u = 0.f;
+            if constexpr (kStaged) {
+                g = to_f32(*reinterpret_cast<const T*>(gst + lds_byte(rl, cb >> 4) + (cb & 15)));
+                u = to_f32(*reinterpret_cast<const T*>(gst + lds_byte(rl, (cb + 64) >> 4) + (cb & 15)));
+            } else if constexpr (SAVED) {
+                if (valid) {
+                    const T* gr = static_cast<const T*>(a.gu) + row * a.ldgu + pc;
+                    g = to_f32(gr[0]);
+                    u = to_f32(gr[32]);
+                }
+            } else {
+                g = acc_gu[tm][0][i];
+                u = acc_gu[tm][1][i];
+            }
+            const float dh = acc_dh[tm][0][i];
             float mult = mult0;
             if constexpr (ROUTED) {
                 if (routed) {
@@ -343,8 +386,10 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
                 }
             }
             if constexpr (GROUPED) {
-                const int64_t slot = (int64_t)((uint64_t)a.gather[row] / (uint64_t)a.gather_mod);
-                mult = a.rw[slot < kMaxTopK ? slot : kMaxTopK - 1];
+                if (valid) {
+                    const int64_t slot = (int64_t)((uint64_t)a.gather[row] / (uint64_t)a.gather_mod);
+                    mult = a.rw[slot < kMaxTopK ? slot : kMaxTopK - 1];
+                }
             }
             const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
             const float s = __builtin_amdgcn_rcpf(1.0f + e);   // sigmoid(g)
@@ -352,16 +397,57 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
             const float dm = dh * mult;
             const float dgv = dm * u * (s + sl * (1.0f - s));   // silu'(g) = s + g s (1 - s)
             const float duv = dm * sl;
-            dgu[row * a.lddgu + pc] = from_f32<T>(dgv);
-            dgu[row * a.lddgu + pc + 32] = from_f32<T>(duv);
-            if (hm != nullptr) {
-                // same expression order as the forward epilogue, so hm is the
-                // forward's h for the shared and dense-routed forms
-                float hv = sl * u * mult0;
-                if (ROUTED && routed) hv *= mult;
-                if (GROUPED) hv = sl * u * mult;
-                hm[row * a.ldhm + f] = from_f32<T>(hv);
+            if constexpr (kLdsOut) {
+                *reinterpret_cast<T*>(gst + lds_byte(rl, cb >> 4) + (cb & 15)) = from_f32<T>(dgv);
+                *reinterpret_cast<T*>(gst + lds_byte(rl, (cb + 64) >> 4) + (cb & 15)) = from_f32<T>(duv);
+            } else {
+                dgu[row * a.lddgu + pc] = from_f32<T>(dgv);
+                dgu[row * a.lddgu + pc + 32] = from_f32<T>(duv);
             }
+            // same expression order as the forward epilogue, so hm is the
+            // forward's h for the shared and dense-routed forms
+            float hv = sl * u * mult0;
+            if (ROUTED && routed) hv *= mult;
+            if (GROUPED) hv = sl * u * mult;
+            if constexpr (kHmLds) hreg[tm][i] = from_f32<T>(hv);
+            else if (hm != nullptr && valid) hm[row * a.ldhm + f] = from_f32<T>(hv);
+        }
+    }
+    if constexpr (kLdsOut) {
+        // copy the dg|du tile out: 256 rows x 4 stages x 8 chunks of 16 bytes
+        wait_lgkmcnt0();
+        __syncthreads();
+        const int64_t cols = 2 * (a.F - f0) < 256 ? 2 * (a.F - f0) : 256;
+        for (int q = threadIdx.x; q < SG::BM * 32; q += SG::NT) {
+            const int kt = q / (SG::BM * 8), r = (q / 8) % SG::BM, c = q % 8;
+            const int col = kt * 64 + c * 8;
+            if (m0 + r < m_end && col < cols)
+                *reinterpret_cast<u32x4*>(dgu + (m0 + r) * a.lddgu + 2 * f0 + col) =
+                    *reinterpret_cast<const u32x4*>(lds + kt * SG::BM * kRowBytes + lds_byte(r, c));
+        }
+    }
+    if constexpr (kHmLds) {
+        if (hm == nullptr) return;
+        // hm: 256 rows x 128 features as two 64-feature stages
+        __syncthreads();
+        const int fl = wf0 + (lane & 31);
+        char* const hst = lds + (fl >> 6) * SG::BM * kRowBytes;
+        const int hb = (fl & 63) * 2;
+#pragma unroll
+        for (int tm = 0; tm < SG::TM; ++tm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                *reinterpret_cast<T*>(hst + lds_byte(wm0 + tm * 32 + acc_row(lane, i), hb >> 4) + (hb & 15)) =
+                    hreg[tm][i];
+        wait_lgkmcnt0();
+        __syncthreads();
+        const int64_t hcols = a.F - f0 < SD::BN ? a.F - f0 : SD::BN;
+        for (int q = threadIdx.x; q < SG::BM * 16; q += SG::NT) {
+            const int kt = q / (SG::BM * 8), r = (q / 8) % SG::BM, c = q % 8;
+            const int col = kt * 64 + c * 8;
+            if (m0 + r < m_end && col < hcols)
+                *reinterpret_cast<u32x4*>(hm + (m0 + r) * a.ldhm + f0 + col) =
+                    *reinterpret_cast<const u32x4*>(lds + kt * SG::BM * kRowBytes + lds_byte(r, c));
         }
     }
 }
@@ -580,9 +666,9 @@ static int bwd_lds(F* fn, int bytes) {
     return set_kernel_lds(reinterpret_cast<const void*>(fn), bytes);
 }
 
-template <class Kind, bool GROUPED, bool ROUTED>
+template <class Kind, bool GROUPED, bool ROUTED, bool SAVED = false>
 static int swiglu_bwd_kind(const SwigluBwdArgs& a, int64_t assignments, hipStream_t stream) {
-    auto kern = k_swiglu_bwd<Kind, GROUPED, ROUTED>;
+    auto kern = k_swiglu_bwd<Kind, GROUPED, ROUTED, SAVED>;
     constexpr int kLds = ShapeBwdGU::kLdsBytes;
     int st = bwd_lds(kern, kLds);
     if (st) return st;
@@ -596,6 +682,15 @@ static int swiglu_bwd_kind(const SwigluBwdArgs& a, int64_t assignments, hipStrea
 
 int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipStream_t stream) {
     const bool grouped = a.offsets != nullptr, routed = a.ids != nullptr;
+    if (a.gu != nullptr) {
+        // saved pre-activations (shared and dense-routed forms)
+        if (grouped) return set_error(TRMOE_ERR_UNSUPPORTED, "swiglu_backward: saved gate|up for grouped rows");
+        if (act == TRMOE_BF16)
+            return routed ? swiglu_bwd_kind<KindBF16, false, true, true>(a, assignments, stream)
+                          : swiglu_bwd_kind<KindBF16, false, false, true>(a, assignments, stream);
+        return routed ? swiglu_bwd_kind<KindF32, false, true, true>(a, assignments, stream)
+                      : swiglu_bwd_kind<KindF32, false, false, true>(a, assignments, stream);
+    }
     if (act == TRMOE_BF16) {
         if (grouped) return swiglu_bwd_kind<KindBF16, true, false>(a, assignments, stream);
         if (routed) return swiglu_bwd_kind<KindBF16, false, true>(a, assignments, stream);

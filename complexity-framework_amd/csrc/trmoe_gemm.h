@@ -47,6 +47,11 @@ struct GateUpArgs {
     int top_k;
     float rw[4];            // per-slot route weight times the routed scale
     int64_t n_base;         // first packed row of blockIdx.y == 0 (tail launches)
+    // Saved pre-activations for the backward (null: not written): gu[row,
+    // packed column] = the raw gate / up GEMM outputs (times the e4m3 scale),
+    // in the packed column order of the weights.
+    void* gu;
+    int64_t ldgu;
     // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
     // (expert, row tile) pairs of a K1 partition; A rows are
     // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
@@ -156,6 +161,8 @@ struct SwigluBwdArgs {
     int64_t ldwgu;
     const void* wdt;         // W_down^T rows [F, K]
     int64_t ldwdt;
+    const void* gu;          // saved gate|up pre-activations [M, 2F] (null: recomputed from x)
+    int64_t ldgu;
     int64_t F;               // features (per expert when grouped)
     void* dgu;
     int64_t lddgu;

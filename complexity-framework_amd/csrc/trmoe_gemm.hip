@@ -166,10 +166,48 @@ __device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&a
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
+// Raw gate|up accumulators to a.gu (the pre-activations the backward reads
+// instead of recomputing them), from the accumulator layout with buffer
+// stores: cells past the rows or columns get offsets with bit 31 set, past
+// any range, and are dropped.
+template <class Kind, class Shape>
+__device__ __forceinline__ void gate_up_save(const GateUpArgs& a, const f32x16 (&acc)[Shape::TM][Shape::TN],
+                                             int64_t m0, int64_t n0, int64_t packed_rows) {
+    using T = typename Kind::T;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
+    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
+    const int mlim = (int)(a.M - m0 < Shape::BM ? a.M - m0 : Shape::BM);
+    const int nlim = (int)(packed_rows - n0 < Shape::BN ? packed_rows - n0 : Shape::BN);
+    if (mlim <= 0 || nlim <= 0) return;
+    const int ld = (int)a.ldgu;
+    const auto rsrc = make_rsrc(static_cast<T*>(a.gu) + m0 * a.ldgu + n0,
+                                (uint32_t)(((int64_t)(mlim - 1) * ld + nlim) * (int64_t)sizeof(T)));
+#pragma unroll
+    for (int tn = 0; tn < Shape::TN; ++tn) {
+        const int c = wn0 + tn * 32 + (lane & 31);
+        const float sc = a.w_scale ? a.w_scale[n0 + c] : 1.0f;
+#pragma unroll
+        for (int tm = 0; tm < Shape::TM; ++tm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = wm0 + tm * 32 + acc_row(lane, i);
+                const int off = ((r * ld + c) * (int)sizeof(T)) | ((r < mlim && c < nlim) ? 0 : kOutOfRange);
+                const float v = acc[tm][tn][i] * sc;
+                if constexpr (sizeof(T) == 2)
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), rsrc, off, 0,
+                                                          0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rsrc, off, 0, 0);
+            }
+    }
+}
+
 // ROUTED: the tile may hold dense-routed expert features (route gather and
 // per-token expert weights compiled in); the shared-feature launches leave
-// that code out.
-template <class Kind, bool FP8, class Shape, bool GROUPED = false, bool ROUTED = false>
+// that code out.  SAVE: also write the raw gate|up outputs to a.gu (training
+// forwards), passed the launch's packed row count as gridDim-independent bound.
+template <class Kind, bool FP8, class Shape, bool GROUPED = false, bool ROUTED = false, bool SAVE = false>
 __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     using T = typename Kind::T;
     extern __shared__ __align__(16) char lds[];
@@ -208,6 +246,7 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     f32x16 acc[Shape::TM][Shape::TN];
     zero_acc<Kind>(acc);
     tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
+    if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * Shape::BN);
     gate_up_epilogue<Kind, Shape, ROUTED>(a, acc, m0, n0, lds, s_route);
 }
 
@@ -808,7 +847,55 @@ static int launch_gate_up_routed_cols(const GateUpArgs& a, int64_t packed_rows, 
         a, packed_rows, stream);
 }
 
+// Training forwards (a.gu set): the direct-load tiles with the raw gate|up
+// store, 256x256 where the packed rows allow it, else 256x128 (2 W rows of
+// 64-feature blocks always do); dense-routed expert columns with the routing
+// epilogue.  Every M takes the tile kernels (the decode-shape kernels have
+// no save).
+template <class Kind, class Shape, bool ROUTED>
+static int launch_gate_up_save_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    dim3 grid((unsigned)((a.M + Shape::BM - 1) / Shape::BM), (unsigned)((packed_rows - a.n_base) / Shape::BN));
+    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
+    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
+    auto kern = k_gate_up_swiglu<Kind, false, Shape, false, ROUTED, true>;
+    int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    if (grid.x == 0 || grid.y == 0) return TRMOE_OK;
+    hipLaunchKernelGGL(kern, grid, dim3(Shape::NT), kLds, stream, a);
+    return check_launch("gate_up (saving pre-activations)");
+}
+
+template <class Kind, bool ROUTED>
+static int launch_gate_up_save_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if ((packed_rows - a.n_base) % 256 == 0) return launch_gate_up_save_shape<Kind, ShapeBigDma, ROUTED>(a, packed_rows, stream);
+    return launch_gate_up_save_shape<Kind, ShapeGroupNarrowDma, ROUTED>(a, packed_rows, stream);
+}
+
+static int launch_gate_up_save(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if (act != wdt || (act != TRMOE_BF16 && act != TRMOE_F32))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "gate_up: saving pre-activations needs bf16/f32 weights");
+    if (packed_rows % 128 != 0) return set_error(TRMOE_ERR_INVALID, "gate_up: packed rows not a multiple of 128");
+    const bool bf = act == TRMOE_BF16;
+    if (a.ids != nullptr) {
+        const int64_t shared_rows = 2 * a.shared_feats;
+        if (shared_rows > 0) {
+            GateUpArgs sh = a;
+            sh.ids = nullptr;
+            const int st = bf ? launch_gate_up_save_kind<KindBF16, false>(sh, shared_rows, stream)
+                              : launch_gate_up_save_kind<KindF32, false>(sh, shared_rows, stream);
+            if (st) return st;
+        }
+        GateUpArgs ex = a;
+        ex.n_base = shared_rows;
+        return bf ? launch_gate_up_save_kind<KindBF16, true>(ex, packed_rows, stream)
+                  : launch_gate_up_save_kind<KindF32, true>(ex, packed_rows, stream);
+    }
+    return bf ? launch_gate_up_save_kind<KindBF16, false>(a, packed_rows, stream)
+              : launch_gate_up_save_kind<KindF32, false>(a, packed_rows, stream);
+}
+
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if (a.gu != nullptr) return launch_gate_up_save(act, wdt, a, packed_rows, stream);
     if (a.M <= kSkinnyMaxTokens && tile_override() == kTileAuto && packed_rows % 64 == 0)
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
     if (a.ids != nullptr) {

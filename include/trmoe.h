@@ -255,15 +255,21 @@ int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y
  * ------------------------------------------------------------------------- */
 
 /*
- * SwiGLU backward.  For every row r and feature f (gate|up recomputed from
- * x, not saved by the forward):
+ * SwiGLU backward.  For every row r and feature f (gate|up either saved by
+ * the forward, see gu below, or recomputed from x):
  *     g, u = x_r . Wg_f, x_r . Wu_f          w_gate_up: the forward's GATE_UP pack
  *     dh   = dout_r . Wd[:, f]               w_down_t: W_down^T, PLAIN-packed [F, hidden]
  *     dgu[r, 64*(f/32) + f%32]      = dh * m * u * silu'(g)
  *     dgu[r, 64*(f/32) + 32 + f%32] = dh * m * silu(g)
  *     hm[r, f]                      = m * silu(g) * u      (hm may be NULL)
  * so dgu is the gradient of the gate|up GEMM output in the packed column
- * order and hm the forward's (scaled) SwiGLU output.  dgu/hm are act_dtype.
+ * order and hm the forward's (scaled) SwiGLU output.  dgu/hm are act_dtype;
+ * their rows (and gu's) are 16-byte aligned with a stride that is a multiple
+ * of 16 bytes, like the activation rows.
+ *
+ * gu (shared and dense-routed forms; NULL = recompute g|u from x): the raw
+ * gate|up outputs the *_gate_up_save forward wrote, [n, ldgu] in the packed
+ * column order; the backward then runs one GEMM (dh) instead of three.
  *
  * shared:        rows = tokens, F = round_up(shared_width, 128), m = shared_scale;
  *                w_down_t from shared_down.weight [hidden, S] (out = S rows)
@@ -279,21 +285,39 @@ int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y
  */
 int trmoe_shared_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
                                  int64_t ldx, int64_t ldd, const void* w_gate_up, const void* w_down_t,
-                                 int64_t shared_width, float shared_scale, void* dgu, int64_t lddgu, void* hm,
-                                 int64_t ldhm, void* stream);
+                                 int64_t shared_width, float shared_scale, const void* gu, int64_t ldgu, void* dgu,
+                                 int64_t lddgu, void* hm, int64_t ldhm, void* stream);
 int trmoe_dense_routed_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens,
                                        int64_t hidden, int64_t ldx, int64_t ldd, const void* w_gate_up,
                                        const void* w_down_t, int64_t shared_width, int num_experts,
                                        int64_t expert_width, const int64_t* token_ids, const int64_t* route_table,
                                        int64_t vocab_size, int top_k, const float* route_weights,
-                                       float shared_scale, float routed_scale, void* dgu, int64_t lddgu, void* hm,
-                                       int64_t ldhm, void* stream);
+                                       float shared_scale, float routed_scale, const void* gu, int64_t ldgu,
+                                       void* dgu, int64_t lddgu, void* hm, int64_t ldhm, void* stream);
 int trmoe_routed_swiglu_backward(int act_dtype, const void* x, const void* dout, int64_t n_tokens, int64_t hidden,
                                  int64_t ldx, int64_t ldd, const int64_t* sorted_indices,
                                  const int32_t* expert_offsets, int num_experts, int top_k, const void* w_gate_up,
                                  const void* w_down_t, int64_t expert_width, const float* route_weights,
                                  float routed_scale, void* dgu, int64_t lddgu, void* hm, int64_t ldhm,
                                  void* stream);
+
+/*
+ * Training forwards: trmoe_shared_gate_up / trmoe_dense_routed_gate_up with
+ * bf16/f32 weights that also write the raw gate|up GEMM outputs (the
+ * pre-activations) to gu [n, ldgu] in the packed column order, ldgu >= twice
+ * the feature count; the backward reads them instead of recomputing (the
+ * reference's autograd saves the same tensors: the gate and up nn.Linear
+ * outputs, engine.py:333-349).  Any n takes the tile kernels.
+ */
+int trmoe_shared_gate_up_save(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                              const void* w_packed, int64_t shared_width, void* h, int64_t ldh, void* gu,
+                              int64_t ldgu, void* stream);
+int trmoe_dense_routed_gate_up_save(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                                    const void* w_packed, int64_t shared_width, int num_experts,
+                                    int64_t expert_width, const int64_t* token_ids, const int64_t* route_table,
+                                    int64_t vocab_size, int top_k, const float* route_weights, float shared_scale,
+                                    float routed_scale, void* h, int64_t ldh, void* gu, int64_t ldgu,
+                                    void* stream);
 
 /*
  * Weight gradients as token-reduction GEMMs; replaces cggr_grad_w /

@@ -133,6 +133,19 @@ def test_shared_swiglu_backward(gpu, dtype, n, H, S):
     assert _err(hm[:, :S], rh) <= BOUND[dtype]
     if F > S:   # padded features: zero weights give zero gradients
         assert dg[:, S:].abs().max().item() == 0 and hm[:, S:].abs().max().item() == 0
+    # the training forward's saved gate|up outputs instead of the recomputation
+    hs, gus = ops.shared_gate_up(x.to(gpu), gu, None, S, save=True)
+    h_plain = ops.shared_gate_up(x.to(gpu), gu, None, S)
+    dgu2, hm2 = ops.shared_swiglu_backward(x.to(gpu), dout.to(gpu), gu, wdt, S, 1.5, gu=gus)
+    torch.cuda.synchronize()
+    assert _err(hs, h_plain) <= BOUND[dtype]   # other tiles, same h to rounding
+    g_ref = (x.double() @ wg.double().T, x.double() @ wu.double().T)
+    sg, su = _split_dgu(gus, F)
+    assert _err(sg[:, :S], g_ref[0]) <= BOUND[dtype] and _err(su[:, :S], g_ref[1]) <= BOUND[dtype]
+    dg2, du2 = _split_dgu(dgu2, F)
+    assert _err(dg2[:, :S], rdg) <= BOUND[dtype]
+    assert _err(du2[:, :S], rdu) <= BOUND[dtype]
+    assert _err(hm2[:, :S], rh) <= BOUND[dtype]
 
 
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])

@@ -6,12 +6,12 @@
 // CUs allow and to touch each weight byte once:
 //
 //   k_gate_up_skinny   one workgroup per 16 output features (16 gate + 16 up
-//                      packed rows) and all M tokens; the waves split K, each
-//                      loading its operands straight into 16x16 MFMA
-//                      registers (no LDS staging), and reduce through LDS
-//                      before the SwiGLU epilogue (same epilogue contract as
+//                      packed rows) and all M tokens; the waves split K, copy
+//                      their K spans of the operands into LDS with direct
+//                      loads (staged_k_loop), and reduce through LDS before
+//                      the SwiGLU epilogue (same epilogue contract as
 //                      k_gate_up_swiglu, including the dense-routed scaling)
-//   k_down_skinny      split-K: workgroup (32 output columns, K chunk)
+//   k_down_skinny      split-K: workgroup (16 or 32 output columns, K chunk)
 //                      writes an fp32 partial [split][M][N] to the caller's
 //                      workspace
 //   k_down_reduce      sums the partials in split order (deterministic),
@@ -22,6 +22,8 @@
 #include "trmoe_gemm.h"
 
 #include <stdlib.h>
+
+#include <algorithm>
 
 namespace trmoe {
 
@@ -63,40 +65,106 @@ struct WFrag<Kind, true> {
     static __device__ __forceinline__ u32x4 expand(Reg v) { return fp8x8_to_bf16x8(v); }
 };
 
-// acc[tm][u] += A(rows tm*16..+15) . W(rows u*16..+15)^T over the K groups
-// [g0, g1) of this wave, loading GB groups at a time.  a_off[tm] / w_off[u]
-// are the byte offsets of the lane's row in each operand (kOutOfRange for
-// absent rows); kb_a is the byte length of K in an activation row.
-template <class Kind, bool FP8, int MT, int NU, int GB>
-__device__ __forceinline__ void skinny_k_loop(__amdgpu_buffer_rsrc_t ar, const int (&a_off)[MT],
-                                              __amdgpu_buffer_rsrc_t wr, const int (&w_off)[NU], int g0, int g1,
-                                              int kb_a, f32x4 (&acc)[MT][NU]) {
+// One direct buffer -> LDS load of 16 bytes per lane (lane l's bytes land at
+// lds + 16 l).  A plain function: the host pass of hipcc rejects a second
+// use of a function template specialization that calls the builtin itself.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, TRMOE_LDS_PTR(lds), 16, off, 0, 0, 0);
+}
+
+// The K loop of the decode kernels, operands staged through LDS.  The
+// accumulators are 16x16x32 MFMA tiles: acc[tm][u] += A(rows tm*16..+15) .
+// W(rows of block u)^T.  A 16x16x32 operand load straight into registers
+// takes 16 rows x 64 bytes, so each instruction touches 16 cache lines
+// in every 16-lane quarter, and that -- not bytes -- is what limits the
+// loop (the activations are read by every workgroup).  Here each wave
+// copies its own K spans (128 bytes) of all MT*16 activation rows, and with
+// SW also of its 16*NU weight rows, into its LDS region with direct loads
+// (8 rows x 128 bytes per instruction, lds_byte() layout) and reads the MFMA
+// fragments back from LDS; without SW the weight fragments come straight
+// into registers (16 rows x 64 bytes per instruction).  Weight block u is the 16 rows from
+// row w_row0[u] of the weight descriptor (whose byte offsets, with SW off,
+// are w_off[u] for the lane's row).  Spans [s0, s1) in batches of SB;
+// `region` holds SB * (MT + (SW ? NU : 0)) * 16 rows of 128 bytes.
+template <class Kind, bool FP8, int MT, int NU, int SB, bool SW>
+__device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_rows, int lda_b, char* region,
+                                              __amdgpu_buffer_rsrc_t wr, const int (&w_row0)[NU], int ldw_b,
+                                              const int (&w_off)[NU], int s0, int s1, int kb_a,
+                                              f32x4 (&acc)[MT][NU]) {
+    static_assert(!(SW && FP8), "e4m3 weight rows are 64 bytes per span: not staged");
     using WF = WFrag<Kind, FP8>;
-    const int q = (threadIdx.x & 63) >> 4;
-    for (int gb = g0; gb < g1; gb += GB) {
-        u32x4 av[GB][MT];
-        typename WF::Reg wv[GB][NU];
+    constexpr int kRowsA = MT * 16;
+    constexpr int kRows = kRowsA + (SW ? NU * 16 : 0);
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 4;
+    int xo[MT * 2];   // the lane's row offset + chunk for each 8-row copy instruction
 #pragma unroll
-        for (int j = 0; j < GB; ++j) {
-            const int g = gb + j;
-            const bool ok = g < g1;
-            const int ao = 64 * g + 16 * q;
+    for (int j = 0; j < MT * 2; ++j) {
+        const int row = j * 8 + (lane >> 3);
+        xo[j] = row < a_rows ? row * lda_b + 16 * ((lane & 7) ^ lds_swz(row)) : kOutOfRange;
+    }
+    int wo[SW ? NU * 2 : 1];
+    if constexpr (SW) {
 #pragma unroll
-            for (int tm = 0; tm < MT; ++tm)
-                av[j][tm] = buffer_load16(ar, (ok && ao < kb_a) ? a_off[tm] + ao : kOutOfRange);
+        for (int j = 0; j < NU * 2; ++j)
+            wo[j] = (w_row0[j >> 1] + (j & 1) * 8 + (lane >> 3)) * ldw_b +
+                    16 * ((lane & 7) ^ lds_swz(kRowsA + j * 8 + (lane >> 3)));
+    }
+    for (int sb = s0; sb < s1; sb += SB) {
+        typename WF::Reg wv[SW ? 1 : SB][2][NU];
 #pragma unroll
-            for (int u = 0; u < NU; ++u) wv[j][u] = WF::load(wr, ok ? w_off[u] : kOutOfRange, g, q, kb_a);
-        }
-        // every load of the batch is in flight before the first MFMA waits
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < SB; ++j) {
+            const int sp = sb + j;
+            if (sp < s1) {
+                char* st = region + j * kRows * kRowBytes;
 #pragma unroll
-        for (int j = 0; j < GB; ++j)
+                for (int i = 0; i < MT * 2; ++i) {
+                    const int o = 128 * sp + 16 * ((lane & 7) ^ lds_swz(i * 8 + (lane >> 3)));
+                    dma16(ar, st + i * 8 * kRowBytes, o < kb_a ? xo[i] + 128 * sp : kOutOfRange);
+                }
+                if constexpr (SW) {
 #pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const u32x4 b = WF::expand(wv[j][u]);
+                    for (int i = 0; i < NU * 2; ++i) {
+                        const int o = 128 * sp + 16 * ((lane & 7) ^ lds_swz(kRowsA + i * 8 + (lane >> 3)));
+                        dma16(wr, st + (kRowsA + i * 8) * kRowBytes, o < kb_a ? wo[i] + 128 * sp : kOutOfRange);
+                    }
+                } else {
 #pragma unroll
-                for (int tm = 0; tm < MT; ++tm) mfma16(Kind{}, av[j][tm], b, acc[tm][u]);
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int u = 0; u < NU; ++u) wv[j][h][u] = WF::load(wr, w_off[u], 2 * sp + h, q, kb_a);
+                }
             }
+        }
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            if (sb + j < s1) {
+                const char* st = region + j * kRows * kRowBytes;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    u32x4 av[MT];
+#pragma unroll
+                    for (int tm = 0; tm < MT; ++tm)
+                        av[tm] = *reinterpret_cast<const u32x4*>(st + lds_byte(tm * 16 + (lane & 15), 4 * h + q));
+#pragma unroll
+                    for (int u = 0; u < NU; ++u) {
+                        u32x4 b;
+                        if constexpr (SW)
+                            b = *reinterpret_cast<const u32x4*>(st + lds_byte(kRowsA + u * 16 + (lane & 15), 4 * h + q));
+                        else
+                            b = WF::expand(wv[j][h][u]);
+#pragma unroll
+                        for (int tm = 0; tm < MT; ++tm) mfma16(Kind{}, av[tm], b, acc[tm][u]);
+                    }
+                }
+            }
+        }
+        // this wave's LDS reads of the batch are consumed before the next
+        // batch's copies are issued
+        wait_lgkmcnt0();
+        asm volatile("" ::: "memory");
     }
 }
 
@@ -152,7 +220,22 @@ __device__ __forceinline__ void down_finish(const DownArgs& a, int64_t row, int6
 
 // One workgroup per 16 output features (32 packed rows: 16 gate rows and the
 // matching 16 up rows of a 64-row packed group) and all M tokens.
-template <class Kind, bool FP8, int MT, int NW, int GB>
+// Spans (128 bytes of K) per batch of staged_k_loop with ROWS staged rows
+// per span: as many as fit 144 KiB of LDS over the workgroup's waves, at
+// most 8.  Weights are staged too (SW) when both operands fit two spans.
+template <int ROWS, int NW>
+constexpr int staged_batch() {
+    constexpr int per = 147456 / (NW * ROWS * kRowBytes);
+    return per < 1 ? 1 : (per > 8 ? 8 : per);
+}
+template <int ROWS, int NW>
+constexpr int staged_lds_bytes() { return NW * staged_batch<ROWS, NW>() * ROWS * kRowBytes; }
+template <bool FP8, int MT, int NU, int NW>
+constexpr bool stage_weights() { return !FP8 && staged_batch<(MT + NU) * 16, NW>() >= 2; }
+template <bool FP8, int MT, int NU, int NW>
+constexpr int staged_rows() { return (MT + (stage_weights<FP8, MT, NU, NW>() ? NU : 0)) * 16; }
+
+template <class Kind, bool FP8, int MT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
@@ -170,29 +253,33 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     const auto wr = make_rsrc(static_cast<const char*>(a.w) + pg * a.ldw * kWB, (uint32_t)(48 * a.ldw * kWB));
 
     const bool routed = a.ids != nullptr && f0 >= a.shared_feats;
-    if (routed && threadIdx.x < MT * 16) {
-        const int64_t row = threadIdx.x;
+    // the route gather (two dependent loads) runs on the last waves, which
+    // have the fewest K spans
+    if (routed && threadIdx.x >= NT - MT * 16) {
+        const int64_t row = threadIdx.x - (NT - MT * 16);
         int64_t id = row < a.M ? a.ids[row] : 0;
         id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
         for (int j = 0; j < kMaxTopK; ++j)
             s_route[row][j] = (j < a.top_k && row < a.M) ? (int)a.table[(int64_t)j * a.vocab + id] : -1;
     }
-    int a_off[MT], w_off[2];
-#pragma unroll
-    for (int tm = 0; tm < MT; ++tm) {
-        const int row = tm * 16 + r;
-        a_off[tm] = row < a.M ? (int)(row * a.ldx * (int64_t)sizeof(T)) : kOutOfRange;
-    }
+    int w_off[2];
     w_off[0] = (int)(r * a.ldw * kWB);          // gate row pg + r
     w_off[1] = (int)((32 + r) * a.ldw * kWB);   // up row pg + 32 + r
 
-    const int groups = (kb_a + 63) / 64;
-    const int per_wave = (groups + NW - 1) / NW;
-    const int g0 = wave * per_wave;
-    const int g1 = g0 + per_wave < groups ? g0 + per_wave : groups;
+    constexpr bool SW = stage_weights<FP8, MT, 2, NW>();
+    constexpr int kRows = staged_rows<FP8, MT, 2, NW>();
+    constexpr int SB = staged_batch<kRows, NW>();
+    const int w_row0[2] = {0, 32};
+    const int spans = (kb_a + 127) / 128;
+    const int per_wave = (spans + NW - 1) / NW;
+    const int s0 = wave * per_wave;
+    const int s1 = s0 + per_wave < spans ? s0 + per_wave : spans;
     f32x4 acc[MT][2];
     zero_acc16<MT, 2>(acc);
-    skinny_k_loop<Kind, FP8, MT, 2, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
+    char* region = reinterpret_cast<char*>(red) + wave * SB * kRows * kRowBytes;
+    staged_k_loop<Kind, FP8, MT, 2, SB, SW>(ar, (int)a.M, (int)(a.ldx * (int64_t)sizeof(T)), region, wr, w_row0,
+                                            (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc);
+    __syncthreads();   // every wave is done with its staging region
     skinny_stash<MT, 2>(red, acc);
     __syncthreads();
 
@@ -222,8 +309,8 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
 // Split-K partial of the down GEMM: block (x = 16*NU-column tile, y = K
 // split) writes part[(split * M + row) * N + col] for its rows and columns;
 // with a single split it finishes the output itself.
-template <class Kind, bool FP8, int MT, int NU, int NW, int GB>
-__global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int groups_per_split) {
+template <class Kind, bool FP8, int MT, int NU, int NW>
+__global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int spans_per_split) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
     constexpr int kWB = FP8 ? 1 : (int)sizeof(T);
@@ -237,24 +324,28 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.h, (uint32_t)(a.M * a.ldh * (int64_t)sizeof(T)));
     const auto wr = make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(kCols * a.ldw * kWB));
-    int a_off[MT], w_off[NU];
-#pragma unroll
-    for (int tm = 0; tm < MT; ++tm) {
-        const int row = tm * 16 + r;
-        a_off[tm] = row < a.M ? (int)(row * a.ldh * (int64_t)sizeof(T)) : kOutOfRange;
-    }
+    int w_off[NU];
 #pragma unroll
     for (int u = 0; u < NU; ++u) w_off[u] = (int)((u * 16 + r) * a.ldw * kWB);
 
-    const int groups = (kb_a + 63) / 64;
-    const int s0 = split * groups_per_split;
-    const int s1 = s0 + groups_per_split < groups ? s0 + groups_per_split : groups;
-    const int per_wave = (s1 - s0 + NW - 1) / NW;
-    const int g0 = s0 + wave * per_wave;
-    const int g1 = g0 + per_wave < s1 ? g0 + per_wave : s1;
+    constexpr bool SW = stage_weights<FP8, MT, NU, NW>();
+    constexpr int kRows = staged_rows<FP8, MT, NU, NW>();
+    constexpr int SB = staged_batch<kRows, NW>();
+    int w_row0[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) w_row0[u] = u * 16;
+    const int spans = (kb_a + 127) / 128;
+    const int p0 = split * spans_per_split;
+    const int p1 = p0 + spans_per_split < spans ? p0 + spans_per_split : spans;
+    const int per_wave = (p1 - p0 + NW - 1) / NW;
+    const int s0 = p0 + wave * per_wave;
+    const int s1 = s0 + per_wave < p1 ? s0 + per_wave : p1;
     f32x4 acc[MT][NU];
     zero_acc16<MT, NU>(acc);
-    skinny_k_loop<Kind, FP8, MT, NU, GB>(ar, a_off, wr, w_off, g0, g1, kb_a, acc);
+    char* region = reinterpret_cast<char*>(red) + wave * SB * kRows * kRowBytes;
+    staged_k_loop<Kind, FP8, MT, NU, SB, SW>(ar, (int)a.M, (int)(a.ldh * (int64_t)sizeof(T)), region, wr, w_row0,
+                                             (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc);
+    __syncthreads();   // every wave is done with its staging region
     skinny_stash<MT, NU>(red, acc);
     __syncthreads();
 
@@ -302,10 +393,10 @@ int set_lds(F* fn, int bytes) {
 
 constexpr int red_bytes(int mt, int nu, int nw) { return nw * mt * nu * 4 * 64 * 4; }
 
-template <class Kind, bool FP8, int MT, int NW, int GB>
+template <class Kind, bool FP8, int MT, int NW>
 int gate_up_skinny_mt(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    auto kern = k_gate_up_skinny<Kind, FP8, MT, NW, GB>;
-    constexpr int kLds = red_bytes(MT, 2, NW);
+    auto kern = k_gate_up_skinny<Kind, FP8, MT, NW>;
+    constexpr int kLds = std::max(red_bytes(MT, 2, NW), staged_lds_bytes<staged_rows<FP8, MT, 2, NW>(), NW>());
     int st = set_lds(kern, kLds);
     if (st) return st;
     hipLaunchKernelGGL(kern, dim3((unsigned)(packed_rows / 32)), dim3(64 * NW), kLds, stream, a);
@@ -314,36 +405,34 @@ int gate_up_skinny_mt(const GateUpArgs& a, int64_t packed_rows, hipStream_t stre
 
 template <class Kind, bool FP8>
 int gate_up_skinny_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if (a.M <= 16) return gate_up_skinny_mt<Kind, FP8, 1, 8, 8>(a, packed_rows, stream);
-    if (a.M <= 32) return gate_up_skinny_mt<Kind, FP8, 2, 8, 8>(a, packed_rows, stream);
-    if (a.M <= 64) return gate_up_skinny_mt<Kind, FP8, 4, 8, 4>(a, packed_rows, stream);
-    return gate_up_skinny_mt<Kind, FP8, 8, 4, 2>(a, packed_rows, stream);
+    if (a.M <= 16) return gate_up_skinny_mt<Kind, FP8, 1, 8>(a, packed_rows, stream);
+    if (a.M <= 32) return gate_up_skinny_mt<Kind, FP8, 2, 8>(a, packed_rows, stream);
+    if (a.M <= 64) return gate_up_skinny_mt<Kind, FP8, 4, 8>(a, packed_rows, stream);
+    return gate_up_skinny_mt<Kind, FP8, 8, 4>(a, packed_rows, stream);
 }
 
-// K groups (64 bytes of K) per split: the whole K (no reduction launch) up
-// to 8 tokens; then 32 groups (2 KiB of K: four splits at K = 3328) up to 64
-// tokens and 16 above -- the measured optimum of a sweep over 8..56 groups
-// and 16/32-column tiles at C3's shapes.  At least two groups per wave.
-int down_groups_per_split(int64_t M, int groups, int nw) {
-    int gps = M <= 8 ? groups : (M <= 64 ? 32 : 16);
-    if (gps < 2 * nw) gps = 2 * nw;
-    const char* e = getenv("TRMOE_SKINNY_GPS");
-    if (e != nullptr && atoi(e) > 0) gps = atoi(e);
-    gps = (gps + nw - 1) / nw * nw;
-    if (gps > groups) gps = (groups + nw - 1) / nw * nw;
-    return gps;
+// K spans (128 bytes of K) per split: the whole K (no reduction launch) up
+// to 8 tokens; about 16 spans (2 KiB of K: four splits at K = 3328) up to 64
+// tokens and 8 above, spread evenly over the splits.  TRMOE_SKINNY_SPS
+// overrides the target.
+int down_spans_per_split(int64_t M, int spans) {
+    int target = M <= 8 ? spans : (M <= 64 ? 16 : 8);
+    const char* e = getenv("TRMOE_SKINNY_SPS");
+    if (e != nullptr && atoi(e) > 0) target = atoi(e);
+    if (target > spans) target = spans;
+    if (target < 1) target = 1;
+    const int splits = (spans + target - 1) / target;
+    return (spans + splits - 1) / splits;
 }
 
-int down_nw(int64_t M) { return M <= 64 ? 8 : 4; }
-
-template <class Kind, bool FP8, int MT, int NU, int NW, int GB>
-int down_skinny_mt(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    auto kern = k_down_skinny<Kind, FP8, MT, NU, NW, GB>;
-    constexpr int kLds = red_bytes(MT, NU, NW);
+template <class Kind, bool FP8, int MT, int NU, int NW>
+int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
+    auto kern = k_down_skinny<Kind, FP8, MT, NU, NW>;
+    constexpr int kLds = std::max(red_bytes(MT, NU, NW), staged_lds_bytes<staged_rows<FP8, MT, NU, NW>(), NW>());
     int st = set_lds(kern, kLds);
     if (st) return st;
     hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * NU - 1) / (16 * NU)), (unsigned)splits), dim3(64 * NW), kLds,
-                       stream, a, part, gps);
+                       stream, a, part, sps);
     st = check_launch("shared_down_combine (skinny)");
     if (st || splits == 1) return st;
     const int64_t total = a.M * (int64_t)a.N;
@@ -352,8 +441,8 @@ int down_skinny_mt(const DownArgs& a, float* part, int gps, int splits, hipStrea
     return check_launch("shared_down_combine (skinny reduce)");
 }
 
-// Column tile: 16 columns (twice the workgroups) up to 64 tokens, 32 above
-// (half the re-reads of the activations).  TRMOE_SKINNY_NU=1/2 forces.
+// Column tile: 16 columns (twice the workgroups) up to 64 tokens, 32 above.
+// TRMOE_SKINNY_NU=1/2 forces.
 int down_nu(int64_t M) {
     const char* e = getenv("TRMOE_SKINNY_NU");
     if (e != nullptr && (atoi(e) == 1 || atoi(e) == 2)) return atoi(e);
@@ -361,17 +450,17 @@ int down_nu(int64_t M) {
 }
 
 template <class Kind, bool FP8, int NU>
-int down_skinny_nu(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, NU, 8, 8>(a, part, gps, splits, stream);
-    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, NU, 8, 8>(a, part, gps, splits, stream);
-    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, NU, 8, 4>(a, part, gps, splits, stream);
-    return down_skinny_mt<Kind, FP8, 8, NU, 4, 2>(a, part, gps, splits, stream);
+int down_skinny_nu(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
+    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, NU, 8>(a, part, sps, splits, stream);
+    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, NU, 8>(a, part, sps, splits, stream);
+    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, NU, 8>(a, part, sps, splits, stream);
+    return down_skinny_mt<Kind, FP8, 8, NU, 4>(a, part, sps, splits, stream);
 }
 
 template <class Kind, bool FP8>
-int down_skinny_kind(const DownArgs& a, float* part, int gps, int splits, hipStream_t stream) {
-    if (down_nu(a.M) == 1) return down_skinny_nu<Kind, FP8, 1>(a, part, gps, splits, stream);
-    return down_skinny_nu<Kind, FP8, 2>(a, part, gps, splits, stream);
+int down_skinny_kind(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
+    if (down_nu(a.M) == 1) return down_skinny_nu<Kind, FP8, 1>(a, part, sps, splits, stream);
+    return down_skinny_nu<Kind, FP8, 2>(a, part, sps, splits, stream);
 }
 
 }  // namespace
@@ -386,22 +475,21 @@ int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_
 size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act) {
     if (M < 1 || M > kSkinnyMaxTokens) return 0;
     const int eb = act == TRMOE_F32 ? 4 : 2;
-    const int groups = (int)((K * eb + 63) / 64);
-    const int gps = down_groups_per_split(M, groups, down_nw(M));
-    const int64_t splits = (groups + gps - 1) / gps;
+    const int spans = (int)((K * eb + 127) / 128);
+    const int64_t splits = (spans + down_spans_per_split(M, spans) - 1) / down_spans_per_split(M, spans);
     return (size_t)(splits * M * N * (int64_t)sizeof(float));
 }
 
 int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream) {
     const int eb = act == TRMOE_F32 ? 4 : 2;
-    const int groups = (int)(((int64_t)a.K * eb + 63) / 64);
-    const int gps = down_groups_per_split(a.M, groups, down_nw(a.M));
-    const int splits = (groups + gps - 1) / gps;
+    const int spans = (int)(((int64_t)a.K * eb + 127) / 128);
+    const int sps = down_spans_per_split(a.M, spans);
+    const int splits = (spans + sps - 1) / sps;
     float* part = static_cast<float*>(workspace);
-    if (act == TRMOE_F32 && wdt == TRMOE_F32) return down_skinny_kind<KindF32, false>(a, part, gps, splits, stream);
-    if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return down_skinny_kind<KindBF16, false>(a, part, gps, splits, stream);
+    if (act == TRMOE_F32 && wdt == TRMOE_F32) return down_skinny_kind<KindF32, false>(a, part, sps, splits, stream);
+    if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return down_skinny_kind<KindBF16, false>(a, part, sps, splits, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_FP8_E4M3)
-        return down_skinny_kind<KindBF16, true>(a, part, gps, splits, stream);
+        return down_skinny_kind<KindBF16, true>(a, part, sps, splits, stream);
     return set_error(TRMOE_ERR_UNSUPPORTED, "shared_down_combine: unsupported dtype pair");
 }
 

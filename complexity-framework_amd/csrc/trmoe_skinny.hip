@@ -24,6 +24,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace trmoe {
 
@@ -369,15 +370,32 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
 // separate launch: the kernel boundary publishes the partials of every XCD
 // (a device-scope release inside k_down_skinny would write back the whole
 // L2 of each XCD per workgroup, which costs far more than the launch).
-template <class T>
+template <class T, int V>
 __global__ __launch_bounds__(256) void k_down_reduce(DownArgs a, const float* part, int splits) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.M * (int64_t)a.N) return;
-    const int64_t row = idx / a.N, col = idx % a.N;
-    const int64_t plane = a.M * (int64_t)a.N;
-    float s = 0.f;
-    for (int sp = 0; sp < splits; ++sp) s += part[sp * plane + idx];
-    down_finish<T>(a, row, col, s);
+    // V consecutive columns per thread (16-byte partial loads when V = 4);
+    // the launcher keeps M * N below 2^31, so every index fits an int
+    const int nv = (int)a.N / V;
+    const int idx = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (idx >= (int)a.M * nv) return;
+    const int row = idx / nv, c0 = (idx - row * nv) * V;
+    const int plane = (int)a.M * (int)a.N;
+    const float* p = part + row * (int)a.N + c0;
+    using VT = typename std::conditional<V == 4, f32x4, float>::type;
+    VT acc{};
+    int sp = 0;
+    for (; sp + 2 <= splits; sp += 2) {   // two partials in flight; the sum keeps split order
+        const VT v0 = *reinterpret_cast<const VT*>(p + sp * plane);
+        const VT v1 = *reinterpret_cast<const VT*>(p + (sp + 1) * plane);
+        acc += v0;
+        acc += v1;
+    }
+    for (; sp < splits; ++sp) acc += *reinterpret_cast<const VT*>(p + sp * plane);
+    if constexpr (V == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) down_finish<T>(a, row, c0 + j, acc[j]);
+    } else {
+        down_finish<T>(a, row, c0, acc);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -435,9 +453,10 @@ int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStrea
                        stream, a, part, sps);
     st = check_launch("shared_down_combine (skinny)");
     if (st || splits == 1) return st;
-    const int64_t total = a.M * (int64_t)a.N;
-    hipLaunchKernelGGL(k_down_reduce<typename Kind::T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
-                       a, (const float*)part, splits);
+    const bool vec = a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0;
+    auto red = vec ? k_down_reduce<typename Kind::T, 4> : k_down_reduce<typename Kind::T, 1>;
+    const int64_t total = a.M * (int64_t)(vec ? a.N / 4 : a.N);
+    hipLaunchKernelGGL(red, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, (const float*)part, splits);
     return check_launch("shared_down_combine (skinny reduce)");
 }
 
@@ -481,6 +500,8 @@ size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act) {
 }
 
 int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream) {
+    if (a.M * (int64_t)a.N >= ((int64_t)1 << 31))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "shared_down_combine: decode path needs tokens * hidden < 2^31");
     const int eb = act == TRMOE_F32 ? 4 : 2;
     const int spans = (int)(((int64_t)a.K * eb + 127) / 128);
     const int sps = down_spans_per_split(a.M, spans);

@@ -11,7 +11,7 @@
 //                      loads (staged_k_loop), and reduce through LDS before
 //                      the SwiGLU epilogue (same epilogue contract as
 //                      k_gate_up_swiglu, including the dense-routed scaling)
-//   k_down_skinny      split-K: workgroup (16 or 32 output columns, K chunk)
+//   k_down_skinny      split-K: workgroup (8, 16 or 32 output columns, K chunk)
 //                      writes an fp32 partial [split][M][N] to the caller's
 //                      workspace
 //   k_down_reduce      sums the partials in split order (deterministic),
@@ -85,9 +85,10 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, int o
 // fragments back from LDS; without SW the weight fragments come straight
 // into registers (16 rows x 64 bytes per instruction).  Weight block u is the 16 rows from
 // row w_row0[u] of the weight descriptor (whose byte offsets, with SW off,
-// are w_off[u] for the lane's row).  Spans [s0, s1) in batches of SB;
+// are w_off[u] for the lane's row); with BR = 8 only its first 8 rows are
+// staged and the other 8 output columns of the block are to be ignored.  Spans [s0, s1) in batches of SB;
 // `region` holds SB * (MT + (SW ? NU : 0)) * 16 rows of 128 bytes.
-template <class Kind, bool FP8, int MT, int NU, int SB, bool SW>
+template <class Kind, bool FP8, int MT, int NU, int SB, bool SW, int BR = 16>
 __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_rows, int lda_b, char* region,
                                               __amdgpu_buffer_rsrc_t wr, const int (&w_row0)[NU], int ldw_b,
                                               const int (&w_off)[NU], int s0, int s1, int kb_a,
@@ -104,12 +105,15 @@ __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_r
         const int row = j * 8 + (lane >> 3);
         xo[j] = row < a_rows ? row * lda_b + 16 * ((lane & 7) ^ lds_swz(row)) : kOutOfRange;
     }
-    int wo[SW ? NU * 2 : 1];
+    static_assert(BR == 8 || BR == 16, "weight blocks of 8 or 16 rows");
+    constexpr int kWI = BR / 8;   // copy instructions per weight block
+    int wo[SW ? NU * kWI : 1];
     if constexpr (SW) {
 #pragma unroll
-        for (int j = 0; j < NU * 2; ++j)
-            wo[j] = (w_row0[j >> 1] + (j & 1) * 8 + (lane >> 3)) * ldw_b +
-                    16 * ((lane & 7) ^ lds_swz(kRowsA + j * 8 + (lane >> 3)));
+        for (int j = 0; j < NU * kWI; ++j) {
+            const int lr = (j / kWI) * 16 + (j % kWI) * 8 + (lane >> 3);   // row within the staged weight rows
+            wo[j] = (w_row0[j / kWI] + (j % kWI) * 8 + (lane >> 3)) * ldw_b + 16 * ((lane & 7) ^ lds_swz(kRowsA + lr));
+        }
     }
     for (int sb = s0; sb < s1; sb += SB) {
         typename WF::Reg wv[SW ? 1 : SB][2][NU];
@@ -125,9 +129,10 @@ __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_r
                 }
                 if constexpr (SW) {
 #pragma unroll
-                    for (int i = 0; i < NU * 2; ++i) {
-                        const int o = 128 * sp + 16 * ((lane & 7) ^ lds_swz(kRowsA + i * 8 + (lane >> 3)));
-                        dma16(wr, st + (kRowsA + i * 8) * kRowBytes, o < kb_a ? wo[i] + 128 * sp : kOutOfRange);
+                    for (int i = 0; i < NU * kWI; ++i) {
+                        const int r0 = kRowsA + (i / kWI) * 16 + (i % kWI) * 8;   // first LDS row of the copy
+                        const int o = 128 * sp + 16 * ((lane & 7) ^ lds_swz(r0 + (lane >> 3)));
+                        dma16(wr, st + r0 * kRowBytes, o < kb_a ? wo[i] + 128 * sp : kOutOfRange);
                     }
                 } else {
 #pragma unroll
@@ -307,15 +312,17 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     }
 }
 
-// Split-K partial of the down GEMM: block (x = 16*NU-column tile, y = K
+// Split-K partial of the down GEMM: block (x = COLS-column tile, y = K
 // split) writes part[(split * M + row) * N + col] for its rows and columns;
-// with a single split it finishes the output itself.
-template <class Kind, bool FP8, int MT, int NU, int NW>
+// with a single split it finishes the output itself.  COLS = 8 uses half of
+// a 16-row weight block (twice the workgroups for the same columns).
+template <class Kind, bool FP8, int MT, int COLS, int NW>
 __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int spans_per_split) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
     constexpr int kWB = FP8 ? 1 : (int)sizeof(T);
-    constexpr int kCols = 16 * NU;
+    constexpr int NU = (COLS + 15) / 16;
+    constexpr int kCols = COLS;
     extern __shared__ __align__(16) float red[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15;
@@ -344,8 +351,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     f32x4 acc[MT][NU];
     zero_acc16<MT, NU>(acc);
     char* region = reinterpret_cast<char*>(red) + wave * SB * kRows * kRowBytes;
-    staged_k_loop<Kind, FP8, MT, NU, SB, SW>(ar, (int)a.M, (int)(a.ldh * (int64_t)sizeof(T)), region, wr, w_row0,
-                                             (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc);
+    staged_k_loop<Kind, FP8, MT, NU, SB, SW, (COLS < 16 ? 8 : 16)>(ar, (int)a.M, (int)(a.ldh * (int64_t)sizeof(T)),
+                                                                   region, wr, w_row0, (int)(a.ldw * kWB), w_off,
+                                                                   s0, s1, kb_a, acc);
     __syncthreads();   // every wave is done with its staging region
     skinny_stash<MT, NU>(red, acc);
     __syncthreads();
@@ -355,8 +363,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     for (int qi = threadIdx.x; qi < MT * NU * 4 * 64; qi += NT) {
         const int l = qi & 63, i = (qi >> 6) & 3, u = (qi >> 8) % NU, tm = (qi >> 8) / NU;
         const int row = tm * 16 + 4 * (l >> 4) + i;
-        const int64_t col = n0 + u * 16 + (l & 15);
-        if (row >= a.M || col >= a.N) continue;
+        const int cl = u * 16 + (l & 15);
+        const int64_t col = n0 + cl;
+        if (row >= a.M || cl >= kCols || col >= a.N) continue;
         const float v = skinny_sum<MT, NU, NW>(red, tm, u, i, l);
         if (single)
             down_finish<T>(a, row, col, v);
@@ -443,14 +452,15 @@ int down_spans_per_split(int64_t M, int spans) {
     return (spans + splits - 1) / splits;
 }
 
-template <class Kind, bool FP8, int MT, int NU, int NW>
+template <class Kind, bool FP8, int MT, int COLS, int NW>
 int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
-    auto kern = k_down_skinny<Kind, FP8, MT, NU, NW>;
+    constexpr int NU = (COLS + 15) / 16;
+    auto kern = k_down_skinny<Kind, FP8, MT, COLS, NW>;
     constexpr int kLds = std::max(red_bytes(MT, NU, NW), staged_lds_bytes<staged_rows<FP8, MT, NU, NW>(), NW>());
     int st = set_lds(kern, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * NU - 1) / (16 * NU)), (unsigned)splits), dim3(64 * NW), kLds,
-                       stream, a, part, sps);
+    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + COLS - 1) / COLS), (unsigned)splits), dim3(64 * NW), kLds, stream,
+                       a, part, sps);
     st = check_launch("shared_down_combine (skinny)");
     if (st || splits == 1) return st;
     const bool vec = a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0;
@@ -460,26 +470,29 @@ int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStrea
     return check_launch("shared_down_combine (skinny reduce)");
 }
 
-// Column tile: 16 columns (twice the workgroups) up to 64 tokens, 32 above.
-// TRMOE_SKINNY_NU=1/2 forces.
-int down_nu(int64_t M) {
-    const char* e = getenv("TRMOE_SKINNY_NU");
-    if (e != nullptr && (atoi(e) == 1 || atoi(e) == 2)) return atoi(e);
-    return M <= 64 ? 1 : 2;
+// Column tile: 8 columns up to 16 tokens (the whole K in one workgroup, so
+// twice the workgroups), 16 up to 64 tokens, 32 above (half the re-reads of
+// the activations).  TRMOE_SKINNY_COLS=8/16/32 forces.
+int down_cols(int64_t M) {
+    const char* e = getenv("TRMOE_SKINNY_COLS");
+    if (e != nullptr && (atoi(e) == 8 || atoi(e) == 16 || atoi(e) == 32)) return atoi(e);
+    return M <= 16 ? 8 : (M <= 64 ? 16 : 32);
 }
 
-template <class Kind, bool FP8, int NU>
-int down_skinny_nu(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
-    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, NU, 8>(a, part, sps, splits, stream);
-    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, NU, 8>(a, part, sps, splits, stream);
-    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, NU, 8>(a, part, sps, splits, stream);
-    return down_skinny_mt<Kind, FP8, 8, NU, 4>(a, part, sps, splits, stream);
+template <class Kind, bool FP8, int COLS>
+int down_skinny_cols(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
+    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, COLS, 8>(a, part, sps, splits, stream);
+    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, COLS, 8>(a, part, sps, splits, stream);
+    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, COLS, 8>(a, part, sps, splits, stream);
+    return down_skinny_mt<Kind, FP8, 8, COLS, 4>(a, part, sps, splits, stream);
 }
 
 template <class Kind, bool FP8>
 int down_skinny_kind(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
-    if (down_nu(a.M) == 1) return down_skinny_nu<Kind, FP8, 1>(a, part, sps, splits, stream);
-    return down_skinny_nu<Kind, FP8, 2>(a, part, sps, splits, stream);
+    const int cols = down_cols(a.M);
+    if (cols == 8) return down_skinny_cols<Kind, FP8, 8>(a, part, sps, splits, stream);
+    if (cols == 16) return down_skinny_cols<Kind, FP8, 16>(a, part, sps, splits, stream);
+    return down_skinny_cols<Kind, FP8, 32>(a, part, sps, splits, stream);
 }
 
 }  // namespace

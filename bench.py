@@ -26,6 +26,7 @@ import statistics
 import sys
 import time
 from pathlib import Path
+from typing import Optional
 
 ROOT = Path(__file__).resolve().parent
 for _p in (ROOT, ROOT / "complexity-framework_amd"):
@@ -151,7 +152,7 @@ def cpu_baseline(w, sample_tokens: int, reps: int = 5):
 
 
 def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50, warmup: int = 5,
-               per_layer_tables: bool = False):
+               per_layer_tables: bool = False, block: Optional[str] = None):
     """Decode: w's tokens (C3: 64; C4: 8) through `layers` distinct weight sets
     per step (286 MB of bf16 weights > the 256 MB Infinity Cache), per-layer
     time and HBM GB/s.  per_layer_tables: layer i routes with layer_index i
@@ -159,7 +160,13 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
 
     A decode step of the stack is captured once as a HIP graph (the serving
     form of the reference's CUDA_GRAPH backend, engine.py:597-716) and
-    replayed; the eager per-layer time is reported beside it."""
+    replayed; the eager per-layer time is reported beside it.
+
+    block: the MLP half of a decoder block instead of the bare layer,
+    x + mlp(rmsnorm(x)) (block.py:271-278): "fused" runs
+    forward_norm_residual (the norm inside the gate|up kernel, the residual in
+    the down epilogue); "unfused" runs the norm as torch ops and then
+    forward_with_residual."""
     w = w or workloads.C3
     engines = [workloads.build_engine(w, dev, backend="hip", seed=i,
                                       **({"layer_index": i} if per_layer_tables else {}))
@@ -167,10 +174,20 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
     x = workloads.make_hidden(w).to(dev).to(torch.bfloat16)
     ids = workloads.make_token_ids(w).to(dev)
 
+    nw = (torch.rand(w.hidden, generator=torch.Generator().manual_seed(5)) + 0.5).to(dev).to(torch.bfloat16)
+
+    def layer(e):
+        if block == "fused":
+            return e.forward_norm_residual(x, ids, nw, 1e-6)
+        if block == "unfused":
+            normed = nw * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6))
+            return e.forward_with_residual(normed, ids, x)
+        return e(x, ids)
+
     def stack():
         out = None
         for e in engines:
-            out = e(x, ids)
+            out = layer(e)
         return out
 
     def timed(fn, n):
@@ -205,7 +222,7 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
     weight_bytes = 2 * (3 * H * S + 3 * E * H * Wd)
     bytes_per_layer = weight_bytes + 2 * 2 * w.tokens * H + 8 * w.tokens + 8 * 2 * w.tokens
     return {
-        "workload": w.name,
+        "workload": w.name if block is None else f"{w.name}_block_{block}",
         "layers_rotated": layers,
         "mode": "hip_graph_replay",
         "ms_per_layer": per_layer_ms,
@@ -414,6 +431,15 @@ def main():
     if not args.no_decode:
         result["decode"] = decode_hbm(torch, workloads, dev)
         result["decode_c4"] = decode_hbm(torch, workloads, dev, w=workloads.C4_DECODE, per_layer_tables=True)
+        # the block's MLP half with the post-attention RMSNorm and residual fused
+        # (F2) and unfused, C3
+        fused = decode_hbm(torch, workloads, dev, block="fused")
+        unfused = decode_hbm(torch, workloads, dev, block="unfused")
+        result["decode_block"] = {
+            "workload": workloads.C3.name,
+            "fused_us_per_layer": fused["ms_per_layer"] * 1e3,
+            "unfused_us_per_layer": unfused["ms_per_layer"] * 1e3,
+        }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(w, min(args.cpu_sample, tokens))
     if args.calibrate_copy:

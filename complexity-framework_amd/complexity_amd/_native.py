@@ -73,6 +73,22 @@ SIGNATURES = {
         [_c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp, _c_float, _c_vp, _c_i64,
          _c_vp, _c_i64, _c_vp],
     ),
+    "trmoe_rms_row_scale": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _c_vp, _c_vp]),
+    "trmoe_shared_gate_up_rms": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_float, _c_vp, _c_i64,
+         _c_vp],
+    ),
+    "trmoe_dense_routed_gate_up_rms": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_i64, _c_vp,
+         _c_vp, _c_i64, _c_int, _c_vp, _c_float, _c_float, _c_vp, _c_float, _c_vp, _c_i64, _c_vp],
+    ),
+    "trmoe_routed_experts_rms": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp,
+         _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_size, _c_vp],
+    ),
     "trmoe_shared_gate_up_save": (
         _c_int,
         [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],

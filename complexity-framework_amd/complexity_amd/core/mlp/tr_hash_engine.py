@@ -120,6 +120,20 @@ class TRHashEngineMLP(MLPBase):
             raise ValueError("tr_hash_engine requires token_ids")
         return self.engine(hidden_states, token_ids)
 
+    def forward_with_residual(self, hidden_states, residual, token_ids=None):
+        """``residual + forward(hidden_states)`` (block.py:278), the add fused
+        into the down projection on the HIP backend."""
+        if token_ids is None:
+            raise ValueError("tr_hash_engine requires token_ids")
+        return self.engine.forward_with_residual(hidden_states, token_ids, residual)
+
+    def forward_norm_residual(self, hidden_states, norm, token_ids=None):
+        """``hidden + forward(norm(hidden))`` for the block's RMSNorm module
+        ``norm`` (weight, eps; block.py:271-278), fused on the HIP backend."""
+        if token_ids is None:
+            raise ValueError("tr_hash_engine requires token_ids")
+        return self.engine.forward_norm_residual(hidden_states, token_ids, norm.weight, norm.eps)
+
     def set_top_k_primary_weight(self, weight: float) -> None:
         if self.top_k == 1:
             self._primary_weight = 1.0

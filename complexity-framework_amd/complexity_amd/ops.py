@@ -22,6 +22,7 @@ ORDER_ASSIGNMENT = N.ORDER_ASSIGNMENT
 
 # Padding the packed layouts use (must match the kernel tiles).
 SHARED_GATE_UP_ALIGN = 256   # rows = 2 * round_up(S, 128)
+SKINNY_MAX_TOKENS = 128      # token counts the decode-shape kernels take
 EXPERT_GATE_UP_ALIGN = 128   # rows = 2 * round_up(W, 64)
 DOWN_ALIGN = 256             # rows = round_up(H, 256)
 
@@ -226,9 +227,10 @@ def pack_dense_routed(shared_gate, shared_up, shared_down, gate, up, down):
 def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: int, num_experts: int,
                          expert_width: int, token_ids: torch.Tensor, route_table: torch.Tensor,
                          route_weights: Sequence[float], shared_scale: float, routed_scale: float,
-                         save: bool = False):
+                         save: bool = False, row_scale: Optional[torch.Tensor] = None, rms_eps: float = 0.0):
     """h_ext[N, F]: shared SwiGLU features and route-weighted expert features.
-    save: also return the raw gate|up outputs gu[N, 2F] (packed column order)."""
+    save: also return the raw gate|up outputs gu[N, 2F] (packed column order).
+    row_scale / rms_eps: fused RMSNorm (trmoe_dense_routed_gate_up_rms)."""
     lib = _lib()
     _require_cuda(x, w_packed, token_ids, route_table)
     x = rows16(x)
@@ -248,6 +250,15 @@ def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: 
                                                  _stream(x))
         N.check(st, "trmoe_dense_routed_gate_up_save")
         return h, gu
+    if row_scale is not None or rms_eps > 0.0:
+        st = lib.trmoe_dense_routed_gate_up_rms(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
+                                                x.stride(0), _p(w_packed), None, shared_width, num_experts,
+                                                expert_width, _p(ids), _p(table), table.shape[1], table.shape[0],
+                                                ctypes.cast(rw, ctypes.c_void_p), float(shared_scale),
+                                                float(routed_scale), _p(row_scale), float(rms_eps), _p(h), F,
+                                                _stream(x))
+        N.check(st, "trmoe_dense_routed_gate_up_rms")
+        return h
     st = lib.trmoe_dense_routed_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
                                         x.stride(0), _p(w_packed), None, shared_width, num_experts, expert_width,
                                         _p(ids), _p(table), table.shape[1], table.shape[0],
@@ -262,9 +273,11 @@ def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: 
 # ---------------------------------------------------------------------------
 
 def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[torch.Tensor],
-                   shared_width: int, save: bool = False):
+                   shared_width: int, save: bool = False, row_scale: Optional[torch.Tensor] = None,
+                   rms_eps: float = 0.0):
     """h[N, round_up(S,128)] = silu(x Wg^T) * (x Wu^T).  save: also return the
-    raw gate|up outputs gu[N, 2 round_up(S,128)] (bf16/f32 weights)."""
+    raw gate|up outputs gu[N, 2 round_up(S,128)] (bf16/f32 weights).
+    row_scale / rms_eps: fused RMSNorm (trmoe_shared_gate_up_rms)."""
     lib = _lib()
     _require_cuda(x, w_packed)
     x = rows16(x)
@@ -277,6 +290,12 @@ def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[to
                                            shared_width, _p(h), ldh, _p(gu), 2 * ldh, _stream(x))
         N.check(st, "trmoe_shared_gate_up_save")
         return h, gu
+    if row_scale is not None or rms_eps > 0.0:
+        st = lib.trmoe_shared_gate_up_rms(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
+                                          x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(row_scale),
+                                          float(rms_eps), _p(h), ldh, _stream(x))
+        N.check(st, "trmoe_shared_gate_up_rms")
+        return h
     st = lib.trmoe_shared_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
                                   x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(h), ldh,
                                   _stream(x))
@@ -286,10 +305,12 @@ def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[to
 
 def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Tensor, num_experts: int,
                    top_k: int, w_gate_up: torch.Tensor, s_gate_up, w_down: torch.Tensor, s_down,
-                   expert_width: int, two_pass: bool = True) -> torch.Tensor:
+                   expert_width: int, two_pass: bool = True,
+                   row_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y[k*N, H] in partition order.  two_pass: grouped gate|up and down
     GEMMs through a workspace (the default when y rows are 16-byte aligned);
-    False: the fused per-tile kernel."""
+    False: the fused per-tile kernel.  row_scale: fused RMSNorm scales
+    (trmoe_routed_experts_rms, two-pass only)."""
     lib = _lib()
     _require_cuda(x, sorted_idx, offsets, w_gate_up, w_down)
     x = rows16(x)
@@ -300,12 +321,32 @@ def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Ten
         ws_bytes = lib.trmoe_routed_experts_workspace_bytes(dtype_code(x.dtype), top_k * n, expert_width)
         if ws_bytes:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    if row_scale is not None:
+        st = lib.trmoe_routed_experts_rms(dtype_code(x.dtype), dtype_code(w_gate_up.dtype), _p(x), n, hidden,
+                                          x.stride(0), _p(sorted_idx), _p(offsets), num_experts, top_k,
+                                          _p(w_gate_up), _p(s_gate_up), _p(w_down), _p(s_down), expert_width,
+                                          _p(row_scale), _p(y), hidden, _p(ws), ws_bytes, _stream(x))
+        N.check(st, "trmoe_routed_experts_rms")
+        return y
     st = lib.trmoe_routed_experts(dtype_code(x.dtype), dtype_code(w_gate_up.dtype), _p(x), n, hidden,
                                   x.stride(0), _p(sorted_idx), _p(offsets), num_experts, top_k,
                                   _p(w_gate_up), _p(s_gate_up), _p(w_down), _p(s_down), expert_width,
                                   _p(y), hidden, _p(ws), ws_bytes, _stream(x))
     N.check(st, "trmoe_routed_experts")
     return y
+
+
+def rms_row_scale(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """r[N] fp32 = 1 / sqrt(mean_k x[t, k]^2 + eps): the per-token factor of
+    RMSNorm (complexity/core/normalization/norms.py:53-54)."""
+    lib = _lib()
+    _require_cuda(x)
+    x = rows16(x)
+    n, hidden = x.shape
+    r = torch.empty(n, dtype=torch.float32, device=x.device)
+    st = lib.trmoe_rms_row_scale(dtype_code(x.dtype), _p(x), n, hidden, x.stride(0), float(eps), _p(r), _stream(x))
+    N.check(st, "trmoe_rms_row_scale")
+    return r
 
 
 def _weights_arg(route_weights: Sequence[float]):
@@ -407,12 +448,17 @@ class PackedLayer:
 
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
                   route_weights: Sequence[float], shared_scale: float, routed_scale: float,
-                  order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None, save: bool = False):
+                  order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None, save: bool = False,
+                  norm_eps: Optional[float] = None):
     """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual).
 
     grouped: K1 partition, K3 grouped experts, K2 shared gate|up, K4 down with
     the un-permute in its epilogue.  dense: fused gate|up over shared and
-    expert features with route-weighted expert outputs, then one down GEMM."""
+    expert features with route-weighted expert outputs, then one down GEMM.
+    norm_eps: the layer runs on rmsnorm(x) (the packs must hold the gate/up
+    weights times the norm weight); the per-token scales come from the decode
+    kernels themselves up to 128 tokens (dense strategy), else from
+    rms_row_scale."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
     if n == 0:
@@ -420,10 +466,18 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
         return (out, None) if save else out
     x = rows16(x)
     gu = None
+    rscale, eps_in = None, 0.0
+    if norm_eps is not None:
+        if save:
+            raise ValueError("layer_forward: the fused RMSNorm is inference-only")
+        if packed.strategy == STRATEGY_DENSE and n <= SKINNY_MAX_TOKENS:
+            eps_in = float(norm_eps)
+        else:
+            rscale = rms_row_scale(x, norm_eps)
     if packed.strategy == STRATEGY_DENSE:
         h = dense_routed_gate_up(x, packed.dense_gate_up, packed.shared_width, packed.num_experts,
                                  packed.expert_width, token_ids, route_table, route_weights, shared_scale,
-                                 routed_scale, save=save)
+                                 routed_scale, save=save, row_scale=rscale, rms_eps=eps_in)
         if save:
             h, gu = h
         out = shared_down_combine(h, packed.dense_features, packed.dense_down, None, hidden, None, None,
@@ -432,9 +486,10 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
     sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, packed.num_experts, order)
     y = routed_experts(x, sorted_idx, offsets, packed.num_experts, top_k, packed.expert_gate_up,
                        packed.expert_gate_up_scale, packed.expert_down, packed.expert_down_scale,
-                       packed.expert_width)
+                       packed.expert_width, row_scale=rscale)
     if packed.shared_width > 0:
-        h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width, save=save)
+        h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width, save=save,
+                           row_scale=rscale)
         if save:
             h, gu = h
         out = shared_down_combine(h, packed.shared_width, packed.shared_down, packed.shared_down_scale,

@@ -144,6 +144,7 @@ class TRHashEngine(nn.Module):
         self._active_route_table = self.route_table
         self._fused_shared_gate_up_weight: Optional[torch.Tensor] = None
         self._packed_key = None
+        self._packed_norm = None   # (key, pack) with a block RMSNorm weight folded in
         self._bwd_packed = None
         self._decision_cache: Dict[tuple, BackendDecision] = {}
         self._packed: Optional[ops.PackedLayer] = None
@@ -167,6 +168,7 @@ class TRHashEngine(nn.Module):
             self._fused_shared_gate_up_weight = fn(self._fused_shared_gate_up_weight)
         self._packed_key = None
         self._packed = None
+        self._packed_norm = None
         return self
 
     @property
@@ -203,6 +205,7 @@ class TRHashEngine(nn.Module):
             self._graph_pool.clear()
             self._packed_key = None
             self._packed = None
+            self._packed_norm = None
 
     def _compile_fused_metadata(self, route_table: torch.Tensor):
         if supports_fused_cuda(self.config):
@@ -261,6 +264,7 @@ class TRHashEngine(nn.Module):
         self._fp8 = True
         self._packed_key = None
         self._packed = None
+        self._packed_norm = None
 
     def _dequantized(self, name: str, dtype: torch.dtype) -> torch.Tensor:
         q = getattr(self, name + "_fp8")
@@ -345,9 +349,13 @@ class TRHashEngine(nn.Module):
             srcs += [self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight]
         return srcs
 
-    def _hip_packed(self) -> ops.PackedLayer:
+    def _hip_packed(self, norm_weight: Optional[torch.Tensor] = None) -> ops.PackedLayer:
         """Weights in kernel layout, rebuilt when a source tensor or the active
-        capacity changes (keyed on storage pointer and in-place version)."""
+        capacity changes (keyed on storage pointer and in-place version).
+
+        norm_weight: a block's RMSNorm weight folded into the gate/up weights
+        (their input axis), for forward_norm_residual; cached apart from the
+        plain pack."""
         srcs = self._hip_sources()
         E, W = self._active_num_experts, self._active_expert_width
         strategy = self.routed_strategy
@@ -355,21 +363,45 @@ class TRHashEngine(nn.Module):
             strategy = ops.choose_strategy(self.config.shared_width, E, W, self.config.top_k, self._fp8)
         if strategy == ops.STRATEGY_DENSE and self._fp8:
             raise NotImplementedError("the dense-routed strategy needs bf16/f32 weights")
+        if norm_weight is not None and self._fp8:
+            raise NotImplementedError("the fused RMSNorm folds its weight into bf16/f32 gate/up weights")
         key = (
             tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in srcs),
             E,
             W,
             strategy,
+            None if norm_weight is None else (norm_weight.data_ptr(), norm_weight._version, norm_weight.dtype),
         )
+        if norm_weight is not None:
+            cached = self._packed_norm
+            if cached is not None and cached[0] == key:
+                return cached[1]
+            packed = self._build_packed(E, W, strategy, norm_weight)
+            self._packed_norm = (key, packed)
+            return packed
         if self._packed is not None and self._packed_key == key:
             return self._packed
+        packed = self._build_packed(E, W, strategy, None)
+        self._packed, self._packed_key = packed, key
+        return packed
+
+    def _build_packed(self, E: int, W: int, strategy: str, norm_weight: Optional[torch.Tensor]) -> ops.PackedLayer:
+        def fold(w: torch.Tensor, shape) -> torch.Tensor:
+            # W * norm_weight along the input axis, rounded once to w's dtype
+            if norm_weight is None:
+                return w
+            return (w.float() * norm_weight.float().reshape(shape)).to(w.dtype)
+
         with torch.no_grad():
             if strategy == ops.STRATEGY_DENSE:
                 shared = (None, None, None)
                 if self.shared_gate is not None:
                     shared = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight)
+                if shared[0] is not None:
+                    shared = (fold(shared[0], (1, -1)), fold(shared[1], (1, -1)), shared[2])
                 gu, dd, feats = ops.pack_dense_routed(
-                    *shared, self.expert_gate[:E, :, :W], self.expert_up[:E, :, :W], self.expert_down[:E, :W, :]
+                    *shared, fold(self.expert_gate[:E, :, :W], (1, -1, 1)), fold(self.expert_up[:E, :, :W], (1, -1, 1)),
+                    self.expert_down[:E, :W, :]
                 )
                 packed = ops.PackedLayer(
                     act_dtype=self._hip_act_dtype(),
@@ -381,7 +413,6 @@ class TRHashEngine(nn.Module):
                     dense_down=dd,
                     dense_features=feats,
                 )
-                self._packed, self._packed_key = packed, key
                 return packed
             if self._fp8:
                 gq, gs = self.expert_gate_fp8[:E, :, :W], self.expert_gate_scale[:E, :W]
@@ -390,7 +421,8 @@ class TRHashEngine(nn.Module):
                 egu, egu_s = ops.pack_expert_gate_up(gq, uq, gs, us)
                 ed, ed_s = ops.pack_expert_down(dq, ds)
             else:
-                egu, egu_s = ops.pack_expert_gate_up(self.expert_gate[:E, :, :W], self.expert_up[:E, :, :W])
+                egu, egu_s = ops.pack_expert_gate_up(fold(self.expert_gate[:E, :, :W], (1, -1, 1)),
+                                                     fold(self.expert_up[:E, :, :W], (1, -1, 1)))
                 ed, ed_s = ops.pack_expert_down(self.expert_down[:E, :W, :])
             packed = ops.PackedLayer(
                 act_dtype=self._hip_act_dtype(),
@@ -410,11 +442,11 @@ class TRHashEngine(nn.Module):
                     )
                     sd, sd_s = ops.pack_linear_down(self.shared_down_fp8, self.shared_down_scale)
                 else:
-                    sgu, sgu_s = ops.pack_linear_gate_up(self.shared_gate.weight, self.shared_up.weight)
+                    sgu, sgu_s = ops.pack_linear_gate_up(fold(self.shared_gate.weight, (1, -1)),
+                                                         fold(self.shared_up.weight, (1, -1)))
                     sd, sd_s = ops.pack_linear_down(self.shared_down.weight)
                 packed.shared_gate_up, packed.shared_gate_up_scale = sgu, sgu_s
                 packed.shared_down, packed.shared_down_scale = sd, sd_s
-        self._packed, self._packed_key = packed, key
         return packed
 
     def _hip_forward(self, flat_x: torch.Tensor, flat_ids: torch.Tensor, decision: BackendDecision,
@@ -573,6 +605,52 @@ class TRHashEngine(nn.Module):
             out = self._hip_forward(hidden_states.reshape(-1, h), token_ids.reshape(-1), decision, residual)
             return out.view(b, t, h)
         return residual + self.forward(hidden_states, token_ids)
+
+    def forward_norm_residual(self, hidden_states: torch.Tensor, token_ids: torch.Tensor,
+                              norm_weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+        """``hidden + forward(rmsnorm(hidden), token_ids)``: the MLP half of a
+        block (block.py:271-278) with its post-attention RMSNorm
+        (norms.py:46-55) fused.  On the HIP backend, outside autograd and with
+        bf16/f32 weights, the norm weight is folded into the packed gate/up
+        weights, each token's 1/rms scales its gate and up accumulators (the
+        decode kernels compute it from the activations they already stage),
+        and the residual add runs in the down epilogue.  Otherwise the norm
+        runs as the reference writes it, then forward_with_residual."""
+        if norm_weight.shape != (hidden_states.shape[-1],):
+            raise ValueError("norm_weight must have shape (hidden_size,)")
+        decision = self._decide(hidden_states)
+        self.last_backend = decision
+        grad = torch.is_grad_enabled() and (
+            hidden_states.requires_grad
+            or norm_weight.requires_grad
+            or any(p is not None and p.requires_grad for p in self._hip_params())
+        )
+        if (decision.selected is TRHashBackend.HIP and hidden_states.ndim == 3 and not grad and not self._fp8
+                and eps > 0.0):
+            b, t, h = hidden_states.shape
+            if token_ids.shape != hidden_states.shape[:2]:
+                raise ValueError("token_ids must match hidden batch/sequence dimensions")
+            packed = self._hip_packed(norm_weight)
+            flat = hidden_states.reshape(-1, h)
+            x = (flat if flat.dtype == packed.act_dtype else flat.to(packed.act_dtype)).contiguous()
+            order = ops.ORDER_ASSIGNMENT if decision.partition == PARTITION_ASSIGNMENT else ops.ORDER_TOKEN
+            out = ops.layer_forward(
+                x,
+                token_ids.reshape(-1),
+                self._active_route_table,
+                packed,
+                self.config.route_weights,
+                self.config.shared_output_scale,
+                self.config.routed_output_scale,
+                order=order,
+                residual=x,
+                norm_eps=float(eps),
+            )
+            out = out if out.dtype == hidden_states.dtype else out.to(hidden_states.dtype)
+            return out.view(b, t, h)
+        variance = hidden_states.pow(2).mean(-1, keepdim=True)
+        normed = norm_weight * (hidden_states * torch.rsqrt(variance + eps))
+        return self.forward_with_residual(normed, token_ids, hidden_states)
 
     def _forward_cuda_graph(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
         if self.training or torch.is_grad_enabled():

@@ -177,9 +177,25 @@ int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* 
                              workspace_bytes, as_stream(stream));
 }
 
+// Fused RMSNorm scales of the *_rms entry points: a row_scale array, or
+// (row_scale null) eps > 0 for scales computed by the decode kernels.
+static int rms_args_ok(const char* who, const float* row_scale, float eps, int64_t n_tokens) {
+    if (row_scale != nullptr) return TRMOE_OK;
+    if (!(eps > 0.0f)) {
+        std::string m = std::string(who) + ": row_scale null needs eps > 0";
+        return set_error(TRMOE_ERR_INVALID, m.c_str());
+    }
+    if (n_tokens > kSkinnyMaxTokens) {
+        std::string m = std::string(who) + ": in-kernel RMSNorm scales need n_tokens <= 128 (else trmoe_rms_row_scale)";
+        return set_error(TRMOE_ERR_INVALID, m.c_str());
+    }
+    return TRMOE_OK;
+}
+
 static int shared_gate_up_impl(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
                                int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
-                               void* h, int64_t ldh, void* gu, int64_t ldgu, void* stream) {
+                               void* h, int64_t ldh, void* gu, int64_t ldgu, void* stream,
+                               const float* row_scale = nullptr, float rms_eps = 0.0f) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_gate_up: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_gate_up: bad dimensions");
     TRMOE_REQUIRE(ldx >= hidden, "shared_gate_up: ldx < hidden");
@@ -213,7 +229,31 @@ static int shared_gate_up_impl(int act_dtype, int w_dtype, const void* x, int64_
     for (int j = 0; j < 4; ++j) a.rw[j] = 0.f;
     a.gu = gu;
     a.ldgu = ldgu;
+    a.row_scale = row_scale;
+    a.rms_eps = rms_eps;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * round_up(shared_width, 128), as_stream(stream));
+}
+
+int trmoe_rms_row_scale(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx, float eps,
+                        float* row_scale, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "rms_row_scale: bf16 or f32 activations");
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && hidden < (int64_t)1 << 30, "rms_row_scale: bad dimensions");
+    TRMOE_REQUIRE(ldx >= hidden, "rms_row_scale: ldx < hidden");
+    TRMOE_REQUIRE(eps >= 0.0f, "rms_row_scale: eps must be non-negative");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x && row_scale, "rms_row_scale: null pointer");
+    TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)),
+                  "rms_row_scale: x rows must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    return launch_rms_row_scale(act_dtype, x, n_tokens, hidden, ldx, eps, row_scale, as_stream(stream));
+}
+
+int trmoe_shared_gate_up_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                             int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                             const float* row_scale, float eps, void* h, int64_t ldh, void* stream) {
+    const int st = rms_args_ok("shared_gate_up_rms", row_scale, eps, n_tokens);
+    if (st) return st;
+    return shared_gate_up_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, w_packed, w_scale, shared_width, h,
+                               ldh, nullptr, 0, stream, row_scale, row_scale ? 0.0f : eps);
 }
 
 int trmoe_shared_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
@@ -244,7 +284,8 @@ static int dense_routed_gate_up_impl(int act_dtype, int w_dtype, const void* x, 
                                      int num_experts, int64_t expert_width, const int64_t* token_ids,
                                      const int64_t* route_table, int64_t vocab_size, int top_k,
                                      const float* route_weights, float shared_scale, float routed_scale, void* h,
-                                     int64_t ldh, void* gu, int64_t ldgu, void* stream) {
+                                     int64_t ldh, void* gu, int64_t ldgu, void* stream,
+                                     const float* row_scale = nullptr, float rms_eps = 0.0f) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "dense_routed_gate_up: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width >= 0 && expert_width > 0,
                   "dense_routed_gate_up: bad dimensions");
@@ -284,7 +325,23 @@ static int dense_routed_gate_up_impl(int act_dtype, int w_dtype, const void* x, 
     for (int j = 0; j < 4; ++j) a.rw[j] = j < top_k ? routed_scale * route_weights[j] : 0.f;
     a.gu = gu;
     a.ldgu = ldgu;
+    a.row_scale = row_scale;
+    a.rms_eps = rms_eps;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * feats, as_stream(stream));
+}
+
+int trmoe_dense_routed_gate_up_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                                   int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                                   int num_experts, int64_t expert_width, const int64_t* token_ids,
+                                   const int64_t* route_table, int64_t vocab_size, int top_k,
+                                   const float* route_weights, float shared_scale, float routed_scale,
+                                   const float* row_scale, float eps, void* h, int64_t ldh, void* stream) {
+    const int st = rms_args_ok("dense_routed_gate_up_rms", row_scale, eps, n_tokens);
+    if (st) return st;
+    return dense_routed_gate_up_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, w_packed, w_scale, shared_width,
+                                     num_experts, expert_width, token_ids, route_table, vocab_size, top_k,
+                                     route_weights, shared_scale, routed_scale, h, ldh, nullptr, 0, stream,
+                                     row_scale, row_scale ? 0.0f : eps);
 }
 
 int trmoe_dense_routed_gate_up(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
@@ -314,12 +371,11 @@ int trmoe_dense_routed_gate_up_save(int act_dtype, const void* x, int64_t n_toke
                                      top_k, route_weights, shared_scale, routed_scale, h, ldh, gu, ldgu, stream);
 }
 
-int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
-                         int64_t hidden, int64_t ldx, const int64_t* sorted_indices,
-                         const int32_t* expert_offsets, int num_experts, int top_k,
-                         const void* w_gate_up, const float* s_gate_up, const void* w_down,
-                         const float* s_down, int64_t expert_width, void* y, int64_t ldy,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+static int routed_experts_impl(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                               int64_t ldx, const int64_t* sorted_indices, const int32_t* expert_offsets,
+                               int num_experts, int top_k, const void* w_gate_up, const float* s_gate_up,
+                               const void* w_down, const float* s_down, int64_t expert_width, void* y, int64_t ldy,
+                               void* workspace, size_t workspace_bytes, void* stream, const float* row_scale) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "routed_experts: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && expert_width > 0, "routed_experts: bad dimensions");
     TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "routed_experts: num_experts must be in [1, 16]");
@@ -361,8 +417,11 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     a.ldy = ldy;
     const int64_t assignments = n_tokens * top_k;
     const size_t need = trmoe_routed_experts_workspace_bytes(act_dtype, assignments, expert_width);
-    if (workspace == nullptr || workspace_bytes < need)
+    if (workspace == nullptr || workspace_bytes < need) {
+        if (row_scale != nullptr)
+            return set_error(TRMOE_ERR_INVALID, "routed_experts_rms: needs trmoe_routed_experts_workspace_bytes()");
         return launch_routed(act_dtype, w_dtype, a, assignments, as_stream(stream));
+    }
     TRMOE_REQUIRE(aligned16(workspace), "routed_experts: workspace must be 16-byte aligned");
     TRMOE_REQUIRE(aligned16(y) && (ldy * elem_bytes(act_dtype)) % 16 == 0,
                   "routed_experts: y must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
@@ -386,6 +445,7 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     g.gather_mod = n_tokens;
     g.w_expert_stride = 2 * f_pad * a.wgu_ld;
     g.scale_expert_stride = 2 * f_pad;
+    g.row_scale = row_scale;
     int st = launch_gate_up_grouped(act_dtype, w_dtype, g, assignments, 2 * f_pad, as_stream(stream));
     if (st) return st;
     // down: h rows (partition order) -> y rows
@@ -408,6 +468,28 @@ int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_to
     d.w_expert_stride = a.H_pad * a.wd_ld;
     d.scale_expert_stride = a.H_pad;
     return launch_down_grouped(act_dtype, w_dtype, d, assignments, as_stream(stream));
+}
+
+int trmoe_routed_experts(int act_dtype, int w_dtype, const void* x, int64_t n_tokens,
+                         int64_t hidden, int64_t ldx, const int64_t* sorted_indices,
+                         const int32_t* expert_offsets, int num_experts, int top_k,
+                         const void* w_gate_up, const float* s_gate_up, const void* w_down,
+                         const float* s_down, int64_t expert_width, void* y, int64_t ldy,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    return routed_experts_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, sorted_indices, expert_offsets,
+                               num_experts, top_k, w_gate_up, s_gate_up, w_down, s_down, expert_width, y, ldy,
+                               workspace, workspace_bytes, stream, nullptr);
+}
+
+int trmoe_routed_experts_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                             int64_t ldx, const int64_t* sorted_indices, const int32_t* expert_offsets,
+                             int num_experts, int top_k, const void* w_gate_up, const float* s_gate_up,
+                             const void* w_down, const float* s_down, int64_t expert_width, const float* row_scale,
+                             void* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+    TRMOE_REQUIRE(n_tokens == 0 || row_scale != nullptr, "routed_experts_rms: null row_scale");
+    return routed_experts_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, sorted_indices, expert_offsets,
+                               num_experts, top_k, w_gate_up, s_gate_up, w_down, s_down, expert_width, y, ldy,
+                               workspace, workspace_bytes, stream, row_scale);
 }
 
 size_t trmoe_routed_experts_workspace_bytes(int act_dtype, int64_t n_assignments, int64_t expert_width) {

@@ -52,6 +52,12 @@ struct GateUpArgs {
     // in the packed column order of the weights.
     void* gu;
     int64_t ldgu;
+    // Fused RMSNorm (the weights hold W * norm_weight per input column): the
+    // gate and up accumulators of token t are multiplied by row_scale[t]
+    // before the SwiGLU.  row_scale == nullptr and rms_eps > 0: the decode
+    // kernels compute 1 / sqrt(mean(x_t^2) + rms_eps) themselves.
+    const float* row_scale;
+    float rms_eps;
     // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
     // (expert, row tile) pairs of a K1 partition; A rows are
     // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
@@ -215,6 +221,9 @@ int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_
 size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act);
 int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream);
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
+// row_scale[t] = 1 / sqrt(mean_k x[t, k]^2 + eps) in fp32 for t < n.
+int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, float eps, float* row_scale,
+                         hipStream_t stream);
 int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream);
 int routed_lds_bytes(int act, int64_t f_pad);
 int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t assignments, hipStream_t stream);

@@ -98,7 +98,8 @@ __device__ __forceinline__ void gate_up_routes(const GateUpArgs& a, int64_t m0, 
 // with LDS still in use by the copy (callers that reuse LDS barrier first).
 template <class Kind, class Shape, bool ROUTED = true>
 __device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
-                                                 int64_t n0, char* lds, const int (*s_route)[kMaxTopK]) {
+                                                 int64_t n0, char* lds, const int (*s_route)[kMaxTopK],
+                                                 const float* s_rscale = nullptr) {
     using T = typename Kind::T;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
@@ -123,8 +124,9 @@ __device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&a
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int rl = wm0 + tm * 32 + acc_row(lane, i);
-                const float g = acc[tm][2 * p][i] * sg;
-                const float u = acc[tm][2 * p + 1][i] * su;
+                const float rs = s_rscale != nullptr ? s_rscale[rl] : 1.0f;   // fused RMSNorm
+                const float g = acc[tm][2 * p][i] * sg * rs;
+                const float u = acc[tm][2 * p + 1][i] * su * rs;
                 float hv = silu_f(g) * u * mult;
                 if (routed) {
                     const int* rr = s_route[rl];
@@ -159,8 +161,9 @@ __device__ __forceinline__ void gate_up_epi_store(const GateUpArgs& a, int64_t m
 template <class Kind, class Shape, bool ROUTED = true>
 __device__ __forceinline__ void gate_up_epilogue(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
                                                  int64_t m0, int64_t n0, char* lds,
-                                                 const int (*s_route)[kMaxTopK]) {
-    gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route);
+                                                 const int (*s_route)[kMaxTopK],
+                                                 const float* s_rscale = nullptr) {
+    gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route, s_rscale);
     wait_lgkmcnt0();   // LDS tile complete; outstanding global loads (a next tile's operands) keep flying
     lds_barrier();
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
@@ -235,6 +238,17 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     } else {
         init_a<Shape>(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
     }
+    // fused RMSNorm: the row scales of the tile's rows (partition rows read
+    // their token's), read back in the epilogue after the main loop's barriers
+    __shared__ float s_rscale[Shape::BM];
+    if (a.row_scale != nullptr && threadIdx.x < Shape::BM) {
+        const int64_t row = m0 + threadIdx.x;
+        int64_t tok = row;
+        if constexpr (GROUPED) {
+            if (a.gather != nullptr && row < a.M) tok = (int64_t)((uint64_t)a.gather[row] % (uint64_t)a.gather_mod);
+        }
+        s_rscale[threadIdx.x] = row < a.M ? a.row_scale[tok] : 0.0f;
+    }
     typename BProvOf<Kind, FP8, Shape>::type bp;
     init_b<Kind, FP8, Shape>(bp, a.w, a.ldw, n0, a.K);
 
@@ -247,7 +261,8 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     zero_acc<Kind>(acc);
     tile_loop<Kind, Shape>(ap, bp, a.K, lds, wm0, wn0, acc);
     if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * Shape::BN);
-    gate_up_epilogue<Kind, Shape, ROUTED>(a, acc, m0, n0, lds, s_route);
+    gate_up_epilogue<Kind, Shape, ROUTED>(a, acc, m0, n0, lds, s_route,
+                                          a.row_scale != nullptr ? s_rscale : nullptr);
 }
 
 // Persistent form: gridDim.x workgroups walk the tiles (M fastest).  The
@@ -779,7 +794,7 @@ static int launch_gate_up_dma_balanced(const GateUpArgs& a, int64_t packed_rows,
 template <class Kind, bool FP8>
 static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int64_t big_blocks = ((a.M + 255) / 256) * (packed_rows / 256);
-    int ov = tile_override();
+    int ov = a.row_scale != nullptr ? (int)kTileAuto : tile_override();   // the default tiles apply row scales
     if (ov == kTileAuto)
         ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? (FP8 ? kTileF8Dma : kTileDma) : kTileSmall;
     if (packed_rows % 256 != 0) ov = kTileSmall;
@@ -894,10 +909,63 @@ static int launch_gate_up_save(int act, int wdt, const GateUpArgs& a, int64_t pa
               : launch_gate_up_save_kind<KindF32, false>(a, packed_rows, stream);
 }
 
+// One wave per token: the sum of squares of its row (16-byte loads, an
+// element tail for hidden % (16 / sizeof(T)) != 0), reduced across the wave.
+template <class T>
+__global__ __launch_bounds__(256) void k_rms_row_scale(const T* x, int64_t n, int hidden, int64_t ldx, float eps,
+                                                       float* out) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= n) return;
+    constexpr int kV = 16 / (int)sizeof(T);
+    const T* xr = x + row * ldx;
+    float s = 0.f;
+    const int full = hidden / kV * kV;
+    for (int k = lane * kV; k < full; k += 64 * kV) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(xr + k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (sizeof(T) == 2) {
+                const float lo = __builtin_bit_cast(float, v[j] << 16);
+                const float hi = __builtin_bit_cast(float, v[j] & 0xffff0000u);
+                s += lo * lo;
+                s += hi * hi;
+            } else {
+                const float f = __builtin_bit_cast(float, (uint32_t)v[j]);
+                s += f * f;
+            }
+        }
+    }
+    for (int k = full + lane; k < hidden; k += 64) {
+        const float f = to_f32(xr[k]);
+        s += f * f;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) out[row] = rsqrtf(s / (float)hidden + eps);
+}
+
+int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, float eps, float* row_scale,
+                         hipStream_t stream) {
+    if (n <= 0) return TRMOE_OK;
+    const dim3 grid((unsigned)((n + 3) / 4));
+    if (act == TRMOE_BF16)
+        hipLaunchKernelGGL(k_rms_row_scale<bf16_t>, grid, dim3(256), 0, stream, static_cast<const bf16_t*>(x), n,
+                           (int)hidden, ldx, eps, row_scale);
+    else if (act == TRMOE_F32)
+        hipLaunchKernelGGL(k_rms_row_scale<float>, grid, dim3(256), 0, stream, static_cast<const float*>(x), n,
+                           (int)hidden, ldx, eps, row_scale);
+    else
+        return set_error(TRMOE_ERR_UNSUPPORTED, "rms_row_scale: bf16 or f32 activations");
+    return check_launch("rms_row_scale");
+}
+
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     if (a.gu != nullptr) return launch_gate_up_save(act, wdt, a, packed_rows, stream);
-    if (a.M <= kSkinnyMaxTokens && tile_override() == kTileAuto && packed_rows % 64 == 0)
+    if (a.M <= kSkinnyMaxTokens && (tile_override() == kTileAuto || a.rms_eps > 0.0f) && packed_rows % 64 == 0)
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
+    if (a.row_scale == nullptr && a.rms_eps > 0.0f)
+        return set_error(TRMOE_ERR_INVALID, "gate_up: in-kernel RMSNorm scales need the decode kernels (n <= 128)");
     if (a.ids != nullptr) {
         // dense-routed: the shared columns as a plain gate|up launch, then the
         // expert columns with the routing epilogue

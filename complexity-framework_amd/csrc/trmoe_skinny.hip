@@ -88,11 +88,37 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, int o
 // are w_off[u] for the lane's row); with BR = 8 only its first 8 rows are
 // staged and the other 8 output columns of the block are to be ignored.  Spans [s0, s1) in batches of SB;
 // `region` holds SB * (MT + (SW ? NU : 0)) * 16 rows of 128 bytes.
+// Sum of squares of the activation elements in one 16-byte chunk.
+__device__ __forceinline__ float chunk_sumsq(KindBF16, u32x4 v) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float lo = __builtin_bit_cast(float, v[j] << 16);
+        const float hi = __builtin_bit_cast(float, v[j] & 0xffff0000u);
+        s += lo * lo;
+        s += hi * hi;
+    }
+    return s;
+}
+__device__ __forceinline__ float chunk_sumsq(KindF32, u32x4 v) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float f = __builtin_bit_cast(float, (uint32_t)v[j]);
+        s += f * f;
+    }
+    return s;
+}
+
+template <int MT>
+constexpr int ssq_rows() { return (MT * 16 + 63) / 64; }
+
 template <class Kind, bool FP8, int MT, int NU, int SB, bool SW, int BR = 16>
 __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_rows, int lda_b, char* region,
                                               __amdgpu_buffer_rsrc_t wr, const int (&w_row0)[NU], int ldw_b,
                                               const int (&w_off)[NU], int s0, int s1, int kb_a,
-                                              f32x4 (&acc)[MT][NU]) {
+                                              f32x4 (&acc)[MT][NU], bool ssq_on = false,
+                                              float* ssq = nullptr) {
     static_assert(!(SW && FP8), "e4m3 weight rows are 64 bytes per span: not staged");
     using WF = WFrag<Kind, FP8>;
     constexpr int kRowsA = MT * 16;
@@ -144,6 +170,25 @@ __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_r
         }
         wait_vmcnt<0>();
         asm volatile("" ::: "memory");
+        if (ssq_on) {
+            // fused RMSNorm: the lane's activation rows (lane, lane + 64) summed
+            // over this batch's spans, straight from the staged copies
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                if (sb + j < s1) {
+                    const char* st = region + j * kRows * kRowBytes;
+#pragma unroll
+                    for (int rr = 0; rr < ssq_rows<MT>(); ++rr) {
+                        const int row = lane + 64 * rr;
+                        if (row < kRowsA) {
+#pragma unroll
+                            for (int c = 0; c < 8; ++c)
+                                ssq[rr] += chunk_sumsq(Kind{}, *reinterpret_cast<const u32x4*>(st + lds_byte(row, c)));
+                        }
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < SB; ++j) {
             if (sb + j < s1) {
@@ -240,6 +285,8 @@ template <bool FP8, int MT, int NU, int NW>
 constexpr bool stage_weights() { return !FP8 && staged_batch<(MT + NU) * 16, NW>() >= 2; }
 template <bool FP8, int MT, int NU, int NW>
 constexpr int staged_rows() { return (MT + (stage_weights<FP8, MT, NU, NW>() ? NU : 0)) * 16; }
+template <int MT, int NW>
+constexpr int rms_slots() { return NW * MT * 16; }
 
 template <class Kind, bool FP8, int MT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
@@ -283,9 +330,34 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     f32x4 acc[MT][2];
     zero_acc16<MT, 2>(acc);
     char* region = reinterpret_cast<char*>(red) + wave * SB * kRows * kRowBytes;
+    // fused RMSNorm: per-token scales given (row_scale) or computed here from
+    // the staged activations (the sum over the waves' K spans)
+    const bool rms_in = a.row_scale == nullptr && a.rms_eps > 0.0f;
+    const bool rms = rms_in || a.row_scale != nullptr;
+    float ssq[ssq_rows<MT>()] = {};
     staged_k_loop<Kind, FP8, MT, 2, SB, SW>(ar, (int)a.M, (int)(a.ldx * (int64_t)sizeof(T)), region, wr, w_row0,
-                                            (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc);
+                                            (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc, rms_in, ssq);
+    __shared__ float s_ssq[rms_slots<MT, NW>()];
+    __shared__ float s_rs[MT * 16];
+    if (rms_in) {
+#pragma unroll
+        for (int rr = 0; rr < ssq_rows<MT>(); ++rr) {
+            const int row = (threadIdx.x & 63) + 64 * rr;
+            if (row < MT * 16) s_ssq[wave * MT * 16 + row] = ssq[rr];
+        }
+    }
     __syncthreads();   // every wave is done with its staging region
+    if (rms && threadIdx.x < MT * 16) {
+        float rs;
+        if (rms_in) {
+            float t = 0.f;
+            for (int w = 0; w < NW; ++w) t += s_ssq[w * MT * 16 + threadIdx.x];
+            rs = rsqrtf(t / (float)a.K + a.rms_eps);
+        } else {
+            rs = (int64_t)threadIdx.x < a.M ? a.row_scale[threadIdx.x] : 0.0f;
+        }
+        s_rs[threadIdx.x] = rs;
+    }
     skinny_stash<MT, 2>(red, acc);
     __syncthreads();
 
@@ -299,8 +371,9 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
         const int fl = l & 15;
         const float sg = a.w_scale ? a.w_scale[pg + fl] : 1.0f;
         const float su = a.w_scale ? a.w_scale[pg + 32 + fl] : 1.0f;
-        const float g = skinny_sum<MT, 2, NW>(red, tm, 0, i, l) * sg;
-        const float u = skinny_sum<MT, 2, NW>(red, tm, 1, i, l) * su;
+        const float rs = rms ? s_rs[row] : 1.0f;
+        const float g = skinny_sum<MT, 2, NW>(red, tm, 0, i, l) * sg * rs;
+        const float u = skinny_sum<MT, 2, NW>(red, tm, 1, i, l) * su * rs;
         float hv = silu_f(g) * u * mult;
         if (routed) {
             float tw = 0.f;

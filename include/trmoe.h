@@ -245,6 +245,41 @@ int trmoe_combine(int act_dtype, int64_t n_tokens, int64_t hidden, const void* y
                   void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Block MLP with the post-attention RMSNorm fused (F2; replaces, in
+ * complexity/models/block.py:271-278, `post_attention_layernorm` (RMSNorm,
+ * complexity/core/normalization/norms.py:46-55) feeding the MLP, as
+ * fused_rmsnorm_gate_up does in complexity_cuda/fused_mlp.py:362-428).
+ *
+ *     rmsnorm(x)_t = x_t * r_t * norm_weight,   r_t = 1 / sqrt(mean_k x_t,k^2 + eps)
+ *
+ * norm_weight scales input channels, so it is folded into the gate/up
+ * weights once (pack W * norm_weight[None, :], expert weights along their
+ * input axis) and r_t multiplies token t's gate and up accumulators before
+ * the SwiGLU.  The *_rms entry points are the ones above with that scale:
+ *   row_scale != NULL: r from trmoe_rms_row_scale (fp32 [n_tokens]);
+ *   row_scale == NULL: eps > 0 and n_tokens <= 128 -- the decode kernels sum
+ *   the squares of the activation rows they stage anyway (no extra launch).
+ * The residual add is trmoe_shared_down_combine's `residual` (x itself).
+ * ------------------------------------------------------------------------- */
+int trmoe_rms_row_scale(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx, float eps,
+                        float* row_scale, void* stream);
+int trmoe_shared_gate_up_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                             int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                             const float* row_scale, float eps, void* h, int64_t ldh, void* stream);
+int trmoe_dense_routed_gate_up_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                                   int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                                   int num_experts, int64_t expert_width, const int64_t* token_ids,
+                                   const int64_t* route_table, int64_t vocab_size, int top_k,
+                                   const float* route_weights, float shared_scale, float routed_scale,
+                                   const float* row_scale, float eps, void* h, int64_t ldh, void* stream);
+/* row_scale required; the workspace of trmoe_routed_experts_workspace_bytes() too. */
+int trmoe_routed_experts_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                             int64_t ldx, const int64_t* sorted_indices, const int32_t* expert_offsets,
+                             int num_experts, int top_k, const void* w_gate_up, const float* s_gate_up,
+                             const void* w_down, const float* s_down, int64_t expert_width, const float* row_scale,
+                             void* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Backward (bf16 / f32 weights; fp8 weights are inference-only).
  *
  * Together these keep the HIP path differentiable: they replace the autograd

@@ -35,6 +35,8 @@ Pinning (what checks each function beyond retyping it):
 * layer backward -- ``engine_backward`` (autograd of ``engine_forward``)
   against central finite differences in f64 (``torch.autograd.gradcheck``);
   the closed-form ``swiglu_backward`` against that autograd.
+* ``rms_norm`` -- torch's own ``F.rms_norm`` (an independent implementation)
+  and the closed form of a constant row (every element becomes sign * weight).
 """
 
 from __future__ import annotations
@@ -318,6 +320,19 @@ def engine_forward(x, token_ids, table, params: dict, *, route_weights: Sequence
                            params.get("shared_down"))
     routed = reference_topk_swiglu(flat_x, routes, g, u, d, route_weights)
     return (shared_scale * shared + routed_scale * routed).view(shape)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm.forward's formula (complexity/core/normalization/norms.py:53-55):
+    x * rsqrt(mean(x^2) + eps) * weight, in x's dtype."""
+    variance = x.pow(2).mean(-1, keepdim=True)
+    return weight * (x * torch.rsqrt(variance + eps))
+
+
+def engine_forward_norm_residual(x, token_ids, table, params: dict, norm_weight, eps: float, **kw):
+    """The MLP half of a block with its post-attention RMSNorm
+    (complexity/models/block.py:271-278): x + engine_forward(rms_norm(x))."""
+    return x + engine_forward(rms_norm(x, norm_weight, eps), token_ids, table, params, **kw)
 
 
 def engine_backward(x, token_ids, table, params: dict, dout, *, route_weights: Sequence[float],

@@ -266,6 +266,28 @@ def test_pytorch_backend_matches_token_by_token_definition():
     assert torch.allclose(out.double(), want, rtol=1e-5, atol=1e-5)
 
 
+def test_norm_residual_on_cpu_is_the_reference_block_formula():
+    """forward_norm_residual off the HIP backend: RMSNorm as norms.py:53-55
+    writes it, then residual + forward (block.py:271-278); also through the
+    MLP wrapper's norm-module form."""
+    eng = _engine()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 9, 32, generator=g) * 2.0
+    ids = torch.randint(0, 257, (2, 9), generator=g)
+    nw = torch.rand(32, generator=g) + 0.5
+    with torch.no_grad():
+        out = eng.forward_norm_residual(x, ids, nw, 1e-6)
+    assert eng.last_backend.selected is TRHashBackend.PYTORCH
+    params = {"expert_gate": eng.expert_gate, "expert_up": eng.expert_up, "expert_down": eng.expert_down,
+              "shared_gate": eng.shared_gate.weight, "shared_up": eng.shared_up.weight,
+              "shared_down": eng.shared_down.weight}
+    want = O.engine_forward_norm_residual(x.double(), ids, eng.route_table, {k: v.double() for k, v in params.items()},
+                                          nw.double(), 1e-6, route_weights=eng.config.route_weights)
+    assert torch.allclose(out.double(), want, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        eng.forward_norm_residual(x, ids, nw[:16], 1e-6)
+
+
 def test_capability_summary_contract_is_stable_across_shapes():
     keys = None
     for experts, k in ((4, 2), (16, 2), (8, 4), (1, 1)):

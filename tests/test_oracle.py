@@ -14,6 +14,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import trmoe_oracle as O
 
@@ -334,3 +335,46 @@ def test_swiglu_backward_closed_form_matches_autograd():
     torch.testing.assert_close(dg, dg_ref, rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(du, du_ref, rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(hm, h.detach(), rtol=1e-12, atol=1e-12)
+
+
+# --------------------------------------------------------------------------- RMSNorm (F2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_rms_norm_matches_torch_rms_norm(dtype):
+    """The oracle's restatement of norms.py:53-55 against torch's own
+    implementation of the same normalisation."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(37, 96, generator=g, dtype=dtype) * 3.0
+    w = torch.rand(96, generator=g, dtype=dtype) + 0.5
+    ref = F.rms_norm(x, (96,), weight=w, eps=1e-6)
+    assert torch.allclose(O.rms_norm(x, w, 1e-6), ref, rtol=1e-6 if dtype == torch.float64 else 1e-5, atol=0)
+
+
+def test_rms_norm_constant_rows_closed_form():
+    """A row of constant c normalises to sign(c) * weight (up to eps)."""
+    w = torch.linspace(0.5, 2.0, 64, dtype=torch.float64)
+    x = torch.tensor([[2.5] * 64, [-0.75] * 64], dtype=torch.float64)
+    y = O.rms_norm(x, w, 0.0)
+    assert torch.allclose(y[0], w, atol=1e-12)
+    assert torch.allclose(y[1], -w, atol=1e-12)
+
+
+def test_norm_residual_oracle_composes():
+    """engine_forward_norm_residual is x + engine_forward(rms_norm(x))."""
+    g = torch.Generator().manual_seed(3)
+    H, S, E, W, V = 32, 48, 4, 8, 50
+    params = {
+        "shared_gate": torch.randn(S, H, generator=g) * 0.1, "shared_up": torch.randn(S, H, generator=g) * 0.1,
+        "shared_down": torch.randn(H, S, generator=g) * 0.1,
+        "expert_gate": torch.randn(E, H, W, generator=g) * 0.1, "expert_up": torch.randn(E, H, W, generator=g) * 0.1,
+        "expert_down": torch.randn(E, W, H, generator=g) * 0.1,
+    }
+    table = torch.as_tensor(O.multi_hash_table(V, E, 2, 0))
+    x = torch.randn(2, 5, H, generator=g)
+    ids = torch.randint(0, V, (2, 5), generator=g)
+    nw = torch.rand(H, generator=g) + 0.5
+    got = O.engine_forward_norm_residual(x, ids, table, params, nw, 1e-6, route_weights=(0.6, 0.4))
+    xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * nw
+    want = x + O.engine_forward(xn, ids, table, params, route_weights=(0.6, 0.4))
+    assert torch.allclose(got, want, atol=1e-6)

@@ -288,6 +288,56 @@ def test_norm_residual_on_cpu_is_the_reference_block_formula():
         eng.forward_norm_residual(x, ids, nw[:16], 1e-6)
 
 
+def test_fp8_state_dict_round_trips_through_safetensors(tmp_path):
+    """F3: an fp8 engine's e4m3 weights, scales and persisted route table go
+    to disk with safetensors and come back into an engine built from another
+    seed and route seed: same keys as the reference plus the fp8 buffers,
+    identical tensors, identical outputs (the table is transplanted, not
+    regenerated; docs/tr-hash-engine.md:64-66)."""
+    from safetensors.torch import load_file, save_file
+
+    torch.manual_seed(1)
+    a = TRHashEngine(_config(precision=TRHashPrecision.FP8)).eval()
+    with torch.no_grad():
+        for p in a.parameters():
+            p.normal_(0.0, 0.2)
+    a.quantize_fp8_()
+    sd = a.state_dict()
+    for key in ("route_table", "fused_route_codes", "fused_expert_pairs", "expert_gate_fp8", "expert_gate_scale",
+                "shared_down_fp8", "shared_down_scale"):
+        assert key in sd, key
+    assert sd["expert_gate_fp8"].dtype == torch.float8_e4m3fn
+    path = tmp_path / "layer.safetensors"
+    save_file({k: v.contiguous() for k, v in sd.items()}, str(path))
+
+    torch.manual_seed(2)
+    b = TRHashEngine(_config(precision=TRHashPrecision.FP8, route_seed=0x1234567)).eval()
+    assert not torch.equal(b.route_table, a.route_table)
+    b.load_state_dict(load_file(str(path)))
+    for k, v in a.state_dict().items():
+        assert torch.equal(b.state_dict()[k].view(torch.uint8) if v.dtype == torch.float8_e4m3fn
+                           else b.state_dict()[k], v.view(torch.uint8) if v.dtype == torch.float8_e4m3fn else v), k
+    x = torch.randn(2, 7, 32)
+    ids = torch.randint(0, 257, (2, 7))
+    with torch.no_grad():
+        assert torch.equal(a(x, ids), b(x, ids))
+
+
+def test_load_route_table_transplants_and_validates():
+    eng = _engine()
+    other = _engine(route_seed=0x2468ACE)
+    assert not torch.equal(eng.route_table, other.route_table)
+    eng.load_route_table(other.route_table)
+    assert torch.equal(eng.route_table, other.route_table)
+    assert torch.equal(eng._active_route_table, other.route_table)
+    bad = other.route_table.clone()
+    bad[0, 0] = eng.config.num_experts
+    with pytest.raises(ValueError):
+        eng.load_route_table(bad)
+    with pytest.raises(ValueError):
+        eng.load_route_table(other.route_table[:, :10])
+
+
 def test_capability_summary_contract_is_stable_across_shapes():
     keys = None
     for experts, k in ((4, 2), (16, 2), (8, 4), (1, 1)):

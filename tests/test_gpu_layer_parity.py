@@ -321,3 +321,25 @@ def test_out_of_range_token_ids_are_clamped(gpu, strategy, n):
     assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["bf16"]
     clamped = _run(engine, x, ids.clamp(0, 999))
     assert torch.equal(out, clamped)
+
+
+def test_fp8_state_dict_loads_into_the_hip_path(gpu):
+    """F3 on the HIP backend: an fp8 engine's state dict (e4m3 codes, scales,
+    route table) loaded into an engine of another seed and route seed repacks
+    the kernel weights and reproduces the outputs bit for bit; the result
+    matches the oracle on the dequantised weights."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    common = dict(hidden_size=256, vocab_size=1000, num_experts=4, top_k=2, shared_width=512, expert_width=64,
+                  precision="fp8", backend="hip")
+    torch.manual_seed(21)
+    a = TRHashEngine(TRHashEngineConfig(**common)).to(gpu).eval()
+    torch.manual_seed(22)
+    b = TRHashEngine(TRHashEngineConfig(**common, route_seed=0x13579BD)).to(gpu).eval()
+    ids = torch.randint(0, 1000, (2, 40), device=gpu)
+    x = torch.randn(2, 40, 256, device=gpu).to(torch.bfloat16)
+    _run(b, x, ids)   # b's own packs exist before the load
+    b.load_state_dict(a.state_dict())
+    ya, yb = _run(a, x, ids), _run(b, x, ids)
+    assert torch.equal(ya, yb)
+    assert O.normwise_rel_err(ya, _oracle(a, x, ids, dequant_fp8=True)) <= BOUND["fp8"]

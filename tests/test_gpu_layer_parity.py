@@ -343,3 +343,31 @@ def test_fp8_state_dict_loads_into_the_hip_path(gpu):
     ya, yb = _run(a, x, ids), _run(b, x, ids)
     assert torch.equal(ya, yb)
     assert O.normwise_rel_err(ya, _oracle(a, x, ids, dequant_fp8=True)) <= BOUND["fp8"]
+
+
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("experts,top_k", [(8, 4), (16, 4), (16, 2), (2, 1)])
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_expert_topk_matrix_against_oracle(gpu, strategy, experts, top_k, precision):
+    """The FUSED/CGGR-vs-PYTORCH checks of test_tr_hash_engine.py:328-398 and
+    test_tr_hash_fused_kernel_parity.py:148-201, widened to the supported
+    (E, k) matrix and both routed strategies; shape (2, 11, 16) at V = 257 as
+    there, plus a 300-token batch (tile kernels) with ragged widths."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    print(f"matrix {strategy} E={experts} k={top_k} {precision}", flush=True)
+    dt = torch.float32 if precision == "fp32" else torch.bfloat16
+    for (b, t, hidden, shared, width) in ((2, 11, 16, 24, 8), (3, 100, 72, 200, 40)):
+        torch.manual_seed(experts * 10 + top_k + hidden)
+        eng = TRHashEngine(TRHashEngineConfig(hidden_size=hidden, vocab_size=257, num_experts=experts, top_k=top_k,
+                                              shared_width=shared, expert_width=width, precision=precision,
+                                              backend="hip")).to(gpu)
+        with torch.no_grad():
+            for p in eng.parameters():
+                p.normal_(0.0, 0.2)
+        eng = eng.to(dt).eval()
+        eng.routed_strategy = strategy
+        x = torch.randn(b, t, hidden, device=gpu).to(dt)
+        ids = torch.randint(0, 257, (b, t), device=gpu)
+        out = _run(eng, x, ids)
+        assert O.normwise_rel_err(out, _oracle(eng, x, ids)) <= BOUND[precision]

@@ -338,6 +338,29 @@ def test_load_route_table_transplants_and_validates():
         eng.load_route_table(other.route_table[:, :10])
 
 
+def test_capacity_change_and_table_load_invalidate_captured_graphs():
+    """test_tr_hash_dynamic_moe.py:166-170: captured graphs are dropped when
+    the routing they baked in changes."""
+    eng = _engine(num_experts=8, top_k=2)
+    eng._graph_pool["sentinel"] = object()
+    eng.set_active_capacity(num_experts=4)
+    assert eng._graph_pool == {}
+    eng._graph_pool["sentinel"] = object()
+    eng.load_route_table(eng.route_table.clone())
+    assert eng._graph_pool == {}
+
+
+def test_engine_materialises_every_shared_swiglu_projection():
+    """test_tr_hash_shared_swiglu_contract.py:103-125: gate/up [S, H] and
+    down [H, S] exist as linears whenever shared_width > 0."""
+    eng = TRHashEngine(_config(hidden_size=32, shared_width=16, expert_width=8))
+    assert tuple(eng.shared_gate.weight.shape) == (16, 32)
+    assert tuple(eng.shared_up.weight.shape) == (16, 32)
+    assert tuple(eng.shared_down.weight.shape) == (32, 16)
+    none = TRHashEngine(_config(hidden_size=32, shared_width=0, expert_width=8))
+    assert none.shared_gate is None and none.shared_up is None and none.shared_down is None
+
+
 def test_capability_summary_contract_is_stable_across_shapes():
     keys = None
     for experts, k in ((4, 2), (16, 2), (8, 4), (1, 1)):

@@ -237,8 +237,9 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
 def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
     """Forward + backward through autograd on the HIP backend (the layer's
     gradients of x and every weight), timed with HIP events like the forward.
-    Useful backward work is twice the forward's FLOPs; the backward kernel
-    recomputes gate|up, so it executes 1.5x that."""
+    Useful backward work is twice the forward's FLOPs.  Above 128 tokens the
+    forward also stores the raw gate|up outputs and the backward reads them
+    back, so it executes exactly that (decode sizes recompute gate|up)."""
     from complexity_amd.tr_hash import TRHashBackend
 
     xg = x.detach().clone().requires_grad_(True)

@@ -30,6 +30,19 @@ _c_size = ctypes.c_size_t
 _c_float = ctypes.c_float
 
 # name -> (restype, argtypes); mirrors include/trmoe.h exactly
+class CallExtras(ctypes.Structure):
+    """trmoe_call_extras (include/trmoe.h): optional extras of the *_ex calls."""
+
+    _fields_ = [
+        ("row_scale", ctypes.c_void_p),
+        ("rms_eps", ctypes.c_float),
+        ("w_frag", ctypes.c_void_p),
+        ("w_frag_cols", ctypes.c_int64),
+    ]
+
+
+_c_extras = ctypes.POINTER(CallExtras)
+
 SIGNATURES = {
     "trmoe_abi_version": (_c_int, []),
     "trmoe_last_error": (ctypes.c_char_p, []),
@@ -88,6 +101,22 @@ SIGNATURES = {
         _c_int,
         [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp,
          _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_size, _c_vp],
+    ),
+    "trmoe_fragment_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "trmoe_pack_fragments": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "trmoe_shared_gate_up_ex": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_extras, _c_vp],
+    ),
+    "trmoe_dense_routed_gate_up_ex": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_i64, _c_vp,
+         _c_vp, _c_i64, _c_int, _c_vp, _c_float, _c_float, _c_vp, _c_i64, _c_extras, _c_vp],
+    ),
+    "trmoe_shared_down_combine_ex": (
+        _c_int,
+        [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,
+         _c_int, _c_vp, _c_float, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_size, _c_extras, _c_vp],
     ),
     "trmoe_shared_gate_up_save": (
         _c_int,

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -227,10 +227,12 @@ def pack_dense_routed(shared_gate, shared_up, shared_down, gate, up, down):
 def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: int, num_experts: int,
                          expert_width: int, token_ids: torch.Tensor, route_table: torch.Tensor,
                          route_weights: Sequence[float], shared_scale: float, routed_scale: float,
-                         save: bool = False, row_scale: Optional[torch.Tensor] = None, rms_eps: float = 0.0):
+                         save: bool = False, row_scale: Optional[torch.Tensor] = None, rms_eps: float = 0.0,
+                         w_frag=None):
     """h_ext[N, F]: shared SwiGLU features and route-weighted expert features.
     save: also return the raw gate|up outputs gu[N, 2F] (packed column order).
-    row_scale / rms_eps: fused RMSNorm (trmoe_dense_routed_gate_up_rms)."""
+    row_scale / rms_eps: fused RMSNorm; w_frag: (pack_fragments copy, cols) for
+    decode sizes (trmoe_dense_routed_gate_up_ex)."""
     lib = _lib()
     _require_cuda(x, w_packed, token_ids, route_table)
     x = rows16(x)
@@ -250,14 +252,14 @@ def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: 
                                                  _stream(x))
         N.check(st, "trmoe_dense_routed_gate_up_save")
         return h, gu
-    if row_scale is not None or rms_eps > 0.0:
-        st = lib.trmoe_dense_routed_gate_up_rms(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
-                                                x.stride(0), _p(w_packed), None, shared_width, num_experts,
-                                                expert_width, _p(ids), _p(table), table.shape[1], table.shape[0],
-                                                ctypes.cast(rw, ctypes.c_void_p), float(shared_scale),
-                                                float(routed_scale), _p(row_scale), float(rms_eps), _p(h), F,
-                                                _stream(x))
-        N.check(st, "trmoe_dense_routed_gate_up_rms")
+    if row_scale is not None or rms_eps > 0.0 or w_frag is not None:
+        ex, _keep = _extras(row_scale, rms_eps, w_frag)
+        st = lib.trmoe_dense_routed_gate_up_ex(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
+                                               x.stride(0), _p(w_packed), None, shared_width, num_experts,
+                                               expert_width, _p(ids), _p(table), table.shape[1], table.shape[0],
+                                               ctypes.cast(rw, ctypes.c_void_p), float(shared_scale),
+                                               float(routed_scale), _p(h), F, ex, _stream(x))
+        N.check(st, "trmoe_dense_routed_gate_up_ex")
         return h
     st = lib.trmoe_dense_routed_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
                                         x.stride(0), _p(w_packed), None, shared_width, num_experts, expert_width,
@@ -274,10 +276,11 @@ def dense_routed_gate_up(x: torch.Tensor, w_packed: torch.Tensor, shared_width: 
 
 def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[torch.Tensor],
                    shared_width: int, save: bool = False, row_scale: Optional[torch.Tensor] = None,
-                   rms_eps: float = 0.0):
+                   rms_eps: float = 0.0, w_frag=None):
     """h[N, round_up(S,128)] = silu(x Wg^T) * (x Wu^T).  save: also return the
     raw gate|up outputs gu[N, 2 round_up(S,128)] (bf16/f32 weights).
-    row_scale / rms_eps: fused RMSNorm (trmoe_shared_gate_up_rms)."""
+    row_scale / rms_eps: fused RMSNorm; w_frag: (pack_fragments copy, cols)
+    for decode sizes (trmoe_shared_gate_up_ex)."""
     lib = _lib()
     _require_cuda(x, w_packed)
     x = rows16(x)
@@ -290,11 +293,12 @@ def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[to
                                            shared_width, _p(h), ldh, _p(gu), 2 * ldh, _stream(x))
         N.check(st, "trmoe_shared_gate_up_save")
         return h, gu
-    if row_scale is not None or rms_eps > 0.0:
-        st = lib.trmoe_shared_gate_up_rms(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
-                                          x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(row_scale),
-                                          float(rms_eps), _p(h), ldh, _stream(x))
-        N.check(st, "trmoe_shared_gate_up_rms")
+    if row_scale is not None or rms_eps > 0.0 or w_frag is not None:
+        ex, _keep = _extras(row_scale, rms_eps, w_frag)
+        st = lib.trmoe_shared_gate_up_ex(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
+                                         x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(h), ldh, ex,
+                                         _stream(x))
+        N.check(st, "trmoe_shared_gate_up_ex")
         return h
     st = lib.trmoe_shared_gate_up(dtype_code(x.dtype), dtype_code(w_packed.dtype), _p(x), n, hidden,
                                   x.stride(0), _p(w_packed), _p(w_scale), shared_width, _p(h), ldh,
@@ -349,6 +353,33 @@ def rms_row_scale(x: torch.Tensor, eps: float) -> torch.Tensor:
     return r
 
 
+def _extras(row_scale: Optional[torch.Tensor] = None, rms_eps: float = 0.0, w_frag=None):
+    """trmoe_call_extras for the *_ex calls; w_frag = (fragment copy, cols)."""
+    e = N.CallExtras()
+    e.row_scale = _p(row_scale)
+    e.rms_eps = float(rms_eps)
+    if w_frag is not None:
+        e.w_frag = _p(w_frag[0])
+        e.w_frag_cols = int(w_frag[1])
+    return ctypes.byref(e), e
+
+
+def pack_fragments(w_packed: torch.Tensor, cols: int) -> tuple:
+    """(fragment-major copy of a packed bf16/f32 weight, cols) for the decode
+    kernels (trmoe_pack_fragments); cols is the K of the calls that use it."""
+    lib = _lib()
+    _require_cuda(w_packed)
+    rows, ld = w_packed.shape
+    nbytes = lib.trmoe_fragment_bytes(dtype_code(w_packed.dtype), rows, cols)
+    if nbytes == 0:
+        raise ValueError("pack_fragments: bf16/f32 weights with rows % 16 == 0")
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=w_packed.device)
+    st = lib.trmoe_pack_fragments(dtype_code(w_packed.dtype), _p(w_packed), rows, cols, ld, _p(dst),
+                                  _stream(w_packed))
+    N.check(st, "trmoe_pack_fragments")
+    return dst, int(cols)
+
+
 def _weights_arg(route_weights: Sequence[float]):
     arr = (ctypes.c_float * 4)(*[float(w) for w in list(route_weights)[:4]])
     return arr
@@ -373,7 +404,9 @@ def _down_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor, w_scale, hidden: int,
                         y: Optional[torch.Tensor], inverse: Optional[torch.Tensor], top_k: int,
                         route_weights: Sequence[float], shared_scale: float, routed_scale: float,
-                        residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                        residual: Optional[torch.Tensor] = None, w_frag=None) -> torch.Tensor:
+    """out = shared_scale * h Wd^T + routed_scale * combine(y) (+ residual);
+    w_frag: (pack_fragments copy of w_down, shared_width) for decode sizes."""
     lib = _lib()
     _require_cuda(h, w_down, y, inverse, residual)
     n = h.shape[0]
@@ -381,6 +414,15 @@ def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor
     rw = _weights_arg(route_weights)
     ws_bytes = lib.trmoe_shared_down_combine_workspace_bytes(dtype_code(h.dtype), n, shared_width, hidden)
     ws = _down_workspace(h.device, ws_bytes) if ws_bytes else None
+    if w_frag is not None:
+        ex, _keep = _extras(w_frag=w_frag)
+        st = lib.trmoe_shared_down_combine_ex(
+            dtype_code(h.dtype), dtype_code(w_down.dtype), _p(h), n, shared_width, h.stride(0), _p(w_down),
+            _p(w_scale), hidden, _p(y), hidden, _p(inverse), top_k, ctypes.cast(rw, ctypes.c_void_p),
+            float(shared_scale), float(routed_scale), _p(residual),
+            residual.stride(0) if residual is not None else 0, _p(out), hidden, _p(ws), ws_bytes, ex, _stream(h))
+        N.check(st, "trmoe_shared_down_combine_ex")
+        return out
     st = lib.trmoe_shared_down_combine(
         dtype_code(h.dtype), dtype_code(w_down.dtype), _p(h), n, shared_width, h.stride(0), _p(w_down),
         _p(w_scale), hidden, _p(y), hidden, _p(inverse), top_k, ctypes.cast(rw, ctypes.c_void_p),
@@ -444,6 +486,22 @@ class PackedLayer:
     dense_gate_up: Optional[torch.Tensor] = None     # dense-routed fused weights
     dense_down: Optional[torch.Tensor] = None
     dense_features: int = 0
+    # fragment-major copies for decode-sized calls, built on first use:
+    # name -> (copy, cols)
+    frag: dict = field(default_factory=dict)
+
+    def fragments(self, name: str, cols: int):
+        """pack_fragments of the bf16/f32 weight `name` (None for fp8)."""
+        if self.act_dtype not in (torch.bfloat16, torch.float32):
+            return None
+        w = getattr(self, name)
+        if w is None or w.dtype != self.act_dtype:
+            return None
+        got = self.frag.get(name)
+        if got is None:
+            got = pack_fragments(w, cols)
+            self.frag[name] = got
+        return got
 
 
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
@@ -474,14 +532,18 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
             eps_in = float(norm_eps)
         else:
             rscale = rms_row_scale(x, norm_eps)
+    # decode sizes read the weights through their fragment-major copies
+    decode = n <= SKINNY_MAX_TOKENS and not save
     if packed.strategy == STRATEGY_DENSE:
         h = dense_routed_gate_up(x, packed.dense_gate_up, packed.shared_width, packed.num_experts,
                                  packed.expert_width, token_ids, route_table, route_weights, shared_scale,
-                                 routed_scale, save=save, row_scale=rscale, rms_eps=eps_in)
+                                 routed_scale, save=save, row_scale=rscale, rms_eps=eps_in,
+                                 w_frag=packed.fragments("dense_gate_up", hidden) if decode else None)
         if save:
             h, gu = h
         out = shared_down_combine(h, packed.dense_features, packed.dense_down, None, hidden, None, None,
-                                  top_k, route_weights, 1.0, 1.0, residual)
+                                  top_k, route_weights, 1.0, 1.0, residual,
+                                  w_frag=packed.fragments("dense_down", packed.dense_features) if decode else None)
         return (out, gu) if save else out
     sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, packed.num_experts, order)
     y = routed_experts(x, sorted_idx, offsets, packed.num_experts, top_k, packed.expert_gate_up,
@@ -489,12 +551,14 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
                        packed.expert_width, row_scale=rscale)
     if packed.shared_width > 0:
         h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width, save=save,
-                           row_scale=rscale)
+                           row_scale=rscale,
+                           w_frag=packed.fragments("shared_gate_up", hidden) if decode else None)
         if save:
             h, gu = h
         out = shared_down_combine(h, packed.shared_width, packed.shared_down, packed.shared_down_scale,
                                   hidden, y, inverse, top_k, route_weights, shared_scale, routed_scale,
-                                  residual)
+                                  residual,
+                                  w_frag=packed.fragments("shared_down", packed.shared_width) if decode else None)
     else:
         out = combine(y, inverse, n, top_k, route_weights, routed_scale, residual)
     return (out, gu) if save else out

@@ -195,7 +195,8 @@ static int rms_args_ok(const char* who, const float* row_scale, float eps, int64
 static int shared_gate_up_impl(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
                                int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
                                void* h, int64_t ldh, void* gu, int64_t ldgu, void* stream,
-                               const float* row_scale = nullptr, float rms_eps = 0.0f) {
+                               const float* row_scale = nullptr, float rms_eps = 0.0f,
+                               const void* w_frag = nullptr) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_gate_up: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_gate_up: bad dimensions");
     TRMOE_REQUIRE(ldx >= hidden, "shared_gate_up: ldx < hidden");
@@ -231,6 +232,7 @@ static int shared_gate_up_impl(int act_dtype, int w_dtype, const void* x, int64_
     a.ldgu = ldgu;
     a.row_scale = row_scale;
     a.rms_eps = rms_eps;
+    a.w_frag = w_frag;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * round_up(shared_width, 128), as_stream(stream));
 }
 
@@ -285,7 +287,8 @@ static int dense_routed_gate_up_impl(int act_dtype, int w_dtype, const void* x, 
                                      const int64_t* route_table, int64_t vocab_size, int top_k,
                                      const float* route_weights, float shared_scale, float routed_scale, void* h,
                                      int64_t ldh, void* gu, int64_t ldgu, void* stream,
-                                     const float* row_scale = nullptr, float rms_eps = 0.0f) {
+                                     const float* row_scale = nullptr, float rms_eps = 0.0f,
+                                     const void* w_frag = nullptr) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "dense_routed_gate_up: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width >= 0 && expert_width > 0,
                   "dense_routed_gate_up: bad dimensions");
@@ -327,6 +330,7 @@ static int dense_routed_gate_up_impl(int act_dtype, int w_dtype, const void* x, 
     a.ldgu = ldgu;
     a.row_scale = row_scale;
     a.rms_eps = rms_eps;
+    a.w_frag = w_frag;
     return launch_gate_up(act_dtype, w_dtype, a, 2 * feats, as_stream(stream));
 }
 
@@ -497,13 +501,12 @@ size_t trmoe_routed_experts_workspace_bytes(int act_dtype, int64_t n_assignments
     return (size_t)(n_assignments * round_up(expert_width, 64) * elem_bytes(act_dtype));
 }
 
-int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
-                              int64_t shared_width, int64_t ldh, const void* w_down,
-                              const float* w_scale, int64_t hidden, const void* y, int64_t ldy,
-                              const int64_t* inverse, int top_k, const float* route_weights,
-                              float shared_scale, float routed_scale, const void* residual,
-                              int64_t ldr, void* out, int64_t ldo, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+static int shared_down_combine_impl(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
+                                    int64_t shared_width, int64_t ldh, const void* w_down, const float* w_scale,
+                                    int64_t hidden, const void* y, int64_t ldy, const int64_t* inverse, int top_k,
+                                    const float* route_weights, float shared_scale, float routed_scale,
+                                    const void* residual, int64_t ldr, void* out, int64_t ldo, void* workspace,
+                                    size_t workspace_bytes, void* stream, const void* w_frag) {
     TRMOE_REQUIRE(valid_pair(act_dtype, w_dtype), "shared_down_combine: unsupported dtype pair");
     TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_down_combine: bad dimensions");
     TRMOE_REQUIRE(ldh >= shared_width && ldo >= hidden, "shared_down_combine: bad leading dimension");
@@ -546,12 +549,104 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
         a.vec_ok = aligned16(out) && (ldo * eb) % 16 == 0 && (y == nullptr || (aligned16(y) && (ldy * eb) % 16 == 0)) &&
                    (residual == nullptr || (aligned16(residual) && (ldr * eb) % 16 == 0));
     }
+    a.w_frag = w_frag;
     const size_t need = down_skinny_workspace_bytes(n_tokens, hidden, shared_width, act_dtype);
     if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
         TRMOE_REQUIRE(aligned16(workspace), "shared_down_combine: workspace must be 16-byte aligned");
         return launch_down_skinny(act_dtype, w_dtype, a, workspace, as_stream(stream));
     }
     return launch_down_combine(act_dtype, w_dtype, a, as_stream(stream));
+}
+
+int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t n_tokens,
+                              int64_t shared_width, int64_t ldh, const void* w_down,
+                              const float* w_scale, int64_t hidden, const void* y, int64_t ldy,
+                              const int64_t* inverse, int top_k, const float* route_weights,
+                              float shared_scale, float routed_scale, const void* residual,
+                              int64_t ldr, void* out, int64_t ldo, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+    return shared_down_combine_impl(act_dtype, w_dtype, h, n_tokens, shared_width, ldh, w_down, w_scale, hidden, y,
+                                    ldy, inverse, top_k, route_weights, shared_scale, routed_scale, residual, ldr,
+                                    out, ldo, workspace, workspace_bytes, stream, nullptr);
+}
+
+size_t trmoe_fragment_bytes(int dtype, int64_t rows, int64_t cols) {
+    const int eb = elem_bytes(dtype);
+    if ((dtype != TRMOE_F32 && dtype != TRMOE_BF16) || rows <= 0 || rows % 16 != 0 || cols <= 0) return 0;
+    return (size_t)(rows / 16) * (size_t)((cols * eb + 63) / 64) * 1024;
+}
+
+int trmoe_pack_fragments(int dtype, const void* packed, int64_t rows, int64_t cols, int64_t ld, void* dst,
+                         void* stream) {
+    TRMOE_REQUIRE(dtype == TRMOE_F32 || dtype == TRMOE_BF16, "pack_fragments: bf16 or f32 weights");
+    TRMOE_REQUIRE(rows > 0 && rows % 16 == 0 && cols > 0 && ld >= round_up(cols, 8),
+                  "pack_fragments: rows must be a positive multiple of 16, ld >= round_up(cols, 8)");
+    TRMOE_REQUIRE(packed && dst, "pack_fragments: null pointer");
+    TRMOE_REQUIRE(aligned16(packed) && aligned16(dst), "pack_fragments: buffers must be 16-byte aligned");
+    TRMOE_REQUIRE(rows * ld * elem_bytes(dtype) < ((int64_t)1 << 40), "pack_fragments: too large");
+    return launch_pack_fragments(packed, rows, cols * elem_bytes(dtype), ld * elem_bytes(dtype), dst,
+                                 as_stream(stream));
+}
+
+// Extras of the *_ex entry points: validated against the call they ride on.
+static int extras_ok(const char* who, const trmoe_call_extras* ex, int act_dtype, int w_dtype, int64_t k,
+                     int64_t n_tokens, bool rms_allowed) {
+    if (ex == nullptr) return TRMOE_OK;
+    if (ex->w_frag != nullptr) {
+        if (w_dtype != act_dtype || (act_dtype != TRMOE_F32 && act_dtype != TRMOE_BF16)) {
+            std::string m = std::string(who) + ": w_frag needs bf16 or f32 weights";
+            return set_error(TRMOE_ERR_INVALID, m.c_str());
+        }
+        if (!aligned16(ex->w_frag) || ex->w_frag_cols != k) {
+            std::string m = std::string(who) + ": w_frag must be 16-byte aligned and packed with cols = " +
+                            std::to_string(k);
+            return set_error(TRMOE_ERR_INVALID, m.c_str());
+        }
+    }
+    if (!rms_allowed && (ex->row_scale != nullptr || ex->rms_eps != 0.0f)) {
+        std::string m = std::string(who) + ": no RMSNorm scales on this call";
+        return set_error(TRMOE_ERR_INVALID, m.c_str());
+    }
+    if (ex->row_scale != nullptr || ex->rms_eps > 0.0f) return rms_args_ok(who, ex->row_scale, ex->rms_eps, n_tokens);
+    return TRMOE_OK;
+}
+
+int trmoe_shared_gate_up_ex(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                            int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width, void* h,
+                            int64_t ldh, const trmoe_call_extras* extras, void* stream) {
+    const int st = extras_ok("shared_gate_up_ex", extras, act_dtype, w_dtype, hidden, n_tokens, true);
+    if (st) return st;
+    const trmoe_call_extras e = extras ? *extras : trmoe_call_extras{};
+    return shared_gate_up_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, w_packed, w_scale, shared_width, h,
+                               ldh, nullptr, 0, stream, e.row_scale, e.row_scale ? 0.0f : e.rms_eps, e.w_frag);
+}
+
+int trmoe_dense_routed_gate_up_ex(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                                  int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                                  int num_experts, int64_t expert_width, const int64_t* token_ids,
+                                  const int64_t* route_table, int64_t vocab_size, int top_k,
+                                  const float* route_weights, float shared_scale, float routed_scale, void* h,
+                                  int64_t ldh, const trmoe_call_extras* extras, void* stream) {
+    const int st = extras_ok("dense_routed_gate_up_ex", extras, act_dtype, w_dtype, hidden, n_tokens, true);
+    if (st) return st;
+    const trmoe_call_extras e = extras ? *extras : trmoe_call_extras{};
+    return dense_routed_gate_up_impl(act_dtype, w_dtype, x, n_tokens, hidden, ldx, w_packed, w_scale, shared_width,
+                                     num_experts, expert_width, token_ids, route_table, vocab_size, top_k,
+                                     route_weights, shared_scale, routed_scale, h, ldh, nullptr, 0, stream,
+                                     e.row_scale, e.row_scale ? 0.0f : e.rms_eps, e.w_frag);
+}
+
+int trmoe_shared_down_combine_ex(int act_dtype, int w_dtype, const void* h, int64_t n_tokens, int64_t shared_width,
+                                 int64_t ldh, const void* w_down, const float* w_scale, int64_t hidden, const void* y,
+                                 int64_t ldy, const int64_t* inverse, int top_k, const float* route_weights,
+                                 float shared_scale, float routed_scale, const void* residual, int64_t ldr, void* out,
+                                 int64_t ldo, void* workspace, size_t workspace_bytes,
+                                 const trmoe_call_extras* extras, void* stream) {
+    const int st = extras_ok("shared_down_combine_ex", extras, act_dtype, w_dtype, shared_width, n_tokens, false);
+    if (st) return st;
+    return shared_down_combine_impl(act_dtype, w_dtype, h, n_tokens, shared_width, ldh, w_down, w_scale, hidden, y,
+                                    ldy, inverse, top_k, route_weights, shared_scale, routed_scale, residual, ldr,
+                                    out, ldo, workspace, workspace_bytes, stream, extras ? extras->w_frag : nullptr);
 }
 
 size_t trmoe_shared_down_combine_workspace_bytes(int act_dtype, int64_t n_tokens, int64_t shared_width,

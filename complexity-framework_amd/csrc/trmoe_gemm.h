@@ -58,6 +58,9 @@ struct GateUpArgs {
     // kernels compute 1 / sqrt(mean(x_t^2) + rms_eps) themselves.
     const float* row_scale;
     float rms_eps;
+    // Fragment-major copy of w (trmoe_pack_fragments) for the decode kernels,
+    // or null: bf16/f32 weights, K groups of 64 bytes per 16-row block.
+    const void* w_frag;
     // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
     // (expert, row tile) pairs of a K1 partition; A rows are
     // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
@@ -93,6 +96,7 @@ struct DownArgs {
     void* out;
     int64_t ldo;
     int vec_ok;             // y / residual / out rows 16-byte aligned (vector epilogue)
+    const void* w_frag;     // fragment-major copy of w for the decode kernels, or null
     // Expert-grouped mode (offsets != nullptr): blockIdx.x walks the
     // (expert, row tile) pairs of a K1 partition; A rows are
     // a[gather[r] % gather_mod] (contiguous partition rows r when gather is
@@ -221,6 +225,11 @@ int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_
 size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act);
 int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream);
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
+// Fragment-major copy of a packed [rows, ld] weight (rows % 16 == 0):
+// block (r / 16, K group g of 64 bytes) is 1 KiB at (r/16 * G + g) * 1024,
+// laid out [16-byte chunk q][row r % 16][16 bytes], zeros past kbytes.
+int launch_pack_fragments(const void* src, int64_t rows, int64_t kbytes, int64_t ld_bytes, void* dst,
+                          hipStream_t stream);
 // row_scale[t] = 1 / sqrt(mean_k x[t, k]^2 + eps) in fp32 for t < n.
 int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, float eps, float* row_scale,
                          hipStream_t stream);

@@ -86,7 +86,9 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, int o
 // into registers (16 rows x 64 bytes per instruction).  Weight block u is the 16 rows from
 // row w_row0[u] of the weight descriptor (whose byte offsets, with SW off,
 // are w_off[u] for the lane's row); with BR = 8 only its first 8 rows are
-// staged and the other 8 output columns of the block are to be ignored.  Spans [s0, s1) in batches of SB;
+// staged and the other 8 output columns of the block are to be ignored.
+// FRAG (with SW off): the descriptor is a fragment-major copy whose block 0
+// is row 0, and weight fragments are 1 KiB contiguous loads.  Spans [s0, s1) in batches of SB;
 // `region` holds SB * (MT + (SW ? NU : 0)) * 16 rows of 128 bytes.
 // Sum of squares of the activation elements in one 16-byte chunk.
 __device__ __forceinline__ float chunk_sumsq(KindBF16, u32x4 v) {
@@ -113,7 +115,7 @@ __device__ __forceinline__ float chunk_sumsq(KindF32, u32x4 v) {
 template <int MT>
 constexpr int ssq_rows() { return (MT * 16 + 63) / 64; }
 
-template <class Kind, bool FP8, int MT, int NU, int SB, bool SW, int BR = 16>
+template <class Kind, bool FP8, int MT, int NU, int SB, bool SW, int BR = 16, bool FRAG = false>
 __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_rows, int lda_b, char* region,
                                               __amdgpu_buffer_rsrc_t wr, const int (&w_row0)[NU], int ldw_b,
                                               const int (&w_off)[NU], int s0, int s1, int kb_a,
@@ -164,7 +166,18 @@ __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_r
 #pragma unroll
                     for (int h = 0; h < 2; ++h)
 #pragma unroll
-                        for (int u = 0; u < NU; ++u) wv[j][h][u] = WF::load(wr, w_off[u], 2 * sp + h, q, kb_a);
+                        for (int u = 0; u < NU; ++u) {
+                            const int gg = 2 * sp + h;
+                            if constexpr (FRAG) {
+                                // fragment-major weights: block w_row0[u] / 16, group gg is
+                                // 1 KiB, and lane l's 16 bytes sit at 16 l
+                                const int G = (kb_a + 63) / 64;
+                                wv[j][h][u] = buffer_load16(
+                                    wr, 64 * gg < kb_a ? ((w_row0[u] >> 4) * G + gg) * 1024 + 16 * lane : kOutOfRange);
+                            } else {
+                                wv[j][h][u] = WF::load(wr, w_off[u], gg, q, kb_a);
+                            }
+                        }
                 }
             }
         }
@@ -288,7 +301,7 @@ constexpr int staged_rows() { return (MT + (stage_weights<FP8, MT, NU, NW>() ? N
 template <int MT, int NW>
 constexpr int rms_slots() { return NW * MT * 16; }
 
-template <class Kind, bool FP8, int MT, int NW>
+template <class Kind, bool FP8, int MT, int NW, bool FRAG = false>
 __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
@@ -303,7 +316,11 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     // in scalar registers
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.x, (uint32_t)(a.M * a.ldx * (int64_t)sizeof(T)));
-    const auto wr = make_rsrc(static_cast<const char*>(a.w) + pg * a.ldw * kWB, (uint32_t)(48 * a.ldw * kWB));
+    // fragment-major weights: the 16-row blocks pg / 16 .. + 2 (gate, -, up)
+    const int frag_g = (kb_a + 63) / 64;
+    const auto wr = FRAG ? make_rsrc(static_cast<const char*>(a.w_frag) + (pg >> 4) * (int64_t)frag_g * 1024,
+                                     (uint32_t)(3 * frag_g * 1024))
+                         : make_rsrc(static_cast<const char*>(a.w) + pg * a.ldw * kWB, (uint32_t)(48 * a.ldw * kWB));
 
     const bool routed = a.ids != nullptr && f0 >= a.shared_feats;
     // the route gather (two dependent loads) runs on the last waves, which
@@ -319,8 +336,8 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     w_off[0] = (int)(r * a.ldw * kWB);          // gate row pg + r
     w_off[1] = (int)((32 + r) * a.ldw * kWB);   // up row pg + 32 + r
 
-    constexpr bool SW = stage_weights<FP8, MT, 2, NW>();
-    constexpr int kRows = staged_rows<FP8, MT, 2, NW>();
+    constexpr bool SW = !FRAG && stage_weights<FP8, MT, 2, NW>();
+    constexpr int kRows = (MT + (SW ? 2 : 0)) * 16;
     constexpr int SB = staged_batch<kRows, NW>();
     const int w_row0[2] = {0, 32};
     const int spans = (kb_a + 127) / 128;
@@ -335,8 +352,9 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     const bool rms_in = a.row_scale == nullptr && a.rms_eps > 0.0f;
     const bool rms = rms_in || a.row_scale != nullptr;
     float ssq[ssq_rows<MT>()] = {};
-    staged_k_loop<Kind, FP8, MT, 2, SB, SW>(ar, (int)a.M, (int)(a.ldx * (int64_t)sizeof(T)), region, wr, w_row0,
-                                            (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc, rms_in, ssq);
+    staged_k_loop<Kind, FP8, MT, 2, SB, SW, 16, FRAG>(ar, (int)a.M, (int)(a.ldx * (int64_t)sizeof(T)), region, wr,
+                                                      w_row0, (int)(a.ldw * kWB), w_off, s0, s1, kb_a, acc, rms_in,
+                                                      ssq);
     __shared__ float s_ssq[rms_slots<MT, NW>()];
     __shared__ float s_rs[MT * 16];
     if (rms_in) {
@@ -389,7 +407,7 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
 // split) writes part[(split * M + row) * N + col] for its rows and columns;
 // with a single split it finishes the output itself.  COLS = 8 uses half of
 // a 16-row weight block (twice the workgroups for the same columns).
-template <class Kind, bool FP8, int MT, int COLS, int NW>
+template <class Kind, bool FP8, int MT, int COLS, int NW, bool FRAG = false>
 __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int spans_per_split) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
@@ -404,13 +422,19 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
 
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.h, (uint32_t)(a.M * a.ldh * (int64_t)sizeof(T)));
-    const auto wr = make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(kCols * a.ldw * kWB));
+    // fragment-major weights start at the 16-row block holding n0; an 8-column
+    // tile at n0 % 16 == 8 uses lanes 8..15 of its block
+    const int frag_g = (kb_a + 63) / 64;
+    const int64_t cbase = FRAG ? (n0 & ~(int64_t)15) : n0;
+    const auto wr = FRAG ? make_rsrc(static_cast<const char*>(a.w_frag) + (cbase >> 4) * (int64_t)frag_g * 1024,
+                                     (uint32_t)(NU * frag_g * 1024))
+                         : make_rsrc(static_cast<const char*>(a.w) + n0 * a.ldw * kWB, (uint32_t)(kCols * a.ldw * kWB));
     int w_off[NU];
 #pragma unroll
     for (int u = 0; u < NU; ++u) w_off[u] = (int)((u * 16 + r) * a.ldw * kWB);
 
-    constexpr bool SW = stage_weights<FP8, MT, NU, NW>();
-    constexpr int kRows = staged_rows<FP8, MT, NU, NW>();
+    constexpr bool SW = !FRAG && stage_weights<FP8, MT, NU, NW>();
+    constexpr int kRows = (MT + (SW ? NU : 0)) * 16;
     constexpr int SB = staged_batch<kRows, NW>();
     int w_row0[NU];
 #pragma unroll
@@ -424,9 +448,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     f32x4 acc[MT][NU];
     zero_acc16<MT, NU>(acc);
     char* region = reinterpret_cast<char*>(red) + wave * SB * kRows * kRowBytes;
-    staged_k_loop<Kind, FP8, MT, NU, SB, SW, (COLS < 16 ? 8 : 16)>(ar, (int)a.M, (int)(a.ldh * (int64_t)sizeof(T)),
-                                                                   region, wr, w_row0, (int)(a.ldw * kWB), w_off,
-                                                                   s0, s1, kb_a, acc);
+    staged_k_loop<Kind, FP8, MT, NU, SB, SW, (COLS < 16 ? 8 : 16), FRAG>(
+        ar, (int)a.M, (int)(a.ldh * (int64_t)sizeof(T)), region, wr, w_row0, (int)(a.ldw * kWB), w_off, s0, s1, kb_a,
+        acc);
     __syncthreads();   // every wave is done with its staging region
     skinny_stash<MT, NU>(red, acc);
     __syncthreads();
@@ -436,9 +460,8 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     for (int qi = threadIdx.x; qi < MT * NU * 4 * 64; qi += NT) {
         const int l = qi & 63, i = (qi >> 6) & 3, u = (qi >> 8) % NU, tm = (qi >> 8) / NU;
         const int row = tm * 16 + 4 * (l >> 4) + i;
-        const int cl = u * 16 + (l & 15);
-        const int64_t col = n0 + cl;
-        if (row >= a.M || cl >= kCols || col >= a.N) continue;
+        const int64_t col = cbase + u * 16 + (l & 15);
+        if (row >= a.M || col < n0 || col >= n0 + kCols || col >= a.N) continue;
         const float v = skinny_sum<MT, NU, NW>(red, tm, u, i, l);
         if (single)
             down_finish<T>(a, row, col, v);
@@ -493,22 +516,35 @@ int set_lds(F* fn, int bytes) {
 
 constexpr int red_bytes(int mt, int nu, int nw) { return nw * mt * nu * 4 * 64 * 4; }
 
-template <class Kind, bool FP8, int MT, int NW>
+// Staged rows per span: the activations, plus the weight rows when they are
+// staged (never with fragment-major weights).
+template <bool FP8, int MT, int NU, int NW, bool FRAG>
+constexpr int skinny_rows() { return FRAG ? MT * 16 : staged_rows<FP8, MT, NU, NW>(); }
+
+template <class Kind, bool FP8, int MT, int NW, bool FRAG>
 int gate_up_skinny_mt(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    auto kern = k_gate_up_skinny<Kind, FP8, MT, NW>;
-    constexpr int kLds = std::max(red_bytes(MT, 2, NW), staged_lds_bytes<staged_rows<FP8, MT, 2, NW>(), NW>());
+    auto kern = k_gate_up_skinny<Kind, FP8, MT, NW, FRAG>;
+    constexpr int kLds = std::max(red_bytes(MT, 2, NW), staged_lds_bytes<skinny_rows<FP8, MT, 2, NW, FRAG>(), NW>());
     int st = set_lds(kern, kLds);
     if (st) return st;
     hipLaunchKernelGGL(kern, dim3((unsigned)(packed_rows / 32)), dim3(64 * NW), kLds, stream, a);
     return check_launch("shared_gate_up (skinny)");
 }
 
+template <class Kind, bool FP8, bool FRAG>
+int gate_up_skinny_frag(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    if (a.M <= 16) return gate_up_skinny_mt<Kind, FP8, 1, 8, FRAG>(a, packed_rows, stream);
+    if (a.M <= 32) return gate_up_skinny_mt<Kind, FP8, 2, 8, FRAG>(a, packed_rows, stream);
+    if (a.M <= 64) return gate_up_skinny_mt<Kind, FP8, 4, 8, FRAG>(a, packed_rows, stream);
+    return gate_up_skinny_mt<Kind, FP8, 8, 4, FRAG>(a, packed_rows, stream);
+}
+
 template <class Kind, bool FP8>
 int gate_up_skinny_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if (a.M <= 16) return gate_up_skinny_mt<Kind, FP8, 1, 8>(a, packed_rows, stream);
-    if (a.M <= 32) return gate_up_skinny_mt<Kind, FP8, 2, 8>(a, packed_rows, stream);
-    if (a.M <= 64) return gate_up_skinny_mt<Kind, FP8, 4, 8>(a, packed_rows, stream);
-    return gate_up_skinny_mt<Kind, FP8, 8, 4>(a, packed_rows, stream);
+    if constexpr (!FP8) {
+        if (a.w_frag != nullptr) return gate_up_skinny_frag<Kind, FP8, true>(a, packed_rows, stream);
+    }
+    return gate_up_skinny_frag<Kind, FP8, false>(a, packed_rows, stream);
 }
 
 // K spans (128 bytes of K) per split: the whole K (no reduction launch) up
@@ -525,11 +561,11 @@ int down_spans_per_split(int64_t M, int spans) {
     return (spans + splits - 1) / splits;
 }
 
-template <class Kind, bool FP8, int MT, int COLS, int NW>
+template <class Kind, bool FP8, int MT, int COLS, int NW, bool FRAG>
 int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
     constexpr int NU = (COLS + 15) / 16;
-    auto kern = k_down_skinny<Kind, FP8, MT, COLS, NW>;
-    constexpr int kLds = std::max(red_bytes(MT, NU, NW), staged_lds_bytes<staged_rows<FP8, MT, NU, NW>(), NW>());
+    auto kern = k_down_skinny<Kind, FP8, MT, COLS, NW, FRAG>;
+    constexpr int kLds = std::max(red_bytes(MT, NU, NW), staged_lds_bytes<skinny_rows<FP8, MT, NU, NW, FRAG>(), NW>());
     int st = set_lds(kern, kLds);
     if (st) return st;
     hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + COLS - 1) / COLS), (unsigned)splits), dim3(64 * NW), kLds, stream,
@@ -552,23 +588,60 @@ int down_cols(int64_t M) {
     return M <= 16 ? 8 : (M <= 64 ? 16 : 32);
 }
 
-template <class Kind, bool FP8, int COLS>
+template <class Kind, bool FP8, int COLS, bool FRAG>
 int down_skinny_cols(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
-    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, COLS, 8>(a, part, sps, splits, stream);
-    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, COLS, 8>(a, part, sps, splits, stream);
-    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, COLS, 8>(a, part, sps, splits, stream);
-    return down_skinny_mt<Kind, FP8, 8, COLS, 4>(a, part, sps, splits, stream);
+    if (a.M <= 16) return down_skinny_mt<Kind, FP8, 1, COLS, 8, FRAG>(a, part, sps, splits, stream);
+    if (a.M <= 32) return down_skinny_mt<Kind, FP8, 2, COLS, 8, FRAG>(a, part, sps, splits, stream);
+    if (a.M <= 64) return down_skinny_mt<Kind, FP8, 4, COLS, 8, FRAG>(a, part, sps, splits, stream);
+    return down_skinny_mt<Kind, FP8, 8, COLS, 4, FRAG>(a, part, sps, splits, stream);
+}
+
+template <class Kind, bool FP8, bool FRAG>
+int down_skinny_frag(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
+    const int cols = down_cols(a.M);
+    if (cols == 8) return down_skinny_cols<Kind, FP8, 8, FRAG>(a, part, sps, splits, stream);
+    if (cols == 16) return down_skinny_cols<Kind, FP8, 16, FRAG>(a, part, sps, splits, stream);
+    return down_skinny_cols<Kind, FP8, 32, FRAG>(a, part, sps, splits, stream);
 }
 
 template <class Kind, bool FP8>
 int down_skinny_kind(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {
-    const int cols = down_cols(a.M);
-    if (cols == 8) return down_skinny_cols<Kind, FP8, 8>(a, part, sps, splits, stream);
-    if (cols == 16) return down_skinny_cols<Kind, FP8, 16>(a, part, sps, splits, stream);
-    return down_skinny_cols<Kind, FP8, 32>(a, part, sps, splits, stream);
+    if constexpr (!FP8) {
+        if (a.w_frag != nullptr) return down_skinny_frag<Kind, FP8, true>(a, part, sps, splits, stream);
+    }
+    return down_skinny_frag<Kind, FP8, false>(a, part, sps, splits, stream);
 }
 
 }  // namespace
+
+// One 16-byte chunk per thread: destination chunk d of block (b, g) is
+// lane l = d % 64 of that block's 1 KiB, i.e. row 16 b + (l & 15), K bytes
+// 64 g + 16 (l >> 4); chunks at or past kbytes are zero.
+__global__ __launch_bounds__(256) void k_pack_fragments(const char* src, int64_t rows, int64_t kbytes,
+                                                        int64_t ld_bytes, char* dst, int64_t groups) {
+    const int64_t total = rows / 16 * groups * 64;
+    for (int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x; d < total; d += (int64_t)gridDim.x * 256) {
+        const int64_t blk = d / (groups * 64), rem = d % (groups * 64);
+        const int64_t g = rem / 64;
+        const int l = (int)(rem % 64);
+        const int64_t row = blk * 16 + (l & 15), kb = g * 64 + 16 * (l >> 4);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (kb < kbytes) v = *reinterpret_cast<const u32x4*>(src + row * ld_bytes + kb);
+        *reinterpret_cast<u32x4*>(dst + d * 16) = v;
+    }
+}
+
+int launch_pack_fragments(const void* src, int64_t rows, int64_t kbytes, int64_t ld_bytes, void* dst,
+                          hipStream_t stream) {
+    const int64_t groups = (kbytes + 63) / 64;
+    const int64_t total = rows / 16 * groups * 64;
+    if (total <= 0) return TRMOE_OK;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_pack_fragments, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const char*>(src),
+                       rows, kbytes, ld_bytes, static_cast<char*>(dst), groups);
+    return check_launch("pack_fragments");
+}
 
 int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     if (act == TRMOE_F32 && wdt == TRMOE_F32) return gate_up_skinny_kind<KindF32, false>(a, packed_rows, stream);

@@ -280,6 +280,56 @@ int trmoe_routed_experts_rms(int act_dtype, int w_dtype, const void* x, int64_t 
                              void* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Fragment-major weights for decode-sized calls (no reference counterpart:
+ * a second layout of the same packed weights).
+ *
+ * A 16x16x32 MFMA operand is 16 rows x 64 bytes.  trmoe_pack_fragments
+ * copies a packed [rows, ld] weight (rows % 16 == 0; bf16/f32) so that each
+ * such fragment is 1 KiB contiguous:
+ *     dst[((r / 16) * G + k / 64) * 1024 + ((k % 64) / 16) * 256 + (r % 16) * 16 + k % 16]
+ *         = byte k of packed row r,      G = ceil(cols * elem / 64)
+ * with zeros past cols.  The decode kernels (n_tokens <= 128) then load
+ * weights with whole-line 1 KiB reads instead of 16 rows x 64 bytes.  cols
+ * must be the K of the calls that use it: `hidden` for gate|up packs,
+ * `shared_width` (the value passed to trmoe_shared_down_combine_ex) for down
+ * packs.  The copy doubles the weight memory of the layers that keep it.
+ * ------------------------------------------------------------------------- */
+size_t trmoe_fragment_bytes(int dtype, int64_t rows, int64_t cols);
+int trmoe_pack_fragments(int dtype, const void* packed, int64_t rows, int64_t cols, int64_t ld, void* dst,
+                         void* stream);
+
+/*
+ * Optional extras of the *_ex entry points (all-zero = the plain call):
+ *   row_scale / rms_eps: the fused RMSNorm scales of the *_rms entry points
+ *                        (gate|up calls only);
+ *   w_frag / w_frag_cols: a trmoe_pack_fragments copy of the call's packed
+ *                        weights and the cols it was packed with (checked
+ *                        against the call's K); used when n_tokens <= 128.
+ */
+typedef struct trmoe_call_extras {
+    const float* row_scale;
+    float rms_eps;
+    const void* w_frag;
+    int64_t w_frag_cols;
+} trmoe_call_extras;
+
+int trmoe_shared_gate_up_ex(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                            int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width, void* h,
+                            int64_t ldh, const trmoe_call_extras* extras, void* stream);
+int trmoe_dense_routed_gate_up_ex(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
+                                  int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
+                                  int num_experts, int64_t expert_width, const int64_t* token_ids,
+                                  const int64_t* route_table, int64_t vocab_size, int top_k,
+                                  const float* route_weights, float shared_scale, float routed_scale, void* h,
+                                  int64_t ldh, const trmoe_call_extras* extras, void* stream);
+int trmoe_shared_down_combine_ex(int act_dtype, int w_dtype, const void* h, int64_t n_tokens, int64_t shared_width,
+                                 int64_t ldh, const void* w_down, const float* w_scale, int64_t hidden, const void* y,
+                                 int64_t ldy, const int64_t* inverse, int top_k, const float* route_weights,
+                                 float shared_scale, float routed_scale, const void* residual, int64_t ldr, void* out,
+                                 int64_t ldo, void* workspace, size_t workspace_bytes,
+                                 const trmoe_call_extras* extras, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Backward (bf16 / f32 weights; fp8 weights are inference-only).
  *
  * Together these keep the HIP path differentiable: they replace the autograd

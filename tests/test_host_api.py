@@ -433,9 +433,21 @@ def test_mlp_registry_builds_the_engine_and_requires_token_ids():
     assert out.shape == (1, 4, 32)
 
 
-@pytest.mark.parametrize("switch,expected", [(False, TRHashBackend.PYTORCH), ("hip", TRHashBackend.HIP)])
-def test_use_custom_kernels_switch_maps_to_backends(switch, expected):
-    mlp = TRHashEngineMLP(_mlp_config(use_custom_kernels=switch))
+@pytest.mark.parametrize("kw,expected", [
+    ({"use_custom_kernels": False}, TRHashBackend.PYTORCH),
+    ({"use_custom_kernels": " False "}, TRHashBackend.PYTORCH),
+    ({"use_custom_kernels": "hip"}, TRHashBackend.HIP),
+    ({}, TRHashBackend.AUTO),
+    ({"use_custom_kernels": True}, TRHashBackend.AUTO),
+    ({"use_cggr": True}, TRHashBackend.CGGR),
+    ({"use_cggr": " TRUE"}, TRHashBackend.CGGR),
+    # the kernel switch is read first (tr_hash_engine.py:59-62)
+    ({"use_custom_kernels": False, "use_cggr": True}, TRHashBackend.PYTORCH),
+])
+def test_use_custom_kernels_switch_maps_to_backends(kw, expected):
+    """The reference's backend policy (core/mlp/tr_hash_engine.py:52-63),
+    plus "hip" forcing the gfx950 kernels."""
+    mlp = TRHashEngineMLP(_mlp_config(**kw))
     assert mlp.engine.config.backend is expected
 
 

@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <set>
 #include <string>
@@ -35,6 +36,22 @@ int set_kernel_lds(const void* kernel, int bytes) {
     if (err != hipSuccess) return set_error(TRMOE_ERR_HIP, hipGetErrorString(err));
     done.insert(key);
     return TRMOE_OK;
+}
+
+int current_device_cus() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];   // 0 = not yet read
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    const bool cached = dev >= 0 && dev < kMaxDevices;
+    if (cached) {
+        const int v = cache[dev].load(std::memory_order_relaxed);
+        if (v > 0) return v;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (cached) cache[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 int check_launch(const char* what) {

@@ -701,15 +701,7 @@ int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipS
     return swiglu_bwd_kind<KindF32, false, false>(a, assignments, stream);
 }
 
-static int bwd_device_cus() {
-    static int cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return 256;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-        return n;
-    }();
-    return cus;
-}
+static int bwd_device_cus() { return current_device_cus(); }
 
 // Split count: a workgroup holds a CU (128 KiB of LDS), so the launch runs
 // in ceil(tiles * s / CUs) rounds of rows/s rows each; every split adds an

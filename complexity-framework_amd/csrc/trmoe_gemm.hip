@@ -707,15 +707,7 @@ static int tile_override() {
     return v;
 }
 
-static int device_cus() {
-    static int cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return 256;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
-        return n;
-    }();
-    return cus;
-}
+static int device_cus() { return current_device_cus(); }
 
 template <class Kind, bool FP8, class Shape>
 static int launch_gate_up_persistent(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {

@@ -20,6 +20,10 @@ int check_launch(const char* what);
 // (kernel, device): the runtime call is not repeated on every launch.
 int set_kernel_lds(const void* kernel, int bytes);
 
+// Compute units of the current device (cached per device; 256 when the
+// runtime cannot say).  Used only to balance tile rounds.
+int current_device_cus();
+
 int64_t route_sort_blocks(int64_t n, int k, int order);
 int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,
                       int order, int64_t* routes, int64_t* sorted, int64_t* inverse, int32_t* offsets,

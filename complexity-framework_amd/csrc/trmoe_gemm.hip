@@ -709,6 +709,21 @@ static int tile_override() {
 
 static int device_cus() { return current_device_cus(); }
 
+// Tuning switches read once per process (set before the first call).
+static bool env_flag(const char* name) { return getenv(name) != nullptr; }
+static bool no_tail_split() {
+    static const bool v = env_flag("TRMOE_NO_TAIL_SPLIT");
+    return v;
+}
+static bool tail_narrow() {
+    static const bool v = env_flag("TRMOE_TAIL_NARROW");
+    return v;
+}
+static bool routed_narrow() {
+    static const bool v = env_flag("TRMOE_ROUTED_NARROW");
+    return v;
+}
+
 template <class Kind, bool FP8, class Shape>
 static int launch_gate_up_persistent(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int tiles_m = (int)((a.M + Shape::BM - 1) / Shape::BM);
@@ -764,7 +779,7 @@ static int launch_gate_up_dma_balanced(const GateUpArgs& a, int64_t packed_rows,
     const int64_t cols = (packed_rows - a.n_base) / 256;
     const int64_t cus = device_cus();
     int64_t tail_cols = 0;
-    if (getenv("TRMOE_NO_TAIL_SPLIT") == nullptr) {
+    if (!no_tail_split()) {
         // smallest number of trailing columns whose removal leaves whole rounds
         for (int64_t k = 1; k < cols; ++k)
             if ((tiles_m * (cols - k)) % cus == 0 && tiles_m * k * 2 <= cus) {
@@ -778,7 +793,7 @@ static int launch_gate_up_dma_balanced(const GateUpArgs& a, int64_t packed_rows,
     if (st) return st;
     GateUpArgs t = a;
     t.n_base = split;
-    if (getenv("TRMOE_TAIL_NARROW") != nullptr)
+    if (tail_narrow())
         return launch_gate_up_shape<Kind, false, ShapeGroupNarrowDma>(t, packed_rows, stream);
     return launch_gate_up_shape<Kind, false, ShapeTallDma>(t, packed_rows, stream);
 }
@@ -847,7 +862,7 @@ static int launch_gate_up_routed_cols_shape(const GateUpArgs& a, int64_t packed_
 
 template <class Kind, bool FP8>
 static int launch_gate_up_routed_cols(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if (!FP8 && (packed_rows - a.n_base) % 256 == 0 && getenv("TRMOE_ROUTED_NARROW") == nullptr)
+    if (!FP8 && (packed_rows - a.n_base) % 256 == 0 && !routed_narrow())
         return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeTallDma>>(
             a, packed_rows, stream);
     return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeGroupNarrowDma>>(

@@ -2,13 +2,17 @@
 
 Every function here launches HIP kernels on the current stream of the
 tensors' device and returns freshly allocated outputs (torch's caching
-allocator); inputs are never modified.  There is no fallback: if the library
-is missing or a call fails, an exception is raised.
+allocator); inputs are never modified.  The layer-level entry points and the
+packers make the tensors' GPU current for the call (the library launches on
+the current device); the per-kernel wrappers they chain expect it current
+already.  There is no fallback: if the library is missing or a call fails, an
+exception is raised.
 """
 
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from dataclasses import dataclass, field
 from typing import Optional, Sequence, Tuple
@@ -58,6 +62,23 @@ def _lib():
     return N.load()
 
 
+def _on_tensor_device(fn):
+    """Runs fn with the first tensor argument's GPU as torch's (and so HIP's)
+    current device: the library launches on the current device, and a tensor
+    on another GPU would otherwise get kernels of the wrong one."""
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        for a in args:
+            if isinstance(a, torch.Tensor):
+                dev = a.device
+                if dev.type == "cuda" and dev.index is not None and dev.index != torch.cuda.current_device():
+                    with torch.cuda.device(dev):
+                        return fn(*args, **kwargs)
+                break
+        return fn(*args, **kwargs)
+    return wrapper
+
+
 def rows16(x: torch.Tensor) -> torch.Tensor:
     """x[n, k] laid out as the kernels read activations: 16-byte-aligned rows,
     a row stride that is a multiple of 16 bytes, and zeros between k and the
@@ -84,6 +105,7 @@ def _require_cuda(*tensors):
 # K1
 # ---------------------------------------------------------------------------
 
+@_on_tensor_device
 def route_sort(token_ids: torch.Tensor, route_table: torch.Tensor, num_experts: int,
                order: int = ORDER_TOKEN, return_routes: bool = False):
     """(sorted int64[kN], inverse int64[kN], offsets int32[E+1], counts int32[E][, routes int64[k,N]])."""
@@ -153,6 +175,7 @@ def _pack(kind: int, a: torch.Tensor, b: Optional[torch.Tensor], groups: int, ou
     return dst, dst_scale
 
 
+@_on_tensor_device
 def pack_linear_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor, scale_gate=None, scale_up=None):
     """nn.Linear weights [S, H] (gate, up) -> packed [2*round_up(S,128), round_up(H,8)]."""
     S, H = w_gate.shape
@@ -163,6 +186,7 @@ def pack_linear_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor, scale_gate=Non
     return dst[0], (sc[0] if sc is not None else None)
 
 
+@_on_tensor_device
 def pack_linear_down(w_down: torch.Tensor, scale=None):
     """nn.Linear weight [H, S] -> packed [round_up(H,256), round_up(S,8)]."""
     H, S = w_down.shape
@@ -171,6 +195,7 @@ def pack_linear_down(w_down: torch.Tensor, scale=None):
     return dst[0], (sc[0] if sc is not None else None)
 
 
+@_on_tensor_device
 def pack_expert_gate_up(gate: torch.Tensor, up: torch.Tensor, scale_gate=None, scale_up=None):
     """Expert tensors [E, H, W] (any strides, e.g. an active-capacity slice)
     -> packed [E, 2*round_up(W,64), round_up(H,8)]; scales [E, W] (stride given)."""
@@ -181,6 +206,7 @@ def pack_expert_gate_up(gate: torch.Tensor, up: torch.Tensor, scale_gate=None, s
                  EXPERT_GATE_UP_ALIGN, scale_gate, scale_up)
 
 
+@_on_tensor_device
 def pack_expert_down(down: torch.Tensor, scale=None):
     """Expert down [E, W, H] -> packed [E, round_up(H,256), round_up(W,8)]; scale [E, H]."""
     E, W, H = down.shape
@@ -192,6 +218,7 @@ def dense_routed_features(shared_width: int, num_experts: int, expert_width: int
     return int(_lib().trmoe_dense_routed_features(shared_width, num_experts, expert_width))
 
 
+@_on_tensor_device
 def pack_dense_routed(shared_gate, shared_up, shared_down, gate, up, down):
     """Fused weights of the dense-routed strategy (bf16 / f32 only).
 
@@ -340,6 +367,7 @@ def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Ten
     return y
 
 
+@_on_tensor_device
 def rms_row_scale(x: torch.Tensor, eps: float) -> torch.Tensor:
     """r[N] fp32 = 1 / sqrt(mean_k x[t, k]^2 + eps): the per-token factor of
     RMSNorm (complexity/core/normalization/norms.py:53-54)."""
@@ -364,6 +392,7 @@ def _extras(row_scale: Optional[torch.Tensor] = None, rms_eps: float = 0.0, w_fr
     return ctypes.byref(e), e
 
 
+@_on_tensor_device
 def pack_fragments(w_packed: torch.Tensor, cols: int) -> tuple:
     """(fragment-major copy of a packed bf16/f32 weight, cols) for the decode
     kernels (trmoe_pack_fragments); cols is the K of the calls that use it."""
@@ -504,6 +533,7 @@ class PackedLayer:
         return got
 
 
+@_on_tensor_device
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
                   route_weights: Sequence[float], shared_scale: float, routed_scale: float,
                   order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None, save: bool = False,
@@ -568,6 +598,7 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
 # backward (bf16 / f32 weights)
 # ---------------------------------------------------------------------------
 
+@_on_tensor_device
 def pack_linear_down_t(w_down: torch.Tensor) -> torch.Tensor:
     """shared_down.weight [H, S] -> W_down^T packed [round_up(S,128), round_up(H,8)]."""
     H, S = w_down.shape
@@ -575,6 +606,7 @@ def pack_linear_down_t(w_down: torch.Tensor) -> torch.Tensor:
     return dst[0]
 
 
+@_on_tensor_device
 def pack_expert_down_t(down: torch.Tensor) -> torch.Tensor:
     """Expert down [E, W, H] -> [E, round_up(W,64), round_up(H,8)] (rows = features)."""
     E, W, H = down.shape
@@ -582,12 +614,14 @@ def pack_expert_down_t(down: torch.Tensor) -> torch.Tensor:
     return dst
 
 
+@_on_tensor_device
 def pack_dense_down_t(dense_down: torch.Tensor, features: int, hidden: int) -> torch.Tensor:
     """The dense-routed packed down [round_up(H,256), F] -> [F, round_up(H,8)]."""
     dst, _ = _pack(N.PACK_PLAIN, dense_down, None, 1, features, hidden, (0, 1, dense_down.stride(0)), 64)
     return dst[0]
 
 
+@_on_tensor_device
 def pack_gate_up_t(gate_up_packed: torch.Tensor, hidden: int) -> torch.Tensor:
     """A GATE_UP pack [G, 2F, ld] (or [2F, ld]) -> its transpose [G, round_up(H,256), 2F]:
     the down-style weight of the data gradient [dg|du] . [Wg; Wu]."""
@@ -771,6 +805,7 @@ def _gate_up_rows(g: torch.Tensor, features: int):
     return v[:, 0].reshape(features, -1), v[:, 1].reshape(features, -1)
 
 
+@_on_tensor_device
 def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor,
                    packed: PackedLayer, bwd: BackwardPacks, route_weights: Sequence[float], shared_scale: float,
                    routed_scale: float, order: int = ORDER_TOKEN, need_dx: bool = True, need_dw: bool = True,

@@ -21,6 +21,9 @@
  *   - the library never allocates or frees device memory; scratch is passed
  *     in (see *_workspace_bytes);
  *   - work is enqueued asynchronously on `stream`; no call synchronises;
+ *   - kernels launch on the calling thread's current HIP device: `stream`
+ *     and every pointer must belong to that device (make it current with
+ *     hipSetDevice first);
  *   - the return value is a trmoe_status; on failure trmoe_last_error()
  *     returns a message that stays valid until the calling thread's next
  *     call into the library;

@@ -489,3 +489,23 @@ def test_shared_lora_adapters_resolve_to_pytorch_with_reason(monkeypatch):
         hip.shared_up = _Adapter(hip.shared_up)
         with pytest.raises(RuntimeError, match="LoRA"):
             hip._decide(fake_cuda)
+
+
+def test_device_guard_is_transparent_for_host_tensors():
+    """The entry points' device guard only switches devices for a GPU tensor
+    on a non-current device; for other arguments it calls straight through."""
+    from complexity_amd import ops
+
+    calls = []
+
+    @ops._on_tensor_device
+    def probe(x, k=1):
+        calls.append((x.device.type, k))
+        return x * k
+
+    out = probe(torch.ones(2), k=3)
+    assert torch.equal(out, torch.full((2,), 3.0)) and calls == [("cpu", 3)]
+    assert probe.__name__ == "probe"
+    for name in ("layer_forward", "layer_backward", "route_sort", "pack_dense_routed", "pack_fragments",
+                 "rms_row_scale"):
+        assert getattr(ops, name).__wrapped__ is not None

@@ -85,3 +85,53 @@ def test_irregular_shapes_match_oracle(gpu, case):
     assert out.shape == x.shape and out.dtype == act
     err = O.normwise_rel_err(out, _oracle(engine, x, ids))
     assert err <= BOUND[c["dtype"]], (c, err)
+
+
+BWD_CASES = 16
+
+
+@pytest.mark.parametrize("case", range(BWD_CASES))
+def test_irregular_shapes_backward_match_oracle(gpu, case):
+    """The differentiable HIP call on the same kind of draws (hidden rounded up
+    to a multiple of 8, the HIP backward's requirement): the gradients of x
+    and of every parameter against autograd of the oracle's forward in f64."""
+    from complexity_amd.tr_hash import TRHashBackend, TRHashEngine, TRHashEngineConfig
+
+    c = _draw(1000 + case)
+    c["hidden"] += -c["hidden"] % 8
+    print(f"backward case {case}: {c}", flush=True)
+    torch.manual_seed(c["seed"])
+    engine = TRHashEngine(TRHashEngineConfig(
+        hidden_size=c["hidden"], vocab_size=c["vocab"], num_experts=c["E"], top_k=c["k"],
+        shared_width=c["shared"], expert_width=c["W"], routing_strategy=c["routing"],
+        route_weights=c["weights"], shared_output_scale=c["shared_scale"],
+        routed_output_scale=c["routed_scale"], precision=c["dtype"], backend="hip")).to(gpu)
+    act = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
+    engine = engine.to(act)
+    engine.routed_strategy = c["strategy"]
+    ids = torch.randint(0, c["vocab"], (c["batch"], c["seq"]), device=gpu)
+    x = torch.randn(c["batch"], c["seq"], c["hidden"], device=gpu, dtype=act).requires_grad_(True)
+    dout = torch.randn(c["batch"], c["seq"], c["hidden"], device=gpu, dtype=act)
+    out = engine(x, ids)
+    assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
+    out.backward(dout)
+    torch.cuda.synchronize()
+    got = {"x": x.grad}
+    names = ["expert_gate", "expert_up", "expert_down"]
+    params = {n: getattr(engine, n) for n in names}
+    if engine.shared_gate is not None:
+        for n in ("shared_gate", "shared_up", "shared_down"):
+            params[n] = getattr(engine, n).weight
+    got.update({n: p.grad for n, p in params.items()})
+    cfg = engine.config
+    ref = O.engine_backward(
+        x.detach().cpu().double(), ids.cpu(), engine._active_route_table.cpu(),
+        {n: p.detach().cpu().double() for n, p in params.items()}, dout.cpu().double(),
+        route_weights=cfg.route_weights, shared_scale=cfg.shared_output_scale,
+        routed_scale=cfg.routed_output_scale, active_experts=engine.active_num_experts,
+        active_width=engine.active_expert_width)
+    for name, r in ref.items():
+        g = got[name]
+        assert g is not None and g.shape == r.shape, (name, c)
+        err = O.normwise_rel_err(g, r)
+        assert err <= BOUND[c["dtype"]], (name, c, err)

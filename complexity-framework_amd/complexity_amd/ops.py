@@ -416,11 +416,38 @@ def _weights_arg(route_weights: Sequence[float]):
 
 # Scratch of the decode-sized down GEMM (split-K partials): one cached buffer
 # per (device, stream), so that calls on one stream (which are ordered) share
-# it and no call allocates after the first.
+# it and no call allocates after the first.  Inside a `workspace_scope` the
+# scope's own buffer is used instead: a captured graph bakes the buffer's
+# address into its launches, so every graph owns one (two graphs replayed on
+# different streams then never share partials).
 _DOWN_WS: dict = {}
+_WS_SCOPE: list = []
+
+
+class workspace_scope:
+    """Context in which the down GEMM's split-K scratch comes from this object
+    (grown on demand) rather than the per-stream cache.  Keep the object alive
+    as long as anything recorded inside the scope (a graph) may run."""
+
+    def __init__(self):
+        self.buffer: Optional[torch.Tensor] = None
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        if self.buffer is None or self.buffer.device != device or self.buffer.numel() < nbytes:
+            self.buffer = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        return self.buffer
+
+    def __enter__(self):
+        _WS_SCOPE.append(self)
+        return self
+
+    def __exit__(self, *exc):
+        _WS_SCOPE.remove(self)
 
 
 def _down_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    if _WS_SCOPE:
+        return _WS_SCOPE[-1].get(device, nbytes)
     key = (device.index, _RAW_STREAM(device.index) if _RAW_STREAM is not None
            else torch.cuda.current_stream(device).cuda_stream)
     ws = _DOWN_WS.get(key)
@@ -519,6 +546,15 @@ class PackedLayer:
     # name -> (copy, cols)
     frag: dict = field(default_factory=dict)
 
+    @property
+    def fp8(self) -> bool:
+        """True when any packed weight holds e4m3 codes (inference-only)."""
+        for name in ("expert_gate_up", "expert_down", "shared_gate_up", "shared_down", "dense_gate_up", "dense_down"):
+            t = getattr(self, name)
+            if t is not None and t.dtype == torch.float8_e4m3fn:
+                return True
+        return False
+
     def fragments(self, name: str, cols: int):
         """pack_fragments of the bf16/f32 weight `name` (None for fp8)."""
         if self.act_dtype not in (torch.bfloat16, torch.float32):
@@ -549,6 +585,8 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
     rms_row_scale."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
+    if save and packed.fp8:
+        raise ValueError("layer_forward: e4m3 weights are inference-only (no saved pre-activations, no backward)")
     if n == 0:
         out = torch.empty(0, hidden, dtype=x.dtype, device=x.device)
         return (out, None) if save else out

@@ -65,14 +65,16 @@ def supports_hip(config: TRHashEngineConfig) -> bool:
     return config.num_experts <= 16 and config.top_k in (1, 2, 4)
 
 
-_NO_HIP_BACKWARD = "HIP backward needs bf16/f32 weights and hidden_size % 8 == 0"
+_NO_HIP_BACKWARD = "HIP backward needs bf16/f32 weights (not e4m3 copies) and hidden_size % 8 == 0"
 
 
-def supports_hip_backward(config: TRHashEngineConfig) -> bool:
+def supports_hip_backward(config: TRHashEngineConfig, quantized_weights: bool = False) -> bool:
     """Differentiable HIP calls: bf16/f32 weights (e4m3 copies are
-    inference-only) and a hidden size that is a multiple of 8 (the
-    weight-gradient GEMMs read 16-byte column chunks)."""
-    return config.precision is not TRHashPrecision.FP8 and config.hidden_size % 8 == 0
+    inference-only, whether the config asks for fp8 or the engine was
+    quantised with ``quantize_fp8_()``) and a hidden size that is a multiple
+    of 8 (the weight-gradient GEMMs read 16-byte column chunks)."""
+    return (config.precision is not TRHashPrecision.FP8 and not quantized_weights
+            and config.hidden_size % 8 == 0)
 
 
 def _allow_fallback() -> bool:
@@ -98,13 +100,15 @@ def select_backend(
     fused_cuda_available: Optional[bool] = None,
     hip_available: Optional[bool] = None,
     autograd: bool = False,
+    quantized_weights: bool = False,
 ) -> BackendDecision:
     """Resolve the backend for one forward.
 
     ``autograd`` is True when the forward must be differentiable.  The HIP
     backend has a backward for bf16/f32 weights (``supports_hip_backward``);
     other differentiable calls resolve to PYTORCH with a reason (or raise when
-    HIP was requested explicitly).
+    HIP was requested explicitly).  ``quantized_weights`` is True when the
+    engine computes from e4m3 copies whatever its config precision says.
     """
 
     if cggr_available is None:
@@ -139,10 +143,10 @@ def select_backend(
             raise RuntimeError(f"HIP backend requested but the TR-MoE library is unavailable: {_hip_load_error()}")
         if not supports_hip(config):
             raise RuntimeError("HIP backend supports top_k in {1, 2, 4} and at most 16 experts")
-        if autograd and not supports_hip_backward(config):
+        if autograd and not supports_hip_backward(config, quantized_weights):
             raise RuntimeError(
-                "HIP backward needs bf16/f32 weights and hidden_size % 8 == 0; run under torch.no_grad() "
-                "or select pytorch"
+                "HIP backward needs bf16/f32 weights (not e4m3 copies) and hidden_size % 8 == 0; run under "
+                "torch.no_grad() or select pytorch"
             )
         return _decision(requested, TRHashBackend.HIP, quantized=quantized, partition=partition)
 
@@ -158,7 +162,7 @@ def select_backend(
                 "fused CUDA backend requested but neither Triton kernels nor the HIP library are available: "
                 + _hip_load_error()
             )
-        if autograd and not supports_hip_backward(config):
+        if autograd and not supports_hip_backward(config, quantized_weights):
             return _decision(requested, TRHashBackend.PYTORCH, [_NO_HIP_BACKWARD], quantized=quantized)
         return _decision(requested, TRHashBackend.HIP, ["fused_cuda served by HIP kernels"], quantized=quantized)
 
@@ -169,7 +173,7 @@ def select_backend(
             return _decision(requested, TRHashBackend.CGGR, quantized=quantized, partition=PARTITION_ASSIGNMENT)
         if not hip_available:
             raise RuntimeError("CGGR backend requested but Triton CGGR and the HIP library are unavailable")
-        if autograd and not supports_hip_backward(config):
+        if autograd and not supports_hip_backward(config, quantized_weights):
             return _decision(requested, TRHashBackend.PYTORCH, [_NO_HIP_BACKWARD], quantized=quantized)
         return _decision(requested, TRHashBackend.HIP, ["cggr served by HIP kernels"], quantized=quantized,
                          partition=PARTITION_ASSIGNMENT)
@@ -180,7 +184,7 @@ def select_backend(
         reasons.append("CGGR requires CUDA")
         return _decision(requested, TRHashBackend.PYTORCH, reasons, quantized=quantized)
     if hip_available and supports_hip(config):
-        if autograd and not supports_hip_backward(config):
+        if autograd and not supports_hip_backward(config, quantized_weights):
             return _decision(requested, TRHashBackend.PYTORCH, [_NO_HIP_BACKWARD], quantized=quantized)
         return _decision(requested, TRHashBackend.HIP, quantized=quantized, partition=partition)
     if fused_cuda_available and supports_fused_cuda(config):

@@ -169,6 +169,8 @@ class TRHashEngine(nn.Module):
         self._packed_key = None
         self._packed = None
         self._packed_norm = None
+        # captured graphs hold the old tensors' addresses
+        self._graph_pool.clear()
         return self
 
     @property
@@ -265,6 +267,8 @@ class TRHashEngine(nn.Module):
         self._packed_key = None
         self._packed = None
         self._packed_norm = None
+        self._decision_cache.clear()
+        self._graph_pool.clear()
 
     def _dequantized(self, name: str, dtype: torch.dtype) -> torch.Tensor:
         q = getattr(self, name + "_fp8")
@@ -562,7 +566,7 @@ class TRHashEngine(nn.Module):
         # the call is differentiable and the shared modules; cached on those
         mods = self._modules
         key = (hidden_states.device.type, self._needs_autograd(hidden_states), id(self.config),
-               id(mods.get("shared_gate")), id(mods.get("shared_up")), id(mods.get("shared_down")))
+               id(mods.get("shared_gate")), id(mods.get("shared_up")), id(mods.get("shared_down")), self._fp8)
         cached = self._decision_cache.get(key)
         if cached is not None:
             return cached
@@ -570,6 +574,7 @@ class TRHashEngine(nn.Module):
             self.config,
             device_type=hidden_states.device.type,
             autograd=key[1],
+            quantized_weights=self._fp8,
         )
         if decision.selected is TRHashBackend.HIP and self._shared_lora():
             # LoRA adapters on the shared linears add a low-rank residual (with
@@ -705,6 +710,12 @@ class _CapturedTRHashGraph:
     and allocate nothing outside torch's graph pool).  Without the library
     the capture raises, unless TRMOE_ALLOW_PYTORCH_FALLBACK=1 asks for the
     PYTORCH definition explicitly.
+
+    The reference's graph reads the live parameters.  Here the kernels read
+    the engine's packed copies, so the runner keeps the pack it captured
+    (and its split-K scratch) alive and captures again at replay when the
+    engine's current pack is another one: after load_state_dict, an in-place
+    weight update or a change of routing strategy.
     """
 
     def __init__(self, engine: TRHashEngine, bucket: GraphBucket, sample: torch.Tensor):
@@ -724,18 +735,32 @@ class _CapturedTRHashGraph:
         self.hidden = torch.zeros(shape, dtype=sample.dtype, device=sample.device)
         self.token_ids = torch.zeros(bucket.batch_size, bucket.sequence_length, dtype=torch.long,
                                      device=sample.device)
-        self.graph = torch.cuda.CUDAGraph()
+        self._capture()
+
+    def _current_pack(self):
+        return self.engine._hip_packed() if self.inner is TRHashBackend.HIP else None
+
+    def _capture(self) -> None:
+        engine = self.engine
+        self.graph = None
+        self.output = None
+        self.packed = self._current_pack()
+        self.scratch = ops.workspace_scope()
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
+        with self.scratch, torch.cuda.stream(stream):
             for _ in range(3):
                 self.output = engine._forward_eager(self.hidden, self.token_ids, self.inner)
         stream.synchronize()
-        with torch.cuda.graph(self.graph):
+        graph = torch.cuda.CUDAGraph()
+        with self.scratch, torch.cuda.graph(graph):
             self.output = engine._forward_eager(self.hidden, self.token_ids, self.inner)
+        self.graph = graph
 
     def replay(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
         batch, sequence, _ = hidden_states.shape
+        if self.inner is TRHashBackend.HIP and self._current_pack() is not self.packed:
+            self._capture()
         self.hidden.zero_()
         self.token_ids.zero_()
         self.hidden[:batch, :sequence].copy_(hidden_states)

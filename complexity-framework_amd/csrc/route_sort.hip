@@ -4,198 +4,236 @@
 // (complexity_cuda/triton_token_routed.py:172-277, host glue :2205-2318) and
 // its CPU/CGGR sort semantics (:69-93, :2320-2351).
 //
+// Every assignment a = slot*N + t (token t's slot-th route) is one item, so a
+// token whose slots name the same expert gets one partition row per slot.
 // Items are walked in a fixed order and each expert segment receives its
 // items in that order:
-//   order 0 (token)      item = token t, contributing one assignment
-//                        a = slot*N + t per selected expert; segment order is
-//                        token order (the reference's fused GPU partition);
-//   order 1 (assignment) item = assignment a in [0, k*N); segment order is
-//                        a (the reference's stable CPU sort / CGGR).
-// Ranks come from wavefront ballots plus an LDS prefix over (iteration,
-// wave); block prefixes come from per-block histograms, so no global atomics
-// are used and the output is identical on every launch.
+//   order 0 (token)      item i = t*k + slot: segment order (token, slot),
+//                        the reference's fused GPU partition (which has
+//                        distinct experts per token, so (expert, token));
+//   order 1 (assignment) item i = a: segment order a, the reference's stable
+//                        CPU sort / CGGR.
+// Ranks inside a wave come from ballots; the 256-item chunks of a block are
+// walked in order with a running per-expert base in LDS; block bases come
+// from per-block histograms.  No global atomics: the output is identical on
+// every launch.
+//
+// Work split: at most kMaxSortBlocks blocks.  Up to kMaxSortBlocks * 256
+// items every block takes one 256-item chunk (C2: 128 blocks, C5: 256);
+// beyond that the chunks per block grow instead of the block count, so each
+// block's prefix over the other blocks' histograms stays at most
+// kMaxSortBlocks * E reads whatever the token count.
 #include "trmoe_common.h"
 #include "trmoe_internal.h"
 
 namespace trmoe {
 
 constexpr int kSortThreads = 256;
-constexpr int kSortIters = 4;
-constexpr int kSortItemsPerBlock = kSortThreads * kSortIters;
 constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kMaxSortBlocks = 256;
+constexpr int kSingleMaxChunks = 8;   // one block (one launch) up to 2048 items
 
 struct SortArgs {
     const int64_t* ids;
-    int64_t n;
+    int n;                  // tokens
     const int64_t* table;   // [k, vocab]
     int64_t vocab;
     int k;
     int E;
     int order;
-    int64_t n_items;
+    int items;              // k * n
+    int chunks;             // 256-item chunks per block
+    int nblocks;
     int64_t* routes;        // [k, n] or null
     int64_t* sorted;        // [k*n]
     int64_t* inverse;       // [k*n]
     int32_t* offsets;       // [E+1]
     int32_t* counts;        // [E]
     int32_t* block_counts;  // [nblocks, E] (multi-block only)
-    int nblocks;
 };
 
-// Experts of item i: for token items all k slots, for assignment items one.
-__device__ __forceinline__ int item_experts(const SortArgs& a, int64_t i, int64_t (&assign)[4], int (&ex)[4]) {
-    if (a.order == 0) {
-        int64_t id = a.ids[i];
-        id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
-        for (int s = 0; s < a.k; ++s) {
-            ex[s] = (int)a.table[(int64_t)s * a.vocab + id];
-            assign[s] = (int64_t)s * a.n + i;
-        }
-        return a.k;
+// Expert of item i (-1 past the end) and its assignment index.  Table
+// entries outside [0, E) (a contract violation) are clamped so that no write
+// leaves the outputs; `routes` keeps the raw table value.
+__device__ __forceinline__ int item_expert(const SortArgs& a, int i, int& asg, bool write_routes) {
+    if (i >= a.items) {
+        asg = 0;
+        return -1;
     }
-    int64_t s = i / a.n;
-    int64_t t = i - s * a.n;
+    int s, t;
+    if (a.order == 0) {
+        t = i / a.k;
+        s = i - t * a.k;
+    } else {
+        s = i / a.n;
+        t = i - s * a.n;
+    }
+    asg = s * a.n + t;
     int64_t id = a.ids[t];
     id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
-    ex[0] = (int)a.table[s * a.vocab + id];
-    assign[0] = i;
-    return 1;
+    const int64_t raw = a.table[(int64_t)s * a.vocab + id];
+    if (write_routes && a.routes != nullptr) a.routes[asg] = raw;
+    return raw < 0 ? 0 : (raw >= a.E ? a.E - 1 : (int)raw);
 }
 
+// Rank of this lane among the lanes of its wave with the same expert, and
+// (lane 0 of each wave) the wave's count per expert into wcnt[e].
+__device__ __forceinline__ int wave_rank(int ex, int E, int* wcnt) {
+    const int lane = threadIdx.x & 63;
+    int rank = 0;
+    for (int e = 0; e < E; ++e) {
+        const uint64_t m = __ballot(ex == e);
+        if (lane == 0) wcnt[e] = __popcll(m);
+        if (ex == e)
+            rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+    }
+    return rank;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Launch 1 of the multi-block form: the histogram of each block's items.
 __global__ __launch_bounds__(kSortThreads) void k_route_count(SortArgs a) {
-    __shared__ int cnt[kMaxExperts];
-    if (threadIdx.x < kMaxExperts) cnt[threadIdx.x] = 0;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kSortItemsPerBlock;
-    for (int j = 0; j < kSortIters; ++j) {
-        int64_t i = base + j * kSortThreads + threadIdx.x;
-        if (i < a.n_items) {
-            int64_t asg[4];
-            int ex[4];
-            int m = item_experts(a, i, asg, ex);
-            for (int s = 0; s < m; ++s)
-                if ((unsigned)ex[s] < (unsigned)a.E) atomicAdd(&cnt[ex[s]], 1);
+    __shared__ int s_cnt[kSortWaves][kMaxExperts];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane < kMaxExperts) s_cnt[wave][lane] = 0;
+    const int base = blockIdx.x * a.chunks * kSortThreads;
+    for (int c = 0; c < a.chunks; ++c) {
+        int asg;
+        const int ex = item_expert(a, base + c * kSortThreads + threadIdx.x, asg, true);
+        for (int e = 0; e < a.E; ++e) {
+            const uint64_t m = __ballot(ex == e);
+            if (lane == 0) s_cnt[wave][e] += __popcll(m);
         }
     }
     __syncthreads();
-    if (threadIdx.x < a.E) a.block_counts[(int64_t)blockIdx.x * a.E + threadIdx.x] = cnt[threadIdx.x];
+    if (threadIdx.x < a.E) {
+        int s = 0;
+        for (int w = 0; w < kSortWaves; ++w) s += s_cnt[w][threadIdx.x];
+        a.block_counts[blockIdx.x * a.E + threadIdx.x] = s;
+    }
 }
 
-__device__ __forceinline__ int block_sum(int v, int* red) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    const int wave = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[wave] = v;
-    __syncthreads();
-    int s = 0;
-    for (int w = 0; w < kSortWaves; ++w) s += red[w];
-    return s;
-}
-
+// Scatter: this block's base per expert (offsets + earlier blocks' counts),
+// then its chunks in order.  SINGLE: one block holds every item and counts
+// them itself (items cached in registers between the passes).
 template <bool SINGLE>
 __global__ __launch_bounds__(kSortThreads) void k_route_scatter(SortArgs a) {
-    __shared__ int wcnt[kSortIters][kSortWaves][kMaxExperts];
-    __shared__ int wbase[kSortIters][kSortWaves][kMaxExperts];
-    __shared__ int s_prefix[kMaxExperts];
-    __shared__ int s_offset[kMaxExperts + 1];
-    __shared__ int red[kSortWaves];
+    __shared__ int s_wcnt[kSortWaves][kMaxExperts];
+    __shared__ int s_red[kSortWaves][2][kMaxExperts];
+    __shared__ int s_run[kMaxExperts];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = blockIdx.x;
+    const int base = b * a.chunks * kSortThreads;
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const uint64_t lt_mask = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-    const int64_t base = (int64_t)blockIdx.x * kSortItemsPerBlock;
-
-    // pass 1: per (iteration, wave, expert) counts from ballots
-    for (int j = 0; j < kSortIters; ++j) {
-        int64_t i = base + j * kSortThreads + threadIdx.x;
-        bool valid = i < a.n_items;
-        int64_t asg[4] = {0, 0, 0, 0};
-        int ex[4] = {-1, -1, -1, -1};
-        int m = valid ? item_experts(a, i, asg, ex) : 0;
-        if (valid && a.routes != nullptr) {
-            for (int s = 0; s < m; ++s) a.routes[asg[s]] = ex[s];
-        }
-        for (int e = 0; e < a.E; ++e) {
-            bool match = false;
-            for (int s = 0; s < m; ++s) match |= (ex[s] == e);
-            uint64_t mask = __ballot(match);
-            if (lane == 0) wcnt[j][wave][e] = __popcll(mask);
-        }
-    }
-    __syncthreads();
-
-    // block prefix and expert totals
-    if (SINGLE) {
-        if (threadIdx.x < a.E) {
-            int e = threadIdx.x, tot = 0;
-            for (int j = 0; j < kSortIters; ++j)
-                for (int w = 0; w < kSortWaves; ++w) tot += wcnt[j][w][e];
-            s_prefix[e] = 0;
-            s_offset[e + 1] = tot;  // temporarily the count
-        }
-    } else {
-        for (int e = 0; e < a.E; ++e) {
-            int pre = 0, tot = 0;
-            for (int bb = threadIdx.x; bb < a.nblocks; bb += kSortThreads) {
-                int c = a.block_counts[(int64_t)bb * a.E + e];
-                tot += c;
-                if (bb < (int)blockIdx.x) pre += c;
+    int ex_c[SINGLE ? kSingleMaxChunks : 1], asg_c[SINGLE ? kSingleMaxChunks : 1];
+    if constexpr (SINGLE) {
+        // pass 1: totals over every chunk
+        if (lane < kMaxExperts) s_red[wave][1][lane] = 0;
+#pragma unroll
+        for (int c = 0; c < kSingleMaxChunks; ++c)
+            if (c < a.chunks) ex_c[c] = item_expert(a, c * kSortThreads + threadIdx.x, asg_c[c], true);
+#pragma unroll
+        for (int c = 0; c < kSingleMaxChunks; ++c) {
+            if (c >= a.chunks) break;
+            for (int e = 0; e < a.E; ++e) {
+                const uint64_t m = __ballot(ex_c[c] == e);
+                if (lane == 0) s_red[wave][1][e] += __popcll(m);
             }
-            pre = block_sum(pre, red);
-            tot = block_sum(tot, red);
-            if (threadIdx.x == 0) {
-                s_prefix[e] = pre;
-                s_offset[e + 1] = tot;
+        }
+        if (lane < kMaxExperts) s_red[wave][0][lane] = 0;
+    } else {
+        // prefix over blocks: thread j holds block j's histogram (nblocks <= 256)
+        const int j = threadIdx.x;
+        for (int e = 0; e < a.E; ++e) {
+            const int c = j < a.nblocks ? a.block_counts[j * a.E + e] : 0;
+            const int all = wave_sum(c);
+            const int pre = wave_sum(j < b ? c : 0);
+            if (lane == 0) {
+                s_red[wave][0][e] = pre;
+                s_red[wave][1][e] = all;
             }
         }
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        s_offset[0] = 0;
+        int excl = 0;
         for (int e = 0; e < a.E; ++e) {
-            int c = s_offset[e + 1];
-            if (blockIdx.x == 0) a.counts[e] = c;
-            s_offset[e + 1] = s_offset[e] + c;
-        }
-        if (blockIdx.x == 0)
-            for (int e = 0; e <= a.E; ++e) a.offsets[e] = s_offset[e];
-    }
-    if (threadIdx.x < a.E) {
-        int e = threadIdx.x, run = 0;
-        for (int j = 0; j < kSortIters; ++j)
+            int pre = 0, tot = 0;
             for (int w = 0; w < kSortWaves; ++w) {
-                wbase[j][w][e] = run;
-                run += wcnt[j][w][e];
+                pre += s_red[w][0][e];
+                tot += s_red[w][1][e];
             }
+            s_run[e] = excl + pre;
+            if (b == 0) {
+                a.offsets[e] = excl;
+                a.counts[e] = tot;
+            }
+            excl += tot;
+        }
+        if (b == 0) a.offsets[a.E] = excl;
     }
     __syncthreads();
 
-    // pass 2: scatter
-    for (int j = 0; j < kSortIters; ++j) {
-        int64_t i = base + j * kSortThreads + threadIdx.x;
-        bool valid = i < a.n_items;
-        int64_t asg[4] = {0, 0, 0, 0};
-        int ex[4] = {-1, -1, -1, -1};
-        int m = valid ? item_experts(a, i, asg, ex) : 0;
-        for (int e = 0; e < a.E; ++e) {
-            int slot = -1;
-            for (int s = 0; s < m; ++s)
-                if (ex[s] == e) slot = s;
-            uint64_t mask = __ballot(slot >= 0);
-            if (slot >= 0) {
-                int64_t dest = (int64_t)s_offset[e] + s_prefix[e] + wbase[j][wave][e] + __popcll(mask & lt_mask);
-                int64_t an = asg[slot];
-                a.sorted[dest] = an;
-                a.inverse[an] = dest;
-            }
+    // pass 2: chunks in order; s_wcnt turns from wave counts into wave bases
+    for (int c = 0; c < a.chunks; ++c) {
+        int asg, ex;
+        if constexpr (SINGLE) {
+            ex = -1;
+            asg = 0;
+#pragma unroll
+            for (int q = 0; q < kSingleMaxChunks; ++q)
+                if (q == c) {
+                    ex = ex_c[q];
+                    asg = asg_c[q];
+                }
+        } else {
+            ex = item_expert(a, base + c * kSortThreads + threadIdx.x, asg, false);
         }
+        const int rank = wave_rank(ex, a.E, s_wcnt[wave]);
+        __syncthreads();
+        if (threadIdx.x < a.E) {
+            const int e = threadIdx.x;
+            int r = s_run[e];
+            for (int w = 0; w < kSortWaves; ++w) {
+                const int t = s_wcnt[w][e];
+                s_wcnt[w][e] = r;
+                r += t;
+            }
+            s_run[e] = r;
+        }
+        __syncthreads();
+        if (ex >= 0) {
+            const int dest = s_wcnt[wave][ex] + rank;
+            a.sorted[dest] = asg;
+            a.inverse[asg] = dest;
+        }
+        __syncthreads();
     }
 }
 
+// Blocks and 256-item chunks per block of a partition of `items` items.
+static void sort_split(int64_t items, int* nblocks, int* chunks) {
+    const int64_t total_chunks = (items + kSortThreads - 1) / kSortThreads;
+    if (total_chunks <= kSingleMaxChunks) {
+        *nblocks = 1;
+        *chunks = (int)(total_chunks < 1 ? 1 : total_chunks);
+        return;
+    }
+    const int64_t per = (total_chunks + kMaxSortBlocks - 1) / kMaxSortBlocks;
+    *chunks = (int)per;
+    *nblocks = (int)((total_chunks + per - 1) / per);
+}
+
 int64_t route_sort_blocks(int64_t n, int k, int order) {
-    int64_t items = (order == 0) ? n : n * k;
-    int64_t nb = (items + kSortItemsPerBlock - 1) / kSortItemsPerBlock;
-    return nb < 1 ? 1 : nb;
+    (void)order;
+    int nb, ch;
+    sort_split(n * k, &nb, &ch);
+    return nb;
 }
 
 int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,
@@ -203,19 +241,19 @@ int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64
                       int32_t* counts, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     SortArgs a{};
     a.ids = ids;
-    a.n = n;
+    a.n = (int)n;
     a.table = table;
     a.vocab = vocab;
     a.k = k;
     a.E = E;
     a.order = order;
-    a.n_items = (order == 0) ? n : n * k;
+    a.items = (int)(n * k);
+    sort_split(n * k, &a.nblocks, &a.chunks);
     a.routes = routes;
     a.sorted = sorted;
     a.inverse = inverse;
     a.offsets = offsets;
     a.counts = counts;
-    a.nblocks = (int)route_sort_blocks(n, k, order);
     a.block_counts = static_cast<int32_t*>(workspace);
     if (a.nblocks == 1) {
         hipLaunchKernelGGL(k_route_scatter<true>, dim3(1), dim3(kSortThreads), 0, stream, a);

@@ -760,22 +760,13 @@ static int wgrad_tr(const WgradArgs& a, hipStream_t stream) {
     return check_launch("weight_grad (reduce)");
 }
 
-// bf16: direct loads + transposing fragment reads; TRMOE_WGRAD_REG=1 keeps
-// the register-transposing kernel (the f32 path) for comparison.
-static bool wgrad_use_reg() {
-    static const bool v = getenv("TRMOE_WGRAD_REG") != nullptr;
-    return v;
-}
-
+// bf16: direct loads + transposing fragment reads; f32: the register-
+// transposing kernel.
 int launch_wgrad(int act, const WgradArgs& a, hipStream_t stream) {
     const bool ga = a.a_gather != nullptr, gb = a.b_gather != nullptr;
-    if (act == TRMOE_BF16 && !wgrad_use_reg()) {
+    if (act == TRMOE_BF16) {
         if (ga) return gb ? wgrad_tr<true, true>(a, stream) : wgrad_tr<true, false>(a, stream);
         return gb ? wgrad_tr<false, true>(a, stream) : wgrad_tr<false, false>(a, stream);
-    }
-    if (act == TRMOE_BF16) {
-        if (ga) return gb ? wgrad_kind<KindBF16, true, true>(a, stream) : wgrad_kind<KindBF16, true, false>(a, stream);
-        return gb ? wgrad_kind<KindBF16, false, true>(a, stream) : wgrad_kind<KindBF16, false, false>(a, stream);
     }
     if (ga) return gb ? wgrad_kind<KindF32, true, true>(a, stream) : wgrad_kind<KindF32, true, false>(a, stream);
     return gb ? wgrad_kind<KindF32, false, true>(a, stream) : wgrad_kind<KindF32, false, false>(a, stream);

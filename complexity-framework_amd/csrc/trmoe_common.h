@@ -206,7 +206,7 @@ __device__ __forceinline__ void init_dense_rows(Prov& p, const void* base, int64
 // 2 * (BM + BN) * 128 bytes.
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int PGR_ = 1>
 struct TileShape {
-    // 1, 2: register prefetch depth; 3: full register pipeline (tile_loop_pipe);
+    // 1: register-staged loads, one stage ahead (tile_loop_pgr1);
     // 4: direct buffer->LDS loads (tile_loop_dma, bf16/f32 operands only);
     static constexpr int PGR = PGR_;
     static constexpr int BM = BM_;
@@ -218,12 +218,10 @@ struct TileShape {
     static constexpr int WN = BN / WAVES_N;
     static constexpr int TM = WM / 32;
     static constexpr int TN = WN / 32;
-    // 5: direct loads into four stages of 64-byte rows (tile_loop_dma4, bf16)
     // 6: direct loads, bf16 A rows of 128 bytes + e4m3 B rows of 64 bytes per
     //    64-element K stage, expanded to bf16 at the fragment read
-    static constexpr int kStageRowBytes = PGR == 5 ? 64 : kRowBytes;
-    static constexpr int kStages = PGR == 5 ? 4 : 2;
-    static constexpr int kStageBytes = PGR == 6 ? BM * kRowBytes + BN * 64 : (BM + BN) * kStageRowBytes;
+    static constexpr int kStages = 2;
+    static constexpr int kStageBytes = PGR == 6 ? BM * kRowBytes + BN * 64 : (BM + BN) * kRowBytes;
     static constexpr int kLdsBytes = kStages * kStageBytes;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "tile rows must split evenly over threads");
@@ -274,41 +272,6 @@ __device__ __forceinline__ void mma_stage_f8(const char* As, const char* Bs, int
     }
 }
 
-// One K stage of MFMAs with the LDS writes of the next stage (already in
-// registers) spread over its four K groups, so the writes drain while the
-// matrix pipe is busy instead of after it.
-template <class Kind, int TM, int TN, class AProv, class BProv>
-__device__ __forceinline__ void mma_stage_commit(const char* As, const char* Bs, int wm0, int wn0,
-                                                 f32x16 (&acc)[TM][TN], const AProv& ap,
-                                                 const typename AProv::Reg (&ra)[AProv::kChunks],
-                                                 const BProv& bp, const typename BProv::Reg (&rb)[BProv::kChunks],
-                                                 char* nxt_a, char* nxt_b) {
-    const int lane = threadIdx.x & 63;
-    const int r = lane & 31, h = lane >> 5;
-    constexpr int kAPer = (AProv::kChunks + 3) / 4;
-    constexpr int kBPer = (BProv::kChunks + 3) / 4;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        u32x4 a[TM], b[TN];
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-            a[tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-            b[tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) mfma_group(Kind{}, a[tm], b[tn], acc[tm][tn]);
-#pragma unroll
-        for (int j = g * kAPer; j < (g + 1) * kAPer; ++j)
-            if (j < AProv::kChunks) ap.commit_one(nxt_a, ra, j);
-#pragma unroll
-        for (int j = g * kBPer; j < (g + 1) * kBPer; ++j)
-            if (j < BProv::kChunks) bp.commit_one(nxt_b, rb, j);
-    }
-}
-
 template <class Kind, int TM, int TN>
 __device__ __forceinline__ void zero_acc(f32x16 (&acc)[TM][TN]) {
 #pragma unroll
@@ -347,142 +310,6 @@ __device__ __forceinline__ void tile_loop_pgr1(const AProv& ap, const BProv& bp,
         __builtin_amdgcn_sched_barrier(0);
         ap.commit(nxt, ra);
         bp.commit(nxt + kABytes, rb);
-        __syncthreads();
-    }
-}
-
-// Same contract as tile_loop with two register sets: the loads of stage
-// kt+2 are issued before the MFMAs of stage kt, so a load has two stages of
-// MFMA work to land before its commit.  Unrolled by two with the odd tail
-// after the loop (a mid-loop exit would duplicate the accumulators).
-template <class Kind, class Shape, class AProv, class BProv>
-__device__ __forceinline__ void tile_loop_pgr2(const AProv& ap, const BProv& bp, int K, char* lds, int wm0,
-                                               int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
-    constexpr int kABytes = Shape::BM * kRowBytes;
-    char* st0 = lds;
-    char* st1 = lds + Shape::kStageBytes;
-    typename AProv::Reg ra0[AProv::kChunks], ra1[AProv::kChunks];
-    typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
-    ap.prefetch(0, ra0);
-    bp.prefetch(0, rb0);
-    ap.prefetch(1, ra1);
-    bp.prefetch(1, rb1);
-    ap.commit(st0, ra0);
-    bp.commit(st0 + kABytes, rb0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        // st0 holds stage kt; ra1/rb1 carry stage kt+1
-        ap.prefetch(kt + 2, ra0);
-        bp.prefetch(kt + 2, rb0);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        ap.commit(st1, ra1);
-        bp.commit(st1 + kABytes, rb1);
-        __syncthreads();
-        // st1 holds stage kt+1; ra0/rb0 carry stage kt+2
-        ap.prefetch(kt + 3, ra1);
-        bp.prefetch(kt + 3, rb1);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_stage<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        ap.commit(st0, ra0);
-        bp.commit(st0 + kABytes, rb0);
-        __syncthreads();
-    }
-    if (kt < nk) {  // odd stage count: the last stage sits in st0
-        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
-        __syncthreads();
-    }
-}
-
-// Full software pipeline: loads of stage kt+2 are issued at the top of stage
-// kt (two register sets), and stage kt+1 (already in registers) is written
-// to the other LDS stage between the MFMA groups of stage kt; one barrier per
-// stage.  Loads past the last stage read zeros into a stage nobody reads.
-template <class Kind, class Shape, class AProv, class BProv>
-__device__ __forceinline__ void tile_loop_pipe(const AProv& ap, const BProv& bp, int K, char* lds, int wm0,
-                                               int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
-    constexpr int kABytes = Shape::BM * kRowBytes;
-    char* st0 = lds;
-    char* st1 = lds + Shape::kStageBytes;
-    typename AProv::Reg ra0[AProv::kChunks], ra1[AProv::kChunks];
-    typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
-    ap.prefetch(0, ra0);
-    bp.prefetch(0, rb0);
-    ap.prefetch(1, ra1);
-    bp.prefetch(1, rb1);
-    ap.commit(st0, ra0);
-    bp.commit(st0 + kABytes, rb0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        ap.prefetch(kt + 2, ra0);
-        bp.prefetch(kt + 2, rb0);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc, ap, ra1, bp, rb1, st1,
-                                                      st1 + kABytes);
-        __syncthreads();
-        ap.prefetch(kt + 3, ra1);
-        bp.prefetch(kt + 3, rb1);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc, ap, ra0, bp, rb0, st0,
-                                                      st0 + kABytes);
-        __syncthreads();
-    }
-    if (kt < nk) {  // odd stage count: the last stage sits in st0
-        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
-        __syncthreads();
-    }
-}
-
-// The same pipeline split in two so that a persistent kernel can start the
-// next tile's loads (pipe_start) before the current tile's epilogue and run
-// its K loop later (pipe_body).
-template <class AProv, class BProv>
-struct PipeRegs {
-    typename AProv::Reg ra0[AProv::kChunks], ra1[AProv::kChunks];
-    typename BProv::Reg rb0[BProv::kChunks], rb1[BProv::kChunks];
-};
-
-template <class AProv, class BProv>
-__device__ __forceinline__ void pipe_start(const AProv& ap, const BProv& bp, PipeRegs<AProv, BProv>& rg) {
-    ap.prefetch(0, rg.ra0);
-    bp.prefetch(0, rg.rb0);
-    ap.prefetch(1, rg.ra1);
-    bp.prefetch(1, rg.rb1);
-}
-
-template <class Kind, class Shape, class AProv, class BProv>
-__device__ __forceinline__ void pipe_body(const AProv& ap, const BProv& bp, PipeRegs<AProv, BProv>& rg, int K,
-                                          char* lds, int wm0, int wn0, f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    const int nk = (K + Kind::kStageElems - 1) / Kind::kStageElems;
-    constexpr int kABytes = Shape::BM * kRowBytes;
-    char* st0 = lds;
-    char* st1 = lds + Shape::kStageBytes;
-    ap.commit(st0, rg.ra0);
-    bp.commit(st0 + kABytes, rg.rb0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        ap.prefetch(kt + 2, rg.ra0);
-        bp.prefetch(kt + 2, rg.rb0);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc, ap, rg.ra1, bp, rg.rb1,
-                                                      st1, st1 + kABytes);
-        __syncthreads();
-        ap.prefetch(kt + 3, rg.ra1);
-        bp.prefetch(kt + 3, rg.rb1);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_stage_commit<Kind, Shape::TM, Shape::TN>(st1, st1 + kABytes, wm0, wn0, acc, ap, rg.ra0, bp, rg.rb0,
-                                                      st0, st0 + kABytes);
-        __syncthreads();
-    }
-    if (kt < nk) {  // odd stage count: the last stage sits in st0
-        mma_stage<Kind, Shape::TM, Shape::TN>(st0, st0 + kABytes, wm0, wn0, acc);
         __syncthreads();
     }
 }
@@ -588,34 +415,9 @@ __device__ __forceinline__ void dma_mainloop(const AP& ap, const BP& bp, int nk,
     }
 }
 
-// ---- four stages of 64-byte rows ------------------------------------------
-// A K stage of 32 bf16 per row halves the bytes per stage, so four stages fit
-// where two 128-byte stages did and three stages (96 KB for a 256x256 tile)
-// are in flight while one is multiplied: the loop is bound by memory latency
-// (bytes in flight / latency), not by L2 or LDS bandwidth.  Rows hold four
-// 16-byte chunks swizzled by (r >> 1) & 3, which keeps every 8-lane phase of
-// a ds_read_b128 on distinct bank groups.
-
-template <class Kind, int TM, int TN>
-__device__ __forceinline__ void mma_stage64(const char* As, const char* Bs, int wm0, int wn0,
-                                            f32x16 (&acc)[TM][TN]) {
-    const int lane = threadIdx.x & 63;
-    const int r = lane & 31, h = lane >> 5;
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        u32x4 a[TM], b[TN];
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-            a[tm] = *reinterpret_cast<const u32x4*>(As + lds_byte64(wm0 + tm * 32 + r, 2 * g + h));
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-            b[tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte64(wn0 + tn * 32 + r, 2 * g + h));
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) mfma_group(Kind{}, a[tm], b[tn], acc[tm][tn]);
-    }
-}
+// ---- 64-byte rows (e4m3 weights: 64 K values per stage) --------------------
+// Rows hold four 16-byte chunks swizzled by (r >> 1) & 3, which keeps every
+// 8-lane phase of a ds_read_b128 on distinct bank groups.
 
 template <int ROWS, int NT>
 struct DmaRows64 {
@@ -665,49 +467,6 @@ struct requires_wave_field<DmaRows<R, N>> : std::true_type {};
 template <int R, int N>
 struct requires_wave_field<DmaRows64<R, N>> : std::true_type {};
 
-// K loop over four 64-byte-row stages with stages 0..2 already requested
-// (stage 2's the most recent vector memory operations).  One barrier per
-// stage: it both publishes stage kt and retires stage kt-1, whose buffer
-// then receives stage kt+3 before stage kt is multiplied.
-template <class Kind, class Shape, class AP, class BP>
-__device__ __forceinline__ void dma4_mainloop(const AP& ap, const BP& bp, int nk, char* lds, int wm0, int wn0,
-                                              f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    constexpr int kABytes = Shape::BM * kRow64;
-    constexpr int kPer = AP::kInstr + BP::kInstr;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int younger = nk - 1 - kt;   // stages requested after stage kt (at most 2 here)
-        if (younger >= 2)
-            wait_vmcnt<2 * kPer>();
-        else if (younger == 1)
-            wait_vmcnt<kPer>();
-        else
-            wait_vmcnt<0>();
-        lds_barrier();
-        if (kt + 3 < nk) {
-            char* nx = lds + ((kt + 3) & 3) * Shape::kStageBytes;
-            ap.issue(kt + 3, nx);
-            bp.issue(kt + 3, nx + kABytes);
-        }
-        const char* st = lds + (kt & 3) * Shape::kStageBytes;
-        mma_stage64<Kind, Shape::TM, Shape::TN>(st, st + kABytes, wm0, wn0, acc);
-    }
-}
-
-template <class Kind, class Shape, class AP, class BP>
-__device__ __forceinline__ void tile_loop_dma4(const AP& ap, const BP& bp, int K, char* lds, int wm0, int wn0,
-                                               f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    const int nk = (K * (int)sizeof(typename Kind::T) + kRow64 - 1) / kRow64;
-    constexpr int kABytes = Shape::BM * kRow64;
-#pragma unroll
-    for (int s = 0; s < 3; ++s)
-        if (s < nk) {
-            ap.issue(s, lds + s * Shape::kStageBytes);
-            bp.issue(s, lds + s * Shape::kStageBytes + kABytes);
-        }
-    dma4_mainloop<Kind, Shape>(ap, bp, nk, lds, wm0, wn0, acc);
-    __syncthreads();
-}
-
 // Whole tile: request stages 0 and 1, run the K loop, end with a full
 // barrier (callers reuse LDS in their epilogues).
 template <class Kind, class Shape, class AP, class BP>
@@ -728,14 +487,8 @@ __device__ __forceinline__ void tile_loop_dma(const AP& ap, const BP& bp, int K,
 template <class Kind, class Shape, class AProv, class BProv>
 __device__ __forceinline__ void tile_loop(const AProv& ap, const BProv& bp, int K, char* lds, int wm0, int wn0,
                                           f32x16 (&acc)[Shape::TM][Shape::TN]) {
-    if constexpr (Shape::PGR == 5)
-        tile_loop_dma4<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
-    else if constexpr (Shape::PGR == 4 || Shape::PGR == 6)
+    if constexpr (Shape::PGR == 4 || Shape::PGR == 6)
         tile_loop_dma<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
-    else if constexpr (Shape::PGR == 3)
-        tile_loop_pipe<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
-    else if constexpr (Shape::PGR == 2)
-        tile_loop_pgr2<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
     else
         tile_loop_pgr1<Kind, Shape>(ap, bp, K, lds, wm0, wn0, acc);
 }

@@ -265,116 +265,6 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
                                           a.row_scale != nullptr ? s_rscale : nullptr);
 }
 
-// Persistent form: gridDim.x workgroups walk the tiles (M fastest).  The
-// next tile's first two K stages are loaded into registers before the
-// current tile's epilogue, so the SwiGLU math and stores overlap those loads.
-template <class Kind, bool FP8, class Shape>
-__global__ __launch_bounds__(Shape::NT) void k_gate_up_persistent(GateUpArgs a, int tiles_m, int total) {
-    using T = typename Kind::T;
-    using AProv = BufRows<Shape::BM, Shape::NT>;
-    using BProv = typename BProvSel<Kind, FP8, Shape::BN, Shape::NT>::type;
-    extern __shared__ __align__(16) char lds[];
-    __shared__ int s_route[Shape::BM][kMaxTopK];
-    const int wave = threadIdx.x >> 6;
-    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
-    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
-    int tile = blockIdx.x;
-    if (tile >= total) return;
-
-    AProv ap;
-    BProv bp;
-    PipeRegs<AProv, BProv> rg;
-    int64_t m0 = (int64_t)(tile % tiles_m) * Shape::BM;
-    int64_t n0 = (int64_t)(tile / tiles_m) * Shape::BN;
-    init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
-    init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
-    pipe_start(ap, bp, rg);
-    while (true) {
-        gate_up_routes<Shape>(a, m0, n0, s_route);
-        f32x16 acc[Shape::TM][Shape::TN];
-        zero_acc<Kind>(acc);
-        pipe_body<Kind, Shape>(ap, bp, rg, a.K, lds, wm0, wn0, acc);
-        const int next = tile + (int)gridDim.x;
-        const int64_t cm0 = m0, cn0 = n0;
-        if (next < total) {
-            m0 = (int64_t)(next % tiles_m) * Shape::BM;
-            n0 = (int64_t)(next / tiles_m) * Shape::BN;
-            init_dense_rows(ap, a.x, m0, a.M, a.ldx * (int64_t)sizeof(T), a.K * (int)sizeof(T));
-            init_bprov<Kind, FP8, Shape::BN, Shape::NT>(bp, a.w, a.ldw, n0, a.K);
-            pipe_start(ap, bp, rg);
-        }
-        gate_up_epilogue<Kind, Shape>(a, acc, cm0, cn0, lds, s_route);
-        __syncthreads();  // LDS and s_route are reused by the next tile
-        if (next >= total) break;
-        tile = next;
-    }
-}
-
-// Persistent form over direct buffer->LDS loads (bf16): gridDim.x workgroups
-// walk the tiles (M fastest).  After a tile's last K stage the first K stage
-// of the workgroup's next tile is requested into LDS stage 0 and its second
-// into stage 1 once the epilogue has drained its LDS tile (which overlaps
-// stage 1), so both loads travel while the SwiGLU epilogue runs.
-template <class Kind, class Shape>
-__global__ __launch_bounds__(Shape::NT) void k_gate_up_persist_dma(GateUpArgs a, int tiles_m, int total) {
-    using T = typename Kind::T;
-    static_assert(Shape::PGR == 4, "direct-load shape expected");
-    extern __shared__ __align__(16) char lds[];
-    __shared__ int s_route[Shape::BM][kMaxTopK];
-    constexpr int kABytes = Shape::BM * kRowBytes;
-    const int wave = threadIdx.x >> 6;
-    const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
-    const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
-    int t = blockIdx.x;
-    if (t >= total) return;
-    const int nk = (a.K + Kind::kStageElems - 1) / Kind::kStageElems;
-    const int64_t ldx_b = a.ldx * (int64_t)sizeof(T), ldw_b = a.ldw * (int64_t)sizeof(T);
-    const int kb = a.K * (int)sizeof(T);
-
-    DmaRows<Shape::BM, Shape::NT> ap;
-    DmaRows<Shape::BN, Shape::NT> bp;
-    int64_t m0 = (int64_t)(t % tiles_m) * Shape::BM;
-    int64_t n0 = (int64_t)(t / tiles_m) * Shape::BN;
-    ap.init(a.x, m0, a.M, ldx_b, kb);
-    bp.init(a.w, n0, n0 + Shape::BN, ldw_b, kb);
-    ap.issue(0, lds);
-    bp.issue(0, lds + kABytes);
-    if (nk > 1) {
-        ap.issue(1, lds + Shape::kStageBytes);
-        bp.issue(1, lds + Shape::kStageBytes + kABytes);
-    }
-    while (true) {
-        gate_up_routes<Shape>(a, m0, n0, s_route);
-        f32x16 acc[Shape::TM][Shape::TN];
-        zero_acc<Kind>(acc);
-        dma_mainloop<Kind, Shape>(ap, bp, nk, lds, wm0, wn0, acc);
-        wait_lgkmcnt0();
-        lds_barrier();   // every wave is done with both stages
-        gate_up_epi_tile<Kind, Shape>(a, acc, n0, lds + Shape::kStageBytes, s_route);
-        const int next = t + (int)gridDim.x;
-        const int64_t cm0 = m0, cn0 = n0;
-        if (next < total) {
-            m0 = (int64_t)(next % tiles_m) * Shape::BM;
-            n0 = (int64_t)(next / tiles_m) * Shape::BN;
-            ap.init(a.x, m0, a.M, ldx_b, kb);
-            bp.init(a.w, n0, n0 + Shape::BN, ldw_b, kb);
-            ap.issue(0, lds);
-            bp.issue(0, lds + kABytes);
-        }
-        wait_lgkmcnt0();
-        lds_barrier();   // the LDS tile is complete
-        gate_up_epi_store<Kind, Shape>(a, cm0, cn0, lds + Shape::kStageBytes);
-        wait_lgkmcnt0();
-        lds_barrier();   // ... and has been read out
-        if (next >= total) break;
-        if (nk > 1) {
-            ap.issue(1, lds + Shape::kStageBytes);
-            bp.issue(1, lds + Shape::kStageBytes + kABytes);
-        }
-        t = next;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // K4: shared down + weighted un-permute + combine
 // ---------------------------------------------------------------------------
@@ -679,84 +569,7 @@ static int ensure_lds(F* fn, int bytes) {
 // (PGR 4); e4m3 weights the register-staged loop that expands them.
 constexpr int64_t kBigTileMinBlocks = 512;
 
-// TRMOE_GEMM_TILE forces one tile family for tuning sweeps: small (128x128),
-// big (256x256, 8 waves), big8p2, big4p2 (two-stage prefetch); unset = auto.
-enum TileChoice {
-    kTileAuto = 0, kTileSmall, kTileBig, kTileBig8P2, kTileBig4P2, kTileBig8Pipe, kTileBig4Pipe,
-    kTilePersist8, kTilePersist4, kTileDma, kTilePersistDma, kTileDma4, kTileDma64, kTileF8Dma
-};
-static int tile_override() {
-    static int v = [] {
-        const char* e = getenv("TRMOE_GEMM_TILE");
-        if (e == nullptr) return (int)kTileAuto;
-        if (strcmp(e, "small") == 0) return (int)kTileSmall;
-        if (strcmp(e, "big") == 0) return (int)kTileBig;
-        if (strcmp(e, "big8p2") == 0) return (int)kTileBig8P2;
-        if (strcmp(e, "big4p2") == 0) return (int)kTileBig4P2;
-        if (strcmp(e, "big8pipe") == 0) return (int)kTileBig8Pipe;
-        if (strcmp(e, "big4pipe") == 0) return (int)kTileBig4Pipe;
-        if (strcmp(e, "persist8") == 0) return (int)kTilePersist8;
-        if (strcmp(e, "persist4") == 0) return (int)kTilePersist4;
-        if (strcmp(e, "dma") == 0) return (int)kTileDma;
-        if (strcmp(e, "pdma") == 0) return (int)kTilePersistDma;
-        if (strcmp(e, "dma4") == 0) return (int)kTileDma4;
-        if (strcmp(e, "dma64") == 0) return (int)kTileDma64;
-        if (strcmp(e, "f8dma") == 0) return (int)kTileF8Dma;
-        return (int)kTileAuto;
-    }();
-    return v;
-}
-
 static int device_cus() { return current_device_cus(); }
-
-// Tuning switches read once per process (set before the first call).
-static bool env_flag(const char* name) { return getenv(name) != nullptr; }
-static bool no_tail_split() {
-    static const bool v = env_flag("TRMOE_NO_TAIL_SPLIT");
-    return v;
-}
-static bool tail_narrow() {
-    static const bool v = env_flag("TRMOE_TAIL_NARROW");
-    return v;
-}
-static bool routed_narrow() {
-    static const bool v = env_flag("TRMOE_ROUTED_NARROW");
-    return v;
-}
-
-template <class Kind, bool FP8, class Shape>
-static int launch_gate_up_persistent(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    const int tiles_m = (int)((a.M + Shape::BM - 1) / Shape::BM);
-    const int total = tiles_m * (int)(packed_rows / Shape::BN);
-    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
-    constexpr int kLds = kEpi > Shape::kLdsBytes ? kEpi : Shape::kLdsBytes;
-    auto kern = k_gate_up_persistent<Kind, FP8, Shape>;
-    int st = ensure_lds(kern, kLds);
-    if (st) return st;
-    int per_cu = 1;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, Shape::NT, kLds) != hipSuccess || per_cu < 1)
-        per_cu = 1;
-    int grid = device_cus() * per_cu;
-    if (grid > total) grid = total;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Shape::NT), kLds, stream, a, tiles_m, total);
-    return check_launch("shared_gate_up");
-}
-
-template <class Kind, class Shape>
-static int launch_gate_up_persist_dma(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    const int tiles_m = (int)((a.M + Shape::BM - 1) / Shape::BM);
-    const int total = tiles_m * (int)(packed_rows / Shape::BN);
-    constexpr int kEpi = Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16);
-    constexpr int kLds = Shape::kStageBytes + kEpi > Shape::kLdsBytes ? Shape::kStageBytes + kEpi : Shape::kLdsBytes;
-    static_assert(kLds <= 160 * 1024 - 4096, "stages + epilogue tile must fit in LDS");
-    auto kern = k_gate_up_persist_dma<Kind, Shape>;
-    int st = ensure_lds(kern, kLds);
-    if (st) return st;
-    int grid = device_cus();
-    if (grid > total) grid = total;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Shape::NT), kLds, stream, a, tiles_m, total);
-    return check_launch("shared_gate_up");
-}
 
 template <class Kind, bool FP8, class Shape>
 static int launch_gate_up_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
@@ -779,71 +592,31 @@ static int launch_gate_up_dma_balanced(const GateUpArgs& a, int64_t packed_rows,
     const int64_t cols = (packed_rows - a.n_base) / 256;
     const int64_t cus = device_cus();
     int64_t tail_cols = 0;
-    if (!no_tail_split()) {
-        // smallest number of trailing columns whose removal leaves whole rounds
-        for (int64_t k = 1; k < cols; ++k)
-            if ((tiles_m * (cols - k)) % cus == 0 && tiles_m * k * 2 <= cus) {
-                tail_cols = k;
-                break;
-            }
-    }
+    // smallest number of trailing columns whose removal leaves whole rounds
+    for (int64_t k = 1; k < cols; ++k)
+        if ((tiles_m * (cols - k)) % cus == 0 && tiles_m * k * 2 <= cus) {
+            tail_cols = k;
+            break;
+        }
     if (tail_cols == 0) return launch_gate_up_shape<Kind, false, ShapeBigDma>(a, packed_rows, stream);
     const int64_t split = a.n_base + (cols - tail_cols) * 256;
     int st = launch_gate_up_shape<Kind, false, ShapeBigDma>(a, split, stream);
     if (st) return st;
     GateUpArgs t = a;
     t.n_base = split;
-    if (tail_narrow())
-        return launch_gate_up_shape<Kind, false, ShapeGroupNarrowDma>(t, packed_rows, stream);
     return launch_gate_up_shape<Kind, false, ShapeTallDma>(t, packed_rows, stream);
 }
 
 template <class Kind, bool FP8>
 static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int64_t big_blocks = ((a.M + 255) / 256) * (packed_rows / 256);
-    int ov = a.row_scale != nullptr ? (int)kTileAuto : tile_override();   // the default tiles apply row scales
-    if (ov == kTileAuto)
-        ov = (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) ? (FP8 ? kTileF8Dma : kTileDma) : kTileSmall;
-    if (packed_rows % 256 != 0) ov = kTileSmall;
-    switch (ov) {
-        case kTileBig: return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-        case kTileBig8P2: return launch_gate_up_shape<Kind, FP8, ShapeBig8P2>(a, packed_rows, stream);
-        case kTileBig4P2: return launch_gate_up_shape<Kind, FP8, ShapeBig4P2>(a, packed_rows, stream);
-        case kTileBig8Pipe: return launch_gate_up_shape<Kind, FP8, ShapeBig8Pipe>(a, packed_rows, stream);
-        case kTileBig4Pipe: return launch_gate_up_shape<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
-        case kTilePersist8: return launch_gate_up_persistent<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-        case kTilePersist4: return launch_gate_up_persistent<Kind, FP8, ShapeBig4Pipe>(a, packed_rows, stream);
-        case kTileF8Dma:
-            if constexpr (FP8)
-                return launch_gate_up_shape<Kind, FP8, ShapeBigF8Dma>(a, packed_rows, stream);
-            else
-                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
-        case kTileDma:
-            if constexpr (FP8)
-                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-            else
-                return launch_gate_up_dma_balanced<Kind>(a, packed_rows, stream);
-        case kTileDma64:
-            if constexpr (FP8)
-                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-            else if constexpr (sizeof(typename Kind::T) == 4)
-                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
-            else
-                return launch_gate_up_shape<Kind, FP8, ShapeBigDma64>(a, packed_rows, stream);
-        case kTileDma4:
-            if constexpr (FP8)
-                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-            else
-                return launch_gate_up_shape<Kind, FP8, ShapeBig4Dma>(a, packed_rows, stream);
-        case kTilePersistDma:
-            if constexpr (FP8)
-                return launch_gate_up_shape<Kind, FP8, ShapeBig>(a, packed_rows, stream);
-            else if constexpr (sizeof(typename Kind::T) == 4)
-                return launch_gate_up_shape<Kind, FP8, ShapeBigDma>(a, packed_rows, stream);
-            else
-                return launch_gate_up_persist_dma<Kind, ShapeBigDma>(a, packed_rows, stream);
-        default: return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
+    if (packed_rows % 256 == 0 && big_blocks >= kBigTileMinBlocks) {
+        if constexpr (FP8)
+            return launch_gate_up_shape<Kind, FP8, ShapeBigF8Dma>(a, packed_rows, stream);
+        else
+            return launch_gate_up_dma_balanced<Kind>(a, packed_rows, stream);
     }
+    return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
 }
 
 // Expert columns of a dense-routed gate|up, [a.n_base, packed_rows), in
@@ -862,7 +635,7 @@ static int launch_gate_up_routed_cols_shape(const GateUpArgs& a, int64_t packed_
 
 template <class Kind, bool FP8>
 static int launch_gate_up_routed_cols(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if (!FP8 && (packed_rows - a.n_base) % 256 == 0 && !routed_narrow())
+    if (!FP8 && (packed_rows - a.n_base) % 256 == 0)
         return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeTallDma>>(
             a, packed_rows, stream);
     return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeGroupNarrowDma>>(
@@ -969,7 +742,7 @@ int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int6
 
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     if (a.gu != nullptr) return launch_gate_up_save(act, wdt, a, packed_rows, stream);
-    if (a.M <= kSkinnyMaxTokens && (tile_override() == kTileAuto || a.rms_eps > 0.0f) && packed_rows % 64 == 0)
+    if (a.M <= kSkinnyMaxTokens && packed_rows % 64 == 0)
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
     if (a.row_scale == nullptr && a.rms_eps > 0.0f)
         return set_error(TRMOE_ERR_INVALID, "gate_up: in-kernel RMSNorm scales need the decode kernels (n <= 128)");
@@ -1015,59 +788,17 @@ template <class Kind, bool FP8>
 static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
     const int64_t mt = (a.M + 255) / 256;
     const bool fits224 = a.N % ShapeDown224::BN == 0;
-    int ov = tile_override();
-    if (ov == kTileAuto) {
-        if (FP8 && a.N % 256 == 0 && mt * (a.N / 256) >= 256) ov = kTileF8Dma;
-        else if (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) ov = kTileDma;
-        else ov = (mt * ((a.N + 255) / 256) >= kBigTileMinBlocks) ? kTileDma : kTileSmall;
+    if constexpr (FP8) {
+        if (a.N % 256 == 0 && mt * (a.N / 256) >= 256) return launch_down_shape<Kind, FP8, ShapeBigF8Dma>(a, stream);
     }
-    switch (ov) {
-        case kTileBig:
-            if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
-            return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
-        case kTileBig8P2: return launch_down_shape<Kind, FP8, ShapeBig8P2>(a, stream);
-        case kTileBig4P2:
-            if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224P2>(a, stream);
-            return launch_down_shape<Kind, FP8, ShapeBig4P2>(a, stream);
-        case kTileBig8Pipe: return launch_down_shape<Kind, FP8, ShapeBig8Pipe>(a, stream);
-        case kTileBig4Pipe:
-            if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Pipe>(a, stream);
-            return launch_down_shape<Kind, FP8, ShapeBig4Pipe>(a, stream);
-        case kTileDma64:
-            if constexpr (FP8) {
-                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
-                return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
-            } else if constexpr (sizeof(typename Kind::T) == 4) {
-                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
-                return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
-            } else {
-                // 224 rows do not split into whole 16-row groups per wave
-                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
-                return launch_down_shape<Kind, FP8, ShapeBigDma64>(a, stream);
-            }
-        case kTileDma4:
-            if constexpr (FP8) {
-                return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
-            } else {
-                return launch_down_shape<Kind, FP8, ShapeBig4Dma>(a, stream);
-            }
-        case kTileF8Dma:
-            if constexpr (FP8) {
-                return launch_down_shape<Kind, FP8, ShapeBigF8Dma>(a, stream);
-            } else {
-                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
-                return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
-            }
-        case kTileDma:
-        case kTilePersistDma:
-            if constexpr (FP8) {
-                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
-                return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
-            } else {
-                if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
-                return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
-            }
-        default: return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
+    const bool big = (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) || mt * ((a.N + 255) / 256) >= kBigTileMinBlocks;
+    if (!big) return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
+    if constexpr (FP8) {
+        if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);
+        return launch_down_shape<Kind, FP8, ShapeBig>(a, stream);
+    } else {
+        if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224Dma>(a, stream);
+        return launch_down_shape<Kind, FP8, ShapeBigDma>(a, stream);
     }
 }
 

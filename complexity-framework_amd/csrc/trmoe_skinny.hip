@@ -549,16 +549,9 @@ int gate_up_skinny_kind(const GateUpArgs& a, int64_t packed_rows, hipStream_t st
 
 // K spans (128 bytes of K) per split: the whole K (no reduction launch) up
 // to 8 tokens; about 16 spans (2 KiB of K: four splits at K = 3328) up to 64
-// tokens and 8 above, spread evenly over the splits.  TRMOE_SKINNY_SPS
-// (read once per process) overrides the target.
+// tokens and 8 above, spread evenly over the splits.
 int down_spans_per_split(int64_t M, int spans) {
     int target = M <= 8 ? spans : (M <= 64 ? 16 : 8);
-    // read once: the workspace query and the launch must agree
-    static const int forced = [] {
-        const char* e = getenv("TRMOE_SKINNY_SPS");
-        return e != nullptr && atoi(e) > 0 ? atoi(e) : 0;
-    }();
-    if (forced > 0) target = forced;
     if (target > spans) target = spans;
     if (target < 1) target = 1;
     const int splits = (spans + target - 1) / target;
@@ -585,15 +578,8 @@ int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStrea
 
 // Column tile: 8 columns up to 16 tokens (the whole K in one workgroup, so
 // twice the workgroups), 16 up to 64 tokens, 32 above (half the re-reads of
-// the activations).  TRMOE_SKINNY_COLS=8/16/32 (read once per process) forces.
-int down_cols(int64_t M) {
-    static const int forced = [] {
-        const char* e = getenv("TRMOE_SKINNY_COLS");
-        return e != nullptr && (atoi(e) == 8 || atoi(e) == 16 || atoi(e) == 32) ? atoi(e) : 0;
-    }();
-    if (forced > 0) return forced;
-    return M <= 16 ? 8 : (M <= 64 ? 16 : 32);
-}
+// the activations).
+int down_cols(int64_t M) { return M <= 16 ? 8 : (M <= 64 ? 16 : 32); }
 
 template <class Kind, bool FP8, int COLS, bool FRAG>
 int down_skinny_cols(const DownArgs& a, float* part, int sps, int splits, hipStream_t stream) {

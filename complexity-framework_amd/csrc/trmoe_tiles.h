@@ -34,14 +34,14 @@ __device__ __forceinline__ void init_bprov(typename BProvSel<Kind, FP8, ROWS, NT
 // register-staged loads otherwise (and always for e4m3 weights, which are
 // expanded to bf16 on the way into LDS).
 template <class Shape, int ROWS>
-using DmaProv = std::conditional_t<Shape::PGR == 5, DmaRows64<ROWS, Shape::NT>, DmaRows<ROWS, Shape::NT>>;
+using DmaProv = DmaRows<ROWS, Shape::NT>;
 template <class Shape>
 struct AProvOf {
     using type = std::conditional_t<(Shape::PGR >= 4), DmaProv<Shape, Shape::BM>, BufRows<Shape::BM, Shape::NT>>;
 };
 template <class Kind, bool FP8, class Shape>
 struct BProvOf {
-    static_assert(!(FP8 && (Shape::PGR == 4 || Shape::PGR == 5)), "e4m3 weights: register path or PGR 6");
+    static_assert(!(FP8 && Shape::PGR == 4), "e4m3 weights: register path or PGR 6");
     static_assert(!(!FP8 && Shape::PGR == 6), "PGR 6 is the e4m3 weight layout");
     // PGR 6: e4m3 rows of 64 bytes per K stage, the 64-byte-row DMA layout
     using type = std::conditional_t<
@@ -70,21 +70,12 @@ __device__ __forceinline__ void init_b(typename BProvOf<Kind, FP8, Shape>::type&
 
 using ShapeMain = TileShape<128, 128, 2, 2>;
 using ShapeBig = TileShape<256, 256, 2, 4>;        // 8 waves of 128x64, 2 waves per SIMD
-using ShapeBig8P2 = TileShape<256, 256, 2, 4, 2>;  // same, two stages of global prefetch
-using ShapeBig4P2 = TileShape<256, 256, 2, 2, 2>;  // 4 waves of 128x128, two stages of prefetch
 using ShapeDown224 = TileShape<256, 224, 4, 1>;
-using ShapeDown224P2 = TileShape<256, 224, 4, 1, 2>;
-using ShapeBig8Pipe = TileShape<256, 256, 2, 4, 3>;
-using ShapeBig4Pipe = TileShape<256, 256, 2, 2, 3>;
-using ShapeDown224Pipe = TileShape<256, 224, 4, 1, 3>;
 using ShapeBigDma = TileShape<256, 256, 2, 4, 4>;    // 8 waves, direct buffer->LDS operand loads
 using ShapeDown224Dma = TileShape<256, 224, 4, 1, 4>;
-using ShapeBig4Dma = TileShape<256, 256, 2, 2, 4>;   // 4 waves of 128x128: 2/3 of the LDS reads per MFMA
-using ShapeBigDma64 = TileShape<256, 256, 2, 4, 5>;  // four 64-byte-row stages, three in flight
 using ShapeBigF8Dma = TileShape<256, 256, 2, 4, 6>;  // e4m3 weights loaded straight into LDS
 using ShapeGroupNarrowDma = TileShape<256, 128, 4, 2, 4>;   // 256x128 direct-load tiles
 using ShapeTallDma = TileShape<128, 256, 1, 4, 4>;          // 128x256: 4 waves of 128x64
-using ShapeMainF8Dma = TileShape<128, 128, 2, 2, 6>;
 
 // ---------------------------------------------------------------------------
 // expert-grouped tiles

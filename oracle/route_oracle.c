@@ -87,8 +87,8 @@ int oracle_partition(const int64_t *routes, int64_t n, int top_k, int num_expert
             for (int s = 0; s < top_k; ++s) {
                 int64_t a = (int64_t)s * n + t;
                 int64_t e = routes[a];
-                /* within one token the experts are distinct, and the segment
-                 * of expert e sees tokens in increasing order */
+                /* the segment of expert e sees tokens in increasing order,
+                 * and a token whose slots repeat an expert in slot order */
                 sorted[cursor[e]] = a;
                 inverse[a] = cursor[e];
                 cursor[e] += 1;

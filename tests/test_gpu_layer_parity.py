@@ -259,6 +259,103 @@ def test_graph_backend_replays_hip_kernels(gpu):
             assert torch.equal(got, eager(x, ids)), step
 
 
+@pytest.mark.parametrize("tokens", [(4, 16), (64, 1)])
+def test_graph_replay_follows_weight_changes(gpu, tokens):
+    """A captured graph reads the packed weights it captured.  After
+    load_state_dict (new weights), an in-place update, a routing-strategy
+    change or quantize_fp8_(), replays must give the eager result of the new
+    weights (the runner re-captures), and the old pack must not be read after
+    it was freed.  (64, 1) takes the decode kernels and their split-K
+    scratch, which each captured graph owns."""
+    from complexity_amd.tr_hash import GraphBucket, TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(13)
+    b, t = tokens
+    common = dict(hidden_size=128, vocab_size=997, num_experts=4, top_k=2, shared_width=256, expert_width=64,
+                  precision="bf16", phase="inference")
+    graph = TRHashEngine(TRHashEngineConfig(**common, backend="cuda_graph",
+                                            graph_buckets=(GraphBucket(b, t),))).to(gpu).to(torch.bfloat16).eval()
+    eager = TRHashEngine(TRHashEngineConfig(**common, backend="hip")).to(gpu).to(torch.bfloat16).eval()
+    ids = torch.randint(0, 997, (b, t), device=gpu)
+    x = torch.randn(b, t, 128, device=gpu, dtype=torch.bfloat16)
+
+    def check(tag):
+        with torch.no_grad():
+            got = graph(x, ids)
+            torch.cuda.empty_cache()   # freed packs would now be reused or unmapped
+            _ = torch.randn(1 << 20, device=gpu).sum()
+            torch.cuda.synchronize()
+            want = eager(x, ids)
+        assert torch.equal(got, want), tag
+
+    eager.load_state_dict(graph.state_dict())
+    check("initial")
+    other = TRHashEngine(TRHashEngineConfig(**common, backend="hip", route_seed=7)).to(gpu).to(torch.bfloat16)
+    sd = {k: v for k, v in other.state_dict().items() if "route" not in k and "fused" not in k}
+    graph.load_state_dict(sd, strict=False)
+    eager.load_state_dict(sd, strict=False)
+    check("load_state_dict")
+    with torch.no_grad():
+        graph.expert_down.mul_(1.5)
+        eager.expert_down.mul_(1.5)
+    check("in-place update")
+    graph.routed_strategy = eager.routed_strategy = "grouped"
+    check("strategy")
+    graph.quantize_fp8_()
+    eager.quantize_fp8_()
+    check("quantize_fp8_")
+
+
+def test_quantized_bf16_engine_under_autograd_takes_the_universal_path(gpu):
+    """quantize_fp8_() on a bf16-config engine: differentiable calls resolve
+    to PYTORCH (the e4m3 packs have no backward) and match the oracle on the
+    dequantised weights; no-grad calls stay on HIP."""
+    from complexity_amd.tr_hash import TRHashBackend, TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(17)
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=128, vocab_size=997, num_experts=4, top_k=2,
+                                             shared_width=256, expert_width=64, precision="bf16",
+                                             routing_strategy="token_id_multi_hash")).to(gpu).to(torch.bfloat16)
+    engine.quantize_fp8_()
+    ids = torch.randint(0, 997, (2, 200), device=gpu)
+    x = torch.randn(2, 200, 128, device=gpu, dtype=torch.bfloat16, requires_grad=True)
+    out = engine(x, ids)
+    assert engine.last_backend.selected is TRHashBackend.PYTORCH
+    assert any("e4m3" in r for r in engine.last_backend.reasons)
+    out.float().square().sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad is not None and torch.isfinite(x.grad.float()).all()
+    ref = _oracle(engine, x.detach(), ids, dequant_fp8=True)
+    assert O.normwise_rel_err(out.detach(), ref) <= BOUND["fp8"]
+    with torch.no_grad():
+        hip = engine(x.detach(), ids)
+    assert engine.last_backend.selected is TRHashBackend.HIP
+    assert O.normwise_rel_err(hip, ref) <= BOUND["fp8"]
+
+
+@pytest.mark.parametrize("strategy", ["grouped", "dense"])
+def test_repeated_experts_per_token_match_oracle(gpu, strategy):
+    """A loaded table whose slots name one expert twice for some ids: the
+    reference sums both slots' weights (engine.py:94); the grouped path gives
+    each slot its own partition row and sums them in the un-permute."""
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(19)
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=128, vocab_size=997, num_experts=4, top_k=2,
+                                             shared_width=256, expert_width=64, precision="fp32",
+                                             route_weights=(0.7, 0.3), routed_output_scale=2.0,
+                                             routing_strategy="token_id_multi_hash")).to(gpu)
+    table = engine.route_table.clone()
+    table[1, :300] = table[0, :300]
+    engine.load_route_table(table)
+    engine.routed_strategy = strategy
+    ids = torch.randint(0, 997, (3, 400), device=gpu)
+    ids[0, :300] = torch.arange(300, device=gpu)
+    x = torch.randn(3, 400, 128, device=gpu)
+    out = _run(engine, x, ids)
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["fp32"]
+
+
 def test_fp32_layer_at_prefill_size(gpu):
     """C1's fp32 layer at C2's 16384 tokens: the large-tile fp32 kernels."""
     from dataclasses import replace

@@ -37,6 +37,30 @@ def test_route_sort_small_and_ragged(gpu, order, E, k):
 
 
 @pytest.mark.parametrize("order", [O.ORDER_TOKEN, O.ORDER_ASSIGNMENT])
+@pytest.mark.parametrize("E,k", [(1, 2), (2, 2), (4, 4), (16, 4)])
+def test_route_sort_repeated_experts_per_token(gpu, order, E, k):
+    """Tables whose slots repeat an expert for a token: one partition row per
+    assignment, ties broken by slot (single- and multi-block launches)."""
+    rng = np.random.default_rng(E * 13 + k + order)
+    table = rng.integers(0, E, (k, 503)).astype(np.int64)
+    table[:, :40] = table[0, :40]
+    for n in (1, 100, 2000, 40000):
+        ids = rng.integers(0, 503, n)
+        ids[: min(n, 40)] = np.arange(min(n, 40))
+        _check(gpu, table, ids, E, order)
+
+
+@pytest.mark.parametrize("n", [2048 * 1024 // 2 + 77, 3 * 65536 + 5])
+def test_route_sort_many_chunks_per_block(gpu, n):
+    """Beyond 256 blocks x 256 items the blocks take several chunks each."""
+    table = O.multi_hash_table(32000, 16, 2, 0)
+    rng = np.random.default_rng(n)
+    ids = rng.integers(0, 32000, n)
+    _check(gpu, table, ids, 16, O.ORDER_TOKEN)
+    _check(gpu, table, ids, 16, O.ORDER_ASSIGNMENT)
+
+
+@pytest.mark.parametrize("order", [O.ORDER_TOKEN, O.ORDER_ASSIGNMENT])
 def test_route_sort_c2_zipf_prefill(gpu, order):
     from complexity_amd import workloads as W
 

@@ -195,6 +195,55 @@ def test_auto_backend_on_gpu_selects_hip_also_under_autograd():
         assert d.selected is TRHashBackend.PYTORCH and any("backward" in r for r in d.reasons)
 
 
+def test_quantized_copies_keep_differentiable_calls_off_hip():
+    """An engine quantised with quantize_fp8_() computes from e4m3 copies
+    whatever its config precision: differentiable calls resolve to PYTORCH
+    (AUTO) or raise (explicit HIP), like an fp8 config."""
+    cfg = _config()
+    assert supports_hip_backward(cfg) and not supports_hip_backward(cfg, quantized_weights=True)
+    d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False,
+                       fused_cuda_available=False, autograd=True, quantized_weights=True)
+    assert d.selected is TRHashBackend.PYTORCH and any("e4m3" in r for r in d.reasons)
+    d = select_backend(cfg, device_type="cuda", hip_available=True, cggr_available=False,
+                       fused_cuda_available=False, autograd=False, quantized_weights=True)
+    assert d.selected is TRHashBackend.HIP
+    with pytest.raises(RuntimeError, match="e4m3"):
+        select_backend(_config(backend=TRHashBackend.HIP), device_type="cuda", hip_available=True, autograd=True,
+                       quantized_weights=True)
+
+
+def test_quantize_clears_the_cached_decision(monkeypatch):
+    """The decision cache is keyed on the e4m3 state: a grad-enabled forward
+    after quantize_fp8_() no longer reuses the bf16 decision."""
+    from complexity_amd.tr_hash import capabilities
+
+    monkeypatch.setattr(capabilities, "_hip_available", lambda: True)
+    eng = _engine()
+
+    class _Fake:   # the two attributes _decide reads of a ROCm activation
+        device = torch.device("cuda")
+        requires_grad = True
+
+    fake = _Fake()
+    with torch.enable_grad():
+        assert eng._decide(fake).selected is TRHashBackend.HIP
+        eng.quantize_fp8_()
+        assert eng._decide(fake).selected is TRHashBackend.PYTORCH
+
+
+def test_save_refuses_e4m3_packs():
+    from complexity_amd import ops
+
+    packed = ops.PackedLayer(act_dtype=torch.bfloat16, num_experts=4, expert_width=64,
+                             expert_gate_up=torch.zeros(4, 128, 64, dtype=torch.float8_e4m3fn))
+    assert packed.fp8
+    assert not ops.PackedLayer(act_dtype=torch.bfloat16, num_experts=4, expert_width=64,
+                               expert_gate_up=torch.zeros(4, 128, 64, dtype=torch.bfloat16)).fp8
+    with pytest.raises(ValueError, match="inference-only"):
+        ops.layer_forward(torch.zeros(2, 64), torch.zeros(2, dtype=torch.long), torch.zeros(2, 8, dtype=torch.long),
+                          packed, (0.5, 0.5), 1.0, 1.0, save=True)
+
+
 def test_missing_library_on_gpu_fails_loudly(monkeypatch):
     monkeypatch.delenv("TRMOE_ALLOW_PYTORCH_FALLBACK", raising=False)
     with pytest.raises(RuntimeError):
@@ -347,6 +396,18 @@ def test_capacity_change_and_table_load_invalidate_captured_graphs():
     assert eng._graph_pool == {}
     eng._graph_pool["sentinel"] = object()
     eng.load_route_table(eng.route_table.clone())
+    assert eng._graph_pool == {}
+
+
+def test_quantize_and_module_moves_invalidate_captured_graphs():
+    """A captured graph holds the addresses of the packs and parameters it
+    read: quantize_fp8_() and _apply (.to(), .float(), ...) drop it."""
+    eng = _engine(num_experts=4, top_k=2)
+    eng._graph_pool["sentinel"] = object()
+    eng.quantize_fp8_()
+    assert eng._graph_pool == {}
+    eng._graph_pool["sentinel"] = object()
+    eng.to(torch.float64)
     assert eng._graph_pool == {}
 
 

@@ -160,6 +160,31 @@ def test_partition_brute_force_numpy_and_c(coracle, order, experts, k):
             assert (np.diff(key) > 0).all()
 
 
+@pytest.mark.parametrize("order", [O.ORDER_TOKEN, O.ORDER_ASSIGNMENT])
+@pytest.mark.parametrize("experts,k", [(1, 2), (2, 2), (4, 4), (16, 4)])
+def test_partition_with_repeated_experts_per_token(coracle, order, experts, k):
+    """Tables whose slots may name one expert twice for a token (a loaded
+    table need not be distinct): every assignment keeps its own row, and the
+    token order breaks (expert, token) ties by slot."""
+    rng = np.random.default_rng(experts * 31 + k + order)
+    for n in (1, 5, 64, 300):
+        routes = rng.integers(0, experts, (k, n)).astype(np.int64)
+        routes[:, 0] = routes[0, 0]   # token 0: every slot the same expert
+        s, inv, off, cnt = O.counting_partition(routes, experts, order)
+        assert np.array_equal(s, O.brute_force_partition(routes, experts, order))
+        cs, cinv, coff, ccnt = c_partition(coracle, routes, experts, order)
+        assert np.array_equal(s, cs) and np.array_equal(inv, cinv)
+        assert np.array_equal(off, coff) and np.array_equal(cnt, ccnt)
+        assert np.array_equal(np.sort(s), np.arange(k * n))
+        assert np.array_equal(inv[s], np.arange(k * n))
+        flat = routes.reshape(-1)
+        for e in range(experts):
+            seg = s[off[e]:off[e + 1]]
+            assert (flat[seg] == e).all()
+            key = (seg % n) * k + seg // n if order == O.ORDER_TOKEN else seg
+            assert (np.diff(key) > 0).all()
+
+
 def test_token_and_assignment_orders_differ_but_share_offsets():
     table = O.route_table("token_id_multi_hash", 1000, 4, 2, 0)
     ids = np.arange(0, 1000, 3)
@@ -207,6 +232,26 @@ def test_masked_dense_matches_token_loop(E, k, S, weights, scales):
                          routed_scale=scales[1])
     b = O.naive_engine_output(x, ids, table, p, route_weights=weights, shared_scale=scales[0],
                               routed_scale=scales[1])
+    assert torch.allclose(a, b, atol=1e-12, rtol=1e-12)
+
+
+@pytest.mark.parametrize("E,k", [(4, 2), (8, 4)])
+def test_masked_dense_sums_repeated_slots_like_the_token_loop(E, k):
+    """A table whose slots repeat an expert for some tokens: the masked
+    formula's weight sum_j w_j [route_j == e] (engine.py:94) equals the token
+    loop's one term per slot."""
+    H, W, V, S = 8, 4, 53, 6
+    p = _params(E, H, W, S, seed=4)
+    rng = np.random.default_rng(E + k)
+    table = torch.from_numpy(rng.integers(0, E, (k, V)).astype(np.int64))
+    table[:, :5] = table[0, :5]     # ids 0..4: every slot the same expert
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 7, H, generator=g, dtype=torch.float64)
+    ids = torch.randint(0, V, (3, 7), generator=g)
+    ids[0, :5] = torch.arange(5)
+    weights = tuple(np.linspace(1.0, 2.0, k) / np.linspace(1.0, 2.0, k).sum())
+    a = O.engine_forward(x, ids, table, p, route_weights=weights, routed_scale=2.0)
+    b = O.naive_engine_output(x, ids, table, p, route_weights=weights, routed_scale=2.0)
     assert torch.allclose(a, b, atol=1e-12, rtol=1e-12)
 
 

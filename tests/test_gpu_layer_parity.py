@@ -334,16 +334,19 @@ def test_quantized_bf16_engine_under_autograd_takes_the_universal_path(gpu):
 
 
 @pytest.mark.parametrize("strategy", ["grouped", "dense"])
-def test_repeated_experts_per_token_match_oracle(gpu, strategy):
-    """A loaded table whose slots name one expert twice for some ids: the
-    reference sums both slots' weights (engine.py:94); the grouped path gives
-    each slot its own partition row and sums them in the un-permute."""
+@pytest.mark.parametrize("E,k,weights", [(16, 2, (0.7, 0.3)), (8, 4, (0.4, 0.3, 0.2, 0.1))])
+def test_repeated_experts_per_token_match_oracle(gpu, strategy, E, k, weights):
+    """A loaded table whose slots name one expert twice for some ids (the
+    reference accepts such tables where it compiles no top-2 pair metadata:
+    more than 8 experts or top_k != 2): the reference sums both slots'
+    weights (engine.py:94); the grouped path gives each slot its own
+    partition row and sums them in the un-permute."""
     from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
 
     torch.manual_seed(19)
-    engine = TRHashEngine(TRHashEngineConfig(hidden_size=128, vocab_size=997, num_experts=4, top_k=2,
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=128, vocab_size=997, num_experts=E, top_k=k,
                                              shared_width=256, expert_width=64, precision="fp32",
-                                             route_weights=(0.7, 0.3), routed_output_scale=2.0,
+                                             route_weights=weights, routed_output_scale=2.0,
                                              routing_strategy="token_id_multi_hash")).to(gpu)
     table = engine.route_table.clone()
     table[1, :300] = table[0, :300]

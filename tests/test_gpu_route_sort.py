@@ -37,7 +37,7 @@ def test_route_sort_small_and_ragged(gpu, order, E, k):
 
 
 @pytest.mark.parametrize("order", [O.ORDER_TOKEN, O.ORDER_ASSIGNMENT])
-@pytest.mark.parametrize("E,k", [(1, 2), (2, 2), (4, 4), (16, 4)])
+@pytest.mark.parametrize("E,k", [(2, 2), (4, 4), (8, 2), (16, 4)])
 def test_route_sort_repeated_experts_per_token(gpu, order, E, k):
     """Tables whose slots repeat an expert for a token: one partition row per
     assignment, ties broken by slot (single- and multi-block launches)."""

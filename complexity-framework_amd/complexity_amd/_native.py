@@ -65,6 +65,10 @@ SIGNATURES = {
         [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
          _c_vp, _c_size, _c_vp],
     ),
+    "trmoe_route_sort_noalloc": (
+        _c_int,
+        [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp],
+    ),
     "trmoe_shared_gate_up": (
         _c_int,
         [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],

@@ -26,6 +26,9 @@
 #include "trmoe_common.h"
 #include "trmoe_internal.h"
 
+#include <mutex>
+#include <string>
+
 namespace trmoe {
 
 constexpr int kSortThreads = 256;
@@ -234,6 +237,62 @@ int64_t route_sort_blocks(int64_t n, int k, int order) {
     int nb, ch;
     sort_split(n * k, &nb, &ch);
     return nb;
+}
+
+int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,
+                      int order, int64_t* routes, int64_t* sorted, int64_t* inverse, int32_t* offsets,
+                      int32_t* counts, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// scratch of the entry point that allocates nothing
+// ---------------------------------------------------------------------------
+// The per-block histograms of the multi-block partition, at most
+// kMaxSortBlocks x kMaxExperts int32 (16 KiB), in a file-scope device array:
+// every GPU the library runs on holds its own copy until the process ends.
+// In host code `scratch` names only a host-side stand-in, so its device
+// address is looked up once per device (with that device current) and only
+// that address is passed to kernels.
+static __device__ __align__(256) int32_t scratch[kMaxSortBlocks * kMaxExperts];
+static_assert(sizeof(scratch) == TRMOE_ROUTE_SORT_NOALLOC_SCRATCH_BYTES, "header and array disagree");
+
+static int noalloc_scratch(void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* ptrs[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return set_error(TRMOE_ERR_HIP, "route_sort_noalloc: no current HIP device (or more than 64 devices)");
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || p == nullptr) {
+            const std::string m = std::string("route_sort_noalloc: hipGetSymbolAddress(scratch): ") +
+                                  (err != hipSuccess ? hipGetErrorString(err) : "null address");
+            return set_error(TRMOE_ERR_HIP, m.c_str());
+        }
+        ptrs[dev] = p;
+    }
+    *out = ptrs[dev];
+    return TRMOE_OK;
+}
+
+int launch_route_sort_noalloc(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,
+                              int order, int64_t* routes, int64_t* sorted, int64_t* inverse, int32_t* offsets,
+                              int32_t* counts, hipStream_t stream) {
+    int nb, ch;
+    sort_split(n * k, &nb, &ch);
+    const size_t need = nb > 1 ? (size_t)nb * (size_t)E * sizeof(int32_t) : 0;
+    if (need > sizeof(scratch)) {
+        const std::string m = "route_sort_noalloc: the partition needs " + std::to_string(need) +
+                              " bytes of scratch; the static buffer holds " + std::to_string(sizeof(scratch));
+        return set_error(TRMOE_ERR_INVALID, m.c_str());
+    }
+    void* ws = nullptr;
+    const int st = noalloc_scratch(&ws);
+    if (st) return st;
+    return launch_route_sort(ids, n, table, vocab, k, E, order, routes, sorted, inverse, offsets, counts, ws,
+                             sizeof(scratch), stream);
 }
 
 int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,

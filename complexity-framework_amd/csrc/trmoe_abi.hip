@@ -194,6 +194,27 @@ int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* 
                              workspace_bytes, as_stream(stream));
 }
 
+int trmoe_route_sort_noalloc(const int64_t* token_ids, int64_t n_tokens, const int64_t* route_table,
+                             int64_t vocab_size, int top_k, int num_experts, int order, int64_t* routes,
+                             int64_t* sorted_indices, int64_t* inverse, int32_t* expert_offsets,
+                             int32_t* expert_counts, void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0, "route_sort_noalloc: n_tokens must be non-negative");
+    TRMOE_REQUIRE(top_k == 1 || top_k == 2 || top_k == 4, "route_sort_noalloc: top_k must be 1, 2 or 4");
+    TRMOE_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts,
+                  "route_sort_noalloc: num_experts must be in [1, 16]");
+    TRMOE_REQUIRE(top_k <= num_experts, "route_sort_noalloc: top_k cannot exceed num_experts");
+    TRMOE_REQUIRE(vocab_size > 0, "route_sort_noalloc: vocab_size must be positive");
+    TRMOE_REQUIRE(order == TRMOE_ORDER_TOKEN || order == TRMOE_ORDER_ASSIGNMENT, "route_sort_noalloc: bad order");
+    TRMOE_REQUIRE(route_table != nullptr && expert_offsets != nullptr && expert_counts != nullptr,
+                  "route_sort_noalloc: null pointer");
+    TRMOE_REQUIRE(n_tokens == 0 || (token_ids != nullptr && sorted_indices != nullptr && inverse != nullptr),
+                  "route_sort_noalloc: null pointer");
+    TRMOE_REQUIRE(n_tokens * top_k < (int64_t)1 << 31, "route_sort_noalloc: too many assignments");
+    return launch_route_sort_noalloc(token_ids, n_tokens, route_table, vocab_size, top_k, num_experts, order,
+                                     routes, sorted_indices, inverse, expert_offsets, expert_counts,
+                                     as_stream(stream));
+}
+
 // Fused RMSNorm scales of the *_rms entry points: a row_scale array, or
 // (row_scale null) eps > 0 for scales computed by the decode kernels.
 static int rms_args_ok(const char* who, const float* row_scale, float eps, int64_t n_tokens) {

@@ -28,5 +28,8 @@ int64_t route_sort_blocks(int64_t n, int k, int order);
 int launch_route_sort(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,
                       int order, int64_t* routes, int64_t* sorted, int64_t* inverse, int32_t* offsets,
                       int32_t* counts, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int launch_route_sort_noalloc(const int64_t* ids, int64_t n, const int64_t* table, int64_t vocab, int k, int E,
+                              int order, int64_t* routes, int64_t* sorted, int64_t* inverse, int32_t* offsets,
+                              int32_t* counts, hipStream_t stream);
 
 }  // namespace trmoe

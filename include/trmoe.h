@@ -134,7 +134,12 @@ int trmoe_pack_weight(int kind, int dtype, const void* src_a, const void* src_b,
  *   expert_offsets int32[E+1]    segment starts, offsets[E] = k*n
  *   expert_counts  int32[E]
  * 1 <= num_experts <= 16, top_k in {1, 2, 4}, top_k <= num_experts, entries of
- * the table in [0, num_experts) and distinct per token.
+ * the table in [0, num_experts) (entries outside are clamped into it, so no
+ * write leaves the outputs).  A token's slots may name one expert twice:
+ * every assignment has its own partition row, and the token order breaks
+ * (expert, token) ties by slot.  workspace: per-block histograms,
+ * trmoe_route_sort_workspace_bytes() (at most 256 blocks x num_experts int32;
+ * 0 when one block takes every assignment).
  */
 size_t trmoe_route_sort_workspace_bytes(int64_t n_tokens, int top_k, int num_experts, int order);
 int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* route_table,
@@ -142,6 +147,28 @@ int trmoe_route_sort(const int64_t* token_ids, int64_t n_tokens, const int64_t* 
                      int64_t* sorted_indices, int64_t* inverse, int32_t* expert_offsets,
                      int32_t* expert_counts, void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/*
+ * K1 without a workspace argument.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, validation and results as trmoe_route_sort, bit for bit; the
+ * caller still passes the inputs and outputs.  The per-block histograms of
+ * the multi-block partition live in a file-scope device array of
+ * TRMOE_ROUTE_SORT_NOALLOC_SCRATCH_BYTES (256 blocks x 16 experts of int32),
+ * one copy per GPU held until the process ends; a partition that would need
+ * more is rejected with TRMOE_ERR_INVALID (the block split never asks for
+ * more).  The call allocates and frees nothing; its first call on a device
+ * looks up that device's copy of the array.  Every call on one GPU shares
+ * that GPU's array, which keeps the last call's contents (nothing in it must
+ * start at zero): calls ordered on one stream are safe, calls that overlap
+ * on one GPU (unordered streams) race.
+ */
+#define TRMOE_ROUTE_SORT_NOALLOC_SCRATCH_BYTES 16384
+int trmoe_route_sort_noalloc(const int64_t* token_ids, int64_t n_tokens, const int64_t* route_table,
+                             int64_t vocab_size, int top_k, int num_experts, int order, int64_t* routes,
+                             int64_t* sorted_indices, int64_t* inverse, int32_t* expert_offsets,
+                             int32_t* expert_counts, void* stream);
 
 /*
  * K2 -- shared SwiGLU first half; replaces the two nn.Linear calls and

@@ -234,6 +234,105 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
     }
 
 
+def c4_e2e(torch, dev, steps: int = 128, reps: int = 3):
+    """C4 end to end: the 16-layer TR-GQA 200M decoder (complexity_amd.decoder,
+    random-init bf16, HIP TR-MoE layer in every block, SDPA attention).
+
+    Prefill: 8 x 2048 Zipf(1.1) ids through every layer plus the last
+    position's logits, timed with HIP events (median of `reps`).  Decode:
+    `steps` greedy steps of one token per sequence (8 per step), the step
+    captured once as a HIP graph and replayed.  MLP share: prefill from
+    events around each block's two halves (a separate instrumented run);
+    decode from a graph of the 16 MLP halves alone at the decode shape,
+    against the whole step."""
+    from complexity_amd import workloads
+    from complexity_amd.decoder import TRGQAConfig, TRGQADecoder
+
+    cfg = TRGQAConfig()
+    model = TRGQADecoder(cfg).to(dev, torch.bfloat16).init_weights(0).eval()
+    ids = workloads.zipf_ids(8 * 2048, cfg.vocab_size, 1.1, torch.Generator().manual_seed(0)).view(8, 2048).to(dev)
+
+    def prefill():
+        h = model.prefill(ids, steps + 1, return_logits=False)
+        return model.logits(h[:, -1:]).argmax(dim=-1).view(-1)
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    with torch.no_grad():
+        prefill()
+        torch.cuda.synchronize()
+        gc.collect()
+        gc.disable()
+        pre = []
+        for _ in range(reps):
+            s, e = ev(), ev()
+            s.record()
+            first = prefill()
+            e.record()
+            torch.cuda.synchronize()
+            pre.append(s.elapsed_time(e))
+        prefill_ms = statistics.median(pre)
+        timings = {}
+        model.prefill(ids, steps + 1, return_logits=False, timings=timings)
+        torch.cuda.synchronize()
+        attn_ms = sum(s.elapsed_time(e) for s, e in timings["attention"])
+        mlp_ms = sum(s.elapsed_time(e) for s, e in timings["mlp"])
+        model.capture_decode(8)
+        model._g_ids.copy_(first)
+        s, e = ev(), ev()
+        s.record()
+        for _ in range(steps):
+            model._graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        step_ms = s.elapsed_time(e) / steps
+        # the MLP halves alone at the decode shape, one graph over 16 layers
+        h = (torch.randn(8, 1, cfg.hidden_size, generator=torch.Generator().manual_seed(2)) * 0.5).to(dev, torch.bfloat16)
+        tok = first.view(8, 1)
+
+        def mlps():
+            out = h
+            for b in model.layers:
+                n = b.post_attention_layernorm
+                out = b.mlp.forward_norm_residual(out, tok, n.weight, n.eps)
+            return out
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            mlps()
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            mlps()
+        for _ in range(5):
+            graph.replay()
+        s, e = ev(), ev()
+        s.record()
+        for _ in range(steps):
+            graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        mlp_step_ms = s.elapsed_time(e) / steps
+        gc.enable()
+    return {
+        "workload": "c4_tr_gqa_200m_prefill_8x2048_decode_128",
+        "layers": cfg.num_layers,
+        "prefill_tokens": int(ids.numel()),
+        "prefill_ms": prefill_ms,
+        "prefill_tokens_per_s": ids.numel() / (prefill_ms * 1e-3),
+        "prefill_mlp_share": mlp_ms / (mlp_ms + attn_ms),
+        "decode_steps": steps,
+        "decode_mode": "hip_graph_replay",
+        "decode_ms_per_step": step_ms,
+        "decode_tokens_per_s": 8 / (step_ms * 1e-3),
+        "decode_mlp_ms_per_step": mlp_step_ms,
+        "decode_mlp_share": mlp_step_ms / step_ms,
+        "attention": "torch SDPA (flash causal prefill, memory-efficient masked decode)",
+    }
+
+
 def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
     """Forward + backward through autograd on the HIP backend (the layer's
     gradients of x and every weight), timed with HIP events like the forward.
@@ -360,6 +459,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip timing the second routed strategy")
     ap.add_argument("--no-train", action="store_true", help="skip the forward+backward (autograd) timing")
+    ap.add_argument("--no-c4", action="store_true", help="skip the 16-layer TR-GQA decoder (C4) end to end")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="end with three elementwise copies of MIB MiB (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -441,6 +541,8 @@ def main():
             "fused_us_per_layer": fused["ms_per_layer"] * 1e3,
             "unfused_us_per_layer": unfused["ms_per_layer"] * 1e3,
         }
+    if not args.no_c4:
+        result["c4_e2e"] = c4_e2e(torch, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(w, min(args.cpu_sample, tokens))
     if args.calibrate_copy:

@@ -96,16 +96,53 @@ __device__ __forceinline__ void gate_up_routes(const GateUpArgs& a, int64_t m0, 
 // rows padded by 16 bytes; after a barrier gate_up_epi_store copies the tile
 // out with coalesced 16-byte stores.  gate_up_epilogue runs both; it ends
 // with LDS still in use by the copy (callers that reuse LDS barrier first).
-template <class Kind, class Shape, bool ROUTED = true>
-__device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&acc)[Shape::TM][Shape::TN],
-                                                 int64_t n0, char* lds, const int (*s_route)[kMaxTopK],
-                                                 const float* s_rscale = nullptr) {
+// One 32-feature block (gate accumulators acc[tm][2p], up acc[tm][2p + 1])
+// of a wave, 32 rows at a time: the rows' LDS data (route weights, RMSNorm
+// scales) is read first, then the 16 SwiGLU values per lane are written.  The
+// compiler cannot tell the LDS arrays apart, so reads interleaved with the
+// writes element by element would each wait for an LDS round trip.
+template <class Kind, class Shape, bool RT, bool RS>
+__device__ __forceinline__ void gate_up_epi_block(const GateUpArgs& a, const f32x16 (&acc)[Shape::TM][Shape::TN],
+                                                  int p, int expert, float sg, float su, int wm0, int fl, char* lds,
+                                                  const int (*s_route)[kMaxTopK], const float* s_rscale) {
     using T = typename Kind::T;
+    constexpr int kHRowBytes = Shape::BN / 2 * (int)sizeof(T) + 16;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int tm = 0; tm < Shape::TM; ++tm) {
+        float mult[16], rs[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int rl = wm0 + tm * 32 + acc_row(lane, i);
+            if constexpr (RT) {   // the token's weight for this block's expert: sum_j w_j [route_j == e]
+                const int* rr = s_route[rl];
+                float tw = 0.f;
+#pragma unroll
+                for (int j = 0; j < kMaxTopK; ++j) tw += (rr[j] == expert) ? a.rw[j] : 0.f;
+                mult[i] = tw;
+            } else {
+                mult[i] = a.shared_mult;
+            }
+            rs[i] = RS ? s_rscale[rl] : 1.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int rl = wm0 + tm * 32 + acc_row(lane, i);
+            const float g = acc[tm][2 * p][i] * sg * rs[i];
+            const float u = acc[tm][2 * p + 1][i] * su * rs[i];
+            const float hv = silu_f(g) * u * mult[i];
+            *reinterpret_cast<T*>(lds + rl * kHRowBytes + fl * (int)sizeof(T)) = from_f32<T>(hv);
+        }
+    }
+}
+
+template <class Kind, class Shape, bool ROUTED, bool RS>
+__device__ __forceinline__ void gate_up_epi_tile_rs(const GateUpArgs& a, const f32x16 (&acc)[Shape::TM][Shape::TN],
+                                                    int64_t n0, char* lds, const int (*s_route)[kMaxTopK],
+                                                    const float* s_rscale) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wm0 = (wave / Shape::WAVES_N) * Shape::WM;
     const int wn0 = (wave % Shape::WAVES_N) * Shape::WN;
-    constexpr int kHRowBytes = Shape::BN / 2 * (int)sizeof(T) + 16;
-    static_assert(Shape::BM * kHRowBytes <= 160 * 1024, "h tile must fit in LDS");
     const int r = lane & 31;
 #pragma unroll
     for (int p = 0; p < Shape::TN / 2; ++p) {
@@ -116,29 +153,25 @@ __device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, f32x16 (&a
         const float su = a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f;
         // expert blocks are multiples of 64 features, so a 32-feature block
         // is wholly shared or wholly one expert's
-        const bool routed = ROUTED && a.ids != nullptr && fblock >= a.shared_feats;
-        const int64_t expert = routed ? (fblock - a.shared_feats) / a.expert_feats : -1;
-        const float mult = routed ? 1.0f : a.shared_mult;
-#pragma unroll
-        for (int tm = 0; tm < Shape::TM; ++tm) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int rl = wm0 + tm * 32 + acc_row(lane, i);
-                const float rs = s_rscale != nullptr ? s_rscale[rl] : 1.0f;   // fused RMSNorm
-                const float g = acc[tm][2 * p][i] * sg * rs;
-                const float u = acc[tm][2 * p + 1][i] * su * rs;
-                float hv = silu_f(g) * u * mult;
-                if (routed) {
-                    const int* rr = s_route[rl];
-                    float tw = 0.f;
-#pragma unroll
-                    for (int j = 0; j < kMaxTopK; ++j) tw += (rr[j] == expert) ? a.rw[j] : 0.f;
-                    hv *= tw;
-                }
-                *reinterpret_cast<T*>(lds + rl * kHRowBytes + fl * (int)sizeof(T)) = from_f32<T>(hv);
-            }
+        if (ROUTED && a.ids != nullptr && fblock >= a.shared_feats) {
+            const int expert = (int)((fblock - a.shared_feats) / a.expert_feats);
+            gate_up_epi_block<Kind, Shape, ROUTED, RS>(a, acc, p, expert, sg, su, wm0, fl, lds, s_route, s_rscale);
+        } else {
+            gate_up_epi_block<Kind, Shape, false, RS>(a, acc, p, -1, sg, su, wm0, fl, lds, s_route, s_rscale);
         }
     }
+}
+
+template <class Kind, class Shape, bool ROUTED = true>
+__device__ __forceinline__ void gate_up_epi_tile(const GateUpArgs& a, const f32x16 (&acc)[Shape::TM][Shape::TN],
+                                                 int64_t n0, char* lds, const int (*s_route)[kMaxTopK],
+                                                 const float* s_rscale = nullptr) {
+    static_assert(Shape::BM * (Shape::BN / 2 * (int)sizeof(typename Kind::T) + 16) <= 160 * 1024,
+                  "h tile must fit in LDS");
+    if (s_rscale != nullptr)
+        gate_up_epi_tile_rs<Kind, Shape, ROUTED, true>(a, acc, n0, lds, s_route, s_rscale);
+    else
+        gate_up_epi_tile_rs<Kind, Shape, ROUTED, false>(a, acc, n0, lds, s_route, s_rscale);
 }
 
 template <class Kind, class Shape>
@@ -263,6 +296,199 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
     if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * Shape::BN);
     gate_up_epilogue<Kind, Shape, ROUTED>(a, acc, m0, n0, lds, s_route,
                                           a.row_scale != nullptr ? s_rscale : nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// K2 (bf16 prefill): ping-pong main loop
+// ---------------------------------------------------------------------------
+// 256x256 tiles, 8 waves of 128x64, two LDS stages of 64-element K (A rows
+// then B rows, 128-byte swizzled rows, filled by direct buffer->LDS loads).
+// The two waves of each SIMD alternate roles every phase: while one
+// multiplies a whole K stage from registers, the other reads its next
+// stage's fragments from LDS, so the matrix pipe runs one wave's MFMAs at a
+// time and the LDS reads and load issue of the other hide under them.
+//
+// Group 0 = waves 0..3 (tile rows 0..127), group 1 = waves 4..7 (rows
+// 128..255, one phase behind).  With a barrier closing every phase:
+//   phase 2t    group 0 issues B(t+1) [weights] then reads stage t;
+//               group 1 multiplies stage t-1
+//   phase 2t+1  group 0 multiplies stage t, then waits for its B(t+1);
+//               group 1 reads stage t, issues A(t+2) [activations] into the
+//               buffer it just read, then waits for its A(t+1)
+// so every stage is complete (each issuing group waited for its own loads)
+// one barrier before its first reader, and a buffer is refilled only after
+// both groups have read it.  In the phase after its last multiply group 0
+// writes its half of the epilogue tile to LDS while group 1 multiplies.
+
+// One operand's direct loads by one group of 4 waves: 256 rows x 128 bytes
+// per stage, 8 wave instructions (8 rows each) per wave.
+struct PPRows {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int row0;        // lane's first row: 64 * wave_in_group + lane / 8
+    int row_bytes;   // row stride in bytes
+    int nrows;       // rows present; rows at or past it load zero
+    int c0;          // lane's K chunk for j = 0 (chunk of instruction j: c0 ^ j)
+    int wig;
+
+    __device__ __forceinline__ void init(const void* base, int64_t first_row, int64_t rows_total, int64_t ld_bytes,
+                                         int wave_in_group) {
+        const int64_t avail = rows_total - first_row;
+        nrows = (int)(avail < 256 ? avail : 256);
+        rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
+        const int lane = threadIdx.x & 63;
+        wig = wave_in_group;
+        row0 = 64 * wave_in_group + (lane >> 3);
+        row_bytes = (int)ld_bytes;
+        // LDS slot (lane & 7) of row r holds K chunk slot ^ swz(r); for the
+        // rows of instruction j, swz(r) = (lane / 8) ^ j (mod 8)
+        c0 = ((lane & 7) ^ (lane >> 3)) & 7;
+    }
+    // stage kt (bytes [128 kt, 128 kt + 128) of every row) into `dst` (the
+    // operand's 32 KB half of an LDS stage)
+    __device__ __forceinline__ void issue(int kt, char* dst) const {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = row0 + 8 * j;
+            const int o = r < nrows ? r * row_bytes + kt * kRowBytes + (((c0 ^ j) & 7) << 4) : kOutOfRange;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (wig * 8 + j) * 8 * kRowBytes), 16,
+                                                    o, 0, 0, 0);
+        }
+    }
+};
+
+// Phase boundary: no instruction (MFMAs included) moves across it.
+__device__ __forceinline__ void pp_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The wave's fragments of one K stage: A rows wm0 + 32 tm + r, B rows
+// wn0 + 32 tn + r, 16-byte chunk 2 g + h of the 128-byte row.
+__device__ __forceinline__ void pp_read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][4], u32x4 (&fb)[4][2]) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+    const char* As = st;
+    const char* Bs = st + 256 * kRowBytes;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+            fa[g][tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+            fb[g][tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
+    }
+}
+
+__device__ __forceinline__ void pp_mma(const u32x4 (&fa)[4][4], const u32x4 (&fb)[4][2], f32x16 (&acc)[4][2]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
+}
+
+// gate|up + SwiGLU over bf16 activations and weights, K a multiple of 64.
+// ROUTED: the launch covers dense-routed expert columns (route gather and
+// per-token expert weights for the tiles that hold them).
+template <bool ROUTED>
+__global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
+    using Shape = ShapeBigDma;   // 256 x 256, waves 2 x 4 of 128 x 64: the epilogue's layout
+    using Kind = KindBF16;
+    extern __shared__ __align__(16) char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * 128, wn0 = wig * 64;
+    const int64_t m0 = (int64_t)blockIdx.x * 256;
+    const int64_t n0 = a.n_base + (int64_t)blockIdx.y * 256;
+
+    // per-row data of the epilogue (read there, after the loop's barriers);
+    // gathered before any direct load is issued, so that the loop's load
+    // counters only count direct loads
+    __shared__ float s_rscale[256];
+    __shared__ int s_route[ROUTED ? 256 : 1][kMaxTopK];
+    bool gathered = false;
+    if (a.row_scale != nullptr) {
+        if (threadIdx.x < 256) {
+            const int64_t row = m0 + threadIdx.x;
+            s_rscale[threadIdx.x] = row < a.M ? a.row_scale[row] : 0.0f;
+        }
+        gathered = true;
+    }
+    if constexpr (ROUTED) {
+        if (a.ids != nullptr && ((n0 + 256) >> 1) > a.shared_feats) {
+            gate_up_routes<Shape, true>(a, m0, n0, s_route);
+            gathered = true;
+        }
+    }
+    if (gathered) __syncthreads();
+
+    PPRows ap, bp;
+    if (group == 1) ap.init(a.x, m0, a.M, a.ldx * (int64_t)sizeof(bf16_t), wig);
+    else bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
+    const int nk = a.K / 64;
+    char* st0 = lds;
+    char* st1 = lds + 2 * 256 * kRowBytes;
+    constexpr int kBOff = 256 * kRowBytes;
+
+    f32x16 acc[4][2];
+    zero_acc<Kind>(acc);
+    u32x4 fa[4][4], fb[4][2];
+
+    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
+    if (group == 1) {
+        ap.issue(0, st0);
+        if (nk > 1) ap.issue(1, st1);
+    } else {
+        bp.issue(0, st0 + kBOff);
+        if (nk > 1) bp.issue(1, st1 + kBOff);
+    }
+    if (nk > 1)
+        wait_vmcnt<8>();
+    else
+        wait_vmcnt<0>();
+    pp_barrier();
+
+    if (group == 0) {
+        for (int t = 0; t < nk; ++t) {
+            const char* st = (t & 1) ? st1 : st0;
+            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
+            pp_read(st, wm0, wn0, fa, fb);
+            wait_lgkmcnt0();
+            pp_barrier();
+            pp_mma(fa, fb, acc);
+            wait_vmcnt<0>();
+            pp_barrier();
+        }
+        // phase 2nk: group 1 multiplies the last stage, group 0 writes its
+        // rows of the epilogue tile (every stage has been read)
+        gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
+        wait_lgkmcnt0();
+        pp_barrier();
+        pp_barrier();   // phase 2nk+1: group 1's rows
+    } else {
+        pp_barrier();   // phase 0: group 0 reads stage 0
+        for (int t = 0; t < nk; ++t) {
+            const char* st = (t & 1) ? st1 : st0;
+            pp_read(st, wm0, wn0, fa, fb);
+            wait_lgkmcnt0();
+            if (t + 2 < nk) {
+                ap.issue(t + 2, (t & 1) ? st1 : st0);
+                wait_vmcnt<8>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            pp_barrier();
+            pp_mma(fa, fb, acc);
+            pp_barrier();
+        }
+        gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
+        wait_lgkmcnt0();
+        pp_barrier();
+    }
+    gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -740,12 +966,36 @@ int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int6
     return check_launch("rms_row_scale");
 }
 
+// bf16 prefill-sized gate|up (shared or dense-routed, every column tile in
+// one launch) on the ping-pong tiles: 256x256 tiles over whole 64-element K
+// stages, at least kBigTileMinBlocks tiles.
+static bool pp_eligible(int act, int wdt, const GateUpArgs& a, int64_t packed_rows) {
+    const int64_t cols = packed_rows - a.n_base;
+    return act == TRMOE_BF16 && wdt == TRMOE_BF16 && a.gu == nullptr && a.K > 0 && a.K % 64 == 0 &&
+           cols > 0 && cols % 256 == 0 && ((a.M + 255) / 256) * (cols / 256) >= kBigTileMinBlocks;
+}
+
+template <bool ROUTED>
+static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)((packed_rows - a.n_base) / 256));
+    constexpr int kLds = 2 * 2 * 256 * kRowBytes;   // two stages of A and B rows
+    static_assert(kLds >= 256 * (128 * 2 + 16), "the epilogue tile reuses the stages");
+    auto kern = k_gate_up_pp<ROUTED>;
+    const int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL(kern, grid, dim3(512), kLds, stream, a);
+    return check_launch(ROUTED ? "dense_routed_gate_up" : "shared_gate_up");
+}
+
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     if (a.gu != nullptr) return launch_gate_up_save(act, wdt, a, packed_rows, stream);
     if (a.M <= kSkinnyMaxTokens && packed_rows % 64 == 0)
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
     if (a.row_scale == nullptr && a.rms_eps > 0.0f)
         return set_error(TRMOE_ERR_INVALID, "gate_up: in-kernel RMSNorm scales need the decode kernels (n <= 128)");
+    if (pp_eligible(act, wdt, a, packed_rows))
+        return a.ids != nullptr ? launch_gate_up_pp<true>(a, packed_rows, stream)
+                                : launch_gate_up_pp<false>(a, packed_rows, stream);
     if (a.ids != nullptr) {
         // dense-routed: the shared columns as a plain gate|up launch, then the
         // expert columns with the routing epilogue

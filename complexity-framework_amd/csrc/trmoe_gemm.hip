@@ -311,49 +311,61 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
 // Group 0 = waves 0..3 (tile rows 0..127), group 1 = waves 4..7 (rows
 // 128..255, one phase behind).  With a barrier closing every phase:
 //   phase 2t    group 0 issues B(t+1) [weights] then reads stage t;
-//               group 1 multiplies stage t-1
+//               group 1 issues A(t+1) [activations] into the buffer of
+//               stage t-1, then multiplies stage t-1
 //   phase 2t+1  group 0 multiplies stage t, then waits for its B(t+1);
-//               group 1 reads stage t, issues A(t+2) [activations] into the
-//               buffer it just read, then waits for its A(t+1)
+//               group 1 reads stage t, then waits for its A(t+1)
 // so every stage is complete (each issuing group waited for its own loads)
 // one barrier before its first reader, and a buffer is refilled only after
-// both groups have read it.  In the phase after its last multiply group 0
-// writes its half of the epilogue tile to LDS while group 1 multiplies.
+// every wave of both groups has read it and passed a barrier: a group's
+// waves read a stage in the same phase, so a load issued by one of them in
+// that phase could overwrite rows that another has not read yet.  In the
+// phase after its last multiply group 0 writes its half of the epilogue tile
+// to LDS while group 1 multiplies.
 
-// One operand's direct loads by one group of 4 waves: 256 rows x 128 bytes
-// per stage, 8 wave instructions (8 rows each) per wave.
+// One operand's direct loads by one group of 4 waves: ROWS rows x 128 bytes
+// per stage, ROWS / 32 wave instructions (8 rows each) per wave.
+template <int ROWS>
 struct PPRows {
+    static constexpr int kInstr = ROWS / 32;
     __amdgpu_buffer_rsrc_t rsrc;
-    int row0;        // lane's first row: 64 * wave_in_group + lane / 8
+    int row0;        // lane's first row: ROWS / 4 * wave_in_group + lane / 8
     int row_bytes;   // row stride in bytes
     int nrows;       // rows present; rows at or past it load zero
-    int c0;          // lane's K chunk for j = 0 (chunk of instruction j: c0 ^ j)
+    int c0;          // (lane % 8) ^ (lane / 8), the lane's part of the K chunk
     int wig;
 
     __device__ __forceinline__ void init(const void* base, int64_t first_row, int64_t rows_total, int64_t ld_bytes,
                                          int wave_in_group) {
         const int64_t avail = rows_total - first_row;
-        nrows = (int)(avail < 256 ? avail : 256);
+        nrows = (int)(avail < ROWS ? avail : ROWS);
         rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
         const int lane = threadIdx.x & 63;
         wig = wave_in_group;
-        row0 = 64 * wave_in_group + (lane >> 3);
+        row0 = ROWS / 4 * wave_in_group + (lane >> 3);
         row_bytes = (int)ld_bytes;
-        // LDS slot (lane & 7) of row r holds K chunk slot ^ swz(r); for the
-        // rows of instruction j, swz(r) = (lane / 8) ^ j (mod 8)
         c0 = ((lane & 7) ^ (lane >> 3)) & 7;
     }
     // stage kt (bytes [128 kt, 128 kt + 128) of every row) into `dst` (the
-    // operand's 32 KB half of an LDS stage)
+    // operand's part of an LDS stage).  LDS slot (lane % 8) of row r holds K
+    // chunk slot ^ swz(r); the rows of instruction j have r / 8 = kInstr *
+    // wave_in_group + j, so swz(r) = (lane / 8) ^ (kInstr * wave_in_group + j).
+    __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
+        const int r = row0 + 8 * j;
+        const int chunk = (c0 ^ (kInstr * wig + j)) & 7;
+        const int o = r < nrows ? r * row_bytes + kt * kRowBytes + (chunk << 4) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (kInstr * wig + j) * 8 * kRowBytes), 16,
+                                                o, 0, 0, 0);
+    }
     __device__ __forceinline__ void issue(int kt, char* dst) const {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = row0 + 8 * j;
-            const int o = r < nrows ? r * row_bytes + kt * kRowBytes + (((c0 ^ j) & 7) << 4) : kOutOfRange;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (wig * 8 + j) * 8 * kRowBytes), 16,
-                                                    o, 0, 0, 0);
-        }
+        for (int j = 0; j < kInstr; ++j) issue_one(j, kt, dst);
     }
+};
+
+template <bool V>
+struct BoolC {
+    static constexpr bool value = V;
 };
 
 // Phase boundary: no instruction (MFMAs included) moves across it.
@@ -363,17 +375,20 @@ __device__ __forceinline__ void pp_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// The wave's fragments of one K stage: A rows wm0 + 32 tm + r, B rows
-// wn0 + 32 tn + r, 16-byte chunk 2 g + h of the 128-byte row.
-__device__ __forceinline__ void pp_read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][4], u32x4 (&fb)[4][2]) {
+// The wave's fragments of one K stage: A rows wm0 + 32 tm + r (A block of
+// a_rows rows first in the stage), B rows wn0 + 32 tn + r, 16-byte chunk
+// 2 g + h of the 128-byte row.
+template <int TM>
+__device__ __forceinline__ void pp_read(const char* st, int a_rows, int wm0, int wn0, u32x4 (&fa)[4][TM],
+                                        u32x4 (&fb)[4][2]) {
     const int lane = threadIdx.x & 63;
     const int r = lane & 31, h = lane >> 5;
     const char* As = st;
-    const char* Bs = st + 256 * kRowBytes;
+    const char* Bs = st + a_rows * kRowBytes;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
 #pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
+        for (int tm = 0; tm < TM; ++tm)
             fa[g][tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
 #pragma unroll
         for (int tn = 0; tn < 2; ++tn)
@@ -381,37 +396,74 @@ __device__ __forceinline__ void pp_read(const char* st, int wm0, int wn0, u32x4 
     }
 }
 
-__device__ __forceinline__ void pp_mma(const u32x4 (&fa)[4][4], const u32x4 (&fb)[4][2], f32x16 (&acc)[4][2]) {
+template <int TM>
+__device__ __forceinline__ void pp_mma(const u32x4 (&fa)[4][TM], const u32x4 (&fb)[4][2], f32x16 (&acc)[TM][2]) {
 #pragma unroll
     for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
+        for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < 2; ++tn) mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
 }
 
+// pp_mma with the loads of one stage of an operand issued between the MFMAs
+// (one every 8 TM / kInstr MFMAs), so that their issue hides under the
+// matrix pipe instead of delaying the phase's first MFMA.
+template <int TM, int ROWS>
+__device__ __forceinline__ void pp_mma_load(const u32x4 (&fa)[4][TM], const u32x4 (&fb)[4][2], f32x16 (&acc)[TM][2],
+                                            const PPRows<ROWS>& ld, int kt, char* dst) {
+    constexpr int kMfma = 8 * TM;
+    constexpr int kEvery = kMfma / PPRows<ROWS>::kInstr;
+    static_assert(kEvery >= 1 && kMfma % PPRows<ROWS>::kInstr == 0, "loads must spread evenly over the MFMAs");
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const int i = (g * TM + tm) * 2 + tn;
+                mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
+                if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
+            }
+    // keep that order through scheduling: one MFMA, one load, the rest of its MFMAs
+#pragma unroll
+    for (int j = 0; j < PPRows<ROWS>::kInstr; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);            // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x008, kEvery - 1, 0);   // MFMA
+    }
+}
+
+// Tile of the ping-pong kernel: 64 * TMW rows x 256 packed columns, waves
+// 2 x 4 of 32 * TMW rows x 64 columns (the epilogue's layout).
+template <int TMW>
+using ShapePP = TileShape<64 * TMW, 256, 2, 4, 4>;
+
 // gate|up + SwiGLU over bf16 activations and weights, K a multiple of 64.
 // ROUTED: the launch covers dense-routed expert columns (route gather and
-// per-token expert weights for the tiles that hold them).
-template <bool ROUTED>
+// per-token expert weights for the tiles that hold them).  TMW = 4: 256-row
+// tiles; 2: 128-row tiles (the trailing columns of a launch whose last round
+// of 256-row tiles would leave most CUs idle).
+template <bool ROUTED, int TMW>
 __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
-    using Shape = ShapeBigDma;   // 256 x 256, waves 2 x 4 of 128 x 64: the epilogue's layout
+    using Shape = ShapePP<TMW>;
     using Kind = KindBF16;
+    constexpr int BM = Shape::BM;
     extern __shared__ __align__(16) char lds[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int group = wave >> 2, wig = wave & 3;
-    const int wm0 = group * 128, wn0 = wig * 64;
-    const int64_t m0 = (int64_t)blockIdx.x * 256;
+    const int wm0 = group * (BM / 2), wn0 = wig * 64;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
     const int64_t n0 = a.n_base + (int64_t)blockIdx.y * 256;
 
     // per-row data of the epilogue (read there, after the loop's barriers);
     // gathered before any direct load is issued, so that the loop's load
     // counters only count direct loads
-    __shared__ float s_rscale[256];
-    __shared__ int s_route[ROUTED ? 256 : 1][kMaxTopK];
+    __shared__ float s_rscale[BM];
+    __shared__ int s_route[ROUTED ? BM : 1][kMaxTopK];
     bool gathered = false;
     if (a.row_scale != nullptr) {
-        if (threadIdx.x < 256) {
+        if (threadIdx.x < BM) {
             const int64_t row = m0 + threadIdx.x;
             s_rscale[threadIdx.x] = row < a.M ? a.row_scale[row] : 0.0f;
         }
@@ -425,40 +477,50 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     }
     if (gathered) __syncthreads();
 
-    PPRows ap, bp;
+    PPRows<BM> ap;
+    PPRows<256> bp;
     if (group == 1) ap.init(a.x, m0, a.M, a.ldx * (int64_t)sizeof(bf16_t), wig);
     else bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
     const int nk = a.K / 64;
+    constexpr int kStage = (BM + 256) * kRowBytes;
+    constexpr int kBOff = BM * kRowBytes;
     char* st0 = lds;
-    char* st1 = lds + 2 * 256 * kRowBytes;
-    constexpr int kBOff = 256 * kRowBytes;
+    char* st1 = lds + kStage;
+    constexpr int kAI = PPRows<BM>::kInstr, kBI = PPRows<256>::kInstr;
 
-    f32x16 acc[4][2];
+    f32x16 acc[TMW][2];
     zero_acc<Kind>(acc);
-    u32x4 fa[4][4], fb[4][2];
+    u32x4 fa[4][TMW], fb[4][2];
 
     // prologue: stages 0 and 1 requested, stage 0 landed everywhere
     if (group == 1) {
         ap.issue(0, st0);
-        if (nk > 1) ap.issue(1, st1);
+        if (nk > 1) {
+            ap.issue(1, st1);
+            wait_vmcnt<kAI>();
+        } else {
+            wait_vmcnt<0>();
+        }
     } else {
         bp.issue(0, st0 + kBOff);
-        if (nk > 1) bp.issue(1, st1 + kBOff);
+        if (nk > 1) {
+            bp.issue(1, st1 + kBOff);
+            wait_vmcnt<kBI>();
+        } else {
+            wait_vmcnt<0>();
+        }
     }
-    if (nk > 1)
-        wait_vmcnt<8>();
-    else
-        wait_vmcnt<0>();
     pp_barrier();
 
     if (group == 0) {
         for (int t = 0; t < nk; ++t) {
             const char* st = (t & 1) ? st1 : st0;
             if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
-            pp_read(st, wm0, wn0, fa, fb);
+            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
             wait_lgkmcnt0();
             pp_barrier();
-            pp_mma(fa, fb, acc);
+            pp_mma<TMW>(fa, fb, acc);
+            __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
             wait_vmcnt<0>();
             pp_barrier();
         }
@@ -470,20 +532,27 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
         pp_barrier();   // phase 2nk+1: group 1's rows
     } else {
         pp_barrier();   // phase 0: group 0 reads stage 0
-        for (int t = 0; t < nk; ++t) {
+        // iteration t: read stage t; multiply it, refilling its buffer with
+        // A(t+2) while t + 2 < nk (two loops rather than a branch around the
+        // MFMAs, which would give each branch its own accumulator registers)
+        auto step = [&](int t, auto load) {
             const char* st = (t & 1) ? st1 : st0;
-            pp_read(st, wm0, wn0, fa, fb);
+            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
             wait_lgkmcnt0();
-            if (t + 2 < nk) {
-                ap.issue(t + 2, (t & 1) ? st1 : st0);
-                wait_vmcnt<8>();
-            } else {
-                wait_vmcnt<0>();
-            }
+            wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
             pp_barrier();
-            pp_mma(fa, fb, acc);
+            // Both groups are done with stage t only now: the other waves of
+            // this group read it in the phase that just ended, so A(t+2)
+            // cannot be issued into it before this barrier.
+            if constexpr (decltype(load)::value)
+                pp_mma_load<TMW, BM>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+            else
+                pp_mma<TMW>(fa, fb, acc);
             pp_barrier();
-        }
+        };
+        int t = 0;
+        for (; t + 2 < nk; ++t) step(t, BoolC<true>{});
+        for (; t < nk; ++t) step(t, BoolC<false>{});
         gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
         wait_lgkmcnt0();
         pp_barrier();
@@ -975,16 +1044,45 @@ static bool pp_eligible(int act, int wdt, const GateUpArgs& a, int64_t packed_ro
            cols > 0 && cols % 256 == 0 && ((a.M + 255) / 256) * (cols / 256) >= kBigTileMinBlocks;
 }
 
-template <bool ROUTED>
-static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)((packed_rows - a.n_base) / 256));
-    constexpr int kLds = 2 * 2 * 256 * kRowBytes;   // two stages of A and B rows
-    static_assert(kLds >= 256 * (128 * 2 + 16), "the epilogue tile reuses the stages");
-    auto kern = k_gate_up_pp<ROUTED>;
+template <bool ROUTED, int TMW>
+static int launch_gate_up_pp_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    constexpr int BM = ShapePP<TMW>::BM;
+    const dim3 grid((unsigned)((a.M + BM - 1) / BM), (unsigned)((packed_rows - a.n_base) / 256));
+    constexpr int kLds = 2 * (BM + 256) * kRowBytes;   // two stages of A and B rows
+    static_assert(kLds >= BM * (128 * 2 + 16), "the epilogue tile reuses the stages");
+    auto kern = k_gate_up_pp<ROUTED, TMW>;
     const int st = ensure_lds(kern, kLds);
     if (st) return st;
+    if (grid.x == 0 || grid.y == 0) return TRMOE_OK;
     hipLaunchKernelGGL(kern, grid, dim3(512), kLds, stream, a);
     return check_launch(ROUTED ? "dense_routed_gate_up" : "shared_gate_up");
+}
+
+// 256-row tiles; when their last round would leave at least half of the CUs
+// idle, the fewest trailing columns whose removal leaves whole rounds run as
+// a second launch of 128-row tiles (C2: 64 x 24 tiles, then 128 x 2 half
+// tiles: seven rounds become six and a round of half tiles).  Launches whose
+// first columns hold no expert features leave the routing code out.
+template <bool ROUTED>
+static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int64_t tiles_m = (a.M + 255) / 256;
+    const int64_t cols = (packed_rows - a.n_base) / 256;
+    const int64_t cus = device_cus();
+    int64_t tail = 0;
+    if ((tiles_m * cols) % cus != 0)
+        for (int64_t k = 1; k < cols; ++k)
+            if ((tiles_m * (cols - k)) % cus == 0 && tiles_m * k * 2 <= cus) {
+                tail = k;
+                break;
+            }
+    const int64_t split = a.n_base + (cols - tail) * 256;
+    const bool head_routed = ROUTED && a.ids != nullptr && split > 2 * a.shared_feats;
+    int st = head_routed ? launch_gate_up_pp_shape<ROUTED, 4>(a, split, stream)
+                         : launch_gate_up_pp_shape<false, 4>(a, split, stream);
+    if (st || tail == 0) return st;
+    GateUpArgs t = a;
+    t.n_base = split;
+    return launch_gate_up_pp_shape<ROUTED, 2>(t, packed_rows, stream);
 }
 
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {

@@ -354,3 +354,63 @@ def test_shared_down_combine_decode_fp8(gpu):
     out = ops.shared_down_combine(h.to(gpu), S, pd, ps, H, None, None, 2, (0.5, 0.5), 1.0, 1.0).cpu()
     ref = h.double() @ O.dequantize_e4m3(q, s, 1).double().T
     assert nerr(out, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("routed", [False, True])
+def test_prefill_gate_up_every_row_and_repeatable_with_cold_caches(gpu, routed):
+    """Regression test for an LDS race in the prefill gate|up main loop: one
+    wave refilled a stage while other waves of its group could still be
+    reading it, so with cold caches a few rows per call came out wrong (too
+    few to move a normwise bound over sampled rows).  At the C2 shape (16384
+    tokens, 256-row tiles plus the 128-row tail launch over the expert
+    columns) every row is checked against a torch fp32 reference, and calls
+    separated by a cache-evicting write agree bit for bit."""
+    from complexity_amd import ops
+    from complexity_amd import workloads as W
+
+    w = W.C2
+    eng = W.build_engine(w, gpu, backend="hip")
+    p = eng._hip_packed()
+    x = W.make_hidden(w).to(gpu).to(torch.bfloat16).reshape(-1, w.hidden).contiguous()
+    ids = W.make_token_ids(w).to(gpu).reshape(-1).contiguous()
+    table = eng._active_route_table
+    rw, shared_scale, routed_scale = eng.config.route_weights, 0.5, 2.0
+    S, E, Wd = p.shared_width, p.num_experts, p.expert_width
+    xf = x.float()
+    g = xf @ eng.shared_gate.weight.detach().float().T
+    u = xf @ eng.shared_up.weight.detach().float().T
+    if routed:
+        F_ = p.dense_features
+        ref = torch.zeros(x.shape[0], F_, device=gpu)
+        ref[:, :S] = shared_scale * F.silu(g) * u
+        routes = table[:, ids]  # [k, N]
+        for e in range(E):
+            mult = sum(routed_scale * rw[j] * (routes[j] == e).float() for j in range(routes.shape[0]))
+            ge = xf @ eng.expert_gate.detach()[e].float()
+            ue = xf @ eng.expert_up.detach()[e].float()
+            c0 = (S + 127) // 128 * 128 + e * ((Wd + 63) // 64 * 64)  # shared block, then 64-aligned experts
+            ref[:, c0:c0 + Wd] = mult[:, None] * F.silu(ge) * ue
+
+        def call():
+            return ops.dense_routed_gate_up(x, p.dense_gate_up, S, E, Wd, ids, table, rw, shared_scale, routed_scale)
+    else:
+        pg, _ = ops.pack_linear_gate_up(eng.shared_gate.weight.detach(), eng.shared_up.weight.detach())
+        ref = F.silu(g) * u
+
+        def call():
+            return ops.shared_gate_up(x, pg, None, S)[:, :S]
+
+    evict = torch.empty(1 << 28, dtype=torch.float32, device=gpu)  # 1 GiB: more than L2 and MALL together
+    outs = []
+    for _ in range(6):
+        evict.add_(1.0)
+        outs.append(call())
+    torch.cuda.synchronize()
+    first = outs[0]
+    for i, o in enumerate(outs[1:], 1):
+        assert torch.equal(o.view(torch.int16), first.view(torch.int16)), f"call {i} differs from call 0"
+    # every row: max |h - ref| within two bf16 roundings of the row's largest value
+    err = (first.float() - ref).abs().amax(1)
+    scale = ref.abs().amax(1).clamp_min(1e-6)
+    worst = int(torch.argmax(err / scale))
+    assert float(err[worst] / scale[worst]) <= 2 ** -7, (worst, float(err[worst]), float(scale[worst]))

@@ -310,9 +310,9 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
 //
 // Group 0 = waves 0..3 (tile rows 0..127), group 1 = waves 4..7 (rows
 // 128..255, one phase behind).  With a barrier closing every phase:
-//   phase 2t    group 0 issues B(t+1) [weights] then reads stage t;
-//               group 1 issues A(t+1) [activations] into the buffer of
-//               stage t-1, then multiplies stage t-1
+//   phase 2t    group 0 reads stage t, then issues B(t+1) [weights] into
+//               the other buffer; group 1 multiplies stage t-1 and, between
+//               its MFMAs, issues A(t+1) [activations] into that buffer
 //   phase 2t+1  group 0 multiplies stage t, then waits for its B(t+1);
 //               group 1 reads stage t, then waits for its A(t+1)
 // so every stage is complete (each issuing group waited for its own loads)
@@ -515,9 +515,12 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     if (group == 0) {
         for (int t = 0; t < nk; ++t) {
             const char* st = (t & 1) ? st1 : st0;
-            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
             pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
             wait_lgkmcnt0();
+            // B(t+1) goes out after this wave's reads: LDS reads issued
+            // behind a wave's own buffer->LDS loads wait for those loads
+            __builtin_amdgcn_sched_barrier(0);
+            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
             pp_barrier();
             pp_mma<TMW>(fa, fb, acc);
             __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them

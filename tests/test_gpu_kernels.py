@@ -343,6 +343,31 @@ def test_shared_down_combine_decode_without_workspace_uses_tile_kernel(gpu):
     assert nerr(a.cpu(), out.cpu()) <= 1e-2
 
 
+@pytest.mark.parametrize("N", [16, 64, 128])
+def test_decode_down_split_k_reduction_is_repeatable(gpu, N):
+    """Decode-sized down GEMM: the split-K partials are summed in split order,
+    so 40 calls in a row, every other one behind a cache-evicting write,
+    give bit-identical outputs within the bf16 bound of the reference."""
+    from complexity_amd import ops
+
+    S, H, k = 3328, 896, 2
+    h, wd, hpad, y, perm, res = _down_case(N, S, H, k, torch.bfloat16, 70)
+    pd, _ = ops.pack_linear_down(wd.to(gpu))
+    hg, yg, pg_, rg = hpad.to(gpu), y.to(gpu), perm.to(gpu), res.to(gpu)
+    evict = torch.empty(1 << 28, dtype=torch.float32, device=gpu)
+    outs = []
+    for i in range(40):
+        if i % 2:
+            evict.add_(1.0)
+        outs.append(ops.shared_down_combine(hg, S, pd, None, H, yg, pg_, k, (0.6, 0.4), 0.5, 2.0, rg))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs[1:], 1):
+        assert torch.equal(o, outs[0]), f"call {i} differs from call 0"
+    ref = 0.5 * (h.double() @ wd.double().T) + 2.0 * (0.6 * y.double()[perm[:N]] + 0.4 * y.double()[perm[N:]])
+    ref = ref + res.double()
+    assert nerr(outs[0].cpu(), ref) <= TOL[torch.bfloat16]
+
+
 def test_shared_down_combine_decode_fp8(gpu):
     from complexity_amd import ops
 

@@ -203,35 +203,87 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
         gc.enable()
         return s.elapsed_time(t) / (n * layers)
 
+    H, S, E, Wd = w.hidden, w.shared, w.experts, w.width
+    weight_bytes = 2 * (3 * H * S + 3 * E * H * Wd)
+    bytes_per_layer = weight_bytes + 2 * 2 * w.tokens * H + 8 * w.tokens + 8 * 2 * w.tokens
+
+    def graphed(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        for _ in range(warmup):
+            graph.replay()
+        return graph
+
     with torch.no_grad():
         for _ in range(warmup):
             stack()
         eager_ms = timed(stack, steps)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            stack()
-        side.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            stack()
-        for _ in range(warmup):
-            graph.replay()
-        per_layer_ms = timed(graph.replay, steps)
-    H, S, E, Wd = w.hidden, w.shared, w.experts, w.width
-    weight_bytes = 2 * (3 * H * S + 3 * E * H * Wd)
-    bytes_per_layer = weight_bytes + 2 * 2 * w.tokens * H + 8 * w.tokens + 8 * 2 * w.tokens
-    return {
-        "workload": w.name if block is None else f"{w.name}_block_{block}",
+        per_layer_ms = timed(graphed(stack).replay, steps)
+        floor_ms = None
+        if block is None:
+            # the same bytes per layer in one streaming launch each (16
+            # distinct buffers, as many bytes as the layers' weights), replayed
+            # the same way: the gap to it is what the two kernels lose
+            from complexity_amd import ops
+
+            bufs = [torch.full(((bytes_per_layer + 15) // 16 * 4,), i, dtype=torch.int32, device=dev)
+                    for i in range(layers)]
+            sink = torch.empty(1024, dtype=torch.int32, device=dev)
+
+            def streams():
+                for b in bufs:
+                    ops.stream_read(b, sink)
+
+            floor_ms = timed(graphed(streams).replay, steps)
+            del bufs
+    gbps = bytes_per_layer / (per_layer_ms * 1e-3) / 1e9
+    name = w.name if block is None else f"{w.name}_block_{block}"
+    out = {
+        "workload": name,
         "layers_rotated": layers,
         "mode": "hip_graph_replay",
         "ms_per_layer": per_layer_ms,
         "eager_ms_per_layer": eager_ms,
         "tokens_per_s": w.tokens / (per_layer_ms * 1e-3),
-        "hbm_gbps": bytes_per_layer / (per_layer_ms * 1e-3) / 1e9,
-        "hbm_frac": bytes_per_layer / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK,
+        "hbm_gbps": gbps,
+        "hbm_frac": gbps / HBM_PEAK,
         "algorithmic_bytes_per_layer": bytes_per_layer,
     }
+    if floor_ms is not None:
+        out["stream_floor_us_per_layer"] = floor_ms * 1e3
+        out["stream_floor_gbps"] = bytes_per_layer / (floor_ms * 1e-3) / 1e9
+        out["kernel_loss_us_per_layer"] = (per_layer_ms - floor_ms) * 1e3
+        out["roofline"] = {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK, "unit": "GB/s",
+                           "frac": gbps / HBM_PEAK, "traffic": measured_traffic(w.name, "decode_layer"),
+                           "kernel": "decode layer (gate|up + down launches)",
+                           "algorithmic_bytes_per_launch": bytes_per_layer, "avg_us": per_layer_ms * 1e3}
+    return out
+
+
+def c5_layer(torch, workloads, ops, dev, steps: int = 10, warmup: int = 3):
+    """C5: the fp8-e4m3 W8A16 layer at 32768 tokens (E=16, H=2048, S=5632,
+    W=256), the quantised path the north star names.  The MFMAs run in bf16,
+    so the roofline uses the bf16 dense peak."""
+    w = workloads.C5
+    engine = workloads.build_engine(w, dev, backend="hip")
+    x = workloads.make_hidden(w).to(dev).to(torch.bfloat16)
+    ids = workloads.make_token_ids(w).to(dev)
+    timer = KernelTimer(ops, torch)
+    try:
+        ms, kernel_ms, _, strategy = time_engine(torch, engine, x, ids, steps, warmup, timer)
+    finally:
+        timer.restore()
+    kernels, _, roof = kernel_report(w, kernel_ms, strategy)
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    return {"workload": w.name, "ms_per_layer": ms, "tokens_per_s": w.tokens / (ms * 1e-3),
+            "layer_tflops": tflops, "layer_mfma_frac": tflops / PEAK["fp8"], "strategy": strategy,
+            "kernels": kernels, "roofline": roof}
 
 
 def c4_e2e(torch, dev, steps: int = 128, reps: int = 3):
@@ -460,6 +512,7 @@ def main():
     ap.add_argument("--no-other", action="store_true", help="skip timing the second routed strategy")
     ap.add_argument("--no-train", action="store_true", help="skip the forward+backward (autograd) timing")
     ap.add_argument("--no-c4", action="store_true", help="skip the 16-layer TR-GQA decoder (C4) end to end")
+    ap.add_argument("--no-c5", action="store_true", help="skip the fp8 W8A16 layer (C5)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="end with three elementwise copies of MIB MiB (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -543,6 +596,8 @@ def main():
         }
     if not args.no_c4:
         result["c4_e2e"] = c4_e2e(torch, dev)
+    if not args.no_c5 and w.name != workloads.C5.name:
+        result["c5"] = c5_layer(torch, workloads, ops, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(w, min(args.cpu_sample, tokens))
     if args.calibrate_copy:

@@ -65,6 +65,7 @@ SIGNATURES = {
         [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
          _c_vp, _c_size, _c_vp],
     ),
+    "trmoe_stream_read": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_vp]),
     "trmoe_route_sort_noalloc": (
         _c_int,
         [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp],

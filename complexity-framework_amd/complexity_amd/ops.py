@@ -488,6 +488,20 @@ def shared_down_combine(h: torch.Tensor, shared_width: int, w_down: torch.Tensor
     return out
 
 
+def stream_read(src: torch.Tensor, sink: torch.Tensor) -> None:
+    """One launch that reads src's bytes once (trmoe_stream_read): the
+    single-launch streaming floor the decode kernels are compared with.
+    sink: int32 [G], G workgroups; word g receives the XOR of the 32-bit words
+    workgroup g read."""
+    lib = _lib()
+    _require_cuda(src, sink)
+    if not src.is_contiguous() or sink.dtype != torch.int32:
+        raise ValueError("stream_read: contiguous src and an int32 sink")
+    nbytes = src.numel() * src.element_size()
+    st = lib.trmoe_stream_read(_p(src), nbytes, _p(sink), sink.numel(), _stream(src))
+    N.check(st, "trmoe_stream_read")
+
+
 def combine(y: torch.Tensor, inverse: torch.Tensor, n_tokens: int, top_k: int,
             route_weights: Sequence[float], routed_scale: float,
             residual: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -954,4 +954,12 @@ int trmoe_grouped_linear(int act_dtype, const void* h, int64_t ldh, int64_t n_ro
     return launch_down_grouped(act_dtype, act_dtype, d, n_rows, as_stream(stream));
 }
 
+int trmoe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int sink_words, void* stream) {
+    TRMOE_REQUIRE(src != nullptr && sink != nullptr, "stream_read: null pointer");
+    TRMOE_REQUIRE(bytes > 0 && bytes % 16 == 0 && aligned16(src),
+                  "stream_read: bytes must be a positive multiple of 16 and src 16-byte aligned");
+    TRMOE_REQUIRE(sink_words >= 1 && sink_words <= 65535, "stream_read: sink_words must be in [1, 65535]");
+    return launch_stream_read(src, bytes, sink, sink_words, as_stream(stream));
+}
+
 }  // extern "C"

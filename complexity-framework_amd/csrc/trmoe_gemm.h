@@ -223,6 +223,7 @@ struct WgradArgs {
 int launch_pack(const PackArgs& p, hipStream_t stream);
 int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
 size_t down_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int act);
+int launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks, hipStream_t stream);
 int launch_down_skinny(int act, int wdt, const DownArgs& a, void* workspace, hipStream_t stream);
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
 // Fragment-major copy of a packed [rows, ld] weight (rows % 16 == 0):

@@ -636,6 +636,37 @@ int launch_pack_fragments(const void* src, int64_t rows, int64_t kbytes, int64_t
     return check_launch("pack_fragments");
 }
 
+// Streaming floor of the decode kernels: one pass over a byte range with
+// 16-byte loads, eight in flight per thread before any is used; each
+// workgroup XOR-folds what it read into sink[blockIdx.x], so no load is dead.
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4* __restrict__ src, int64_t n16,
+                                                     uint32_t* __restrict__ sink) {
+    __shared__ uint32_t s_fold[4];
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    uint32_t fold = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += 8 * stride) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t j = i + u * stride;
+            v[u] = j < n16 ? src[j] : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fold ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) fold ^= (uint32_t)__shfl_xor((int)fold, off);
+    if ((threadIdx.x & 63) == 0) s_fold[threadIdx.x >> 6] = fold;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = s_fold[0] ^ s_fold[1] ^ s_fold[2] ^ s_fold[3];
+}
+
+int launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks, hipStream_t stream) {
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const u32x4*>(src), bytes / 16, sink);
+    return check_launch("stream_read");
+}
+
 int launch_gate_up_skinny(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     if (act == TRMOE_F32 && wdt == TRMOE_F32) return gate_up_skinny_kind<KindF32, false>(a, packed_rows, stream);
     if (act == TRMOE_BF16 && wdt == TRMOE_BF16) return gate_up_skinny_kind<KindBF16, false>(a, packed_rows, stream);

@@ -469,6 +469,17 @@ int trmoe_grouped_linear(int act_dtype, const void* h, int64_t ldh, int64_t n_ro
                          const int32_t* expert_offsets, int num_experts, const void* w, int64_t out_features,
                          void* y, int64_t ldy, void* stream);
 
+/*
+ * Measurement aid with no counterpart in the reference: one kernel launch that
+ * reads bytes [src, src + bytes) once with 16-byte loads over sink_words
+ * workgroups and writes the XOR of the 32-bit words each workgroup read to
+ * sink[workgroup] (the XOR of all sink words is the XOR of the range).  It
+ * times the single-launch streaming floor that the decode kernels' weight
+ * bytes are compared with.  bytes: a positive multiple of 16, src 16-byte
+ * aligned; 1 <= sink_words <= 65535.
+ */
+int trmoe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int sink_words, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

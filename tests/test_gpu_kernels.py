@@ -439,3 +439,20 @@ def test_prefill_gate_up_every_row_and_repeatable_with_cold_caches(gpu, routed):
     scale = ref.abs().amax(1).clamp_min(1e-6)
     worst = int(torch.argmax(err / scale))
     assert float(err[worst] / scale[worst]) <= 2 ** -7, (worst, float(err[worst]), float(scale[worst]))
+
+
+@pytest.mark.parametrize("nbytes,blocks", [(16, 1), (4096 + 16 * 7, 3), (18 << 20, 512)])
+def test_stream_read_folds_every_word_once(gpu, nbytes, blocks):
+    """The streaming-floor kernel reads each 16-byte chunk exactly once: the
+    XOR of its per-workgroup words equals the XOR of all 32-bit words."""
+    from complexity_amd import ops
+
+    g = torch.Generator().manual_seed(nbytes)
+    words = torch.randint(-(2 ** 31), 2 ** 31 - 1, (nbytes // 4,), generator=g, dtype=torch.int64).to(torch.int32)
+    sink = torch.zeros(blocks, dtype=torch.int32, device=gpu)
+    ops.stream_read(words.to(gpu), sink)
+    got = 0
+    for v in sink.cpu().tolist():
+        got ^= v & 0xFFFFFFFF
+    want = int(np.bitwise_xor.reduce(words.numpy().view(np.uint32)))
+    assert got == want

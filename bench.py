@@ -513,6 +513,8 @@ def main():
     ap.add_argument("--no-train", action="store_true", help="skip the forward+backward (autograd) timing")
     ap.add_argument("--no-c4", action="store_true", help="skip the 16-layer TR-GQA decoder (C4) end to end")
     ap.add_argument("--no-c5", action="store_true", help="skip the fp8 W8A16 layer (C5)")
+    ap.add_argument("--no-block", action="store_true",
+                    help="skip the decode block legs (the C3 MLP half with its norm fused / unfused)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="end with three elementwise copies of MIB MiB (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -585,15 +587,16 @@ def main():
     if not args.no_decode:
         result["decode"] = decode_hbm(torch, workloads, dev)
         result["decode_c4"] = decode_hbm(torch, workloads, dev, w=workloads.C4_DECODE, per_layer_tables=True)
-        # the block's MLP half with the post-attention RMSNorm and residual fused
-        # (F2) and unfused, C3
-        fused = decode_hbm(torch, workloads, dev, block="fused")
-        unfused = decode_hbm(torch, workloads, dev, block="unfused")
-        result["decode_block"] = {
-            "workload": workloads.C3.name,
-            "fused_us_per_layer": fused["ms_per_layer"] * 1e3,
-            "unfused_us_per_layer": unfused["ms_per_layer"] * 1e3,
-        }
+        if not args.no_block:
+            # the block's MLP half with the post-attention RMSNorm and residual
+            # fused (F2) and unfused, C3
+            fused = decode_hbm(torch, workloads, dev, block="fused")
+            unfused = decode_hbm(torch, workloads, dev, block="unfused")
+            result["decode_block"] = {
+                "workload": workloads.C3.name,
+                "fused_us_per_layer": fused["ms_per_layer"] * 1e3,
+                "unfused_us_per_layer": unfused["ms_per_layer"] * 1e3,
+            }
     if not args.no_c4:
         result["c4_e2e"] = c4_e2e(torch, dev)
     if not args.no_c5 and w.name != workloads.C5.name:

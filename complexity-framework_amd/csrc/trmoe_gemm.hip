@@ -439,6 +439,95 @@ __device__ __forceinline__ void pp_mma_load(const u32x4 (&fa)[4][TM], const u32x
 template <int TMW>
 using ShapePP = TileShape<64 * TMW, 256, 2, 4, 4>;
 
+// The ping-pong main loop over nk K stages of two groups' direct loads (A:
+// 64 TMW rows by group 1, B: 256 rows by group 0) into the stages at lds,
+// accumulating each wave's 32 TMW x 64 block (rows wm0.., columns wn0..).
+// rows_out(acc) writes the calling group's rows of the epilogue tile to LDS:
+// group 0 in the phase after its last multiply, while group 1 multiplies the
+// last stage, and group 1 after it.  Every wave leaves after a barrier that
+// follows both groups' rows_out, so the tile can be read right away.
+template <int TMW, class RowsOut>
+__device__ __forceinline__ void pp_main(const PPRows<64 * TMW>& ap, const PPRows<256>& bp, int nk, char* lds,
+                                        int group, int wm0, int wn0, f32x16 (&acc)[TMW][2], RowsOut&& rows_out) {
+    constexpr int BM = 64 * TMW;
+    constexpr int kStage = (BM + 256) * kRowBytes;
+    constexpr int kBOff = BM * kRowBytes;
+    char* st0 = lds;
+    char* st1 = lds + kStage;
+    constexpr int kAI = PPRows<BM>::kInstr, kBI = PPRows<256>::kInstr;
+
+    u32x4 fa[4][TMW], fb[4][2];
+
+    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
+    if (group == 1) {
+        ap.issue(0, st0);
+        if (nk > 1) {
+            ap.issue(1, st1);
+            wait_vmcnt<kAI>();
+        } else {
+            wait_vmcnt<0>();
+        }
+    } else {
+        bp.issue(0, st0 + kBOff);
+        if (nk > 1) {
+            bp.issue(1, st1 + kBOff);
+            wait_vmcnt<kBI>();
+        } else {
+            wait_vmcnt<0>();
+        }
+    }
+    pp_barrier();
+
+    if (group == 0) {
+        for (int t = 0; t < nk; ++t) {
+            const char* st = (t & 1) ? st1 : st0;
+            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
+            wait_lgkmcnt0();
+            // B(t+1) goes out after this wave's reads: LDS reads issued
+            // behind a wave's own buffer->LDS loads wait for those loads
+            __builtin_amdgcn_sched_barrier(0);
+            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
+            pp_barrier();
+            pp_mma<TMW>(fa, fb, acc);
+            __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
+            wait_vmcnt<0>();
+            pp_barrier();
+        }
+        // phase 2nk: group 1 multiplies the last stage, group 0 writes its
+        // rows of the epilogue tile (every stage has been read)
+        rows_out(acc);
+        wait_lgkmcnt0();
+        pp_barrier();
+        pp_barrier();   // phase 2nk+1: group 1's rows
+    } else {
+        pp_barrier();   // phase 0: group 0 reads stage 0
+        // iteration t: read stage t; multiply it, refilling its buffer with
+        // A(t+2) while t + 2 < nk (two loops rather than a branch around the
+        // MFMAs, which would give each branch its own accumulator registers)
+        auto step = [&](int t, auto load) {
+            const char* st = (t & 1) ? st1 : st0;
+            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
+            wait_lgkmcnt0();
+            wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
+            pp_barrier();
+            // Both groups are done with stage t only now: the other waves of
+            // this group read it in the phase that just ended, so A(t+2)
+            // cannot be issued into it before this barrier.
+            if constexpr (decltype(load)::value)
+                pp_mma_load<TMW, BM>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+            else
+                pp_mma<TMW>(fa, fb, acc);
+            pp_barrier();
+        };
+        int t = 0;
+        for (; t + 2 < nk; ++t) step(t, BoolC<true>{});
+        for (; t < nk; ++t) step(t, BoolC<false>{});
+        rows_out(acc);
+        wait_lgkmcnt0();
+        pp_barrier();
+    }
+}
+
 // gate|up + SwiGLU over bf16 activations and weights, K a multiple of 64.
 // ROUTED: the launch covers dense-routed expert columns (route gather and
 // per-token expert weights for the tiles that hold them).  TMW = 4: 256-row
@@ -481,85 +570,11 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     PPRows<256> bp;
     if (group == 1) ap.init(a.x, m0, a.M, a.ldx * (int64_t)sizeof(bf16_t), wig);
     else bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
-    const int nk = a.K / 64;
-    constexpr int kStage = (BM + 256) * kRowBytes;
-    constexpr int kBOff = BM * kRowBytes;
-    char* st0 = lds;
-    char* st1 = lds + kStage;
-    constexpr int kAI = PPRows<BM>::kInstr, kBI = PPRows<256>::kInstr;
-
     f32x16 acc[TMW][2];
     zero_acc<Kind>(acc);
-    u32x4 fa[4][TMW], fb[4][2];
-
-    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
-    if (group == 1) {
-        ap.issue(0, st0);
-        if (nk > 1) {
-            ap.issue(1, st1);
-            wait_vmcnt<kAI>();
-        } else {
-            wait_vmcnt<0>();
-        }
-    } else {
-        bp.issue(0, st0 + kBOff);
-        if (nk > 1) {
-            bp.issue(1, st1 + kBOff);
-            wait_vmcnt<kBI>();
-        } else {
-            wait_vmcnt<0>();
-        }
-    }
-    pp_barrier();
-
-    if (group == 0) {
-        for (int t = 0; t < nk; ++t) {
-            const char* st = (t & 1) ? st1 : st0;
-            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
-            wait_lgkmcnt0();
-            // B(t+1) goes out after this wave's reads: LDS reads issued
-            // behind a wave's own buffer->LDS loads wait for those loads
-            __builtin_amdgcn_sched_barrier(0);
-            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
-            pp_barrier();
-            pp_mma<TMW>(fa, fb, acc);
-            __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
-            wait_vmcnt<0>();
-            pp_barrier();
-        }
-        // phase 2nk: group 1 multiplies the last stage, group 0 writes its
-        // rows of the epilogue tile (every stage has been read)
-        gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
-        wait_lgkmcnt0();
-        pp_barrier();
-        pp_barrier();   // phase 2nk+1: group 1's rows
-    } else {
-        pp_barrier();   // phase 0: group 0 reads stage 0
-        // iteration t: read stage t; multiply it, refilling its buffer with
-        // A(t+2) while t + 2 < nk (two loops rather than a branch around the
-        // MFMAs, which would give each branch its own accumulator registers)
-        auto step = [&](int t, auto load) {
-            const char* st = (t & 1) ? st1 : st0;
-            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
-            wait_lgkmcnt0();
-            wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
-            pp_barrier();
-            // Both groups are done with stage t only now: the other waves of
-            // this group read it in the phase that just ended, so A(t+2)
-            // cannot be issued into it before this barrier.
-            if constexpr (decltype(load)::value)
-                pp_mma_load<TMW, BM>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
-            else
-                pp_mma<TMW>(fa, fb, acc);
-            pp_barrier();
-        };
-        int t = 0;
-        for (; t + 2 < nk; ++t) step(t, BoolC<true>{});
-        for (; t < nk; ++t) step(t, BoolC<false>{});
-        gate_up_epi_tile<Kind, Shape, ROUTED>(a, acc, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
-        wait_lgkmcnt0();
-        pp_barrier();
-    }
+    pp_main<TMW>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
+        gate_up_epi_tile<Kind, Shape, ROUTED>(a, c, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
+    });
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
@@ -851,6 +866,115 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     }
 }
 
+// K4 on the ping-pong main loop (bf16 activations and weights, K a multiple
+// of 64): 256x256 tiles over the hidden columns; weight rows past the hidden
+// size load as zero (the last tile of H = 896 multiplies 128 of them).  Epilogue: each
+// group writes shared_scale * column scale * acc for its rows to LDS as bf16
+// (the tile kernel's rounding), then every thread adds the route-weighted y
+// rows and the residual over 16-byte chunks and stores.
+__global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
+    constexpr int BM = 256, BN = 256;
+    using T = bf16_t;
+    extern __shared__ __align__(16) char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * (BM / 2), wn0 = wig * 64;
+    const int lane = threadIdx.x & 63;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const int64_t n0 = (int64_t)blockIdx.y * BN;
+
+    // y row of each (tile row, slot), clamped so that a malformed inverse
+    // cannot become a wild read; gathered before any direct load is issued
+    __shared__ int s_yrow[BM][kMaxTopK];
+    if (a.y != nullptr) {
+        if (threadIdx.x < BM) {
+            const int64_t row = m0 + threadIdx.x;
+            const int64_t last = (int64_t)a.top_k * a.M - 1;
+            for (int j = 0; j < kMaxTopK; ++j) {
+                int64_t v = (j < a.top_k && row < a.M) ? a.inverse[(int64_t)j * a.M + row] : 0;
+                s_yrow[threadIdx.x][j] = (int)(v < 0 ? 0 : (v > last ? last : v));
+            }
+        }
+        __syncthreads();
+    }
+
+    PPRows<BM> ap;
+    PPRows<256> bp;
+    if (group == 1) ap.init(a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), wig);
+    else bp.init(a.w, n0, a.N, a.ldw * (int64_t)sizeof(T), wig);   // rows past N load as zero
+    f32x16 acc[4][2];
+    zero_acc<KindBF16>(acc);
+    constexpr int kORowBytes = BN * 2 + 16;
+    pp_main<4>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
+        const int r = lane & 31;
+        float cs[2];
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int64_t col = n0 + wn0 + tn * 32 + r;
+            cs[tn] = a.shared_scale * ((a.w_scale != nullptr && col < a.N) ? a.w_scale[col] : 1.0f);
+        }
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int rl = wm0 + tm * 32 + acc_row(lane, i);
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn)
+                    *reinterpret_cast<T*>(lds + rl * kORowBytes + (wn0 + tn * 32 + r) * 2) =
+                        from_f32<T>(c[tm][tn][i] * cs[tn]);
+            }
+    });
+
+    const T* y = static_cast<const T*>(a.y);
+    const T* res = static_cast<const T*>(a.residual);
+    T* out = static_cast<T*>(a.out);
+    constexpr int kChunksPerRow = BN / 8;
+    for (int q = threadIdx.x; q < BM * kChunksPerRow; q += 512) {
+        const int rl = q / kChunksPerRow, c = q % kChunksPerRow;
+        const int64_t row = m0 + rl;
+        const int64_t col = n0 + c * 8;
+        if (row >= a.M || col >= a.N) continue;
+        const bf16x8 sb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + rl * kORowBytes + c * 16));
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)sb[e];
+        if (a.vec_ok && col + 8 <= a.N) {
+            if (y != nullptr) {
+                float acc_r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < a.top_k; ++j) {
+                    const bf16x8 yv = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const u32x4*>(y + (int64_t)s_yrow[rl][j] * a.ldy + col));
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc_r[e] += a.rw[j] * (float)yv[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += a.routed_scale * acc_r[e];
+            }
+            if (res != nullptr) {
+                const bf16x8 rv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(res + row * a.ldr + col));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += (float)rv[e];
+            }
+            bf16x8 ov;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ov[e] = (bf16_t)v[e];
+            *reinterpret_cast<u32x4*>(out + row * a.ldo + col) = __builtin_bit_cast(u32x4, ov);
+        } else {
+            for (int e = 0; e < 8 && col + e < a.N; ++e) {
+                float x = v[e];
+                if (y != nullptr) {
+                    float sacc = 0.f;
+                    for (int j = 0; j < a.top_k; ++j)
+                        sacc += a.rw[j] * to_f32(y[(int64_t)s_yrow[rl][j] * a.ldy + col + e]);
+                    x += a.routed_scale * sacc;
+                }
+                if (res != nullptr) x += to_f32(res[row * a.ldr + col + e]);
+                out[row * a.ldo + col + e] = from_f32<T>(x);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -1133,11 +1257,26 @@ static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
     return check_launch("shared_down_combine");
 }
 
+// bf16 down GEMMs with at least a full round of 256x256 tiles run on the
+// ping-pong main loop.
+static int launch_down_pp(const DownArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)((a.N + 255) / 256));
+    constexpr int kLds = 256 * (256 * 2 + 16) > 2 * (256 + 256) * kRowBytes ? 256 * (256 * 2 + 16)
+                                                                           : 2 * (256 + 256) * kRowBytes;
+    const int st = ensure_lds(k_down_pp, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL(k_down_pp, grid, dim3(512), kLds, stream, a);
+    return check_launch("shared_down_combine");
+}
+
 // The packed down weights have round_up(N, 256) rows, so every tile choice
 // below reads only packed rows.
 template <class Kind, bool FP8>
 static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
     const int64_t mt = (a.M + 255) / 256;
+    if constexpr (std::is_same_v<Kind, KindBF16> && !FP8) {
+        if (a.K > 0 && a.K % 64 == 0 && mt * ((a.N + 255) / 256) >= 256) return launch_down_pp(a, stream);
+    }
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     if constexpr (FP8) {
         if (a.N % 256 == 0 && mt * (a.N / 256) >= 256) return launch_down_shape<Kind, FP8, ShapeBigF8Dma>(a, stream);

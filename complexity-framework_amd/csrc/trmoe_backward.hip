@@ -22,6 +22,7 @@
 #include "trmoe_internal.h"
 #include "trmoe_gemm.h"
 #include "trmoe_tiles.h"
+#include "trmoe_pp.h"
 
 #include <stdlib.h>
 
@@ -201,14 +202,6 @@ struct DmaRowsT {
     }
 };
 
-typedef short trmoe_v4s __attribute__((ext_vector_type(4)));
-
-// 8 bytes of a transposing LDS read: lane i of each 16-lane group receives
-// element i of the 4 rows addressed by lanes 4j + i/4 (j = 0..3).
-__device__ __forceinline__ u32x2 ds_read_tr16(const char* p) {
-    const trmoe_v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) trmoe_v4s*)(p));
-    return __builtin_bit_cast(u32x2, v);
-}
 
 // One 64-K stage of MFMAs from two DmaRowsT stages ([k][256] each).  For
 // K group g, lane l needs K values 16g + 8(l/32) + 0..7 of column l % 32 of
@@ -643,6 +636,57 @@ __global__ __launch_bounds__(ShapeWgradTr::NT) void k_wgrad_tr(WgradArgs a) {
         wgrad_store<Shape, false>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
 }
 
+// bf16 weight gradients of token-major operands without gathered rows, on
+// the ping-pong main loop: each group loads one operand straight into LDS
+// (PPRowsT) and every wave transposes at the fragment read; the workgroup's
+// whole token range (its split) in one pass.  Same arguments, splits and
+// epilogue as k_wgrad_tr.
+__global__ __launch_bounds__(512, 1) void k_wgrad_pp(WgradArgs a) {
+    using Shape = ShapeWgradTr;   // 256 x 256: waves 2 x 4 of 128 x 64, the ping-pong groups' layout
+    extern __shared__ __align__(16) char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * Shape::WM, wn0 = wig * Shape::WN;
+    const int64_t m0 = (int64_t)blockIdx.x * Shape::BM;
+    const int64_t n0 = (int64_t)blockIdx.y * Shape::BN;
+    const int e = (int)blockIdx.z / a.splits, sp = (int)blockIdx.z % a.splits;
+    const int64_t seg0 = a.offsets ? a.offsets[e] : 0;
+    const int64_t seg1 = a.offsets ? a.offsets[e + 1] : a.T;
+    const int64_t per = ((seg1 - seg0 + a.splits - 1) / a.splits + 63) / 64 * 64;
+    const int64_t t0 = seg0 + sp * per;
+    const int64_t t1 = t0 + per < seg1 ? t0 + per : seg1;
+    const int len = t1 > t0 ? (int)(t1 - t0) : 0;
+
+    PPRowsT ap, bp;
+    if (group == 1) {
+        ap.init(a.a, a.a_rows, a.lda * 2, m0, a.M, wig);
+        ap.segment(t0, len);
+    } else {
+        bp.init(a.b, a.b_rows, a.ldb * 2, n0, a.N, wig);
+        bp.segment(t0, len);
+    }
+    f32x16 acc[Shape::TM][Shape::TN];
+    zero_acc<KindBF16>(acc);
+    const int nk = (len + 63) / 64;
+    if (nk > 0) pp_main<4, PPLayoutT>(ap, bp, nk, lds, group, wm0, wn0, acc, [](const f32x16 (&)[4][2]) {});
+
+    const bool direct = a.splits == 1;
+    const int64_t obase_el = direct ? (int64_t)e * a.out_expert_stride + m0 * a.ldo + n0
+                                    : ((int64_t)e * a.splits + sp) * a.M * a.N + m0 * a.N + n0;
+    const int ld = (int)(direct ? a.ldo : a.N);
+    const int mlim = (int)(a.M - m0 < Shape::BM ? a.M - m0 : Shape::BM);
+    const int nlim = (int)(a.N - n0 < Shape::BN ? a.N - n0 : Shape::BN);
+    void* obase = direct ? static_cast<void*>(static_cast<bf16_t*>(a.out) + obase_el)
+                         : static_cast<void*>(a.partial + obase_el);
+    const auto orsrc = make_rsrc(obase, (uint32_t)(((int64_t)(mlim - 1) * ld + nlim) * (direct ? 2 : 4)));
+    const int col = lane & 31;
+    if (direct)
+        wgrad_store<Shape, true>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
+    else
+        wgrad_store<Shape, false>(acc, orsrc, wm0, wn0, col, lane, ld, mlim, nlim);
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
     const int64_t mn = a.M * a.N;
@@ -760,10 +804,26 @@ static int wgrad_tr(const WgradArgs& a, hipStream_t stream) {
     return check_launch("weight_grad (reduce)");
 }
 
-// bf16: direct loads + transposing fragment reads; f32: the register-
-// transposing kernel.
+static int wgrad_pp(const WgradArgs& a, hipStream_t stream) {
+    constexpr int kLds = 2 * PPLayoutT::kStage;
+    int st = bwd_lds(k_wgrad_pp, kLds);
+    if (st) return st;
+    const dim3 grid((unsigned)((a.M + ShapeWgradTr::BM - 1) / ShapeWgradTr::BM),
+                    (unsigned)((a.N + ShapeWgradTr::BN - 1) / ShapeWgradTr::BN), (unsigned)(a.E * a.splits));
+    hipLaunchKernelGGL(k_wgrad_pp, grid, dim3(512), kLds, stream, a);
+    st = check_launch("weight_grad");
+    if (st || a.splits == 1) return st;
+    int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_wgrad_reduce<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    return check_launch("weight_grad (reduce)");
+}
+
+// bf16: direct loads + transposing fragment reads (on the ping-pong loop
+// without gathered rows); f32: the register-transposing kernel.
 int launch_wgrad(int act, const WgradArgs& a, hipStream_t stream) {
     const bool ga = a.a_gather != nullptr, gb = a.b_gather != nullptr;
+    if (act == TRMOE_BF16 && !ga && !gb) return wgrad_pp(a, stream);
     if (act == TRMOE_BF16) {
         if (ga) return gb ? wgrad_tr<true, true>(a, stream) : wgrad_tr<true, false>(a, stream);
         return gb ? wgrad_tr<false, true>(a, stream) : wgrad_tr<false, false>(a, stream);

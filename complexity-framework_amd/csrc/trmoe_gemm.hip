@@ -14,6 +14,7 @@
 #include "trmoe_internal.h"
 #include "trmoe_gemm.h"
 #include "trmoe_tiles.h"
+#include "trmoe_pp.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -298,236 +299,6 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
                                           a.row_scale != nullptr ? s_rscale : nullptr);
 }
 
-// ---------------------------------------------------------------------------
-// K2 (bf16 prefill): ping-pong main loop
-// ---------------------------------------------------------------------------
-// 256x256 tiles, 8 waves of 128x64, two LDS stages of 64-element K (A rows
-// then B rows, 128-byte swizzled rows, filled by direct buffer->LDS loads).
-// The two waves of each SIMD alternate roles every phase: while one
-// multiplies a whole K stage from registers, the other reads its next
-// stage's fragments from LDS, so the matrix pipe runs one wave's MFMAs at a
-// time and the LDS reads and load issue of the other hide under them.
-//
-// Group 0 = waves 0..3 (tile rows 0..127), group 1 = waves 4..7 (rows
-// 128..255, one phase behind).  With a barrier closing every phase:
-//   phase 2t    group 0 reads stage t, then issues B(t+1) [weights] into
-//               the other buffer; group 1 multiplies stage t-1 and, between
-//               its MFMAs, issues A(t+1) [activations] into that buffer
-//   phase 2t+1  group 0 multiplies stage t, then waits for its B(t+1);
-//               group 1 reads stage t, then waits for its A(t+1)
-// so every stage is complete (each issuing group waited for its own loads)
-// one barrier before its first reader, and a buffer is refilled only after
-// every wave of both groups has read it and passed a barrier: a group's
-// waves read a stage in the same phase, so a load issued by one of them in
-// that phase could overwrite rows that another has not read yet.  In the
-// phase after its last multiply group 0 writes its half of the epilogue tile
-// to LDS while group 1 multiplies.
-
-// One operand's direct loads by one group of 4 waves: ROWS rows x 128 bytes
-// per stage, ROWS / 32 wave instructions (8 rows each) per wave.
-template <int ROWS>
-struct PPRows {
-    static constexpr int kInstr = ROWS / 32;
-    __amdgpu_buffer_rsrc_t rsrc;
-    int row0;        // lane's first row: ROWS / 4 * wave_in_group + lane / 8
-    int row_bytes;   // row stride in bytes
-    int nrows;       // rows present; rows at or past it load zero
-    int c0;          // (lane % 8) ^ (lane / 8), the lane's part of the K chunk
-    int wig;
-
-    __device__ __forceinline__ void init(const void* base, int64_t first_row, int64_t rows_total, int64_t ld_bytes,
-                                         int wave_in_group) {
-        const int64_t avail = rows_total - first_row;
-        nrows = (int)(avail < ROWS ? avail : ROWS);
-        rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
-        const int lane = threadIdx.x & 63;
-        wig = wave_in_group;
-        row0 = ROWS / 4 * wave_in_group + (lane >> 3);
-        row_bytes = (int)ld_bytes;
-        c0 = ((lane & 7) ^ (lane >> 3)) & 7;
-    }
-    // stage kt (bytes [128 kt, 128 kt + 128) of every row) into `dst` (the
-    // operand's part of an LDS stage).  LDS slot (lane % 8) of row r holds K
-    // chunk slot ^ swz(r); the rows of instruction j have r / 8 = kInstr *
-    // wave_in_group + j, so swz(r) = (lane / 8) ^ (kInstr * wave_in_group + j).
-    __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
-        const int r = row0 + 8 * j;
-        const int chunk = (c0 ^ (kInstr * wig + j)) & 7;
-        const int o = r < nrows ? r * row_bytes + kt * kRowBytes + (chunk << 4) : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (kInstr * wig + j) * 8 * kRowBytes), 16,
-                                                o, 0, 0, 0);
-    }
-    __device__ __forceinline__ void issue(int kt, char* dst) const {
-#pragma unroll
-        for (int j = 0; j < kInstr; ++j) issue_one(j, kt, dst);
-    }
-};
-
-template <bool V>
-struct BoolC {
-    static constexpr bool value = V;
-};
-
-// Phase boundary: no instruction (MFMAs included) moves across it.
-__device__ __forceinline__ void pp_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// The wave's fragments of one K stage: A rows wm0 + 32 tm + r (A block of
-// a_rows rows first in the stage), B rows wn0 + 32 tn + r, 16-byte chunk
-// 2 g + h of the 128-byte row.
-template <int TM>
-__device__ __forceinline__ void pp_read(const char* st, int a_rows, int wm0, int wn0, u32x4 (&fa)[4][TM],
-                                        u32x4 (&fb)[4][2]) {
-    const int lane = threadIdx.x & 63;
-    const int r = lane & 31, h = lane >> 5;
-    const char* As = st;
-    const char* Bs = st + a_rows * kRowBytes;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-            fa[g][tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
-#pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
-            fb[g][tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
-    }
-}
-
-template <int TM>
-__device__ __forceinline__ void pp_mma(const u32x4 (&fa)[4][TM], const u32x4 (&fb)[4][2], f32x16 (&acc)[TM][2]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
-}
-
-// pp_mma with the loads of one stage of an operand issued between the MFMAs
-// (one every 8 TM / kInstr MFMAs), so that their issue hides under the
-// matrix pipe instead of delaying the phase's first MFMA.
-template <int TM, int ROWS>
-__device__ __forceinline__ void pp_mma_load(const u32x4 (&fa)[4][TM], const u32x4 (&fb)[4][2], f32x16 (&acc)[TM][2],
-                                            const PPRows<ROWS>& ld, int kt, char* dst) {
-    constexpr int kMfma = 8 * TM;
-    constexpr int kEvery = kMfma / PPRows<ROWS>::kInstr;
-    static_assert(kEvery >= 1 && kMfma % PPRows<ROWS>::kInstr == 0, "loads must spread evenly over the MFMAs");
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) {
-                const int i = (g * TM + tm) * 2 + tn;
-                mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
-                if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
-            }
-    // keep that order through scheduling: one MFMA, one load, the rest of its MFMAs
-#pragma unroll
-    for (int j = 0; j < PPRows<ROWS>::kInstr; ++j) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);            // VMEM read
-        __builtin_amdgcn_sched_group_barrier(0x008, kEvery - 1, 0);   // MFMA
-    }
-}
-
-// Tile of the ping-pong kernel: 64 * TMW rows x 256 packed columns, waves
-// 2 x 4 of 32 * TMW rows x 64 columns (the epilogue's layout).
-template <int TMW>
-using ShapePP = TileShape<64 * TMW, 256, 2, 4, 4>;
-
-// The ping-pong main loop over nk K stages of two groups' direct loads (A:
-// 64 TMW rows by group 1, B: 256 rows by group 0) into the stages at lds,
-// accumulating each wave's 32 TMW x 64 block (rows wm0.., columns wn0..).
-// rows_out(acc) writes the calling group's rows of the epilogue tile to LDS:
-// group 0 in the phase after its last multiply, while group 1 multiplies the
-// last stage, and group 1 after it.  Every wave leaves after a barrier that
-// follows both groups' rows_out, so the tile can be read right away.
-template <int TMW, class RowsOut>
-__device__ __forceinline__ void pp_main(const PPRows<64 * TMW>& ap, const PPRows<256>& bp, int nk, char* lds,
-                                        int group, int wm0, int wn0, f32x16 (&acc)[TMW][2], RowsOut&& rows_out) {
-    constexpr int BM = 64 * TMW;
-    constexpr int kStage = (BM + 256) * kRowBytes;
-    constexpr int kBOff = BM * kRowBytes;
-    char* st0 = lds;
-    char* st1 = lds + kStage;
-    constexpr int kAI = PPRows<BM>::kInstr, kBI = PPRows<256>::kInstr;
-
-    u32x4 fa[4][TMW], fb[4][2];
-
-    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
-    if (group == 1) {
-        ap.issue(0, st0);
-        if (nk > 1) {
-            ap.issue(1, st1);
-            wait_vmcnt<kAI>();
-        } else {
-            wait_vmcnt<0>();
-        }
-    } else {
-        bp.issue(0, st0 + kBOff);
-        if (nk > 1) {
-            bp.issue(1, st1 + kBOff);
-            wait_vmcnt<kBI>();
-        } else {
-            wait_vmcnt<0>();
-        }
-    }
-    pp_barrier();
-
-    if (group == 0) {
-        for (int t = 0; t < nk; ++t) {
-            const char* st = (t & 1) ? st1 : st0;
-            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
-            wait_lgkmcnt0();
-            // B(t+1) goes out after this wave's reads: LDS reads issued
-            // behind a wave's own buffer->LDS loads wait for those loads
-            __builtin_amdgcn_sched_barrier(0);
-            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
-            pp_barrier();
-            pp_mma<TMW>(fa, fb, acc);
-            __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
-            wait_vmcnt<0>();
-            pp_barrier();
-        }
-        // phase 2nk: group 1 multiplies the last stage, group 0 writes its
-        // rows of the epilogue tile (every stage has been read)
-        rows_out(acc);
-        wait_lgkmcnt0();
-        pp_barrier();
-        pp_barrier();   // phase 2nk+1: group 1's rows
-    } else {
-        pp_barrier();   // phase 0: group 0 reads stage 0
-        // iteration t: read stage t; multiply it, refilling its buffer with
-        // A(t+2) while t + 2 < nk (two loops rather than a branch around the
-        // MFMAs, which would give each branch its own accumulator registers)
-        auto step = [&](int t, auto load) {
-            const char* st = (t & 1) ? st1 : st0;
-            pp_read<TMW>(st, BM, wm0, wn0, fa, fb);
-            wait_lgkmcnt0();
-            wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
-            pp_barrier();
-            // Both groups are done with stage t only now: the other waves of
-            // this group read it in the phase that just ended, so A(t+2)
-            // cannot be issued into it before this barrier.
-            if constexpr (decltype(load)::value)
-                pp_mma_load<TMW, BM>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
-            else
-                pp_mma<TMW>(fa, fb, acc);
-            pp_barrier();
-        };
-        int t = 0;
-        for (; t + 2 < nk; ++t) step(t, BoolC<true>{});
-        for (; t < nk; ++t) step(t, BoolC<false>{});
-        rows_out(acc);
-        wait_lgkmcnt0();
-        pp_barrier();
-    }
-}
-
 // gate|up + SwiGLU over bf16 activations and weights, K a multiple of 64.
 // ROUTED: the launch covers dense-routed expert columns (route gather and
 // per-token expert weights for the tiles that hold them).  TMW = 4: 256-row
@@ -572,7 +343,7 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     else bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
     f32x16 acc[TMW][2];
     zero_acc<Kind>(acc);
-    pp_main<TMW>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
+    pp_main<TMW, PPLayoutK<TMW>>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
         gate_up_epi_tile<Kind, Shape, ROUTED>(a, c, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
     });
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
@@ -905,7 +676,7 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     f32x16 acc[4][2];
     zero_acc<KindBF16>(acc);
     constexpr int kORowBytes = BN * 2 + 16;
-    pp_main<4>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
+    pp_main<4, PPLayoutK<4>>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
         const int r = lane & 31;
         float cs[2];
 #pragma unroll

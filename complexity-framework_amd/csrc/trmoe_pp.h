@@ -1,0 +1,355 @@
+// Ping-pong main loop of the bf16 prefill GEMMs (gate|up, down, weight
+// gradients): loaders, stage layouts, fragment reads and the loop itself.
+#pragma once
+
+#include "trmoe_common.h"
+
+namespace trmoe {
+
+// ---------------------------------------------------------------------------
+// ping-pong main loop
+// ---------------------------------------------------------------------------
+// 256x256 tiles, 8 waves of 128x64, two LDS stages of 64-element K (A rows
+// then B rows, 128-byte swizzled rows, filled by direct buffer->LDS loads).
+// The two waves of each SIMD alternate roles every phase: while one
+// multiplies a whole K stage from registers, the other reads its next
+// stage's fragments from LDS, so the matrix pipe runs one wave's MFMAs at a
+// time and the LDS reads and load issue of the other hide under them.
+//
+// Group 0 = waves 0..3 (tile rows 0..127), group 1 = waves 4..7 (rows
+// 128..255, one phase behind).  With a barrier closing every phase:
+//   phase 2t    group 0 reads stage t, then issues B(t+1) [weights] into
+//               the other buffer; group 1 multiplies stage t-1 and, between
+//               its MFMAs, issues A(t+1) [activations] into that buffer
+//   phase 2t+1  group 0 multiplies stage t, then waits for its B(t+1);
+//               group 1 reads stage t, then waits for its A(t+1)
+// so every stage is complete (each issuing group waited for its own loads)
+// one barrier before its first reader, and a buffer is refilled only after
+// every wave of both groups has read it and passed a barrier: a group's
+// waves read a stage in the same phase, so a load issued by one of them in
+// that phase could overwrite rows that another has not read yet.  In the
+// phase after its last multiply group 0 writes its half of the epilogue tile
+// to LDS while group 1 multiplies.
+
+// One operand's direct loads by one group of 4 waves: ROWS rows x 128 bytes
+// per stage, ROWS / 32 wave instructions (8 rows each) per wave.
+template <int ROWS>
+struct PPRows {
+    static constexpr int kInstr = ROWS / 32;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int row0;        // lane's first row: ROWS / 4 * wave_in_group + lane / 8
+    int row_bytes;   // row stride in bytes
+    int nrows;       // rows present; rows at or past it load zero
+    int c0;          // (lane % 8) ^ (lane / 8), the lane's part of the K chunk
+    int wig;
+
+    __device__ __forceinline__ void init(const void* base, int64_t first_row, int64_t rows_total, int64_t ld_bytes,
+                                         int wave_in_group) {
+        const int64_t avail = rows_total - first_row;
+        nrows = (int)(avail < ROWS ? avail : ROWS);
+        rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
+        const int lane = threadIdx.x & 63;
+        wig = wave_in_group;
+        row0 = ROWS / 4 * wave_in_group + (lane >> 3);
+        row_bytes = (int)ld_bytes;
+        c0 = ((lane & 7) ^ (lane >> 3)) & 7;
+    }
+    // stage kt (bytes [128 kt, 128 kt + 128) of every row) into `dst` (the
+    // operand's part of an LDS stage).  LDS slot (lane % 8) of row r holds K
+    // chunk slot ^ swz(r); the rows of instruction j have r / 8 = kInstr *
+    // wave_in_group + j, so swz(r) = (lane / 8) ^ (kInstr * wave_in_group + j).
+    __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
+        const int r = row0 + 8 * j;
+        const int chunk = (c0 ^ (kInstr * wig + j)) & 7;
+        const int o = r < nrows ? r * row_bytes + kt * kRowBytes + (chunk << 4) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (kInstr * wig + j) * 8 * kRowBytes), 16,
+                                                o, 0, 0, 0);
+    }
+    __device__ __forceinline__ void issue(int kt, char* dst) const {
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) issue_one(j, kt, dst);
+    }
+};
+
+template <bool V>
+struct BoolC {
+    static constexpr bool value = V;
+};
+
+// Phase boundary: no instruction (MFMAs included) moves across it.
+__device__ __forceinline__ void pp_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The wave's fragments of one K stage: A rows wm0 + 32 tm + r (A block of
+// a_rows rows first in the stage), B rows wn0 + 32 tn + r, 16-byte chunk
+// 2 g + h of the 128-byte row.
+template <int TM>
+__device__ __forceinline__ void pp_read(const char* st, int a_rows, int wm0, int wn0, u32x4 (&fa)[4][TM],
+                                        u32x4 (&fb)[4][2]) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+    const char* As = st;
+    const char* Bs = st + a_rows * kRowBytes;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+            fa[g][tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+            fb[g][tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
+    }
+}
+
+template <int TM>
+__device__ __forceinline__ void pp_mma(const u32x4 (&fa)[4][TM], const u32x4 (&fb)[4][2], f32x16 (&acc)[TM][2]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
+}
+
+// pp_mma with the loads of one stage of an operand issued between the MFMAs
+// (one every 8 TM / kInstr MFMAs), so that their issue hides under the
+// matrix pipe instead of delaying the phase's first MFMA.
+template <int TM, class LD>
+__device__ __forceinline__ void pp_mma_load(const u32x4 (&fa)[4][TM], const u32x4 (&fb)[4][2], f32x16 (&acc)[TM][2],
+                                            const LD& ld, int kt, char* dst) {
+    constexpr int kMfma = 8 * TM;
+    constexpr int kEvery = kMfma / LD::kInstr;
+    static_assert(kEvery >= 1 && kMfma % LD::kInstr == 0, "loads must spread evenly over the MFMAs");
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const int i = (g * TM + tm) * 2 + tn;
+                mfma_group(KindBF16{}, fa[g][tm], fb[g][tn], acc[tm][tn]);
+                if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
+            }
+    // keep that order through scheduling: one MFMA, one load, the rest of its MFMAs
+#pragma unroll
+    for (int j = 0; j < LD::kInstr; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);            // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x008, kEvery - 1, 0);   // MFMA
+    }
+}
+
+// Tile of the ping-pong kernel: 64 * TMW rows x 256 packed columns, waves
+// 2 x 4 of 32 * TMW rows x 64 columns (the epilogue's layout).
+template <int TMW>
+using ShapePP = TileShape<64 * TMW, 256, 2, 4, 4>;
+
+// Stage layouts of the ping-pong loop.  PPLayoutK: operands with K along
+// their rows (activations x, packed weights): A rows then B rows of 128
+// bytes.  PPLayoutT: operands with K across rows (the weight gradients'
+// token-major operands): 64 K rows of 256 A columns, then of 256 B columns.
+template <int TMW>
+struct PPLayoutK {
+    static constexpr int kBOff = 64 * TMW * kRowBytes;
+    static constexpr int kStage = (64 * TMW + 256) * kRowBytes;
+    __device__ __forceinline__ static void read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][TMW],
+                                                u32x4 (&fb)[4][2]) {
+        pp_read<TMW>(st, 64 * TMW, wm0, wn0, fa, fb);
+    }
+};
+
+typedef short trmoe_v4s __attribute__((ext_vector_type(4)));
+
+// 8 bytes of a transposing LDS read: lane i of each 16-lane group receives
+// element i of the 4 rows addressed by lanes 4j + i/4 (j = 0..3).
+__device__ __forceinline__ u32x2 ds_read_tr16(const char* p) {
+    const trmoe_v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) trmoe_v4s*)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// One token-major operand (K across rows) loaded by one group of 4 waves: a
+// stage is 64 K rows of 256 columns (512 bytes), 16-byte chunk c of row k
+// stored at chunk c ^ ((k & 3) << 2), so that the transposing fragment reads
+// of pp_read_tr hit 64 distinct banks.  A wave instruction fills the two rows
+// of a pair (lanes 0..31 the even row, 32..63 the odd one); rows at or past
+// the segment's length and columns at or past ncols load zero.
+struct PPRowsT {
+    static constexpr int kInstr = 8;   // 32 row pairs per stage over 4 waves
+    __amdgpu_buffer_rsrc_t rsrc;
+    int coloff[2];   // the lane's source column bytes for rows with (row & 2) == 0 / 2
+    int h;           // row of the pair this lane fills
+    int wig;
+    int base, len, ld;
+
+    __device__ __forceinline__ void init(const void* base_ptr, int64_t rows_total, int64_t ld_bytes, int64_t col0,
+                                         int64_t ncols, int wave_in_group) {
+        rsrc = make_rsrc(base_ptr, (uint32_t)(rows_total * ld_bytes));
+        const int lane = threadIdx.x & 63;
+        wig = wave_in_group;
+        h = lane >> 5;
+        const int pc = lane & 31;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int c = pc ^ ((2 * p + h) << 2);
+            const int64_t col = col0 + 8 * c;
+            coloff[p] = col < ncols ? (int)(col * 2) : kOutOfRange;
+        }
+        ld = (int)ld_bytes;
+        base = 0;
+        len = 0;
+    }
+    // rows [t0, t0 + n) of the operand are the K range (the caller keeps
+    // (t0 + n) * ld below 2^31)
+    __device__ __forceinline__ void segment(int64_t t0, int n) {
+        base = (int)(t0 * (int64_t)ld);
+        len = n;
+    }
+    __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
+        const int q = wig * kInstr + j;       // row pair of the stage; (q & 1) == (j & 1)
+        const int lk = kt * 64 + 2 * q + h;
+        const int ro = lk < len ? base + lk * ld : kOutOfRange;
+        const int co = coloff[j & 1];         // (row & 3) = 2 (j & 1) + h
+        const int o = (ro < 0 || co < 0) ? kOutOfRange : ro + co;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + q * 1024), 16, o, 0, 0, 0);
+    }
+    __device__ __forceinline__ void issue(int kt, char* dst) const {
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) issue_one(j, kt, dst);
+    }
+};
+
+// The wave's fragments of one K stage from two PPRowsT stages ([64][256]
+// each): for K group g, lane l needs K values 16 g + 8 (l / 32) + 0..7 of
+// column l % 32 of each 32-column block, two transposing reads whose 16
+// source lanes address rows +((l & 15) >> 2) and 8-byte column blocks l & 3.
+template <int TM>
+__device__ __forceinline__ void pp_read_tr(const char* As, const char* Bs, int wm0, int wn0, u32x4 (&fa)[4][TM],
+                                           u32x4 (&fb)[4][2]) {
+    const int lane = threadIdx.x & 63;
+    const int j = (lane & 15) >> 2;
+    const int h = lane >> 5;
+    const int cw = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    const int wb = 8 * (lane & 1);
+    const int swz = j << 2;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int rowb = (16 * g + 8 * h + 4 * r + j) * 512;
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const u32x2 v = ds_read_tr16(As + rowb + ((((wm0 + 32 * tm) >> 3) + cw) ^ swz) * 16 + wb);
+                fa[g][tm][2 * r] = v[0];
+                fa[g][tm][2 * r + 1] = v[1];
+            }
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const u32x2 v = ds_read_tr16(Bs + rowb + ((((wn0 + 32 * tn) >> 3) + cw) ^ swz) * 16 + wb);
+                fb[g][tn][2 * r] = v[0];
+                fb[g][tn][2 * r + 1] = v[1];
+            }
+        }
+}
+
+struct PPLayoutT {
+    static constexpr int kBOff = 64 * 512;
+    static constexpr int kStage = 2 * 64 * 512;
+    __device__ __forceinline__ static void read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][4],
+                                                u32x4 (&fb)[4][2]) {
+        pp_read_tr<4>(st, st + kBOff, wm0, wn0, fa, fb);
+    }
+};
+
+// The ping-pong main loop over nk K stages of two groups' direct loads (A:
+// 64 TMW rows by group 1 through ap, B: 256 rows by group 0 through bp) into
+// the stages at lds (layout Lay), accumulating each wave's 32 TMW x 64 block
+// (rows wm0.., columns wn0..).
+// rows_out(acc) writes the calling group's rows of the epilogue tile to LDS:
+// group 0 in the phase after its last multiply, while group 1 multiplies the
+// last stage, and group 1 after it.  Every wave leaves after a barrier that
+// follows both groups' rows_out, so the tile can be read right away.
+template <int TMW, class Lay, class LA, class LB, class RowsOut>
+__device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char* lds, int group, int wm0, int wn0,
+                                        f32x16 (&acc)[TMW][2], RowsOut&& rows_out) {
+    constexpr int kStage = Lay::kStage;
+    constexpr int kBOff = Lay::kBOff;
+    char* st0 = lds;
+    char* st1 = lds + kStage;
+    constexpr int kAI = LA::kInstr, kBI = LB::kInstr;
+
+    u32x4 fa[4][TMW], fb[4][2];
+
+    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
+    if (group == 1) {
+        ap.issue(0, st0);
+        if (nk > 1) {
+            ap.issue(1, st1);
+            wait_vmcnt<kAI>();
+        } else {
+            wait_vmcnt<0>();
+        }
+    } else {
+        bp.issue(0, st0 + kBOff);
+        if (nk > 1) {
+            bp.issue(1, st1 + kBOff);
+            wait_vmcnt<kBI>();
+        } else {
+            wait_vmcnt<0>();
+        }
+    }
+    pp_barrier();
+
+    if (group == 0) {
+        for (int t = 0; t < nk; ++t) {
+            const char* st = (t & 1) ? st1 : st0;
+            Lay::read(st, wm0, wn0, fa, fb);
+            wait_lgkmcnt0();
+            // B(t+1) goes out after this wave's reads: LDS reads issued
+            // behind a wave's own buffer->LDS loads wait for those loads
+            __builtin_amdgcn_sched_barrier(0);
+            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
+            pp_barrier();
+            pp_mma<TMW>(fa, fb, acc);
+            __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
+            wait_vmcnt<0>();
+            pp_barrier();
+        }
+        // phase 2nk: group 1 multiplies the last stage, group 0 writes its
+        // rows of the epilogue tile (every stage has been read)
+        rows_out(acc);
+        wait_lgkmcnt0();
+        pp_barrier();
+        pp_barrier();   // phase 2nk+1: group 1's rows
+    } else {
+        pp_barrier();   // phase 0: group 0 reads stage 0
+        // iteration t: read stage t; multiply it, refilling its buffer with
+        // A(t+2) while t + 2 < nk (two loops rather than a branch around the
+        // MFMAs, which would give each branch its own accumulator registers)
+        auto step = [&](int t, auto load) {
+            const char* st = (t & 1) ? st1 : st0;
+            Lay::read(st, wm0, wn0, fa, fb);
+            wait_lgkmcnt0();
+            wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
+            pp_barrier();
+            // Both groups are done with stage t only now: the other waves of
+            // this group read it in the phase that just ended, so A(t+2)
+            // cannot be issued into it before this barrier.
+            if constexpr (decltype(load)::value)
+                pp_mma_load<TMW>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+            else
+                pp_mma<TMW>(fa, fb, acc);
+            pp_barrier();
+        };
+        int t = 0;
+        for (; t + 2 < nk; ++t) step(t, BoolC<true>{});
+        for (; t < nk; ++t) step(t, BoolC<false>{});
+        rows_out(acc);
+        wait_lgkmcnt0();
+        pp_barrier();
+    }
+}
+
+}  // namespace trmoe

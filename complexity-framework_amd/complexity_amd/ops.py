@@ -13,7 +13,6 @@ from __future__ import annotations
 
 import ctypes
 import functools
-import os
 from dataclasses import dataclass, field
 from typing import Optional, Sequence, Tuple
 
@@ -804,13 +803,11 @@ def backward_packs(packed: PackedLayer, hidden: int, shared_down=None, expert_do
 # Second stream of the backward: the weight-gradient GEMMs of the gate|up
 # weights run beside the data gradient and the down weights' gradient (they
 # only share read-only inputs), so the launches fill the CUs the others leave
-# idle.  Default priority, one per device.  TRMOE_BWD_STREAMS=0 disables it.
+# idle.  Default priority, one per device.
 _SIDE: dict = {}
 
 
 def _side_stream(device: torch.device):
-    if os.environ.get("TRMOE_BWD_STREAMS", "1") in ("0", ""):
-        return None
     st = _SIDE.get(device.index)
     if st is None:
         st = torch.cuda.Stream(device=device)

@@ -303,8 +303,9 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
 // ROUTED: the launch covers dense-routed expert columns (route gather and
 // per-token expert weights for the tiles that hold them).  TMW = 4: 256-row
 // tiles; 2: 128-row tiles (the trailing columns of a launch whose last round
-// of 256-row tiles would leave most CUs idle).
-template <bool ROUTED, int TMW>
+// of 256-row tiles would leave most CUs idle).  SAVE: also write the raw
+// gate|up outputs to a.gu (training forward).
+template <bool ROUTED, int TMW, bool SAVE = false>
 __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     using Shape = ShapePP<TMW>;
     using Kind = KindBF16;
@@ -346,6 +347,7 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     pp_main<TMW, PPLayoutK<TMW>>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
         gate_up_epi_tile<Kind, Shape, ROUTED>(a, c, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
     });
+    if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * 256);
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
@@ -938,17 +940,17 @@ int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int6
 // stages, at least kBigTileMinBlocks tiles.
 static bool pp_eligible(int act, int wdt, const GateUpArgs& a, int64_t packed_rows) {
     const int64_t cols = packed_rows - a.n_base;
-    return act == TRMOE_BF16 && wdt == TRMOE_BF16 && a.gu == nullptr && a.K > 0 && a.K % 64 == 0 &&
-           cols > 0 && cols % 256 == 0 && ((a.M + 255) / 256) * (cols / 256) >= kBigTileMinBlocks;
+    return act == TRMOE_BF16 && wdt == TRMOE_BF16 && a.K > 0 && a.K % 64 == 0 && cols > 0 && cols % 256 == 0 &&
+           ((a.M + 255) / 256) * (cols / 256) >= kBigTileMinBlocks;
 }
 
-template <bool ROUTED, int TMW>
+template <bool ROUTED, int TMW, bool SAVE>
 static int launch_gate_up_pp_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     constexpr int BM = ShapePP<TMW>::BM;
     const dim3 grid((unsigned)((a.M + BM - 1) / BM), (unsigned)((packed_rows - a.n_base) / 256));
     constexpr int kLds = 2 * (BM + 256) * kRowBytes;   // two stages of A and B rows
     static_assert(kLds >= BM * (128 * 2 + 16), "the epilogue tile reuses the stages");
-    auto kern = k_gate_up_pp<ROUTED, TMW>;
+    auto kern = k_gate_up_pp<ROUTED, TMW, SAVE>;
     const int st = ensure_lds(kern, kLds);
     if (st) return st;
     if (grid.x == 0 || grid.y == 0) return TRMOE_OK;
@@ -961,7 +963,7 @@ static int launch_gate_up_pp_shape(const GateUpArgs& a, int64_t packed_rows, hip
 // a second launch of 128-row tiles (C2: 64 x 24 tiles, then 128 x 2 half
 // tiles: seven rounds become six and a round of half tiles).  Launches whose
 // first columns hold no expert features leave the routing code out.
-template <bool ROUTED>
+template <bool ROUTED, bool SAVE>
 static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int64_t tiles_m = (a.M + 255) / 256;
     const int64_t cols = (packed_rows - a.n_base) / 256;
@@ -975,23 +977,28 @@ static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream
             }
     const int64_t split = a.n_base + (cols - tail) * 256;
     const bool head_routed = ROUTED && a.ids != nullptr && split > 2 * a.shared_feats;
-    int st = head_routed ? launch_gate_up_pp_shape<ROUTED, 4>(a, split, stream)
-                         : launch_gate_up_pp_shape<false, 4>(a, split, stream);
+    int st = head_routed ? launch_gate_up_pp_shape<ROUTED, 4, SAVE>(a, split, stream)
+                         : launch_gate_up_pp_shape<false, 4, SAVE>(a, split, stream);
     if (st || tail == 0) return st;
     GateUpArgs t = a;
     t.n_base = split;
-    return launch_gate_up_pp_shape<ROUTED, 2>(t, packed_rows, stream);
+    return launch_gate_up_pp_shape<ROUTED, 2, SAVE>(t, packed_rows, stream);
 }
 
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if (a.gu != nullptr) return launch_gate_up_save(act, wdt, a, packed_rows, stream);
+    if (a.gu != nullptr) {
+        if (pp_eligible(act, wdt, a, packed_rows))
+            return a.ids != nullptr ? launch_gate_up_pp<true, true>(a, packed_rows, stream)
+                                    : launch_gate_up_pp<false, true>(a, packed_rows, stream);
+        return launch_gate_up_save(act, wdt, a, packed_rows, stream);
+    }
     if (a.M <= kSkinnyMaxTokens && packed_rows % 64 == 0)
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
     if (a.row_scale == nullptr && a.rms_eps > 0.0f)
         return set_error(TRMOE_ERR_INVALID, "gate_up: in-kernel RMSNorm scales need the decode kernels (n <= 128)");
     if (pp_eligible(act, wdt, a, packed_rows))
-        return a.ids != nullptr ? launch_gate_up_pp<true>(a, packed_rows, stream)
-                                : launch_gate_up_pp<false>(a, packed_rows, stream);
+        return a.ids != nullptr ? launch_gate_up_pp<true, false>(a, packed_rows, stream)
+                                : launch_gate_up_pp<false, false>(a, packed_rows, stream);
     if (a.ids != nullptr) {
         // dense-routed: the shared columns as a plain gate|up launch, then the
         // expert columns with the routing epilogue

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
 // tiles; 2: 128-row tiles (the trailing columns of a launch whose last round
 // of 256-row tiles would leave most CUs idle).  SAVE: also write the raw
 // gate|up outputs to a.gu (training forward).
-template <bool ROUTED, int TMW, bool SAVE = false>
+template <bool ROUTED, int TMW, bool SAVE = false, bool FP8 = false>
 __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     using Shape = ShapePP<TMW>;
     using Kind = KindBF16;
@@ -339,12 +339,19 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     if (gathered) __syncthreads();
 
     PPRows<BM> ap;
-    PPRows<256> bp;
-    if (group == 1) ap.init(a.x, m0, a.M, a.ldx * (int64_t)sizeof(bf16_t), wig);
-    else bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
+    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    if (group == 1) {
+        ap.init(a.x, m0, a.M, a.ldx * (int64_t)sizeof(bf16_t), wig);
+    } else {
+        if constexpr (FP8)
+            bp.init(a.w, n0, n0 + 256, a.ldw, a.K, wig);
+        else
+            bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
+    }
     f32x16 acc[TMW][2];
     zero_acc<Kind>(acc);
-    pp_main<TMW, PPLayoutK<TMW>>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
+    using Lay = std::conditional_t<FP8, PPLayoutF8<TMW>, PPLayoutK<TMW>>;
+    pp_main<TMW, Lay>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
         gate_up_epi_tile<Kind, Shape, ROUTED>(a, c, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
     });
     if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * 256);
@@ -639,12 +646,14 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     }
 }
 
-// K4 on the ping-pong main loop (bf16 activations and weights, K a multiple
-// of 64): 256x256 tiles over the hidden columns; weight rows past the hidden
-// size load as zero (the last tile of H = 896 multiplies 128 of them).  Epilogue: each
+// K4 on the ping-pong main loop (bf16 activations; bf16 or, FP8, e4m3
+// weights expanded at the fragment read; K a multiple of 64): 256x256 tiles
+// over the hidden columns; weight rows past the hidden size load as zero (the
+// last tile of H = 896 multiplies 128 of them).  Epilogue: each
 // group writes shared_scale * column scale * acc for its rows to LDS as bf16
 // (the tile kernel's rounding), then every thread adds the route-weighted y
 // rows and the residual over 16-byte chunks and stores.
+template <bool FP8>
 __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     constexpr int BM = 256, BN = 256;
     using T = bf16_t;
@@ -672,13 +681,20 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     }
 
     PPRows<BM> ap;
-    PPRows<256> bp;
-    if (group == 1) ap.init(a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), wig);
-    else bp.init(a.w, n0, a.N, a.ldw * (int64_t)sizeof(T), wig);   // rows past N load as zero
+    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    if (group == 1) {
+        ap.init(a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), wig);
+    } else {   // rows past N load as zero
+        if constexpr (FP8)
+            bp.init(a.w, n0, a.N, a.ldw, a.K, wig);
+        else
+            bp.init(a.w, n0, a.N, a.ldw * (int64_t)sizeof(T), wig);
+    }
     f32x16 acc[4][2];
     zero_acc<KindBF16>(acc);
     constexpr int kORowBytes = BN * 2 + 16;
-    pp_main<4, PPLayoutK<4>>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
+    pp_main<4, Lay>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
         const int r = lane & 31;
         float cs[2];
 #pragma unroll
@@ -940,17 +956,19 @@ int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int6
 // stages, at least kBigTileMinBlocks tiles.
 static bool pp_eligible(int act, int wdt, const GateUpArgs& a, int64_t packed_rows) {
     const int64_t cols = packed_rows - a.n_base;
-    return act == TRMOE_BF16 && wdt == TRMOE_BF16 && a.K > 0 && a.K % 64 == 0 && cols > 0 && cols % 256 == 0 &&
+    const bool types = act == TRMOE_BF16 && (wdt == TRMOE_BF16 || (wdt == TRMOE_FP8_E4M3 && a.gu == nullptr));
+    return types && a.K > 0 && a.K % 64 == 0 && cols > 0 && cols % 256 == 0 &&
            ((a.M + 255) / 256) * (cols / 256) >= kBigTileMinBlocks;
 }
 
-template <bool ROUTED, int TMW, bool SAVE>
+template <bool ROUTED, int TMW, bool SAVE, bool FP8>
 static int launch_gate_up_pp_shape(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     constexpr int BM = ShapePP<TMW>::BM;
     const dim3 grid((unsigned)((a.M + BM - 1) / BM), (unsigned)((packed_rows - a.n_base) / 256));
-    constexpr int kLds = 2 * (BM + 256) * kRowBytes;   // two stages of A and B rows
-    static_assert(kLds >= BM * (128 * 2 + 16), "the epilogue tile reuses the stages");
-    auto kern = k_gate_up_pp<ROUTED, TMW, SAVE>;
+    using Lay = std::conditional_t<FP8, PPLayoutF8<TMW>, PPLayoutK<TMW>>;
+    constexpr int kEpi = BM * (128 * 2 + 16);                // the SwiGLU tile, over the stages
+    constexpr int kLds = 2 * Lay::kStage > kEpi ? 2 * Lay::kStage : kEpi;
+    auto kern = k_gate_up_pp<ROUTED, TMW, SAVE, FP8>;
     const int st = ensure_lds(kern, kLds);
     if (st) return st;
     if (grid.x == 0 || grid.y == 0) return TRMOE_OK;
@@ -963,7 +981,7 @@ static int launch_gate_up_pp_shape(const GateUpArgs& a, int64_t packed_rows, hip
 // a second launch of 128-row tiles (C2: 64 x 24 tiles, then 128 x 2 half
 // tiles: seven rounds become six and a round of half tiles).  Launches whose
 // first columns hold no expert features leave the routing code out.
-template <bool ROUTED, bool SAVE>
+template <bool ROUTED, bool SAVE, bool FP8 = false>
 static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
     const int64_t tiles_m = (a.M + 255) / 256;
     const int64_t cols = (packed_rows - a.n_base) / 256;
@@ -977,12 +995,12 @@ static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream
             }
     const int64_t split = a.n_base + (cols - tail) * 256;
     const bool head_routed = ROUTED && a.ids != nullptr && split > 2 * a.shared_feats;
-    int st = head_routed ? launch_gate_up_pp_shape<ROUTED, 4, SAVE>(a, split, stream)
-                         : launch_gate_up_pp_shape<false, 4, SAVE>(a, split, stream);
+    int st = head_routed ? launch_gate_up_pp_shape<ROUTED, 4, SAVE, FP8>(a, split, stream)
+                         : launch_gate_up_pp_shape<false, 4, SAVE, FP8>(a, split, stream);
     if (st || tail == 0) return st;
     GateUpArgs t = a;
     t.n_base = split;
-    return launch_gate_up_pp_shape<ROUTED, 2, SAVE>(t, packed_rows, stream);
+    return launch_gate_up_pp_shape<ROUTED, 2, SAVE, FP8>(t, packed_rows, stream);
 }
 
 int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
@@ -996,9 +1014,13 @@ int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, h
         return launch_gate_up_skinny(act, wdt, a, packed_rows, stream);
     if (a.row_scale == nullptr && a.rms_eps > 0.0f)
         return set_error(TRMOE_ERR_INVALID, "gate_up: in-kernel RMSNorm scales need the decode kernels (n <= 128)");
-    if (pp_eligible(act, wdt, a, packed_rows))
+    if (pp_eligible(act, wdt, a, packed_rows)) {
+        if (wdt == TRMOE_FP8_E4M3)
+            return a.ids != nullptr ? launch_gate_up_pp<true, false, true>(a, packed_rows, stream)
+                                    : launch_gate_up_pp<false, false, true>(a, packed_rows, stream);
         return a.ids != nullptr ? launch_gate_up_pp<true, false>(a, packed_rows, stream)
                                 : launch_gate_up_pp<false, false>(a, packed_rows, stream);
+    }
     if (a.ids != nullptr) {
         // dense-routed: the shared columns as a plain gate|up launch, then the
         // expert columns with the routing epilogue
@@ -1037,13 +1059,15 @@ static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
 
 // bf16 down GEMMs with at least a full round of 256x256 tiles run on the
 // ping-pong main loop.
+template <bool FP8>
 static int launch_down_pp(const DownArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)((a.N + 255) / 256));
-    constexpr int kLds = 256 * (256 * 2 + 16) > 2 * (256 + 256) * kRowBytes ? 256 * (256 * 2 + 16)
-                                                                           : 2 * (256 + 256) * kRowBytes;
-    const int st = ensure_lds(k_down_pp, kLds);
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
+    constexpr int kEpi = 256 * (256 * 2 + 16);   // the bf16 output tile, over the stages
+    constexpr int kLds = kEpi > 2 * Lay::kStage ? kEpi : 2 * Lay::kStage;
+    const int st = ensure_lds(k_down_pp<FP8>, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(k_down_pp, grid, dim3(512), kLds, stream, a);
+    hipLaunchKernelGGL(k_down_pp<FP8>, grid, dim3(512), kLds, stream, a);
     return check_launch("shared_down_combine");
 }
 
@@ -1052,8 +1076,8 @@ static int launch_down_pp(const DownArgs& a, hipStream_t stream) {
 template <class Kind, bool FP8>
 static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
     const int64_t mt = (a.M + 255) / 256;
-    if constexpr (std::is_same_v<Kind, KindBF16> && !FP8) {
-        if (a.K > 0 && a.K % 64 == 0 && mt * ((a.N + 255) / 256) >= 256) return launch_down_pp(a, stream);
+    if constexpr (std::is_same_v<Kind, KindBF16>) {
+        if (a.K > 0 && a.K % 64 == 0 && mt * ((a.N + 255) / 256) >= 256) return launch_down_pp<FP8>(a, stream);
     }
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     if constexpr (FP8) {

@@ -161,6 +161,69 @@ struct PPLayoutK {
     }
 };
 
+// The e4m3 weight operand loaded by one group of 4 waves: 256 rows of 64
+// bytes (64 K values) per stage, 16 rows per wave instruction, chunk c of
+// row r stored at chunk c ^ lds_swz64(r) (the lds_byte64 layout); rows at or
+// past rows_total and K bytes at or past kbytes load zero.
+struct PPRows64 {
+    static constexpr int kInstr = 4;   // 16 instructions of 16 rows per stage over 4 waves
+    __amdgpu_buffer_rsrc_t rsrc;
+    int off[kInstr];
+    int koff[kInstr];
+    int kbytes;
+    int wig;
+
+    __device__ __forceinline__ void init(const void* base, int64_t row0, int64_t rows_total, int64_t ld_bytes,
+                                         int kbytes_, int wave_in_group) {
+        const int64_t avail = rows_total - row0;
+        const int64_t nrows = avail < 256 ? avail : 256;
+        rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
+        kbytes = kbytes_;
+        wig = wave_in_group;
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int r = (wig * kInstr + j) * 16 + (lane >> 2);
+            koff[j] = ((lane & 3) ^ lds_swz64(r)) * 16;
+            off[j] = r < nrows ? (int)(r * ld_bytes) + koff[j] : kOutOfRange;
+        }
+    }
+    __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
+        const int kb = kt * kRow64;
+        const int o = (kb + koff[j] < kbytes) ? off[j] + kb : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (wig * kInstr + j) * 16 * kRow64), 16, o,
+                                                0, 0, 0);
+    }
+    __device__ __forceinline__ void issue(int kt, char* dst) const {
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) issue_one(j, kt, dst);
+    }
+};
+
+// bf16 activation rows of 128 bytes, then e4m3 weight rows of 64 bytes; the
+// weight fragments are expanded to bf16 at the read (exact).
+template <int TMW>
+struct PPLayoutF8 {
+    static constexpr int kBOff = 64 * TMW * kRowBytes;
+    static constexpr int kStage = 64 * TMW * kRowBytes + 256 * kRow64;
+    __device__ __forceinline__ static void read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][TMW],
+                                                u32x4 (&fb)[4][2]) {
+        const int lane = threadIdx.x & 63;
+        const int r = lane & 31, h = lane >> 5;
+        const char* Bs = st + kBOff;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int tm = 0; tm < TMW; ++tm)
+                fa[g][tm] = *reinterpret_cast<const u32x4*>(st + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+                fb[g][tn] = fp8x8_to_bf16x8(
+                    *reinterpret_cast<const u32x2*>(Bs + lds_byte64(wn0 + tn * 32 + r, g) + 8 * h));
+        }
+    }
+};
+
 typedef short trmoe_v4s __attribute__((ext_vector_type(4)));
 
 // 8 bytes of a transposing LDS read: lane i of each 16-lane group receives

@@ -344,7 +344,7 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
         ap.init(a.x, m0, a.M, a.ldx * (int64_t)sizeof(bf16_t), wig);
     } else {
         if constexpr (FP8)
-            bp.init(a.w, n0, n0 + 256, a.ldw, a.K, wig);
+            bp.init(a.w, n0, n0 + 256, a.ldw, wig);
         else
             bp.init(a.w, n0, n0 + 256, a.ldw * (int64_t)sizeof(bf16_t), wig);
     }
@@ -356,6 +356,142 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     });
     if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * 256);
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
+}
+
+// Tile i of a persistent launch over tiles_m x tiles_n tiles -> (row tile,
+// column tile).  Workgroups are dispatched to the 8 XCDs round-robin, so the
+// 32 workgroups of an XCD that run concurrently get a block of tiles_m / 8
+// consecutive row tiles (their activation rows stay in that XCD's L2 for the
+// whole launch) times the next few column tiles; other shapes walk row tiles
+// first.
+__device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, bool xcd_rows, uint32_t& mt, uint32_t& nt) {
+    if (xcd_rows) {
+        const uint32_t mpx = tiles_m >> 3, j = i >> 3;
+        nt = j / mpx;
+        mt = (i & 7) * mpx + (j - nt * mpx);
+    } else {
+        nt = i / tiles_m;
+        mt = i - nt * tiles_m;
+    }
+}
+
+// SwiGLU of one finished tile straight from the accumulators of the calling
+// wave (no LDS): each lane owns one h feature (its gate column r of the
+// wave's 64 packed rows, up column 32 + r) and 16 rows per 32-row block, one
+// 2-byte store per value.  The offset is a per-lane part plus a row part, and
+// rows at or past M fall past the buffer's range and are dropped.
+template <int TMW>
+__device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
+                                                   int64_t n0, int wm0, int wn0) {
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const int64_t pbase = n0 + wn0;   // packed row of the wave's gate block
+    // h = silu(g) * u * mult, with the shared multiplier folded into u
+    const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
+    const float su = (a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f) * a.shared_mult;
+    const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
+    // the row stride is redefined here so that no offset below is hoisted
+    // out of a caller's loop (64 of them would stay live across every stage)
+    int ld2 = (int)a.ldh * 2;
+    asm volatile("" : "+s"(ld2));
+    const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.h) + m0 * a.ldh, (uint32_t)(mlim * ld2));
+    const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + (int)((pbase >> 1) + r) * 2;
+#pragma unroll
+    for (int tm = 0; tm < TMW; ++tm)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;   // row wm0 + tm*32 + acc_row(lane, i)
+            const float g = acc[tm][0][i] * sg;
+            const float u = acc[tm][1][i] * su;
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<bf16_t>(silu_f(g) * u)),
+                                                  rsrc, off, 0, 0);
+        }
+}
+
+// gate_up_save for the persistent kernel: the raw gate|up outputs of the
+// calling wave (times the e4m3 scale) to a.gu, offsets built like
+// gate_up_epi_direct's so that none is hoisted out of the tile loop.
+template <int TMW>
+__device__ __forceinline__ void gate_up_save_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
+                                                    int64_t n0, int wm0, int wn0) {
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
+    int ld2 = (int)a.ldgu * 2;
+    asm volatile("" : "+s"(ld2));
+    const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.gu) + m0 * a.ldgu, (uint32_t)(mlim * ld2));
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int64_t col = n0 + wn0 + tn * 32 + r;
+        const float sc = a.w_scale ? a.w_scale[col] : 1.0f;
+        const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + (int)col * 2;
+#pragma unroll
+        for (int tm = 0; tm < TMW; ++tm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    __builtin_bit_cast(uint16_t, from_f32<bf16_t>(acc[tm][tn][i] * sc)), rsrc, off, 0, 0);
+            }
+    }
+}
+
+// Persistent gate|up + SwiGLU (shared columns: no routing epilogue, no row
+// scales): one workgroup per CU runs tiles blockIdx.x, + gridDim.x, ... of
+// the tiles_m x (n_tiles / tiles_m) 256-row tiles as one stream of K stages
+// (pp_stream), writing each tile's h from registers while the next tile's
+// stages load and multiply.  SAVE: also the raw gate|up outputs (a.gu).
+template <int TMW, bool SAVE, bool FP8>
+__global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t tiles_m, int64_t n_tiles) {
+    constexpr int BM = 64 * TMW;
+    extern __shared__ __align__(16) char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * (BM / 2), wn0 = wig * 64;
+    const int64_t G = gridDim.x;
+    const int ntiles = (int)((n_tiles - (int64_t)blockIdx.x + G - 1) / G);
+    if (ntiles <= 0) return;
+    const bool xcd_rows = (tiles_m & 7) == 0 && (G & 7) == 0;
+    auto coords = [&](int i, int64_t& m0, int64_t& n0) {
+        uint32_t mt, nt;
+        pps_tile((uint32_t)blockIdx.x + (uint32_t)i * (uint32_t)G, (uint32_t)tiles_m, xcd_rows, mt, nt);
+        m0 = (int64_t)mt * BM;
+        n0 = a.n_base + (int64_t)nt * 256;
+    };
+    const int64_t ldx_b = a.ldx * (int64_t)sizeof(bf16_t);
+    const int64_t ldw_b = FP8 ? a.ldw : a.ldw * (int64_t)sizeof(bf16_t);
+
+    PPRows<BM> ap;
+    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    int64_t m0, n0;
+    coords(0, m0, n0);
+    if (group == 1) {
+        ap.init(a.x, m0, a.M, ldx_b, wig);
+    } else {
+        if constexpr (FP8)
+            bp.init(a.w, n0, n0 + 256, ldw_b, wig);
+        else
+            bp.init(a.w, n0, n0 + 256, ldw_b, wig);
+    }
+    f32x16 acc[TMW][2];
+    zero_acc<KindBF16>(acc);
+    using Lay = std::conditional_t<FP8, PPLayoutF8<TMW, true>, PPLayoutK<TMW, true>>;
+    pp_stream<TMW, Lay>(
+        ap, bp, a.K / 64, ntiles, lds, group, wm0, wn0, acc,
+        [&](int i) {   // i >= ntiles: no rows (the refills past the last stage load zeros)
+            int64_t tm0, tn0;
+            coords(i, tm0, tn0);
+            ap.retarget(a.x, tm0, i < ntiles ? a.M : tm0, ldx_b);
+        },
+        [&](int i) {
+            int64_t tm0, tn0;
+            coords(i, tm0, tn0);
+            bp.retarget(a.w, tn0, i < ntiles ? tn0 + 256 : tn0, ldw_b);
+        },
+        [&](int i, const f32x16 (&c)[TMW][2]) {
+            int64_t tm0, tn0;
+            coords(i, tm0, tn0);
+            if constexpr (SAVE) gate_up_save_direct<TMW>(a, c, tm0, tn0, wm0, wn0);
+            gate_up_epi_direct<TMW>(a, c, tm0, tn0, wm0, wn0);
+        });
 }
 
 // ---------------------------------------------------------------------------
@@ -686,7 +822,7 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
         ap.init(a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), wig);
     } else {   // rows past N load as zero
         if constexpr (FP8)
-            bp.init(a.w, n0, a.N, a.ldw, a.K, wig);
+            bp.init(a.w, n0, a.N, a.ldw, wig);
         else
             bp.init(a.w, n0, a.N, a.ldw * (int64_t)sizeof(T), wig);
     }
@@ -976,6 +1112,24 @@ static int launch_gate_up_pp_shape(const GateUpArgs& a, int64_t packed_rows, hip
     return check_launch(ROUTED ? "dense_routed_gate_up" : "shared_gate_up");
 }
 
+// Persistent 256-row tiles over packed rows [a.n_base, packed_rows): one
+// workgroup per CU (fewer when there are fewer tiles).
+template <bool SAVE, bool FP8>
+static int launch_gate_up_pps(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int64_t tiles_m = (a.M + 255) / 256;
+    const int64_t n_tiles = tiles_m * ((packed_rows - a.n_base) / 256);
+    const int64_t cus = device_cus();
+    const int64_t grid = n_tiles < cus ? n_tiles : cus;
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
+    constexpr int kLds = 2 * Lay::kStage;
+    auto kern = k_gate_up_pps<4, SAVE, FP8>;
+    const int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    if (grid <= 0) return TRMOE_OK;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), kLds, stream, a, tiles_m, n_tiles);
+    return check_launch("shared_gate_up");
+}
+
 // 256-row tiles; when their last round would leave at least half of the CUs
 // idle, the fewest trailing columns whose removal leaves whole rounds run as
 // a second launch of 128-row tiles (C2: 64 x 24 tiles, then 128 x 2 half
@@ -995,8 +1149,9 @@ static int launch_gate_up_pp(const GateUpArgs& a, int64_t packed_rows, hipStream
             }
     const int64_t split = a.n_base + (cols - tail) * 256;
     const bool head_routed = ROUTED && a.ids != nullptr && split > 2 * a.shared_feats;
-    int st = head_routed ? launch_gate_up_pp_shape<ROUTED, 4, SAVE, FP8>(a, split, stream)
-                         : launch_gate_up_pp_shape<false, 4, SAVE, FP8>(a, split, stream);
+    int st = head_routed            ? launch_gate_up_pp_shape<ROUTED, 4, SAVE, FP8>(a, split, stream)
+             : a.row_scale != nullptr ? launch_gate_up_pp_shape<false, 4, SAVE, FP8>(a, split, stream)
+                                      : launch_gate_up_pps<SAVE, FP8>(a, split, stream);
     if (st || tail == 0) return st;
     GateUpArgs t = a;
     t.n_base = split;

@@ -54,6 +54,14 @@ struct PPRows {
         row_bytes = (int)ld_bytes;
         c0 = ((lane & 7) ^ (lane >> 3)) & 7;
     }
+    // the same loader over another row block of the operand (the lane's
+    // position in the stage does not change)
+    __device__ __forceinline__ void retarget(const void* base, int64_t first_row, int64_t rows_total,
+                                             int64_t ld_bytes) {
+        const int64_t avail = rows_total - first_row;
+        nrows = (int)(avail < ROWS ? avail : ROWS);
+        rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
+    }
     // stage kt (bytes [128 kt, 128 kt + 128) of every row) into `dst` (the
     // operand's part of an LDS stage).  LDS slot (lane % 8) of row r holds K
     // chunk slot ^ swz(r); the rows of instruction j have r / 8 = kInstr *
@@ -86,21 +94,58 @@ __device__ __forceinline__ void pp_barrier() {
 // The wave's fragments of one K stage: A rows wm0 + 32 tm + r (A block of
 // a_rows rows first in the stage), B rows wn0 + 32 tn + r, 16-byte chunk
 // 2 g + h of the 128-byte row.
-template <int TM>
-__device__ __forceinline__ void pp_read(const char* st, int a_rows, int wm0, int wn0, u32x4 (&fa)[4][TM],
-                                        u32x4 (&fb)[4][2]) {
+//
+// Addresses: for a row 32 t + r of a block starting at a multiple of 64 rows,
+// lds_swz(row) = lds_swz(r) ^ 4 (t & 1), so every fragment address is one of
+// eight per-lane patterns (K group g, parity of t) plus a uniform offset.
+// The patterns are redefined at each call: kept live across a caller's loop
+// they and their hoisted sums would take registers the loop needs.  The
+// persistent loop (pp_stream), whose tile loop would otherwise spill, reads
+// this way (PAT); pp_main's kernels keep one address per fragment, which
+// measured a few percent faster there.
+__device__ __forceinline__ void pp_patterns(int (&pat)[4][2]) {
     const int lane = threadIdx.x & 63;
     const int r = lane & 31, h = lane >> 5;
-    const char* As = st;
-    const char* Bs = st + a_rows * kRowBytes;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-            fa[g][tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+        for (int p = 0; p < 2; ++p) {
+            pat[g][p] = r * kRowBytes + (((2 * g + h) ^ lds_swz(r) ^ (4 * p)) << 4);
+            asm volatile("" : "+v"(pat[g][p]));
+        }
+}
+
+template <int TM, bool PAT = false>
+__device__ __forceinline__ void pp_read(const char* st, int a_rows, int wm0, int wn0, u32x4 (&fa)[4][TM],
+                                        u32x4 (&fb)[4][2]) {
+    if constexpr (PAT) {
+        int pat[4][2];
+        pp_patterns(pat);
+        const char* As = st + wm0 * kRowBytes;
+        const char* Bs = st + (a_rows + wn0) * kRowBytes;
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
-            fb[g][tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+                fa[g][tm] = *reinterpret_cast<const u32x4*>(As + tm * 32 * kRowBytes + pat[g][tm & 1]);
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+                fb[g][tn] = *reinterpret_cast<const u32x4*>(Bs + tn * 32 * kRowBytes + pat[g][tn & 1]);
+        }
+    } else {
+        const int lane = threadIdx.x & 63;
+        const int r = lane & 31, h = lane >> 5;
+        const char* As = st;
+        const char* Bs = st + a_rows * kRowBytes;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+                fa[g][tm] = *reinterpret_cast<const u32x4*>(As + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+                fb[g][tn] = *reinterpret_cast<const u32x4*>(Bs + lds_byte(wn0 + tn * 32 + r, 2 * g + h));
+        }
     }
 }
 
@@ -151,13 +196,13 @@ using ShapePP = TileShape<64 * TMW, 256, 2, 4, 4>;
 // their rows (activations x, packed weights): A rows then B rows of 128
 // bytes.  PPLayoutT: operands with K across rows (the weight gradients'
 // token-major operands): 64 K rows of 256 A columns, then of 256 B columns.
-template <int TMW>
+template <int TMW, bool PAT = false>
 struct PPLayoutK {
     static constexpr int kBOff = 64 * TMW * kRowBytes;
     static constexpr int kStage = (64 * TMW + 256) * kRowBytes;
     __device__ __forceinline__ static void read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][TMW],
                                                 u32x4 (&fb)[4][2]) {
-        pp_read<TMW>(st, 64 * TMW, wm0, wn0, fa, fb);
+        pp_read<TMW, PAT>(st, 64 * TMW, wm0, wn0, fa, fb);
     }
 };
 
@@ -168,29 +213,31 @@ struct PPLayoutK {
 struct PPRows64 {
     static constexpr int kInstr = 4;   // 16 instructions of 16 rows per stage over 4 waves
     __amdgpu_buffer_rsrc_t rsrc;
-    int off[kInstr];
-    int koff[kInstr];
-    int kbytes;
+    int row;      // lane's row for instruction 0: 64 wave_in_group + lane / 4 (instruction j adds 16 j)
+    int koff;     // lane's byte in the row: chunk (lane % 4) ^ lds_swz64(row), the same for every j
+    int nrows;    // rows present
+    int ld;       // row stride in bytes
     int wig;
 
+    // K (bytes per row) is a multiple of 64 for every caller, so a stage
+    // never reaches past a row's K bytes and only rows need a range check.
     __device__ __forceinline__ void init(const void* base, int64_t row0, int64_t rows_total, int64_t ld_bytes,
-                                         int kbytes_, int wave_in_group) {
-        const int64_t avail = rows_total - row0;
-        const int64_t nrows = avail < 256 ? avail : 256;
-        rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
-        kbytes = kbytes_;
+                                         int wave_in_group) {
         wig = wave_in_group;
         const int lane = threadIdx.x & 63;
-#pragma unroll
-        for (int j = 0; j < kInstr; ++j) {
-            const int r = (wig * kInstr + j) * 16 + (lane >> 2);
-            koff[j] = ((lane & 3) ^ lds_swz64(r)) * 16;
-            off[j] = r < nrows ? (int)(r * ld_bytes) + koff[j] : kOutOfRange;
-        }
+        row = wig * kInstr * 16 + (lane >> 2);
+        koff = ((lane & 3) ^ lds_swz64(row)) * 16;   // lds_swz64(row + 16 j) == lds_swz64(row)
+        retarget(base, row0, rows_total, ld_bytes);
+    }
+    __device__ __forceinline__ void retarget(const void* base, int64_t row0, int64_t rows_total, int64_t ld_bytes) {
+        const int64_t avail = rows_total - row0;
+        nrows = (int)(avail < 256 ? avail : 256);
+        ld = (int)ld_bytes;
+        rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
     }
     __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
-        const int kb = kt * kRow64;
-        const int o = (kb + koff[j] < kbytes) ? off[j] + kb : kOutOfRange;
+        const int r = row + 16 * j;
+        const int o = (r * ld + koff + kt * kRow64) | (r < nrows ? 0 : kOutOfRange);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (wig * kInstr + j) * 16 * kRow64), 16, o,
                                                 0, 0, 0);
     }
@@ -202,7 +249,7 @@ struct PPRows64 {
 
 // bf16 activation rows of 128 bytes, then e4m3 weight rows of 64 bytes; the
 // weight fragments are expanded to bf16 at the read (exact).
-template <int TMW>
+template <int TMW, bool PAT = false>
 struct PPLayoutF8 {
     static constexpr int kBOff = 64 * TMW * kRowBytes;
     static constexpr int kStage = 64 * TMW * kRowBytes + 256 * kRow64;
@@ -211,15 +258,39 @@ struct PPLayoutF8 {
         const int lane = threadIdx.x & 63;
         const int r = lane & 31, h = lane >> 5;
         const char* Bs = st + kBOff;
+        if constexpr (PAT) {
+            int pat[4][2];
+            pp_patterns(pat);
+            // weight rows 32 tn + r (wn0 a multiple of 64): lds_swz64
+            // depends on r only, so four per-lane patterns (K group g) cover them
+            int pb[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+            for (int g = 0; g < 4; ++g) {
+                pb[g] = r * kRow64 + ((g ^ lds_swz64(r)) << 4) + 8 * h;
+                asm volatile("" : "+v"(pb[g]));
+            }
+            const char* As = st + wm0 * kRowBytes;
+            const char* Bw = Bs + wn0 * kRow64;
 #pragma unroll
-            for (int tm = 0; tm < TMW; ++tm)
-                fa[g][tm] = *reinterpret_cast<const u32x4*>(st + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+            for (int g = 0; g < 4; ++g) {
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn)
-                fb[g][tn] = fp8x8_to_bf16x8(
-                    *reinterpret_cast<const u32x2*>(Bs + lds_byte64(wn0 + tn * 32 + r, g) + 8 * h));
+                for (int tm = 0; tm < TMW; ++tm)
+                    fa[g][tm] = *reinterpret_cast<const u32x4*>(As + tm * 32 * kRowBytes + pat[g][tm & 1]);
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn)
+                    fb[g][tn] = fp8x8_to_bf16x8(*reinterpret_cast<const u32x2*>(Bw + tn * 32 * kRow64 + pb[g]));
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int tm = 0; tm < TMW; ++tm)
+                    fa[g][tm] = *reinterpret_cast<const u32x4*>(st + lds_byte(wm0 + tm * 32 + r, 2 * g + h));
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn)
+                    fb[g][tn] = fp8x8_to_bf16x8(
+                        *reinterpret_cast<const u32x2*>(Bs + lds_byte64(wn0 + tn * 32 + r, g) + 8 * h));
+            }
         }
     }
 };
@@ -411,6 +482,140 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
         for (; t < nk; ++t) step(t, BoolC<false>{});
         rows_out(acc);
         wait_lgkmcnt0();
+        pp_barrier();
+    }
+}
+
+// Accumulators set to a zero that is redefined at each use, so that no
+// zero block is hoisted out of a caller's loop.
+template <int TM, int TN>
+__device__ __forceinline__ void zero_acc_opaque(f32x16 (&acc)[TM][TN]) {
+    float z = 0.0f;
+    asm volatile("" : "+v"(z));
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[tm][tn][i] = z;
+}
+
+// Persistent form of pp_main.  The workgroup's ntiles tiles (nk K stages
+// each) run as one stream of stages s = nk * i + kt through the same two LDS
+// buffers, phase schedule and refill rules, so the next tile's first stages
+// are requested while the current one is still being multiplied and no
+// barrier-bound prologue or LDS-staged epilogue sits between tiles.  Each
+// group writes a finished tile straight from its accumulators (epi(i, acc),
+// global stores only, no LDS) at the start of its read phase of the next
+// tile's first stage, before the reads, while the other group multiplies;
+// the last tile's epilogue runs as in pp_main.  retarget_a(i) / retarget_b(i)
+// point the A / B loader at tile i, each called by the group that issues
+// that operand before its first load of tile i (the caller has pointed both
+// at tile 0); for i == ntiles the loader must load nothing (zeros): group 1
+// issues its refills unconditionally, so the last two stages request two
+// stages past the end into buffers nobody reads again.
+template <int TMW, class Lay, class LA, class LB, class RA, class RB, class Epi>
+__device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, char* lds, int group, int wm0,
+                                          int wn0, f32x16 (&acc)[TMW][2], RA&& retarget_a, RB&& retarget_b,
+                                          Epi&& epi) {
+    constexpr int kStage = Lay::kStage;
+    constexpr int kBOff = Lay::kBOff;
+    char* st0 = lds;
+    char* st1 = lds + kStage;
+    constexpr int kAI = LA::kInstr, kBI = LB::kInstr;
+    const int S = nk * ntiles;
+
+    u32x4 fa[4][TMW], fb[4][2];
+
+    // The issuing group's next load: stage `ld_kt` of tile `ld_tile`,
+    // advanced by counting (no division in the loop); the loader is pointed
+    // at a new tile when the count wraps.
+    int ld_kt = 0, ld_tile = 0;
+    auto advance = [&](auto&& retarget) {
+        if (++ld_kt == nk) {
+            ld_kt = 0;
+            retarget(++ld_tile);
+        }
+    };
+
+    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
+    if (group == 1) {
+        ap.issue(0, st0);
+        advance(retarget_a);
+        ap.issue(ld_kt, st1);
+        advance(retarget_a);   // next: stage 2
+        wait_vmcnt<kAI>();
+    } else {
+        bp.issue(0, st0 + kBOff);
+        if (S > 1) {
+            advance(retarget_b);
+            bp.issue(ld_kt, st1 + kBOff);
+            wait_vmcnt<kBI>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        advance(retarget_b);   // next: stage 2
+    }
+    pp_barrier();
+
+    if (group == 0) {
+        int s = 0;
+        for (int i = 0; i < ntiles; ++i) {
+            if (i > 0) {
+                // the previous tile's epilogue, before this stage's reads (its
+                // accumulators and the fragments are never live together),
+                // while group 1 multiplies that tile's last stage
+                epi(i - 1, acc);
+                zero_acc_opaque(acc);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            for (int kt = 0; kt < nk; ++kt, ++s) {
+                const char* st = (s & 1) ? st1 : st0;
+                Lay::read(st, wm0, wn0, fa, fb);
+                wait_lgkmcnt0();
+                // B(s+1) goes out after this wave's reads: LDS reads issued
+                // behind a wave's own buffer->LDS loads wait for those loads
+                __builtin_amdgcn_sched_barrier(0);
+                if (s >= 1 && s + 1 < S) {
+                    bp.issue(ld_kt, ((s + 1) & 1 ? st1 : st0) + kBOff);
+                    advance(retarget_b);
+                }
+                pp_barrier();
+                pp_mma<TMW>(fa, fb, acc);
+                __builtin_amdgcn_sched_barrier(0);   // B(s+1) and the epilogue's stores waited for after the MFMAs
+                wait_vmcnt<0>();
+                pp_barrier();
+            }
+        }
+        // phase 2S: group 1 multiplies the last stage, group 0 writes its rows
+        epi(ntiles - 1, acc);
+        pp_barrier();
+        pp_barrier();   // phase 2S+1: group 1's rows
+    } else {
+        pp_barrier();   // phase 0: group 0 reads stage 0
+        int s = 0;
+        for (int i = 0; i < ntiles; ++i) {
+            if (i > 0) {   // group 0 multiplies this tile's first stage
+                epi(i - 1, acc);
+                zero_acc_opaque(acc);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // stage s: read it; multiply it, refilling its buffer with A(s+2)
+            for (int kt = 0; kt < nk; ++kt, ++s) {
+                const char* st = (s & 1) ? st1 : st0;
+                Lay::read(st, wm0, wn0, fa, fb);
+                wait_lgkmcnt0();
+                wait_vmcnt<0>();   // A(s+1), issued in the previous phase, has landed (and the epilogue's stores)
+                const int kt2 = ld_kt;
+                pp_barrier();
+                pp_mma_load<TMW>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
+                __builtin_amdgcn_sched_barrier(0);
+                advance(retarget_a);   // the loader's registers are read at issue, so it may move now
+                pp_barrier();
+            }
+        }
+        epi(ntiles - 1, acc);
+        wait_vmcnt<0>();   // the two loads past the end land before the workgroup's LDS is released
         pp_barrier();
     }
 }

@@ -758,6 +758,110 @@ __global__ __launch_bounds__(Shape::NT) void k_routed_experts(RoutedArgs a) {
     }
 }
 
+// Row tile rt (256 rows) of a K1 partition: expert e and partition rows
+// [r0, r1); e = -1 past the last tile.  A uniform walk over the E segments.
+__device__ __forceinline__ void pps_grouped_rows(const int32_t* offsets, int E, int rt, int& e, int& r0, int& r1) {
+    int acc_tiles = 0;
+    e = -1;
+    r0 = r1 = 0;
+    for (int q = 0; q < E; ++q) {
+        const int b = offsets[q], c = offsets[q + 1] - b;
+        const int nt = (c + 255) >> 8;
+        if (rt < acc_tiles + nt) {
+            e = q;
+            r0 = b + (rt - acc_tiles) * 256;
+            r1 = r0 + 256 < b + c ? r0 + 256 : b + c;
+            return;
+        }
+        acc_tiles += nt;
+    }
+}
+
+// Expert-grouped down (K3's second GEMM) as a persistent ping-pong stream:
+// y[r, :] = (h[r, :] We^T) * scale_e for the partition rows r of expert e's
+// segment, over (row tile, column tile) pairs of 256 x 256.  The row tiles
+// are padded to a multiple of 8 and tile t is row tile (t % 8) + 8 q, column
+// tile j - q n_ct with j = t / 8, q = j / n_ct: the column tiles of a row
+// tile run on one XCD (workgroups go to XCD t % 8), next to each other, so
+// its h rows are read once into that XCD's L2.  Padding tiles load nothing
+// and store nothing.  K (the expert width) is a multiple of 64.
+template <bool FP8>
+__global__ __launch_bounds__(512, 1) void k_down_grouped_pps(DownArgs a) {
+    extern __shared__ __align__(16) char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * 128, wn0 = wig * 64;
+    int n_rt = 0;
+    for (int q = 0; q < a.E; ++q) n_rt += (a.offsets[q + 1] - a.offsets[q] + 255) >> 8;
+    const int n_ct = (a.N + 255) >> 8;
+    const int n_tiles = ((n_rt + 7) & ~7) * n_ct;
+    const int G = (int)gridDim.x;
+    const int ntiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
+    if (ntiles <= 0) return;
+    auto tile = [&](int i, int& e, int& r0, int& r1, int& n0) {
+        const uint32_t t = blockIdx.x + (uint32_t)i * (uint32_t)G;
+        const uint32_t j = t >> 3, q = j / (uint32_t)n_ct;
+        n0 = (int)(j - q * (uint32_t)n_ct) * 256;
+        pps_grouped_rows(a.offsets, a.E, (int)((t & 7) + 8 * q), e, r0, r1);
+        if (i >= ntiles) e = -1;   // past the workgroup's tiles: nothing
+    };
+    const int64_t ldh_b = a.ldh * 2;
+    const int64_t ldw_b = FP8 ? a.ldw : a.ldw * 2;
+    const int64_t wstride_b = a.w_expert_stride * (FP8 ? 1 : 2);
+    auto point_a = [&](auto& ap, int i, bool first) {
+        int e, r0, r1, n0;
+        tile(i, e, r0, r1, n0);
+        if (first)
+            ap.init(a.h, r0, e >= 0 ? r1 : r0, ldh_b, wig);
+        else
+            ap.retarget(a.h, r0, e >= 0 ? r1 : r0, ldh_b);
+    };
+    auto point_b = [&](auto& bp, int i, bool first) {
+        int e, r0, r1, n0;
+        tile(i, e, r0, r1, n0);
+        const char* w = static_cast<const char*>(a.w) + (int64_t)(e < 0 ? 0 : e) * wstride_b;
+        if (first)
+            bp.init(w, n0, e >= 0 ? a.N : n0, ldw_b, wig);
+        else
+            bp.retarget(w, n0, e >= 0 ? a.N : n0, ldw_b);
+    };
+    PPRows<256> ap;
+    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    if (group == 1)
+        point_a(ap, 0, true);
+    else
+        point_b(bp, 0, true);
+    f32x16 acc[4][2];
+    zero_acc<KindBF16>(acc);
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4, true>, PPLayoutK<4, true>>;
+    pp_stream<4, Lay>(
+        ap, bp, a.K / 64, ntiles, lds, group, wm0, wn0, acc, [&](int i) { point_a(ap, i, false); },
+        [&](int i) { point_b(bp, i, false); },
+        [&](int i, const f32x16 (&c)[4][2]) {
+            int e, r0, r1, n0;
+            tile(i, e, r0, r1, n0);
+            if (e < 0) return;
+            int ld2 = (int)a.ldo * 2;
+            asm volatile("" : "+s"(ld2));   // keeps the offsets below out of the caller's loop
+            const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.out) + (int64_t)r0 * a.ldo, (uint32_t)((r1 - r0) * ld2));
+            const int r = threadIdx.x & 31;
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const int col = n0 + wn0 + tn * 32 + r;
+                const float cs = a.shared_scale *
+                                 ((a.w_scale != nullptr && col < a.N) ? a.w_scale[e * a.scale_expert_stride + col] : 1.0f);
+                const int lb = pair_lane_offset(wm0, col, ld2) | (col < a.N ? 0 : kOutOfRange);
+#pragma unroll
+                for (int tm = 0; tm < 4; ++tm) {
+                    float v[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) v[q] = c[tm][tn][q] * cs;
+                    store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+                }
+            }
+        });
+}
+
 // ---------------------------------------------------------------------------
 // k_combine: routed un-permute without a shared branch
 // ---------------------------------------------------------------------------
@@ -1307,8 +1411,23 @@ static int launch_down_grouped_shape(const DownArgs& a, int64_t assignments, hip
     return check_launch("routed_experts (down)");
 }
 
+// Persistent expert-grouped down: one workgroup per CU (K a multiple of 64,
+// bf16 activations, every shape; column and row tails are masked).
+template <bool FP8>
+static int launch_down_grouped_pps(const DownArgs& a, hipStream_t stream) {
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4, true>, PPLayoutK<4, true>>;
+    constexpr int kLds = 2 * Lay::kStage;
+    const int st = ensure_lds(k_down_grouped_pps<FP8>, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL(k_down_grouped_pps<FP8>, dim3((unsigned)device_cus()), dim3(512), kLds, stream, a);
+    return check_launch("routed_experts (down)");
+}
+
 template <class Kind, bool FP8>
 static int down_grouped_kind(const DownArgs& a, int64_t assignments, hipStream_t stream) {
+    if constexpr (std::is_same_v<Kind, KindBF16>) {
+        if (a.K > 0 && a.K % 64 == 0 && a.y == nullptr && a.residual == nullptr) return launch_down_grouped_pps<FP8>(a, stream);
+    }
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     if constexpr (FP8) {
         if (a.N % 256 == 0) return launch_down_grouped_shape<Kind, FP8, ShapeBigF8Dma>(a, assignments, stream);

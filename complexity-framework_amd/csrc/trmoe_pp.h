@@ -500,6 +500,35 @@ __device__ __forceinline__ void zero_acc_opaque(f32x16 (&acc)[TM][TN]) {
             for (int i = 0; i < 16; ++i) acc[tm][tn][i] = z;
 }
 
+// Stores of one 32x32 accumulator block held as bf16 pairs: lane l owns
+// column c = l % 32 and rows acc_row(l, i); rows i, i + 1 (i even) are
+// consecutive, so adjacent lanes swap one value (DPP quad_perm 1,0,3,2) and
+// each lane writes 4 bytes: the even lane columns c, c + 1 of row i, the odd
+// lane columns c - 1, c of row i + 1.  v[i] is the value of row i; `lb` the
+// lane's byte offset of its pair (its row for i = 0, plus 1 for odd lanes,
+// times the row stride, plus 2 (c & ~1)); rows advance by ld2 bytes.
+// Offsets at or past the buffer's range are dropped.
+__device__ __forceinline__ float dpp_swap_pairs(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ int pair_lane_offset(int row0, int col, int ld2) {
+    const int lane = threadIdx.x & 63;
+    return (row0 + 4 * (lane >> 5) + (lane & 1)) * ld2 + (col & ~1) * 2;
+}
+
+__device__ __forceinline__ void store_bf16_pairs(__amdgpu_buffer_rsrc_t rsrc, int lb, int ld2, const float (&v)[16]) {
+    const bool odd = threadIdx.x & 1;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const float v0 = v[2 * p], v1 = v[2 * p + 1];
+        const float other = dpp_swap_pairs(odd ? v0 : v1);
+        const bf16x2 pr = odd ? bf16x2{(bf16_t)other, (bf16_t)v1} : bf16x2{(bf16_t)v0, (bf16_t)other};
+        const int off = lb + (8 * (p >> 1) + 2 * (p & 1)) * ld2;   // row acc_row(lane, 2 p) - acc_row(lane, 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, pr), rsrc, off, 0, 0);
+    }
+}
+
 // Persistent form of pp_main.  The workgroup's ntiles tiles (nk K stages
 // each) run as one stream of stages s = nk * i + kt through the same two LDS
 // buffers, phase schedule and refill rules, so the next tile's first stages

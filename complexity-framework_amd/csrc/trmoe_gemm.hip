@@ -862,6 +862,85 @@ __global__ __launch_bounds__(512, 1) void k_down_grouped_pps(DownArgs a) {
         });
 }
 
+// Expert-grouped gate|up + SwiGLU (K3's first GEMM) as a persistent
+// ping-pong stream: h[r, :] = SwiGLU(x[gather[r] % gather_mod] We_gu^T) for
+// the partition rows r of expert e's segment, over (row tile, packed column
+// tile) pairs of 256 x 256 in the order of k_down_grouped_pps.  When group 1
+// moves to a new tile each of its lanes loads one tile row's gather index
+// and keeps that row's byte offset in LDS (s_goff); rows past the segment
+// and padding tiles load zeros, and their h rows are not written.  The
+// packed gate|up rows per expert are a multiple of 256; no row scales.
+template <bool FP8>
+__global__ __launch_bounds__(512, 1) void k_gate_up_grouped_pps(GateUpArgs a) {
+    extern __shared__ __align__(16) char lds[];
+    __shared__ int s_goff[256];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * 128, wn0 = wig * 64;
+    int n_rt = 0;
+    for (int q = 0; q < a.E; ++q) n_rt += (a.offsets[q + 1] - a.offsets[q] + 255) >> 8;
+    const int n_ct = (int)(a.w_expert_stride / a.ldw) >> 8;   // packed rows per expert / 256
+    const int n_tiles = ((n_rt + 7) & ~7) * n_ct;
+    const int G = (int)gridDim.x;
+    const int ntiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
+    if (ntiles <= 0) return;
+    auto tile = [&](int i, int& e, int& r0, int& r1, int& n0) {
+        const uint32_t t = blockIdx.x + (uint32_t)i * (uint32_t)G;
+        const uint32_t j = t >> 3, q = j / (uint32_t)n_ct;
+        n0 = (int)(j - q * (uint32_t)n_ct) * 256;
+        pps_grouped_rows(a.offsets, a.E, (int)((t & 7) + 8 * q), e, r0, r1);
+        if (i >= ntiles) e = -1;
+    };
+    const int64_t ldx_b = a.ldx * 2;
+    const int64_t ldw_b = FP8 ? a.ldw : a.ldw * 2;
+    const int64_t wstride_b = a.w_expert_stride * (FP8 ? 1 : 2);
+    // group 1: the x byte offsets of tile i's rows into s_goff (one row per lane)
+    auto gather_rows = [&](int i) {
+        int e, r0, r1, n0;
+        tile(i, e, r0, r1, n0);
+        const int r = (int)threadIdx.x - 256;
+        int off = kOutOfRange;
+        if (e >= 0 && r0 + r < r1) {
+            const int64_t v = a.gather[r0 + r];
+            const int64_t t = (int64_t)((uint64_t)v % (uint64_t)a.gather_mod);
+            off = (int)(t * ldx_b);
+        }
+        s_goff[r] = off;
+    };
+    auto point_b = [&](auto& bp, int i, bool first) {
+        int e, r0, r1, n0;
+        tile(i, e, r0, r1, n0);
+        const char* w = static_cast<const char*>(a.w) + (int64_t)(e < 0 ? 0 : e) * wstride_b;
+        if (first)
+            bp.init(w, n0, e >= 0 ? n0 + 256 : n0, ldw_b, wig);
+        else
+            bp.retarget(w, n0, e >= 0 ? n0 + 256 : n0, ldw_b);
+    };
+    PPGather ap;
+    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    if (group == 1) {
+        ap.init(a.x, a.gather_mod * ldx_b, s_goff, wig);
+        gather_rows(0);
+    } else {
+        point_b(bp, 0, true);
+    }
+    f32x16 acc[4][2];
+    zero_acc<KindBF16>(acc);
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4, true>, PPLayoutK<4, true>>;
+    pp_stream<4, Lay>(
+        ap, bp, a.K / 64, ntiles, lds, group, wm0, wn0, acc, [&](int i) { gather_rows(i); },
+        [&](int i) { point_b(bp, i, false); },
+        [&](int i, const f32x16 (&c)[4][2]) {
+            int e, r0, r1, n0;
+            tile(i, e, r0, r1, n0);
+            if (e < 0) return;
+            GateUpArgs t = a;
+            t.M = r1;
+            if (t.w_scale) t.w_scale += (int64_t)e * a.scale_expert_stride;
+            gate_up_epi_direct<4>(t, c, r0, n0, wm0, wn0);
+        });
+}
+
 // ---------------------------------------------------------------------------
 // k_combine: routed un-permute without a shared branch
 // ---------------------------------------------------------------------------
@@ -1377,8 +1456,26 @@ static int launch_gate_up_grouped_shape(const GateUpArgs& a, int64_t assignments
     return check_launch("routed_experts (gate|up)");
 }
 
+// Persistent expert-grouped gate|up: one workgroup per CU (bf16 activations,
+// K a multiple of 64, packed rows per expert a multiple of 256, gathered
+// rows, no row scales).
+template <bool FP8>
+static int launch_gate_up_grouped_pps(const GateUpArgs& a, hipStream_t stream) {
+    using Lay = std::conditional_t<FP8, PPLayoutF8<4, true>, PPLayoutK<4, true>>;
+    constexpr int kLds = 2 * Lay::kStage;
+    const int st = ensure_lds(k_gate_up_grouped_pps<FP8>, kLds);
+    if (st) return st;
+    hipLaunchKernelGGL(k_gate_up_grouped_pps<FP8>, dim3((unsigned)device_cus()), dim3(512), kLds, stream, a);
+    return check_launch("routed_experts (gate|up)");
+}
+
 template <class Kind, bool FP8>
 static int gate_up_grouped_kind(const GateUpArgs& a, int64_t assignments, int64_t packed_rows, hipStream_t stream) {
+    if constexpr (std::is_same_v<Kind, KindBF16>) {
+        if (a.K > 0 && a.K % 64 == 0 && packed_rows % 256 == 0 && a.gather != nullptr && a.row_scale == nullptr &&
+            a.rms_eps == 0.0f && a.gu == nullptr && a.w_expert_stride == packed_rows * a.ldw)
+            return launch_gate_up_grouped_pps<FP8>(a, stream);
+    }
     const bool wide = packed_rows % 256 == 0;
     if constexpr (FP8) {
         if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBigF8Dma>(a, assignments, packed_rows, stream);

@@ -79,6 +79,39 @@ struct PPRows {
     }
 };
 
+// Gathered activation rows for group 1's loads: 256 tile rows, tile row r
+// read from byte offset goff[r] of the whole operand (kOutOfRange: zeros).
+// goff lives in LDS; the lanes of wave_in_group w load and own rows
+// 64 w .. 64 w + 63, so a wave only reads offsets it wrote itself.
+struct PPGather {
+    static constexpr int kInstr = 8;
+    __amdgpu_buffer_rsrc_t rsrc;
+    const int* goff;
+    int row0;   // 64 wave_in_group + lane / 8
+    int c0;     // (lane % 8) ^ (lane / 8)
+    int wig;
+
+    __device__ __forceinline__ void init(const void* base, int64_t bytes, const int* goff_lds, int wave_in_group) {
+        rsrc = make_rsrc(base, (uint32_t)bytes);
+        goff = goff_lds;
+        const int lane = threadIdx.x & 63;
+        wig = wave_in_group;
+        row0 = 64 * wave_in_group + (lane >> 3);
+        c0 = ((lane & 7) ^ (lane >> 3)) & 7;
+    }
+    __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
+        const int chunk = (c0 ^ (kInstr * wig + j)) & 7;
+        const int g = goff[row0 + 8 * j];
+        const int o = g < 0 ? kOutOfRange : g + kt * kRowBytes + (chunk << 4);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (kInstr * wig + j) * 8 * kRowBytes), 16,
+                                                o, 0, 0, 0);
+    }
+    __device__ __forceinline__ void issue(int kt, char* dst) const {
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) issue_one(j, kt, dst);
+    }
+};
+
 template <bool V>
 struct BoolC {
     static constexpr bool value = V;

@@ -397,6 +397,9 @@ def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
     dout = (torch.randn(x.shape, device=x.device) * 0.1).to(x.dtype)
 
     def step():
+        # a training step starts from cleared gradients (no accumulation kernels)
+        engine.zero_grad(set_to_none=True)
+        xg.grad = None
         out = engine(xg, ids)
         out.backward(dout)
 

@@ -248,6 +248,90 @@ __device__ __forceinline__ void mma_stage_tr(const char* As, const char* Bs, int
 using ShapeBwdGU = TileShape<256, 256, 2, 4, 4>;   // packed gate|up columns of 128 features
 using ShapeBwdDH = TileShape<256, 128, 2, 4, 4>;   // the same 128 features of dh
 
+// Epilogue of the saved-g|u bf16 SwiGLU backward without LDS: lanes pair up
+// (DPP swap of one dh value, as in store_bf16_pairs) so that each lane owns
+// two adjacent features of one row, read as 4-byte pairs from the saved
+// gate|up rows; dg, du (packed gate|up column order) and hm leave as 4-byte
+// pairs.  Rows past the tile's end fall past the buffers' ranges; features
+// past F get out-of-range offsets.
+template <bool ROUTED>
+__device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f32x16 (&acc)[4][1], int64_t m0,
+                                                 int64_t m_end, int64_t f0, int wm0, int wf0,
+                                                 const int (*s_route)[kMaxTopK]) {
+    const int lane = threadIdx.x & 63;
+    const bool odd = lane & 1;
+    const int64_t fb = (f0 + wf0 + (lane & 31)) & ~(int64_t)1;   // first feature of the lane's pair
+    const int pc2 = (int)(64 * (fb >> 5) + (fb & 31)) * 2;       // its packed gate column, in bytes
+    const int rows = (int)(m_end - m0 < 256 ? m_end - m0 : 256);
+    const int ldg2 = (int)a.ldgu * 2, ldd2 = (int)a.lddgu * 2, ldh2 = (int)a.ldhm * 2;
+    const auto rg = make_rsrc(static_cast<const bf16_t*>(a.gu) + m0 * a.ldgu, (uint32_t)(rows * ldg2));
+    const auto rd = make_rsrc(static_cast<bf16_t*>(a.dgu) + m0 * a.lddgu, (uint32_t)(rows * ldd2));
+    const auto rh = make_rsrc(a.hm != nullptr ? static_cast<bf16_t*>(a.hm) + m0 * a.ldhm : a.dgu,
+                              a.hm != nullptr ? (uint32_t)(rows * ldh2) : 0u);
+    const int bad = fb < a.F ? 0 : kOutOfRange;
+    // a 32-feature block is wholly shared or wholly one expert's
+    const bool routed = ROUTED && f0 + wf0 >= a.shared_feats;
+    const int expert = routed ? (int)((f0 + wf0 - a.shared_feats) / a.expert_feats) : -1;
+    const int row_lane = wm0 + 4 * (lane >> 5) + (lane & 1);   // the pair's row for i = 0, 1
+    uint32_t gv[2][8], uv[2][8];
+    auto load = [&](int tm, int buf) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int rl = row_lane + tm * 32 + 8 * (p >> 1) + 2 * (p & 1);
+            const int off = (rl * ldg2 + pc2) | bad;
+            gv[buf][p] = __builtin_amdgcn_raw_buffer_load_b32(rg, off, 0, 0);
+            uv[buf][p] = __builtin_amdgcn_raw_buffer_load_b32(rg, off + 64, 0, 0);
+        }
+    };
+    load(0, 0);
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+        if (tm + 1 < 4) load(tm + 1, (tm + 1) & 1);
+        const int buf = tm & 1;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int rl = row_lane + tm * 32 + 8 * (p >> 1) + 2 * (p & 1);
+            const float v0 = acc[tm][0][2 * p], v1 = acc[tm][0][2 * p + 1];
+            const float other = dpp_swap_pairs(odd ? v0 : v1);
+            const float dh[2] = {odd ? other : v0, odd ? v1 : other};   // features fb, fb + 1 of row rl
+            float mult = a.shared_mult;
+            if constexpr (ROUTED) {
+                if (routed) {
+                    float tw = 0.f;
+#pragma unroll
+                    for (int j = 0; j < kMaxTopK; ++j) tw += (s_route[rl][j] == expert) ? a.rw[j] : 0.f;
+                    mult = tw;
+                }
+            }
+            const bf16x2 g2 = __builtin_bit_cast(bf16x2, gv[buf][p]);
+            const bf16x2 u2 = __builtin_bit_cast(bf16x2, uv[buf][p]);
+            float dg[2], du[2], hv[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float g = (float)g2[q], u = (float)u2[q];
+                const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+                const float sg = __builtin_amdgcn_rcpf(1.0f + e);   // sigmoid(g)
+                const float sl = g * sg;                            // silu(g)
+                const float dm = dh[q] * mult;
+                dg[q] = dm * u * (sg + sl * (1.0f - sg));           // silu'(g) = s + g s (1 - s)
+                du[q] = dm * sl;
+                // the forward epilogue's expression order, so hm is its h
+                hv[q] = (routed ? sl * u : sl * u * a.shared_mult);
+                if (routed) hv[q] *= mult;
+            }
+            const int od = (rl * ldd2 + pc2) | bad;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, bf16x2{(bf16_t)dg[0], (bf16_t)dg[1]}),
+                                                  rd, od, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, bf16x2{(bf16_t)du[0], (bf16_t)du[1]}),
+                                                  rd, od + 64, 0, 0);
+            if (a.hm != nullptr)
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __builtin_bit_cast(uint32_t, bf16x2{(bf16_t)hv[0], (bf16_t)hv[1]}), rh,
+                    (rl * ldh2 + (int)fb * 2) | bad, 0, 0);
+        }
+    }
+}
+
 // SAVED: g|u come from a.gu (written by the forward) instead of a
 // recomputing tile loop.
 template <class Kind, bool GROUPED, bool ROUTED, bool SAVED = false>
@@ -311,6 +395,10 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
     f32x16 acc_dh[SD::TM][SD::TN];
     zero_acc<Kind>(acc_dh);
     tile_loop<Kind, SD>(ad, bdt, a.K, lds, wm0, wf0, acc_dh);
+    if constexpr (SAVED && sizeof(T) == 2 && !GROUPED) {
+        swiglu_bwd_pairs<ROUTED>(a, acc_dh, m0, m_end, f0, wm0, wf0, s_route);
+        return;
+    }
     // bf16 saved g|u: the tile's 256 rows x 256 packed columns (128 KiB)
     // staged in LDS (free after the loop) with direct loads, as four 64-column
     // stages, then read back in the accumulator layout

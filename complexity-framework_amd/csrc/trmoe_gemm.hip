@@ -377,10 +377,11 @@ __device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, bool xcd_
 
 // SwiGLU of one finished tile straight from the accumulators of the calling
 // wave (no LDS): each lane owns one h feature (its gate column r of the
-// wave's 64 packed rows, up column 32 + r) and 16 rows per 32-row block, one
-// 2-byte store per value.  The offset is a per-lane part plus a row part, and
-// rows at or past M fall past the buffer's range and are dropped.
-template <int TMW>
+// wave's 64 packed rows, up column 32 + r) and 16 rows per 32-row block;
+// PAIRS: adjacent lanes pair their values into 4-byte stores
+// (store_bf16_pairs), else one 2-byte store per value.  Rows at or past M
+// fall past the buffer's range and are dropped.
+template <int TMW, bool PAIRS = true>
 __device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
                                                    int64_t n0, int wm0, int wn0) {
     const int lane = threadIdx.x & 63, r = lane & 31;
@@ -390,21 +391,34 @@ __device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f3
     const float su = (a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f) * a.shared_mult;
     const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
     // the row stride is redefined here so that no offset below is hoisted
-    // out of a caller's loop (64 of them would stay live across every stage)
+    // out of a caller's loop (they would stay live across every stage)
     int ld2 = (int)a.ldh * 2;
     asm volatile("" : "+s"(ld2));
     const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.h) + m0 * a.ldh, (uint32_t)(mlim * ld2));
-    const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + (int)((pbase >> 1) + r) * 2;
+    const int col = (int)((pbase >> 1) + r);
+    if constexpr (PAIRS) {
+        const int lb = pair_lane_offset(wm0, col, ld2);
 #pragma unroll
-    for (int tm = 0; tm < TMW; ++tm)
+        for (int tm = 0; tm < TMW; ++tm) {
+            float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;   // row wm0 + tm*32 + acc_row(lane, i)
-            const float g = acc[tm][0][i] * sg;
-            const float u = acc[tm][1][i] * su;
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<bf16_t>(silu_f(g) * u)),
-                                                  rsrc, off, 0, 0);
+            for (int i = 0; i < 16; ++i) v[i] = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
+            store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
         }
+    } else {
+        // one 2-byte store per value (fewer live registers: the e4m3 kernels
+        // keep their loader state out of scratch this way)
+        const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + col * 2;
+#pragma unroll
+        for (int tm = 0; tm < TMW; ++tm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;   // row wm0 + tm*32 + acc_row(lane, i)
+                const float hv = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<bf16_t>(hv)), rsrc, off,
+                                                      0, 0);
+            }
+    }
 }
 
 // gate_up_save for the persistent kernel: the raw gate|up outputs of the
@@ -422,15 +436,14 @@ __device__ __forceinline__ void gate_up_save_direct(const GateUpArgs& a, const f
     for (int tn = 0; tn < 2; ++tn) {
         const int64_t col = n0 + wn0 + tn * 32 + r;
         const float sc = a.w_scale ? a.w_scale[col] : 1.0f;
-        const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + (int)col * 2;
+        const int lb = pair_lane_offset(wm0, (int)col, ld2);
 #pragma unroll
-        for (int tm = 0; tm < TMW; ++tm)
+        for (int tm = 0; tm < TMW; ++tm) {
+            float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;
-                __builtin_amdgcn_raw_buffer_store_b16(
-                    __builtin_bit_cast(uint16_t, from_f32<bf16_t>(acc[tm][tn][i] * sc)), rsrc, off, 0, 0);
-            }
+            for (int i = 0; i < 16; ++i) v[i] = acc[tm][tn][i] * sc;
+            store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+        }
     }
 }
 
@@ -490,7 +503,7 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
             int64_t tm0, tn0;
             coords(i, tm0, tn0);
             if constexpr (SAVE) gate_up_save_direct<TMW>(a, c, tm0, tn0, wm0, wn0);
-            gate_up_epi_direct<TMW>(a, c, tm0, tn0, wm0, wn0);
+            gate_up_epi_direct<TMW, !FP8>(a, c, tm0, tn0, wm0, wn0);
         });
 }
 
@@ -937,7 +950,7 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_grouped_pps(GateUpArgs a) {
             GateUpArgs t = a;
             t.M = r1;
             if (t.w_scale) t.w_scale += (int64_t)e * a.scale_expert_stride;
-            gate_up_epi_direct<4>(t, c, r0, n0, wm0, wn0);
+            gate_up_epi_direct<4, !FP8>(t, c, r0, n0, wm0, wn0);
         });
 }
 

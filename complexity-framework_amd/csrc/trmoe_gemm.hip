@@ -359,16 +359,22 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
 }
 
 // Tile i of a persistent launch over tiles_m x tiles_n tiles -> (row tile,
-// column tile).  Workgroups are dispatched to the 8 XCDs round-robin, so the
-// 32 workgroups of an XCD that run concurrently get a block of tiles_m / 8
-// consecutive row tiles (their activation rows stay in that XCD's L2 for the
-// whole launch) times the next few column tiles; other shapes walk row tiles
-// first.
-__device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, bool xcd_rows, uint32_t& mt, uint32_t& nt) {
+// column tile).  Workgroups are dispatched to the 8 XCDs round-robin, so tile
+// i runs on XCD i % 8.  With xcd_rows, XCD x owns the row tiles
+// [x mpx, x mpx + mpx), mpx = tiles_m / 8, and walks them in groups of bm
+// (4 when mpx allows): row fastest within a group, then every column tile,
+// then the next group.  The 32 workgroups of an XCD that run together then
+// hold bm row panels x 32 / bm column panels (4 x 8), which read each K slice
+// of 12 panels per round instead of 18 for 16 x 2.  Other shapes walk row
+// tiles first.
+__device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, uint32_t tiles_n, bool xcd_rows,
+                                         uint32_t& mt, uint32_t& nt) {
     if (xcd_rows) {
         const uint32_t mpx = tiles_m >> 3, j = i >> 3;
-        nt = j / mpx;
-        mt = (i & 7) * mpx + (j - nt * mpx);
+        const uint32_t bm = (mpx & 3) == 0 ? 4 : ((mpx & 1) == 0 ? 2 : 1);
+        const uint32_t rest = j / bm, mg = rest / tiles_n;
+        nt = rest - mg * tiles_n;
+        mt = (i & 7) * mpx + mg * bm + (j - rest * bm);
     } else {
         nt = i / tiles_m;
         mt = i - nt * tiles_m;
@@ -465,7 +471,8 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
     const bool xcd_rows = (tiles_m & 7) == 0 && (G & 7) == 0;
     auto coords = [&](int i, int64_t& m0, int64_t& n0) {
         uint32_t mt, nt;
-        pps_tile((uint32_t)blockIdx.x + (uint32_t)i * (uint32_t)G, (uint32_t)tiles_m, xcd_rows, mt, nt);
+        pps_tile((uint32_t)blockIdx.x + (uint32_t)i * (uint32_t)G, (uint32_t)tiles_m, (uint32_t)(n_tiles / tiles_m),
+                 xcd_rows, mt, nt);
         m0 = (int64_t)mt * BM;
         n0 = a.n_base + (int64_t)nt * 256;
     };

@@ -595,14 +595,16 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
     norm_eps: the layer runs on rmsnorm(x) (the packs must hold the gate/up
     weights times the norm weight); the per-token scales come from the decode
     kernels themselves up to 128 tokens (dense strategy), else from
-    rms_row_scale."""
+    rms_row_scale.  save: returns (out, gu, h): the raw gate|up outputs and,
+    for the dense strategy, the down GEMM's input h (else None), which the
+    backward reuses."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
     if save and packed.fp8:
         raise ValueError("layer_forward: e4m3 weights are inference-only (no saved pre-activations, no backward)")
     if n == 0:
         out = torch.empty(0, hidden, dtype=x.dtype, device=x.device)
-        return (out, None) if save else out
+        return (out, None, None) if save else out
     x = rows16(x)
     gu = None
     rscale, eps_in = None, 0.0
@@ -625,7 +627,7 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
         out = shared_down_combine(h, packed.dense_features, packed.dense_down, None, hidden, None, None,
                                   top_k, route_weights, 1.0, 1.0, residual,
                                   w_frag=packed.fragments("dense_down", packed.dense_features) if decode else None)
-        return (out, gu) if save else out
+        return (out, gu, h) if save else out
     sorted_idx, inverse, offsets, _ = route_sort(token_ids, route_table, packed.num_experts, order)
     y = routed_experts(x, sorted_idx, offsets, packed.num_experts, top_k, packed.expert_gate_up,
                        packed.expert_gate_up_scale, packed.expert_down, packed.expert_down_scale,
@@ -642,7 +644,7 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
                                   w_frag=packed.fragments("shared_down", packed.shared_width) if decode else None)
     else:
         out = combine(y, inverse, n, top_k, route_weights, routed_scale, residual)
-    return (out, gu) if save else out
+    return (out, gu, None) if save else out
 
 
 # ---------------------------------------------------------------------------
@@ -702,8 +704,10 @@ def shared_swiglu_backward(x: torch.Tensor, dout: torch.Tensor, w_gate_up: torch
 
 
 def dense_routed_swiglu_backward(x, dout, w_gate_up, w_down_t, shared_width, num_experts, expert_width,
-                                 token_ids, route_table, route_weights, shared_scale, routed_scale, gu=None):
-    """(dgu[N, 2F], hm[N, F]) over the dense-routed features."""
+                                 token_ids, route_table, route_weights, shared_scale, routed_scale, gu=None,
+                                 want_hm: bool = True):
+    """(dgu[N, 2F], hm[N, F]) over the dense-routed features; hm is None
+    (not computed) without want_hm."""
     lib = _lib()
     _require_cuda(x, dout, w_gate_up, w_down_t, token_ids, route_table)
     n, hidden = x.shape
@@ -712,7 +716,7 @@ def dense_routed_swiglu_backward(x, dout, w_gate_up, w_down_t, shared_width, num
     ids = (ids if ids.dtype == torch.int64 else ids.to(torch.int64)).contiguous()
     table = route_table.contiguous()
     dgu = torch.empty(n, 2 * F_, dtype=x.dtype, device=x.device)
-    hm = torch.empty(n, F_, dtype=x.dtype, device=x.device)
+    hm = torch.empty(n, F_, dtype=x.dtype, device=x.device) if want_hm else None
     rw = _weights_arg(route_weights)
     st = lib.trmoe_dense_routed_swiglu_backward(dtype_code(x.dtype), _p(x), _p(dout), n, hidden, x.stride(0),
                                                 dout.stride(0), _p(w_gate_up), _p(w_down_t), shared_width,
@@ -759,6 +763,65 @@ def weight_grad(a: torch.Tensor, b: torch.Tensor, m: int, n: int, n_rows: int, a
                                _p(ws), ws_bytes, _stream(a))
     N.check(st, "trmoe_weight_grad")
     return out
+
+
+def weight_grad_mapped(a: torch.Tensor, b: torch.Tensor, m: int, n: int, n_rows: int, mode: int,
+                       map_off: torch.Tensor, map_stride: torch.Tensor, out: torch.Tensor) -> None:
+    """sum_t a[t, i] * b[t, j] over rows t < n_rows written into `out` (flat,
+    bf16) at map_off[i] + j * map_stride[i] (mode 1) or map_off[j] + i *
+    map_stride[j] (mode 2); negative offsets are skipped."""
+    lib = _lib()
+    _require_cuda(a, b, map_off, map_stride, out)
+    ws_bytes = lib.trmoe_weight_grad_mapped_workspace_bytes(dtype_code(a.dtype), m, n, n_rows)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device)
+    st = lib.trmoe_weight_grad_mapped(dtype_code(a.dtype), _p(a), a.stride(0), a.shape[0], _p(b), b.stride(0),
+                                      b.shape[0], m, n, n_rows, mode, _p(map_off), _p(map_stride), _p(out), _p(ws),
+                                      ws_bytes, _stream(a))
+    N.check(st, "trmoe_weight_grad_mapped")
+
+
+# Destination maps of the dense strategy's two weight gradients into one flat
+# buffer holding the six parameter gradients contiguously: shared_gate,
+# shared_up [S, H], shared_down [H, S], expert_gate, expert_up [E, H, W],
+# expert_down [E, W, H].  Cached per shape and device.
+_DENSE_GRAD_MAPS: dict = {}
+
+
+def _dense_grad_maps(S: int, E: int, W: int, hidden: int, device):
+    key = (S, E, W, hidden, str(device))
+    hit = _DENSE_GRAD_MAPS.get(key)
+    if hit is not None:
+        return hit
+    s_pad, w_pad = _round_up(S, 128), _round_up(W, 64)
+    F_ = s_pad + E * w_pad
+    sh, ew = S * hidden, E * W * hidden
+    o_gate, o_up, o_sd = 0, sh, 2 * sh
+    o_eg, o_eu, o_ed = 3 * sh, 3 * sh + ew, 3 * sh + 2 * ew
+    # dWgu rows: packed gate|up row p of feature f = 32 (p // 64) + p % 32
+    p = torch.arange(2 * F_, dtype=torch.int64)
+    f = 32 * (p // 64) + p % 32
+    up = (p // 32) % 2 == 1
+    fe = f - s_pad
+    e, j = fe.div(w_pad, rounding_mode="floor"), fe % w_pad
+    shared, expert = f < S, (f >= s_pad) & (j < W)
+    roff = torch.full_like(p, -1)
+    rstride = torch.ones_like(p)
+    roff[shared] = torch.where(up, o_up, o_gate)[shared] + f[shared] * hidden
+    roff[expert] = torch.where(up, o_eu, o_eg)[expert] + e[expert] * hidden * W + j[expert]
+    rstride[expert] = W
+    # dWd columns: feature f of the down weight [H, F]
+    c = torch.arange(F_, dtype=torch.int64)
+    ce, cj = (c - s_pad).div(w_pad, rounding_mode="floor"), (c - s_pad) % w_pad
+    cshared, cexpert = c < S, (c >= s_pad) & (cj < W)
+    coff = torch.full_like(c, -1)
+    cstride = torch.ones_like(c)
+    coff[cshared] = o_sd + c[cshared]
+    cstride[cshared] = S
+    coff[cexpert] = o_ed + ce[cexpert] * W * hidden + cj[cexpert] * hidden
+    maps = (roff.to(device), rstride.to(device), coff.to(device), cstride.to(device),
+            (o_gate, o_up, o_sd, o_eg, o_eu, o_ed, 3 * sh + 3 * ew))
+    _DENSE_GRAD_MAPS[key] = maps
+    return maps
 
 
 def grouped_linear(h: torch.Tensor, k: int, offsets: torch.Tensor, num_experts: int, w_packed: torch.Tensor,
@@ -858,10 +921,12 @@ def _gate_up_rows(g: torch.Tensor, features: int):
 def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor,
                    packed: PackedLayer, bwd: BackwardPacks, route_weights: Sequence[float], shared_scale: float,
                    routed_scale: float, order: int = ORDER_TOKEN, need_dx: bool = True, need_dw: bool = True,
-                   saved_gu: Optional[torch.Tensor] = None):
+                   saved_gu: Optional[torch.Tensor] = None, saved_h: Optional[torch.Tensor] = None):
     """Gradients of layer_forward: (dx[N, H] or None, grads) with grads a dict of
     shared_gate/shared_up [S, H], shared_down [H, S], expert_gate/expert_up
-    [E, H, W], expert_down [E, W, H] (active sizes; None when not needed)."""
+    [E, H, W], expert_down [E, W, H] (active sizes; None when not needed).
+    saved_gu / saved_h: what layer_forward(save=True) returned (the dense
+    strategy's down weight gradient then reads the forward's h)."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
     E, W, S = packed.num_experts, packed.expert_width, packed.shared_width
@@ -874,17 +939,43 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
     if packed.strategy == STRATEGY_DENSE:
         F_ = packed.dense_features
         dgu, hm = dense_routed_swiglu_backward(x, dout, packed.dense_gate_up, bwd.dense_down_t, S, E, W, token_ids,
-                                               route_table, route_weights, shared_scale, routed_scale, gu=saved_gu)
+                                               route_table, route_weights, shared_scale, routed_scale, gu=saved_gu,
+                                               want_hm=need_dw and saved_h is None)
+        if saved_h is not None:
+            hm = saved_h
         # the gate|up weight gradient (side stream) overlaps dx and dWd
         side = _OnSide(x.device, (dgu, x))
+        # bf16: both weight gradients go straight into one flat buffer in the
+        # parameters' layouts (their views are the gradients, no copies)
+        mapped = need_dw and x.dtype == torch.bfloat16
+        if mapped:
+            roff, rstride, coff, cstride, offs = _dense_grad_maps(S, E, W, hidden, x.device)
+            flat = torch.empty(offs[-1], dtype=x.dtype, device=x.device)
         if need_dw:
             with side:
-                dwgu = weight_grad(dgu, x, 2 * F_, hidden, n)[0]     # [2F, H]
-                side.outputs.append(dwgu)
+                if mapped:
+                    weight_grad_mapped(dgu, x, 2 * F_, hidden, n, 1, roff, rstride, flat)
+                    side.outputs.append(flat)
+                else:
+                    dwgu = weight_grad(dgu, x, 2 * F_, hidden, n)[0]     # [2F, H]
+                    side.outputs.append(dwgu)
         dx = None
         if need_dx:
             dx = shared_down_combine(dgu, 2 * F_, bwd.dense_gate_up_t, None, hidden, None, None, top_k,
                                      (1.0,) * top_k, 1.0, 1.0)
+        if mapped:
+            weight_grad_mapped(dout, hm, hidden, F_, n, 2, coff, cstride, flat)
+            side.join()
+            o_gate, o_up, o_sd, o_eg, o_eu, o_ed, _ = offs
+            sh, ew = S * hidden, E * W * hidden
+            if S:
+                grads["shared_gate"] = flat[o_gate:o_gate + sh].view(S, hidden)
+                grads["shared_up"] = flat[o_up:o_up + sh].view(S, hidden)
+                grads["shared_down"] = flat[o_sd:o_sd + sh].view(hidden, S)
+            grads["expert_gate"] = flat[o_eg:o_eg + ew].view(E, hidden, W)
+            grads["expert_up"] = flat[o_eu:o_eu + ew].view(E, hidden, W)
+            grads["expert_down"] = flat[o_ed:o_ed + ew].view(E, W, hidden)
+            return dx, grads
         if need_dw:
             dwd = weight_grad(dout, hm, hidden, F_, n)[0]            # [H, F]
             side.join()

@@ -6,7 +6,9 @@ Function per kernel (``CGGRGroupedGEMM``, ``HashCGGRGroupedGEMM``,
 nn.Linear autograd for the shared branch (engine.py:333-349).  Here the whole
 layer is one Function: the forward runs the HIP kernels of
 ``ops.layer_forward`` and saves x and, above decode token counts, the raw
-gate|up GEMM outputs (at decode sizes the backward kernel recomputes them);
+gate|up GEMM outputs and (dense strategy) the down GEMM's input h, which
+the down weight gradient reads (at decode sizes the backward kernel
+recomputes them);
 the backward runs
 ``ops.layer_backward``: the SwiGLU backward kernel, the data gradient through
 the down/combine kernels (the routed rows summed per token through the
@@ -60,18 +62,18 @@ class HIPLayerFunction(torch.autograd.Function):
         out = ops.layer_forward(x, plan.token_ids, plan.route_table, plan.packed, plan.route_weights,
                                 plan.shared_scale, plan.routed_scale, order=plan.order, residual=residual,
                                 save=save)
-        gu = None
+        gu = h = None
         if save:
-            out, gu = out
+            out, gu, h = out
         ctx.plan = plan
         ctx.has_residual = residual is not None
         ctx.param_shapes = [None if p is None else (p.shape, p.dtype) for p in params]
-        ctx.save_for_backward(x, gu)
+        ctx.save_for_backward(x, gu, h)
         return out
 
     @staticmethod
     def backward(ctx, dout: torch.Tensor):
-        x, gu = ctx.saved_tensors
+        x, gu, h = ctx.saved_tensors
         plan: _LayerPlan = ctx.plan
         need_dx = ctx.needs_input_grad[1]
         need_dres = ctx.has_residual and ctx.needs_input_grad[2]
@@ -79,7 +81,7 @@ class HIPLayerFunction(torch.autograd.Function):
         need_dw = any(need_params)
         dx, grads = ops.layer_backward(dout, x, plan.token_ids, plan.route_table, plan.packed, plan.bwd_packs(),
                                        plan.route_weights, plan.shared_scale, plan.routed_scale, order=plan.order,
-                                       need_dx=need_dx, need_dw=need_dw, saved_gu=gu)
+                                       need_dx=need_dx, need_dw=need_dw, saved_gu=gu, saved_h=h)
         E, W = plan.active
         out_params = []
         for name, need, meta in zip(_PARAM_NAMES, need_params, ctx.param_shapes):

@@ -918,6 +918,54 @@ int trmoe_weight_grad(int act_dtype, const void* a, int64_t lda, int64_t a_rows,
     return launch_wgrad(act_dtype, w, as_stream(stream));
 }
 
+size_t trmoe_weight_grad_mapped_workspace_bytes(int act_dtype, int64_t m, int64_t n, int64_t n_rows) {
+    if (act_dtype != TRMOE_BF16 || m <= 0 || n <= 0 || n_rows < 0) return 0;
+    const int splits = wgrad_splits(m, n, 1, n_rows);
+    return (size_t)splits * m * n * sizeof(float);
+}
+
+int trmoe_weight_grad_mapped(int act_dtype, const void* a, int64_t lda, int64_t a_rows, const void* b, int64_t ldb,
+                             int64_t b_rows, int64_t m, int64_t n, int64_t n_rows, int map_mode,
+                             const int64_t* map_off, const int64_t* map_stride, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_BF16, "weight_grad_mapped: bf16 only");
+    TRMOE_REQUIRE(m > 0 && n > 0 && n_rows >= 0, "weight_grad_mapped: bad dimensions");
+    TRMOE_REQUIRE(m % 8 == 0 && n % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0,
+                  "weight_grad_mapped: m, n, lda and ldb must be multiples of 8");
+    TRMOE_REQUIRE(lda >= m && ldb >= n, "weight_grad_mapped: bad leading dimension");
+    TRMOE_REQUIRE(map_mode == 1 || map_mode == 2, "weight_grad_mapped: map_mode must be 1 (rows) or 2 (columns)");
+    TRMOE_REQUIRE(a && b && out && map_off && map_stride && workspace, "weight_grad_mapped: null pointer");
+    TRMOE_REQUIRE(aligned16(a) && aligned16(b) && aligned16(workspace),
+                  "weight_grad_mapped: operands and workspace must be 16-byte aligned");
+    if (a_rows * lda * 2 >= ((int64_t)1 << 31) || b_rows * ldb * 2 >= ((int64_t)1 << 31))
+        return set_error(TRMOE_ERR_UNSUPPORTED, "weight_grad_mapped: operands must be smaller than 2 GiB");
+    TRMOE_REQUIRE(a_rows >= n_rows && b_rows >= n_rows && n_rows < ((int64_t)1 << 31),
+                  "weight_grad_mapped: operands have fewer than n_rows rows");
+    const size_t need = trmoe_weight_grad_mapped_workspace_bytes(act_dtype, m, n, n_rows);
+    TRMOE_REQUIRE(workspace_bytes >= need, "weight_grad_mapped: workspace too small");
+    WgradArgs w{};
+    w.a = a;
+    w.lda = lda;
+    w.a_rows = a_rows;
+    w.b = b;
+    w.ldb = ldb;
+    w.b_rows = b_rows;
+    w.gather_mod = 1;
+    w.M = m;
+    w.N = n;
+    w.T = n_rows;
+    w.E = 1;
+    w.out = out;
+    w.ldo = n;
+    w.out_expert_stride = m * n;
+    w.splits = wgrad_splits(m, n, 1, n_rows);
+    w.partial = static_cast<float*>(workspace);
+    w.map_mode = map_mode;
+    w.map_off = map_off;
+    w.map_stride = map_stride;
+    return launch_wgrad(act_dtype, w, as_stream(stream));
+}
+
 int trmoe_grouped_linear(int act_dtype, const void* h, int64_t ldh, int64_t n_rows, int64_t k,
                          const int32_t* expert_offsets, int num_experts, const void* w, int64_t out_features,
                          void* y, int64_t ldy, void* stream) {

@@ -252,18 +252,22 @@ using ShapeBwdDH = TileShape<256, 128, 2, 4, 4>;   // the same 128 features of d
 // (DPP swap of one dh value, as in store_bf16_pairs) so that each lane owns
 // two adjacent features of one row, read as 4-byte pairs from the saved
 // gate|up rows; dg, du (packed gate|up column order) and hm leave as 4-byte
-// pairs.  Rows past the tile's end fall past the buffers' ranges; features
-// past F get out-of-range offsets.
-template <bool ROUTED>
-__device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f32x16 (&acc)[4][1], int64_t m0,
-                                                 int64_t m_end, int64_t f0, int wm0, int wf0,
+// pairs.  acc[.][tn] holds the wave's 32 features from wf0.  Rows past the
+// tile's end fall past the buffers' ranges; features past F get
+// out-of-range offsets.
+template <bool ROUTED, int TN = 1>
+__device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f32x16 (&acc)[4][TN], int tn,
+                                                 int64_t m0, int64_t m_end, int64_t f0, int wm0, int wf0,
                                                  const int (*s_route)[kMaxTopK]) {
     const int lane = threadIdx.x & 63;
     const bool odd = lane & 1;
     const int64_t fb = (f0 + wf0 + (lane & 31)) & ~(int64_t)1;   // first feature of the lane's pair
     const int pc2 = (int)(64 * (fb >> 5) + (fb & 31)) * 2;       // its packed gate column, in bytes
     const int rows = (int)(m_end - m0 < 256 ? m_end - m0 : 256);
-    const int ldg2 = (int)a.ldgu * 2, ldd2 = (int)a.lddgu * 2, ldh2 = (int)a.ldhm * 2;
+    // row strides redefined here, so that no offset below is hoisted out of
+    // a persistent caller's loop (they would stay live across every stage)
+    int ldg2 = (int)a.ldgu * 2, ldd2 = (int)a.lddgu * 2, ldh2 = (int)a.ldhm * 2;
+    asm volatile("" : "+s"(ldg2), "+s"(ldd2), "+s"(ldh2));
     const auto rg = make_rsrc(static_cast<const bf16_t*>(a.gu) + m0 * a.ldgu, (uint32_t)(rows * ldg2));
     const auto rd = make_rsrc(static_cast<bf16_t*>(a.dgu) + m0 * a.lddgu, (uint32_t)(rows * ldd2));
     const auto rh = make_rsrc(a.hm != nullptr ? static_cast<bf16_t*>(a.hm) + m0 * a.ldhm : a.dgu,
@@ -273,12 +277,16 @@ __device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f
     const bool routed = ROUTED && f0 + wf0 >= a.shared_feats;
     const int expert = routed ? (int)((f0 + wf0 - a.shared_feats) / a.expert_feats) : -1;
     const int row_lane = wm0 + 4 * (lane >> 5) + (lane & 1);   // the pair's row for i = 0, 1
+    // lane offsets of row_lane; rows below add uniform multiples of the strides
+    // (opaque, so that no row - row_lane multiple is folded back into a
+    // per-row product the compiler would hoist and keep live)
+    int lg = row_lane * ldg2 + pc2, ld = row_lane * ldd2 + pc2, lh = row_lane * ldh2 + (int)fb * 2;
+    asm volatile("" : "+v"(lg), "+v"(ld), "+v"(lh));
     uint32_t gv[2][8], uv[2][8];
     auto load = [&](int tm, int buf) {
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-            const int rl = row_lane + tm * 32 + 8 * (p >> 1) + 2 * (p & 1);
-            const int off = (rl * ldg2 + pc2) | bad;
+            const int off = (lg + (tm * 32 + 8 * (p >> 1) + 2 * (p & 1)) * ldg2) | bad;
             gv[buf][p] = __builtin_amdgcn_raw_buffer_load_b32(rg, off, 0, 0);
             uv[buf][p] = __builtin_amdgcn_raw_buffer_load_b32(rg, off + 64, 0, 0);
         }
@@ -290,8 +298,9 @@ __device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f
         const int buf = tm & 1;
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-            const int rl = row_lane + tm * 32 + 8 * (p >> 1) + 2 * (p & 1);
-            const float v0 = acc[tm][0][2 * p], v1 = acc[tm][0][2 * p + 1];
+            const int dr = tm * 32 + 8 * (p >> 1) + 2 * (p & 1);   // row - row_lane
+            const int rl = row_lane + dr;
+            const float v0 = acc[tm][tn][2 * p], v1 = acc[tm][tn][2 * p + 1];
             const float other = dpp_swap_pairs(odd ? v0 : v1);
             const float dh[2] = {odd ? other : v0, odd ? v1 : other};   // features fb, fb + 1 of row rl
             float mult = a.shared_mult;
@@ -319,7 +328,7 @@ __device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f
                 hv[q] = (routed ? sl * u : sl * u * a.shared_mult);
                 if (routed) hv[q] *= mult;
             }
-            const int od = (rl * ldd2 + pc2) | bad;
+            const int od = (ld + dr * ldd2) | bad;
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, bf16x2{(bf16_t)dg[0], (bf16_t)dg[1]}),
                                                   rd, od, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, bf16x2{(bf16_t)du[0], (bf16_t)du[1]}),
@@ -327,7 +336,7 @@ __device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f
             if (a.hm != nullptr)
                 __builtin_amdgcn_raw_buffer_store_b32(
                     __builtin_bit_cast(uint32_t, bf16x2{(bf16_t)hv[0], (bf16_t)hv[1]}), rh,
-                    (rl * ldh2 + (int)fb * 2) | bad, 0, 0);
+                    (lh + dr * ldh2) | bad, 0, 0);
         }
     }
 }
@@ -350,7 +359,7 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
     const int wf0 = (wave % SD::WAVES_N) * SD::WN;   // feature within the tile (= wn0 / 2)
     int64_t m0 = (int64_t)blockIdx.x * SG::BM;
     int64_t m_end = a.M;
-    const int64_t f0 = (int64_t)blockIdx.y * SD::BN;
+    const int64_t f0 = a.f_base + (int64_t)blockIdx.y * SD::BN;
     const char* wgu = static_cast<const char*>(a.wgu);
     const char* wdt = static_cast<const char*>(a.wdt);
 
@@ -396,7 +405,7 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
     zero_acc<Kind>(acc_dh);
     tile_loop<Kind, SD>(ad, bdt, a.K, lds, wm0, wf0, acc_dh);
     if constexpr (SAVED && sizeof(T) == 2 && !GROUPED) {
-        swiglu_bwd_pairs<ROUTED>(a, acc_dh, m0, m_end, f0, wm0, wf0, s_route);
+        swiglu_bwd_pairs<ROUTED>(a, acc_dh, 0, m0, m_end, f0, wm0, wf0, s_route);
         return;
     }
     // bf16 saved g|u: the tile's 256 rows x 256 packed columns (128 KiB)
@@ -533,6 +542,61 @@ __global__ __launch_bounds__(512) void k_swiglu_bwd(SwigluBwdArgs a) {
     }
 }
 
+
+// Persistent form of the saved-g|u bf16 SwiGLU backward for shared features
+// (no route multipliers): dh = dout . W_down^T as 256-row x 256-feature tiles
+// on the ping-pong stream (pp_stream, one workgroup per CU), each finished
+// tile's epilogue (swiglu_bwd_pairs, twice: the wave's two 32-feature
+// blocks) straight from the accumulators while the other group multiplies.
+// Tiles cover features [0, 256 * n_tiles / tiles_m); features at or past F
+// load zero weights and store nothing.
+__global__ __launch_bounds__(512, 1) void k_swiglu_bwd_pps(SwigluBwdArgs a, int64_t tiles_m, int64_t n_tiles) {
+    extern __shared__ __align__(16) char lds[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = wave >> 2, wig = wave & 3;
+    const int wm0 = group * 128, wn0 = wig * 64;
+    const int64_t G = gridDim.x;
+    const int ntiles = (int)((n_tiles - (int64_t)blockIdx.x + G - 1) / G);
+    if (ntiles <= 0) return;
+    const bool xcd_rows = (tiles_m & 7) == 0 && (G & 7) == 0;
+    auto coords = [&](int i, int64_t& m0, int64_t& f0) {
+        uint32_t mt, nt;
+        pps_tile((uint32_t)blockIdx.x + (uint32_t)i * (uint32_t)G, (uint32_t)tiles_m, (uint32_t)(n_tiles / tiles_m),
+                 xcd_rows, mt, nt);
+        m0 = (int64_t)mt * 256;
+        f0 = (int64_t)nt * 256;
+    };
+    const int64_t ldd_b = a.ldd * (int64_t)sizeof(bf16_t);
+    const int64_t ldw_b = a.ldwdt * (int64_t)sizeof(bf16_t);
+
+    PPRows<256> ap, bp;
+    int64_t m0, f0;
+    coords(0, m0, f0);
+    if (group == 1)
+        ap.init(a.dout, m0, a.M, ldd_b, wig);
+    else
+        bp.init(a.wdt, f0, a.F, ldw_b, wig);
+    f32x16 acc[4][2];
+    zero_acc<KindBF16>(acc);
+    pp_stream<4, PPLayoutK<4, true>>(
+        ap, bp, a.K / 64, ntiles, lds, group, wm0, wn0, acc,
+        [&](int i) {   // i >= ntiles: no rows (the refills past the last stage load zeros)
+            int64_t tm0, tf0;
+            coords(i, tm0, tf0);
+            ap.retarget(a.dout, tm0, i < ntiles ? a.M : tm0, ldd_b);
+        },
+        [&](int i) {
+            int64_t tm0, tf0;
+            coords(i, tm0, tf0);
+            bp.retarget(a.wdt, tf0, i < ntiles ? a.F : tf0, ldw_b);
+        },
+        [&](int i, const f32x16 (&c)[4][2]) {
+            int64_t tm0, tf0;
+            coords(i, tm0, tf0);
+            swiglu_bwd_pairs<false, 2>(a, c, 0, tm0, a.M, tf0, wm0, wn0, nullptr);
+            swiglu_bwd_pairs<false, 2>(a, c, 1, tm0, a.M, tf0, wm0, wn0 + 32, nullptr);
+        });
+}
 // ---------------------------------------------------------------------------
 // weight gradients
 // ---------------------------------------------------------------------------
@@ -759,7 +823,7 @@ __global__ __launch_bounds__(512, 1) void k_wgrad_pp(WgradArgs a) {
     const int nk = (len + 63) / 64;
     if (nk > 0) pp_main<4, PPLayoutT>(ap, bp, nk, lds, group, wm0, wn0, acc, [](const f32x16 (&)[4][2]) {});
 
-    const bool direct = a.splits == 1;
+    const bool direct = a.partial == nullptr;   // else an fp32 partial for the reduction (which may map it)
     const int64_t obase_el = direct ? (int64_t)e * a.out_expert_stride + m0 * a.ldo + n0
                                     : ((int64_t)e * a.splits + sp) * a.M * a.N + m0 * a.N + n0;
     const int ld = (int)(direct ? a.ldo : a.N);
@@ -786,7 +850,17 @@ __global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
         float s = 0.f;
         for (int sp = 0; sp < a.splits; ++sp) s += p[sp * mn];
         const int64_t m = r / a.N, n = r % a.N;
-        static_cast<T*>(a.out)[e * a.out_expert_stride + m * a.ldo + n] = from_f32<T>(s);
+        int64_t dst = e * a.out_expert_stride + m * a.ldo + n;
+        if (a.map_mode == 1) {
+            const int64_t o = a.map_off[m];
+            if (o < 0) continue;
+            dst = o + n * a.map_stride[m];
+        } else if (a.map_mode == 2) {
+            const int64_t o = a.map_off[n];
+            if (o < 0) continue;
+            dst = o + m * a.map_stride[n];
+        }
+        static_cast<T*>(a.out)[dst] = from_f32<T>(s);
     }
 }
 
@@ -806,9 +880,25 @@ static int swiglu_bwd_kind(const SwigluBwdArgs& a, int64_t assignments, hipStrea
     if (st) return st;
     const int64_t tiles_m =
         GROUPED ? (assignments + ShapeBwdGU::BM - 1) / ShapeBwdGU::BM + a.E : (a.M + ShapeBwdGU::BM - 1) / ShapeBwdGU::BM;
-    const int64_t tiles_f = (a.F + ShapeBwdDH::BN - 1) / ShapeBwdDH::BN;
+    const int64_t tiles_f = (a.F - a.f_base + ShapeBwdDH::BN - 1) / ShapeBwdDH::BN;
     if (tiles_m <= 0 || tiles_f <= 0) return TRMOE_OK;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles_m, (unsigned)tiles_f), dim3(512), kLds, stream, a);
+    return check_launch("swiglu_backward");
+}
+
+static int bwd_device_cus() { return current_device_cus(); }
+
+// The persistent launch: 256-feature tiles over features [0, feats).
+static int launch_swiglu_bwd_pps(const SwigluBwdArgs& a, int64_t feats, hipStream_t stream) {
+    const int64_t tiles_m = (a.M + 255) / 256;
+    const int64_t n_tiles = tiles_m * ((feats + 255) / 256);
+    const int64_t cus = bwd_device_cus();
+    const int64_t grid = n_tiles < cus ? n_tiles : cus;
+    constexpr int kLds = 2 * PPLayoutK<4, true>::kStage;
+    int st = bwd_lds(k_swiglu_bwd_pps, kLds);
+    if (st) return st;
+    if (grid <= 0) return TRMOE_OK;
+    hipLaunchKernelGGL(k_swiglu_bwd_pps, dim3((unsigned)grid), dim3(512), kLds, stream, a, tiles_m, n_tiles);
     return check_launch("swiglu_backward");
 }
 
@@ -817,9 +907,23 @@ int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipS
     if (a.gu != nullptr) {
         // saved pre-activations (shared and dense-routed forms)
         if (grouped) return set_error(TRMOE_ERR_UNSUPPORTED, "swiglu_backward: saved gate|up for grouped rows");
-        if (act == TRMOE_BF16)
+        if (act == TRMOE_BF16) {
+            // features without route multipliers (whole 256-feature tiles of
+            // them when routed) on the persistent stream when that fills at
+            // least a round of CUs; the rest on the tile kernel
+            const int64_t feats = routed ? (a.shared_feats < a.F ? a.shared_feats : a.F) / 256 * 256 : a.F;
+            const int64_t tiles = ((a.M + 255) / 256) * ((feats + 255) / 256);
+            if (a.f_base == 0 && a.K % 64 == 0 && feats > 0 && tiles >= bwd_device_cus()) {
+                const int st = launch_swiglu_bwd_pps(a, feats, stream);
+                if (st || feats >= a.F) return st;
+                SwigluBwdArgs t = a;
+                t.f_base = feats;
+                return routed ? swiglu_bwd_kind<KindBF16, false, true, true>(t, assignments, stream)
+                              : swiglu_bwd_kind<KindBF16, false, false, true>(t, assignments, stream);
+            }
             return routed ? swiglu_bwd_kind<KindBF16, false, true, true>(a, assignments, stream)
                           : swiglu_bwd_kind<KindBF16, false, false, true>(a, assignments, stream);
+        }
         return routed ? swiglu_bwd_kind<KindF32, false, true, true>(a, assignments, stream)
                       : swiglu_bwd_kind<KindF32, false, false, true>(a, assignments, stream);
     }
@@ -833,7 +937,6 @@ int launch_swiglu_bwd(int act, const SwigluBwdArgs& a, int64_t assignments, hipS
     return swiglu_bwd_kind<KindF32, false, false>(a, assignments, stream);
 }
 
-static int bwd_device_cus() { return current_device_cus(); }
 
 // Split count: a workgroup holds a CU (128 KiB of LDS), so the launch runs
 // in ceil(tiles * s / CUs) rounds of rows/s rows each; every split adds an
@@ -900,7 +1003,7 @@ static int wgrad_pp(const WgradArgs& a, hipStream_t stream) {
                     (unsigned)((a.N + ShapeWgradTr::BN - 1) / ShapeWgradTr::BN), (unsigned)(a.E * a.splits));
     hipLaunchKernelGGL(k_wgrad_pp, grid, dim3(512), kLds, stream, a);
     st = check_launch("weight_grad");
-    if (st || a.splits == 1) return st;
+    if (st || a.partial == nullptr) return st;
     int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(k_wgrad_reduce<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, a);

@@ -174,6 +174,7 @@ struct SwigluBwdArgs {
     const void* gu;          // saved gate|up pre-activations [M, 2F] (null: recomputed from x)
     int64_t ldgu;
     int64_t F;               // features (per expert when grouped)
+    int64_t f_base;          // first feature of the launch (the features below it run elsewhere)
     void* dgu;
     int64_t lddgu;
     void* hm;                // may be null
@@ -218,6 +219,12 @@ struct WgradArgs {
     int64_t ldo;
     int64_t out_expert_stride;   // elements
     float* partial;              // [E][splits][M][N] when splits > 1
+    // Destination map of the summed tile (E == 1, through the reduction):
+    // 0 none (out[m * ldo + n]); 1 rows: out[map_off[m] + n * map_stride[m]];
+    // 2 columns: out[map_off[n] + m * map_stride[n]]; negative offsets skip.
+    int map_mode;
+    const int64_t* map_off;
+    const int64_t* map_stride;
 };
 
 int launch_pack(const PackArgs& p, hipStream_t stream);

@@ -358,29 +358,6 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
-// Tile i of a persistent launch over tiles_m x tiles_n tiles -> (row tile,
-// column tile).  Workgroups are dispatched to the 8 XCDs round-robin, so tile
-// i runs on XCD i % 8.  With xcd_rows, XCD x owns the row tiles
-// [x mpx, x mpx + mpx), mpx = tiles_m / 8, and walks them in groups of bm
-// (4 when mpx allows): row fastest within a group, then every column tile,
-// then the next group.  The 32 workgroups of an XCD that run together then
-// hold bm row panels x 32 / bm column panels (4 x 8), which read each K slice
-// of 12 panels per round instead of 18 for 16 x 2.  Other shapes walk row
-// tiles first.
-__device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, uint32_t tiles_n, bool xcd_rows,
-                                         uint32_t& mt, uint32_t& nt) {
-    if (xcd_rows) {
-        const uint32_t mpx = tiles_m >> 3, j = i >> 3;
-        const uint32_t bm = (mpx & 3) == 0 ? 4 : ((mpx & 1) == 0 ? 2 : 1);
-        const uint32_t rest = j / bm, mg = rest / tiles_n;
-        nt = rest - mg * tiles_n;
-        mt = (i & 7) * mpx + mg * bm + (j - rest * bm);
-    } else {
-        nt = i / tiles_m;
-        mt = i - nt * tiles_m;
-    }
-}
-
 // SwiGLU of one finished tile straight from the accumulators of the calling
 // wave (no LDS): each lane owns one h feature (its gate column r of the
 // wave's 64 packed rows, up column 32 + r) and 16 rows per 32-row block;

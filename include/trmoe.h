@@ -457,6 +457,24 @@ int trmoe_weight_grad(int act_dtype, const void* a, int64_t lda, int64_t a_rows,
                       void* stream);
 
 /*
+ * The same token-reduction GEMM (bf16, one segment, no gathered rows) with
+ * its result written straight into the parameters' own layouts, so that no
+ * strided copy of the gradient follows it: the grad-W that the reference's
+ * autograd hands to AccumulateGrad for the shared linears and the expert
+ * tensors (engine.py:333-349, triton_token_routed.py:751-1028), which here
+ * arrive as one packed [m, n] product.  The summed fp32 tile goes to
+ *     map_mode 1 (rows):    out[map_off[i] + j * map_stride[i]]
+ *     map_mode 2 (columns): out[map_off[j] + i * map_stride[j]]
+ * in act_dtype elements; a negative map_off skips the row (column).  The
+ * workspace (trmoe_weight_grad_mapped_workspace_bytes) is required.
+ */
+size_t trmoe_weight_grad_mapped_workspace_bytes(int act_dtype, int64_t m, int64_t n, int64_t n_rows);
+int trmoe_weight_grad_mapped(int act_dtype, const void* a, int64_t lda, int64_t a_rows, const void* b, int64_t ldb,
+                             int64_t b_rows, int64_t m, int64_t n, int64_t n_rows, int map_mode,
+                             const int64_t* map_off, const int64_t* map_stride, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
  * Grouped plain GEMM over a K1 partition: y[r, :] = h[r, :] . W_e^T for the
  * rows r of expert e, with w PLAIN-packed per expert [E, round_up(out, 256),
  * round_up(k, 8)].  The backward uses it for the data gradient of the routed

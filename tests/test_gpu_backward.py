@@ -148,6 +148,44 @@ def test_shared_swiglu_backward(gpu, dtype, n, H, S):
     assert _err(hm2[:, :S], rh) <= BOUND[dtype]
 
 
+def test_shared_swiglu_backward_persistent(gpu):
+    """Saved bf16 g|u at a size that fills a round of CUs: the dh GEMM runs
+    on the persistent stream (256 x 256 tiles, ragged last row tile, padded
+    features past S), checked against the closed form in fp64."""
+    from complexity_amd import ops
+
+    n, H, S = 5500, 896, 3000
+    print(f"shared_swiglu_backward persistent bf16 n={n} H={H} S={S}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(7)
+    x = torch.randn(n, H, generator=g).to(torch.bfloat16).to(gpu)
+    dout = torch.randn(n, H, generator=g).to(torch.bfloat16).to(gpu)
+    wg = (torch.randn(S, H, generator=g) * H ** -0.5).to(torch.bfloat16).to(gpu)
+    wu = (torch.randn(S, H, generator=g) * H ** -0.5).to(torch.bfloat16).to(gpu)
+    wd = (torch.randn(H, S, generator=g) * S ** -0.5).to(torch.bfloat16).to(gpu)
+    gu, _ = ops.pack_linear_gate_up(wg, wu)
+    wdt = ops.pack_linear_down_t(wd)
+    _, gus = ops.shared_gate_up(x, gu, None, S, save=True)
+    dgu, hm = ops.shared_swiglu_backward(x, dout, gu, wdt, S, 1.5, gu=gus)
+    torch.cuda.synchronize()
+    F = -(-S // 128) * 128
+    # the closed form from the same bf16-rounded g|u the kernel reads
+    sg, su = _split_dgu(gus, F)
+    gd, ud = sg[:, :S].double(), su[:, :S].double()
+    dh = dout.double() @ wd.double()
+    s = torch.sigmoid(gd)
+    rdg, rdu, rh = 1.5 * dh * ud * (s + gd * s * (1 - s)), 1.5 * dh * gd * s, 1.5 * gd * s * ud
+    dg, du = _split_dgu(dgu, F)
+    assert _err(dg[:, :S], rdg) <= BOUND["bf16"]
+    assert _err(du[:, :S], rdu) <= BOUND["bf16"]
+    assert _err(hm[:, :S], rh) <= BOUND["bf16"]
+    assert dg[:, S:].abs().max().item() == 0 and du[:, S:].abs().max().item() == 0
+    assert hm[:, S:].abs().max().item() == 0
+    # and the full closed form from x
+    odg, odu, oh = O.swiglu_backward(x.double(), dout.double(), wg.double(), wu.double(), wd.double(), 1.5)
+    assert _err(dg[:, :S], odg) <= BOUND["bf16"] and _err(du[:, :S], odu) <= BOUND["bf16"]
+    assert _err(hm[:, :S], oh) <= BOUND["bf16"]
+
+
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 @pytest.mark.parametrize("E,k,W,n", [(4, 2, 64, 500), (16, 2, 256, 300), (8, 4, 40, 129), (2, 1, 128, 1)])
 def test_routed_swiglu_backward_and_grouped_linear(gpu, dtype, E, k, W, n):

@@ -938,6 +938,12 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
     s_pad, w_pad = _round_up(S, 128), _round_up(W, 64)
     if packed.strategy == STRATEGY_DENSE:
         F_ = packed.dense_features
+        # bf16: both weight gradients go straight into one flat buffer in the
+        # parameters' layouts (their views are the gradients, no copies)
+        mapped = need_dw and x.dtype == torch.bfloat16
+        if mapped:
+            roff, rstride, coff, cstride, offs = _dense_grad_maps(S, E, W, hidden, x.device)
+            flat = torch.empty(offs[-1], dtype=x.dtype, device=x.device)
         dgu, hm = dense_routed_swiglu_backward(x, dout, packed.dense_gate_up, bwd.dense_down_t, S, E, W, token_ids,
                                                route_table, route_weights, shared_scale, routed_scale, gu=saved_gu,
                                                want_hm=need_dw and saved_h is None)
@@ -945,12 +951,6 @@ def layer_backward(dout: torch.Tensor, x: torch.Tensor, token_ids: torch.Tensor,
             hm = saved_h
         # the gate|up weight gradient (side stream) overlaps dx and dWd
         side = _OnSide(x.device, (dgu, x))
-        # bf16: both weight gradients go straight into one flat buffer in the
-        # parameters' layouts (their views are the gradients, no copies)
-        mapped = need_dw and x.dtype == torch.bfloat16
-        if mapped:
-            roff, rstride, coff, cstride, offs = _dense_grad_maps(S, E, W, hidden, x.device)
-            flat = torch.empty(offs[-1], dtype=x.dtype, device=x.device)
         if need_dw:
             with side:
                 if mapped:

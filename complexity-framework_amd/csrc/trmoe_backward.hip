@@ -841,26 +841,43 @@ __global__ __launch_bounds__(512, 1) void k_wgrad_pp(WgradArgs a) {
 
 template <class T>
 __global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
+    // four consecutive columns per thread (N is a multiple of 8): 16-byte
+    // loads of each split's partial, summed in split order per element
     const int64_t mn = a.M * a.N;
-    const int64_t total = (int64_t)a.E * mn;
+    const int64_t q4 = a.N >> 2;
+    const int64_t total = (int64_t)a.E * a.M * q4;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t e = idx / mn, r = idx % mn;
-        const float* p = a.partial + e * a.splits * mn + r;
-        float s = 0.f;
-        for (int sp = 0; sp < a.splits; ++sp) s += p[sp * mn];
-        const int64_t m = r / a.N, n = r % a.N;
-        int64_t dst = e * a.out_expert_stride + m * a.ldo + n;
+        const int64_t row = idx / q4;   // e * M + m
+        const int64_t n = (idx - row * q4) * 4;
+        const int64_t e = row / a.M, m = row - e * a.M;
+        const float* p = a.partial + e * a.splits * mn + m * a.N + n;
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < a.splits; ++sp) {
+            const float4 v = *reinterpret_cast<const float4*>(p + sp * mn);
+            s[0] += v.x;
+            s[1] += v.y;
+            s[2] += v.z;
+            s[3] += v.w;
+        }
+        T* out = static_cast<T*>(a.out);
         if (a.map_mode == 1) {
             const int64_t o = a.map_off[m];
             if (o < 0) continue;
-            dst = o + n * a.map_stride[m];
+            const int64_t st = a.map_stride[m];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) out[o + (n + c) * st] = from_f32<T>(s[c]);
         } else if (a.map_mode == 2) {
-            const int64_t o = a.map_off[n];
-            if (o < 0) continue;
-            dst = o + m * a.map_stride[n];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int64_t o = a.map_off[n + c];
+                if (o >= 0) out[o + m * a.map_stride[n + c]] = from_f32<T>(s[c]);
+            }
+        } else {
+            const int64_t dst = e * a.out_expert_stride + m * a.ldo + n;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) out[dst + c] = from_f32<T>(s[c]);
         }
-        static_cast<T*>(a.out)[dst] = from_f32<T>(s);
     }
 }
 
@@ -972,7 +989,7 @@ static int wgrad_kind(const WgradArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(kern, grid, dim3(ShapeWgrad::NT), kLds, stream, a);
     st = check_launch("weight_grad");
     if (st || a.splits == 1) return st;
-    int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
+    int64_t blocks = ((int64_t)a.E * a.M * (a.N / 4) + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(k_wgrad_reduce<typename Kind::T>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
     return check_launch("weight_grad (reduce)");
@@ -989,7 +1006,7 @@ static int wgrad_tr(const WgradArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(kern, grid, dim3(ShapeWgradTr::NT), kLds, stream, a);
     st = check_launch("weight_grad");
     if (st || a.splits == 1) return st;
-    int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
+    int64_t blocks = ((int64_t)a.E * a.M * (a.N / 4) + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(k_wgrad_reduce<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
     return check_launch("weight_grad (reduce)");
@@ -1004,7 +1021,7 @@ static int wgrad_pp(const WgradArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(k_wgrad_pp, grid, dim3(512), kLds, stream, a);
     st = check_launch("weight_grad");
     if (st || a.partial == nullptr) return st;
-    int64_t blocks = ((int64_t)a.E * a.M * a.N + 255) / 256;
+    int64_t blocks = ((int64_t)a.E * a.M * (a.N / 4) + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(k_wgrad_reduce<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
     return check_launch("weight_grad (reduce)");

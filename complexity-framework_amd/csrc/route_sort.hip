@@ -150,12 +150,18 @@ __global__ __launch_bounds__(kSortThreads) void k_route_scatter(SortArgs a) {
         }
         if (lane < kMaxExperts) s_red[wave][0][lane] = 0;
     } else {
-        // prefix over blocks: thread j holds block j's histogram (nblocks <= 256)
+        // prefix over blocks: thread j holds block j's histogram (nblocks <= 256);
+        // every count is requested before the first sum needs one (one load
+        // latency, not one per expert)
         const int j = threadIdx.x;
-        for (int e = 0; e < a.E; ++e) {
-            const int c = j < a.nblocks ? a.block_counts[j * a.E + e] : 0;
-            const int all = wave_sum(c);
-            const int pre = wave_sum(j < b ? c : 0);
+        int cv[kMaxExperts];
+#pragma unroll
+        for (int e = 0; e < kMaxExperts; ++e) cv[e] = (e < a.E && j < a.nblocks) ? a.block_counts[j * a.E + e] : 0;
+#pragma unroll
+        for (int e = 0; e < kMaxExperts; ++e) {
+            if (e >= a.E) break;
+            const int all = wave_sum(cv[e]);
+            const int pre = wave_sum(j < b ? cv[e] : 0);
             if (lane == 0) {
                 s_red[wave][0][e] = pre;
                 s_red[wave][1][e] = all;
@@ -163,22 +169,29 @@ __global__ __launch_bounds__(kSortThreads) void k_route_scatter(SortArgs a) {
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int excl = 0;
-        for (int e = 0; e < a.E; ++e) {
-            int pre = 0, tot = 0;
+    if (wave == 0) {
+        // lane e: expert e's totals over the waves, then an exclusive scan
+        // of the totals across the lanes (no serial walk over the experts)
+        int pre = 0, tot = 0;
+        if (lane < a.E)
             for (int w = 0; w < kSortWaves; ++w) {
-                pre += s_red[w][0][e];
-                tot += s_red[w][1][e];
+                pre += s_red[w][0][lane];
+                tot += s_red[w][1][lane];
             }
-            s_run[e] = excl + pre;
-            if (b == 0) {
-                a.offsets[e] = excl;
-                a.counts[e] = tot;
-            }
-            excl += tot;
+        int incl = tot;
+#pragma unroll
+        for (int off = 1; off < kMaxExperts; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
         }
-        if (b == 0) a.offsets[a.E] = excl;
+        if (lane < a.E) {
+            s_run[lane] = incl - tot + pre;
+            if (b == 0) {
+                a.offsets[lane] = incl - tot;
+                a.counts[lane] = tot;
+                if (lane == a.E - 1) a.offsets[a.E] = incl;
+            }
+        }
     }
     __syncthreads();
 

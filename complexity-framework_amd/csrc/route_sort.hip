@@ -93,12 +93,6 @@ __device__ __forceinline__ int wave_rank(int ex, int E, int* wcnt) {
     return rank;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // Launch 1 of the multi-block form: the histogram of each block's items.
 __global__ __launch_bounds__(kSortThreads) void k_route_count(SortArgs a) {
     __shared__ int s_cnt[kSortWaves][kMaxExperts];
@@ -150,22 +144,44 @@ __global__ __launch_bounds__(kSortThreads) void k_route_scatter(SortArgs a) {
         }
         if (lane < kMaxExperts) s_red[wave][0][lane] = 0;
     } else {
-        // prefix over blocks: thread j holds block j's histogram (nblocks <= 256);
-        // every count is requested before the first sum needs one (one load
-        // latency, not one per expert)
+        // prefix over blocks (nblocks <= 256): the histograms staged in LDS
+        // (thread j: block j's row), then thread (part, e) sums expert e's
+        // counts over blocks 16 part .. 16 part + 15, all of them and those
+        // before this block, and lane e of wave w adds parts 4w .. 4w + 3
+        // (LDS sums instead of cross-lane reductions per expert)
+        static_assert(kSortThreads == kMaxSortBlocks && kSortThreads % kMaxExperts == 0, "one row per thread");
+        constexpr int kParts = kSortThreads / kMaxExperts;
+        constexpr int kPerPart = kMaxSortBlocks / kParts;
+        __shared__ int s_bc[kMaxSortBlocks][kMaxExperts];
+        __shared__ int s_part[kParts][2][kMaxExperts];
         const int j = threadIdx.x;
-        int cv[kMaxExperts];
 #pragma unroll
-        for (int e = 0; e < kMaxExperts; ++e) cv[e] = (e < a.E && j < a.nblocks) ? a.block_counts[j * a.E + e] : 0;
+        for (int e = 0; e < kMaxExperts; ++e)
+            s_bc[j][e] = (e < a.E && j < a.nblocks) ? a.block_counts[j * a.E + e] : 0;
+        __syncthreads();
+        {
+            const int e = threadIdx.x % kMaxExperts, part = threadIdx.x / kMaxExperts;
+            int tot = 0, pre = 0;
 #pragma unroll
-        for (int e = 0; e < kMaxExperts; ++e) {
-            if (e >= a.E) break;
-            const int all = wave_sum(cv[e]);
-            const int pre = wave_sum(j < b ? cv[e] : 0);
-            if (lane == 0) {
-                s_red[wave][0][e] = pre;
-                s_red[wave][1][e] = all;
+            for (int q = 0; q < kPerPart; ++q) {
+                const int jj = part * kPerPart + q;
+                const int c = s_bc[jj][e];
+                tot += c;
+                pre += jj < b ? c : 0;
             }
+            s_part[part][0][e] = pre;
+            s_part[part][1][e] = tot;
+        }
+        __syncthreads();
+        if (lane < kMaxExperts) {
+            int pre = 0, tot = 0;
+#pragma unroll
+            for (int q = 0; q < kParts / kSortWaves; ++q) {
+                pre += s_part[wave * (kParts / kSortWaves) + q][0][lane];
+                tot += s_part[wave * (kParts / kSortWaves) + q][1][lane];
+            }
+            s_red[wave][0][lane] = pre;
+            s_red[wave][1][lane] = tot;
         }
     }
     __syncthreads();

@@ -97,16 +97,21 @@ __device__ __forceinline__ int wave_rank(int ex, int E, int* wcnt) {
 __global__ __launch_bounds__(kSortThreads) void k_route_count(SortArgs a) {
     __shared__ int s_cnt[kSortWaves][kMaxExperts];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane < kMaxExperts) s_cnt[wave][lane] = 0;
     const int base = blockIdx.x * a.chunks * kSortThreads;
+    // the wave's counts stay in registers (uniform) until one write per expert
+    int cnt[kMaxExperts];
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; ++e) cnt[e] = 0;
     for (int c = 0; c < a.chunks; ++c) {
         int asg;
         const int ex = item_expert(a, base + c * kSortThreads + threadIdx.x, asg, true);
-        for (int e = 0; e < a.E; ++e) {
-            const uint64_t m = __ballot(ex == e);
-            if (lane == 0) s_cnt[wave][e] += __popcll(m);
-        }
+#pragma unroll
+        for (int e = 0; e < kMaxExperts; ++e)
+            if (e < a.E) cnt[e] += __popcll(__ballot(ex == e));
     }
+    if (lane == 0)
+#pragma unroll
+        for (int e = 0; e < kMaxExperts; ++e) s_cnt[wave][e] = cnt[e];
     __syncthreads();
     if (threadIdx.x < a.E) {
         int s = 0;

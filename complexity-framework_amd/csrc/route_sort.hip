@@ -160,9 +160,14 @@ __global__ __launch_bounds__(kSortThreads) void k_route_scatter(SortArgs a) {
         __shared__ int s_bc[kMaxSortBlocks][kMaxExperts];
         __shared__ int s_part[kParts][2][kMaxExperts];
         const int j = threadIdx.x;
+        int cv[kMaxExperts];
 #pragma unroll
-        for (int e = 0; e < kMaxExperts; ++e)
-            s_bc[j][e] = (e < a.E && j < a.nblocks) ? a.block_counts[j * a.E + e] : 0;
+        for (int e = 0; e < kMaxExperts; ++e) cv[e] = (e < a.E && j < a.nblocks) ? a.block_counts[j * a.E + e] : 0;
+        // the first chunk's id -> table lookups go out now, so that their
+        // latency overlaps the prefix instead of following it
+        ex_c[0] = item_expert(a, base + threadIdx.x, asg_c[0], false);
+#pragma unroll
+        for (int e = 0; e < kMaxExperts; ++e) s_bc[j][e] = cv[e];
         __syncthreads();
         {
             const int e = threadIdx.x % kMaxExperts, part = threadIdx.x / kMaxExperts;
@@ -228,6 +233,9 @@ __global__ __launch_bounds__(kSortThreads) void k_route_scatter(SortArgs a) {
                     ex = ex_c[q];
                     asg = asg_c[q];
                 }
+        } else if (c == 0) {
+            ex = ex_c[0];
+            asg = asg_c[0];
         } else {
             ex = item_expert(a, base + c * kSortThreads + threadIdx.x, asg, false);
         }

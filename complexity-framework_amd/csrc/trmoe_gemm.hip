@@ -1010,6 +1010,11 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     zero_acc<KindBF16>(acc);
     constexpr int kORowBytes = BN * 2 + 16;
     using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
+    // nothing to add to the product (no routed rows, no residual): each
+    // group stores its rows straight from the accumulators as bf16 pairs
+    // (group 0 while group 1 multiplies the last stage), with no LDS tile
+    // and no copy-out pass
+    const bool direct = a.y == nullptr && a.residual == nullptr && a.vec_ok;
     pp_main<4, Lay>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
         const int r = lane & 31;
         float cs[2];
@@ -1017,6 +1022,24 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
         for (int tn = 0; tn < 2; ++tn) {
             const int64_t col = n0 + wn0 + tn * 32 + r;
             cs[tn] = a.shared_scale * ((a.w_scale != nullptr && col < a.N) ? a.w_scale[col] : 1.0f);
+        }
+        if (direct) {
+            const int ld2 = (int)a.ldo * 2;
+            const int64_t mlim = a.M - m0 < BM ? a.M - m0 : BM;
+            const auto rsrc = make_rsrc(static_cast<T*>(a.out) + m0 * a.ldo, (uint32_t)(mlim * ld2));
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const int64_t col = n0 + wn0 + tn * 32 + r;
+                const int lb = pair_lane_offset(wm0, (int)col, ld2) | (col < a.N ? 0 : kOutOfRange);
+#pragma unroll
+                for (int tm = 0; tm < 4; ++tm) {
+                    float v[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) v[q] = c[tm][tn][q] * cs[tn];
+                    store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+                }
+            }
+            return;
         }
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm)
@@ -1029,6 +1052,7 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
                         from_f32<T>(c[tm][tn][i] * cs[tn]);
             }
     });
+    if (direct) return;
 
     const T* y = static_cast<const T*>(a.y);
     const T* res = static_cast<const T*>(a.residual);

@@ -299,6 +299,90 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
                                           a.row_scale != nullptr ? s_rscale : nullptr);
 }
 
+// SwiGLU of one finished tile straight from the accumulators of the calling
+// wave (no LDS): each lane owns one h feature (its gate column r of the
+// wave's 64 packed rows, up column 32 + r) and 16 rows per 32-row block;
+// PAIRS: adjacent lanes pair their values into 4-byte stores
+// (store_bf16_pairs), else one 2-byte store per value.  Rows at or past M
+// fall past the buffer's range and are dropped.
+template <int TMW, bool PAIRS = true>
+__device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
+                                                   int64_t n0, int wm0, int wn0) {
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const int64_t pbase = n0 + wn0;   // packed row of the wave's gate block
+    // h = silu(g) * u * mult, with the shared multiplier folded into u
+    const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
+    const float su = (a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f) * a.shared_mult;
+    const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
+    // the row stride is redefined here so that no offset below is hoisted
+    // out of a caller's loop (they would stay live across every stage)
+    int ld2 = (int)a.ldh * 2;
+    asm volatile("" : "+s"(ld2));
+    const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.h) + m0 * a.ldh, (uint32_t)(mlim * ld2));
+    const int col = (int)((pbase >> 1) + r);
+    if constexpr (PAIRS) {
+        const int lb = pair_lane_offset(wm0, col, ld2);
+#pragma unroll
+        for (int tm = 0; tm < TMW; ++tm) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
+            store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+        }
+    } else {
+        // one 2-byte store per value (fewer live registers: the e4m3 kernels
+        // keep their loader state out of scratch this way)
+        const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + col * 2;
+#pragma unroll
+        for (int tm = 0; tm < TMW; ++tm)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;   // row wm0 + tm*32 + acc_row(lane, i)
+                const float hv = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<bf16_t>(hv)), rsrc, off,
+                                                      0, 0);
+            }
+    }
+}
+
+// gate_up_epi_direct for a tile that may hold dense-routed expert features:
+// the calling wave's 32-feature block is wholly shared (gate_up_epi_direct)
+// or wholly one expert's, whose h is silu(g) * u times the token's route
+// weight for that expert (from s_route, as gate_up_epi_block computes it);
+// bf16 pairs straight from the accumulators.
+template <int TMW>
+__device__ __forceinline__ void gate_up_epi_direct_routed(const GateUpArgs& a, const f32x16 (&acc)[TMW][2],
+                                                          int64_t m0, int64_t n0, int wm0, int wn0,
+                                                          const int (*s_route)[kMaxTopK]) {
+    const int64_t pbase = n0 + wn0;   // packed row of the wave's gate block
+    const int64_t fblock = pbase >> 1;
+    if (a.ids == nullptr || fblock < a.shared_feats) {
+        gate_up_epi_direct<TMW, true>(a, acc, m0, n0, wm0, wn0);
+        return;
+    }
+    const int expert = (int)((fblock - a.shared_feats) / a.expert_feats);
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
+    const float su = a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f;
+    const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
+    const int ld2 = (int)a.ldh * 2;
+    const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.h) + m0 * a.ldh, (uint32_t)(mlim * ld2));
+    const int lb = pair_lane_offset(wm0, (int)(fblock + r), ld2);
+#pragma unroll
+    for (int tm = 0; tm < TMW; ++tm) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int* rr = s_route[wm0 + tm * 32 + acc_row(lane, i)];
+            float tw = 0.f;
+#pragma unroll
+            for (int j = 0; j < kMaxTopK; ++j) tw += (rr[j] == expert) ? a.rw[j] : 0.f;
+            v[i] = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su) * tw;
+        }
+        store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+    }
+}
+
 // gate|up + SwiGLU over bf16 activations and weights, K a multiple of 64.
 // ROUTED: the launch covers dense-routed expert columns (route gather and
 // per-token expert weights for the tiles that hold them).  TMW = 4: 256-row
@@ -351,57 +435,23 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
     f32x16 acc[TMW][2];
     zero_acc<Kind>(acc);
     using Lay = std::conditional_t<FP8, PPLayoutF8<TMW>, PPLayoutK<TMW>>;
+    // bf16 weights without row scales: each group stores its h rows straight
+    // from the accumulators (group 0 while group 1 multiplies the last
+    // stage); otherwise, and for the saving 256-row tiles (whose registers
+    // would spill), through the LDS tile
+    const bool direct = !FP8 && (TMW == 2 || !SAVE) && a.row_scale == nullptr;
     pp_main<TMW, Lay>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[TMW][2]) {
+        if (direct) {
+            if constexpr (ROUTED)
+                gate_up_epi_direct_routed<TMW>(a, c, m0, n0, wm0, wn0, s_route);
+            else
+                gate_up_epi_direct<TMW, true>(a, c, m0, n0, wm0, wn0);
+            return;
+        }
         gate_up_epi_tile<Kind, Shape, ROUTED>(a, c, n0, lds, s_route, a.row_scale != nullptr ? s_rscale : nullptr);
     });
     if constexpr (SAVE) gate_up_save<Kind, Shape>(a, acc, m0, n0, a.n_base + (int64_t)gridDim.y * 256);
-    gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
-}
-
-// SwiGLU of one finished tile straight from the accumulators of the calling
-// wave (no LDS): each lane owns one h feature (its gate column r of the
-// wave's 64 packed rows, up column 32 + r) and 16 rows per 32-row block;
-// PAIRS: adjacent lanes pair their values into 4-byte stores
-// (store_bf16_pairs), else one 2-byte store per value.  Rows at or past M
-// fall past the buffer's range and are dropped.
-template <int TMW, bool PAIRS = true>
-__device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
-                                                   int64_t n0, int wm0, int wn0) {
-    const int lane = threadIdx.x & 63, r = lane & 31;
-    const int64_t pbase = n0 + wn0;   // packed row of the wave's gate block
-    // h = silu(g) * u * mult, with the shared multiplier folded into u
-    const float sg = a.w_scale ? a.w_scale[pbase + r] : 1.0f;
-    const float su = (a.w_scale ? a.w_scale[pbase + 32 + r] : 1.0f) * a.shared_mult;
-    const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
-    // the row stride is redefined here so that no offset below is hoisted
-    // out of a caller's loop (they would stay live across every stage)
-    int ld2 = (int)a.ldh * 2;
-    asm volatile("" : "+s"(ld2));
-    const auto rsrc = make_rsrc(static_cast<bf16_t*>(a.h) + m0 * a.ldh, (uint32_t)(mlim * ld2));
-    const int col = (int)((pbase >> 1) + r);
-    if constexpr (PAIRS) {
-        const int lb = pair_lane_offset(wm0, col, ld2);
-#pragma unroll
-        for (int tm = 0; tm < TMW; ++tm) {
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
-            store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
-        }
-    } else {
-        // one 2-byte store per value (fewer live registers: the e4m3 kernels
-        // keep their loader state out of scratch this way)
-        const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + col * 2;
-#pragma unroll
-        for (int tm = 0; tm < TMW; ++tm)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int off = lb + (tm * 32 + 8 * (i >> 2) + (i & 3)) * ld2;   // row wm0 + tm*32 + acc_row(lane, i)
-                const float hv = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
-                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<bf16_t>(hv)), rsrc, off,
-                                                      0, 0);
-            }
-    }
+    if (!direct) gate_up_epi_store<Kind, Shape>(a, m0, n0, lds);
 }
 
 // gate_up_save for the persistent kernel: the raw gate|up outputs of the

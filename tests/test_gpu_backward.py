@@ -148,6 +148,42 @@ def test_shared_swiglu_backward(gpu, dtype, n, H, S):
     assert _err(hm2[:, :S], rh) <= BOUND[dtype]
 
 
+@pytest.mark.parametrize("S,E,W,n", [(3072, 4, 64, 16384), (256, 4, 64, 700), (96, 3, 40, 300)])
+def test_weight_grad_mapped_matches_the_strided_views(gpu, S, E, W, n):
+    """trmoe_weight_grad_mapped (dense strategy's dWgu in row mode, dWd in
+    column mode) against trmoe_weight_grad plus the unmapped path's views:
+    the same fp32 partials summed in the same order, so bit-identical."""
+    from complexity_amd import ops
+
+    print(f"weight_grad_mapped S={S} E={E} W={W} n={n}", flush=True)
+    H = 128 if n < 16384 else 896
+    s_pad, w_pad = -(-S // 128) * 128, -(-W // 64) * 64
+    F_ = s_pad + E * w_pad
+    g = torch.Generator(device="cpu").manual_seed(S + E + W + n)
+    dgu = (torch.randn(n, 2 * F_, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    x = torch.randn(n, H, generator=g).to(torch.bfloat16).to(gpu)
+    dout = torch.randn(n, H, generator=g).to(torch.bfloat16).to(gpu)
+    hm = torch.randn(n, F_, generator=g).to(torch.bfloat16).to(gpu)
+    roff, rstride, coff, cstride, offs = ops._dense_grad_maps(S, E, W, H, x.device)
+    flat = torch.full((offs[-1],), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ops.weight_grad_mapped(dgu, x, 2 * F_, H, n, 1, roff, rstride, flat)
+    ops.weight_grad_mapped(dout, hm, H, F_, n, 2, coff, cstride, flat)
+    dwgu = ops.weight_grad(dgu, x, 2 * F_, H, n)[0]
+    dwd = ops.weight_grad(dout, hm, H, F_, n)[0]
+    torch.cuda.synchronize()
+    assert not torch.isnan(flat).any()
+    o_gate, o_up, o_sd, o_eg, o_eu, o_ed, _ = offs
+    g_rows, u_rows = ops._gate_up_rows(dwgu, F_)
+    sh, ew = S * H, E * W * H
+    assert torch.equal(flat[o_gate:o_gate + sh].view(S, H), g_rows[:S])
+    assert torch.equal(flat[o_up:o_up + sh].view(S, H), u_rows[:S])
+    assert torch.equal(flat[o_sd:o_sd + sh].view(H, S), dwd[:, :S])
+    assert torch.equal(flat[o_eg:o_eg + ew].view(E, H, W), g_rows[s_pad:].view(E, w_pad, H)[:, :W].transpose(1, 2))
+    assert torch.equal(flat[o_eu:o_eu + ew].view(E, H, W), u_rows[s_pad:].view(E, w_pad, H)[:, :W].transpose(1, 2))
+    assert torch.equal(flat[o_ed:o_ed + ew].view(E, W, H),
+                       dwd[:, s_pad:].reshape(H, E, w_pad)[:, :, :W].permute(1, 2, 0))
+
+
 def test_shared_swiglu_backward_persistent(gpu):
     """Saved bf16 g|u at a size that fills a round of CUs: the dh GEMM runs
     on the persistent stream (256 x 256 tiles, ragged last row tile, padded

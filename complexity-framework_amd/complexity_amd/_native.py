@@ -158,7 +158,7 @@ SIGNATURES = {
     "trmoe_weight_grad_mapped": (
         _c_int,
         [_c_int, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _c_vp,
-         _c_vp, _c_vp, _c_size, _c_vp],
+         _c_vp, _c_i64, _c_vp, _c_size, _c_vp],
     ),
     "trmoe_grouped_linear": (
         _c_int,

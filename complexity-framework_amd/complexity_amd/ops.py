@@ -769,14 +769,15 @@ def weight_grad_mapped(a: torch.Tensor, b: torch.Tensor, m: int, n: int, n_rows:
                        map_off: torch.Tensor, map_stride: torch.Tensor, out: torch.Tensor) -> None:
     """sum_t a[t, i] * b[t, j] over rows t < n_rows written into `out` (flat,
     bf16) at map_off[i] + j * map_stride[i] (mode 1) or map_off[j] + i *
-    map_stride[j] (mode 2); negative offsets are skipped."""
+    map_stride[j] (mode 2); negative offsets, and destinations outside
+    `out`, are skipped."""
     lib = _lib()
     _require_cuda(a, b, map_off, map_stride, out)
     ws_bytes = lib.trmoe_weight_grad_mapped_workspace_bytes(dtype_code(a.dtype), m, n, n_rows)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device)
     st = lib.trmoe_weight_grad_mapped(dtype_code(a.dtype), _p(a), a.stride(0), a.shape[0], _p(b), b.stride(0),
-                                      b.shape[0], m, n, n_rows, mode, _p(map_off), _p(map_stride), _p(out), _p(ws),
-                                      ws_bytes, _stream(a))
+                                      b.shape[0], m, n, n_rows, mode, _p(map_off), _p(map_stride), _p(out), out.numel(),
+                                      _p(ws), ws_bytes, _stream(a))
     N.check(st, "trmoe_weight_grad_mapped")
 
 

@@ -44,6 +44,7 @@ from .capabilities import (
 )
 from .config import SUPPORTED_EXPERT_COUNTS, GraphBucket, TRHashBackend, TRHashEngineConfig, TRHashPhase, TRHashPrecision
 from .routing import build_route_table, compile_top2_pair_metadata
+from . import weights
 
 logger = logging.getLogger(__name__)
 
@@ -243,17 +244,12 @@ class TRHashEngine(nn.Module):
                 nn.init.normal_(m.weight, mean=0.0, std=std)
 
     # ------------------------------------------------------------------ fp8
-    def _master(self, name: str) -> Optional[torch.Tensor]:
-        if name.startswith("shared_"):
-            mod = getattr(self, name)
-            return None if mod is None else mod.weight
-        return getattr(self, name)
-
     def quantize_fp8_(self) -> None:
         """(Re)build the e4m3 weight copies and per-output-channel scales from
         the current parameters; forwards then use q * scale."""
+        masters = weights.materialize(self)
         for name in _FP8_WEIGHTS:
-            w = self._master(name)
+            w = masters[name]
             if w is None:
                 continue
             q, s = _quantize_e4m3(w)
@@ -339,28 +335,27 @@ class TRHashEngine(nn.Module):
     def _hip_act_dtype(self) -> torch.dtype:
         if self._fp8:
             return torch.bfloat16
-        dt = self.expert_gate.dtype
+        dt = weights.stored_dtype(self, "expert_gate")
         if dt not in (torch.float32, torch.bfloat16):
             raise NotImplementedError(f"HIP kernels support float32/bfloat16/fp8 weights, got {dt}")
         return dt
 
-    def _hip_sources(self):
-        if self._fp8:
-            names = [n for n in _FP8_WEIGHTS if hasattr(self, n + "_fp8")]
-            return [getattr(self, n + suffix) for n in names for suffix in ("_fp8", "_scale")]
-        srcs = [self.expert_gate, self.expert_up, self.expert_down]
-        if self.shared_gate is not None:
-            srcs += [self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight]
-        return srcs
+    def _hip_packed(self, norm_weight: Optional[torch.Tensor] = None,
+                    current: Optional[dict] = None) -> ops.PackedLayer:
+        """Weights in kernel layout, rebuilt when what a weight would
+        materialise to or the active capacity changes.
 
-    def _hip_packed(self, norm_weight: Optional[torch.Tensor] = None) -> ops.PackedLayer:
-        """Weights in kernel layout, rebuilt when a source tensor or the active
-        capacity changes (keyed on storage pointer and in-place version).
+        The key never materialises a weight: ordinary tensors are keyed on
+        storage pointer and in-place version, a parametrized weight (the
+        reference's expert LoRA, lora.py:93-215) on every tensor of its
+        parametrization, a shared LoRA adapter on its base and factors.  A
+        parametrization in training mode is not cached.  current: the weights
+        this call already materialised (weights.materialize), used when the
+        pack has to be rebuilt; otherwise they are materialised here, once.
 
         norm_weight: a block's RMSNorm weight folded into the gate/up weights
         (their input axis), for forward_norm_residual; cached apart from the
         plain pack."""
-        srcs = self._hip_sources()
         E, W = self._active_num_experts, self._active_expert_width
         strategy = self.routed_strategy
         if strategy == "auto":
@@ -369,27 +364,39 @@ class TRHashEngine(nn.Module):
             raise NotImplementedError("the dense-routed strategy needs bf16/f32 weights")
         if norm_weight is not None and self._fp8:
             raise NotImplementedError("the fused RMSNorm folds its weight into bf16/f32 gate/up weights")
-        key = (
-            tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in srcs),
-            E,
-            W,
-            strategy,
-            None if norm_weight is None else (norm_weight.data_ptr(), norm_weight._version, norm_weight.dtype),
-        )
+        if self._fp8:
+            names = [n for n in _FP8_WEIGHTS if hasattr(self, n + "_fp8")]
+            wkey = tuple(weights._tkey(getattr(self, n + sfx)) for n in names for sfx in ("_fp8", "_scale"))
+        else:
+            wkey = weights.weights_key(self)
+        key = None
+        if wkey is not None:
+            key = (
+                wkey,
+                E,
+                W,
+                strategy,
+                None if norm_weight is None else (norm_weight.data_ptr(), norm_weight._version, norm_weight.dtype),
+            )
         if norm_weight is not None:
             cached = self._packed_norm
-            if cached is not None and cached[0] == key:
+            if key is not None and cached is not None and cached[0] == key:
                 return cached[1]
-            packed = self._build_packed(E, W, strategy, norm_weight)
-            self._packed_norm = (key, packed)
-            return packed
-        if self._packed is not None and self._packed_key == key:
+        elif key is not None and self._packed is not None and self._packed_key == key:
             return self._packed
-        packed = self._build_packed(E, W, strategy, None)
-        self._packed, self._packed_key = packed, key
+        if current is None and not self._fp8:
+            current = weights.materialize(self)
+        packed = self._build_packed(E, W, strategy, norm_weight, current)
+        if norm_weight is not None:
+            self._packed_norm = (key, packed)
+        else:
+            self._packed, self._packed_key = packed, key
         return packed
 
-    def _build_packed(self, E: int, W: int, strategy: str, norm_weight: Optional[torch.Tensor]) -> ops.PackedLayer:
+    def _build_packed(self, E: int, W: int, strategy: str, norm_weight: Optional[torch.Tensor],
+                      cw: Optional[dict]) -> ops.PackedLayer:
+        """cw: name -> weight as materialised for this call (None for e4m3 packs)."""
+
         def fold(w: torch.Tensor, shape) -> torch.Tensor:
             # W * norm_weight along the input axis, rounded once to w's dtype
             if norm_weight is None:
@@ -400,12 +407,12 @@ class TRHashEngine(nn.Module):
             if strategy == ops.STRATEGY_DENSE:
                 shared = (None, None, None)
                 if self.shared_gate is not None:
-                    shared = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight)
+                    shared = (cw["shared_gate"], cw["shared_up"], cw["shared_down"])
                 if shared[0] is not None:
                     shared = (fold(shared[0], (1, -1)), fold(shared[1], (1, -1)), shared[2])
                 gu, dd, feats = ops.pack_dense_routed(
-                    *shared, fold(self.expert_gate[:E, :, :W], (1, -1, 1)), fold(self.expert_up[:E, :, :W], (1, -1, 1)),
-                    self.expert_down[:E, :W, :]
+                    *shared, fold(cw["expert_gate"][:E, :, :W], (1, -1, 1)), fold(cw["expert_up"][:E, :, :W], (1, -1, 1)),
+                    cw["expert_down"][:E, :W, :]
                 )
                 packed = ops.PackedLayer(
                     act_dtype=self._hip_act_dtype(),
@@ -425,9 +432,9 @@ class TRHashEngine(nn.Module):
                 egu, egu_s = ops.pack_expert_gate_up(gq, uq, gs, us)
                 ed, ed_s = ops.pack_expert_down(dq, ds)
             else:
-                egu, egu_s = ops.pack_expert_gate_up(fold(self.expert_gate[:E, :, :W], (1, -1, 1)),
-                                                     fold(self.expert_up[:E, :, :W], (1, -1, 1)))
-                ed, ed_s = ops.pack_expert_down(self.expert_down[:E, :W, :])
+                egu, egu_s = ops.pack_expert_gate_up(fold(cw["expert_gate"][:E, :, :W], (1, -1, 1)),
+                                                     fold(cw["expert_up"][:E, :, :W], (1, -1, 1)))
+                ed, ed_s = ops.pack_expert_down(cw["expert_down"][:E, :W, :])
             packed = ops.PackedLayer(
                 act_dtype=self._hip_act_dtype(),
                 num_experts=E,
@@ -446,16 +453,26 @@ class TRHashEngine(nn.Module):
                     )
                     sd, sd_s = ops.pack_linear_down(self.shared_down_fp8, self.shared_down_scale)
                 else:
-                    sgu, sgu_s = ops.pack_linear_gate_up(fold(self.shared_gate.weight, (1, -1)),
-                                                         fold(self.shared_up.weight, (1, -1)))
-                    sd, sd_s = ops.pack_linear_down(self.shared_down.weight)
+                    sgu, sgu_s = ops.pack_linear_gate_up(fold(cw["shared_gate"], (1, -1)),
+                                                         fold(cw["shared_up"], (1, -1)))
+                    sd, sd_s = ops.pack_linear_down(cw["shared_down"])
                 packed.shared_gate_up, packed.shared_gate_up_scale = sgu, sgu_s
                 packed.shared_down, packed.shared_down_scale = sd, sd_s
         return packed
 
     def _hip_forward(self, flat_x: torch.Tensor, flat_ids: torch.Tensor, decision: BackendDecision,
                      residual: Optional[torch.Tensor] = None) -> torch.Tensor:
-        packed = self._hip_packed()
+        grad = torch.is_grad_enabled() and (
+            flat_x.requires_grad
+            or (residual is not None and residual.requires_grad)
+            or weights.any_requires_grad(self)
+        )
+        # a differentiable call materialises each weight once: the same tensors
+        # feed the pack (when it is rebuilt), the autograd inputs and the
+        # backward packs (the reference fetches each expert tensor once,
+        # engine.py:461-464)
+        current = weights.materialize(self) if grad else None
+        packed = self._hip_packed(current=current)
         x = flat_x if flat_x.dtype == packed.act_dtype else flat_x.to(packed.act_dtype)
         x = x.contiguous()
         order = ops.ORDER_ASSIGNMENT if decision.partition == PARTITION_ASSIGNMENT else ops.ORDER_TOKEN
@@ -463,15 +480,11 @@ class TRHashEngine(nn.Module):
         if residual is not None:
             res = residual.reshape(-1, residual.size(-1))
             res = (res if res.dtype == packed.act_dtype else res.to(packed.act_dtype)).contiguous()
-        params = self._hip_params()
-        if torch.is_grad_enabled() and (
-            x.requires_grad
-            or (res is not None and res.requires_grad)
-            or any(p is not None and p.requires_grad for p in params)
-        ):
+        if grad:
+            params = tuple(current[n] for n in weights.WEIGHT_NAMES)
             plan = _LayerPlan(
                 packed,
-                lambda: self._hip_backward_packs(packed),
+                lambda: self._hip_backward_packs(packed, current),
                 flat_ids,
                 self._active_route_table,
                 self.config.route_weights,
@@ -495,15 +508,9 @@ class TRHashEngine(nn.Module):
             )
         return out if out.dtype == flat_x.dtype else out.to(flat_x.dtype)
 
-    def _hip_params(self):
-        """Parameters the differentiable HIP call returns gradients for."""
-        shared = (None, None, None)
-        if self.shared_gate is not None:
-            shared = (self.shared_gate.weight, self.shared_up.weight, self.shared_down.weight)
-        return (*shared, self.expert_gate, self.expert_up, self.expert_down)
-
-    def _hip_backward_packs(self, packed: ops.PackedLayer) -> ops.BackwardPacks:
-        """Transposed weight packs of the backward, cached with the forward pack."""
+    def _hip_backward_packs(self, packed: ops.PackedLayer, current: dict) -> ops.BackwardPacks:
+        """Transposed weight packs of the backward, cached with the forward pack.
+        current: the weights the forward materialised (weights.materialize)."""
         if self._bwd_packed is not None and self._bwd_packed[0] is packed:
             return self._bwd_packed[1]
         E, W = self._active_num_experts, self._active_expert_width
@@ -511,8 +518,8 @@ class TRHashEngine(nn.Module):
             bp = ops.backward_packs(
                 packed,
                 self.config.hidden_size,
-                self.shared_down.weight if self.shared_gate is not None else None,
-                self.expert_down[:E, :W, :],
+                current["shared_down"],
+                current["expert_down"][:E, :W, :],
             )
         self._bwd_packed = (packed, bp)
         return bp
@@ -557,16 +564,17 @@ class TRHashEngine(nn.Module):
             return False
         return hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())
 
-    def _shared_lora(self) -> bool:
-        mods = self._modules
-        return any(getattr(mods.get(n), "is_lora_adapter", False) for n in ("shared_gate", "shared_up", "shared_down"))
-
     def _decide(self, hidden_states: torch.Tensor) -> BackendDecision:
         # the decision depends on the frozen config, the device type, whether
-        # the call is differentiable and the shared modules; cached on those
+        # the call is differentiable, the shared modules and their adapters'
+        # dropout state; cached on those
         mods = self._modules
+        shared = tuple(mods.get(n) for n in weights.SHARED_NAMES)
         key = (hidden_states.device.type, self._needs_autograd(hidden_states), id(self.config),
-               id(mods.get("shared_gate")), id(mods.get("shared_up")), id(mods.get("shared_down")), self._fp8)
+               tuple(id(m) for m in shared),
+               tuple(m is not None and getattr(m, "is_lora_adapter", False) and weights.lora_dropout_active(m)
+                     for m in shared),
+               self._fp8)
         cached = self._decision_cache.get(key)
         if cached is not None:
             return cached
@@ -576,12 +584,13 @@ class TRHashEngine(nn.Module):
             autograd=key[1],
             quantized_weights=self._fp8,
         )
-        if decision.selected is TRHashBackend.HIP and self._shared_lora():
-            # LoRA adapters on the shared linears add a low-rank residual (with
-            # its own dropout) before the SwiGLU (engine.py:337-345); the HIP
-            # kernels compute the shared branch from one weight, so the layer
-            # runs on the universal path.
-            reason = "LoRA adapters on the shared linears run on PYTORCH"
+        reason = weights.shared_adapter_blocker(self) if decision.selected is TRHashBackend.HIP else None
+        if reason is not None:
+            # A LoRALinear on a shared linear adds a low-rank residual before
+            # the SwiGLU (engine.py:337-345).  The HIP kernels serve it by its
+            # merged weight; active LoRA dropout (or an adapter of unknown
+            # form) has no merged weight, so the layer runs on the universal
+            # path.
             if decision.requested is TRHashBackend.HIP:
                 raise RuntimeError("HIP backend: " + reason)
             decision = replace(decision, selected=TRHashBackend.PYTORCH, reasons=decision.reasons + (reason,))
@@ -628,7 +637,7 @@ class TRHashEngine(nn.Module):
         grad = torch.is_grad_enabled() and (
             hidden_states.requires_grad
             or norm_weight.requires_grad
-            or any(p is not None and p.requires_grad for p in self._hip_params())
+            or weights.any_requires_grad(self)
         )
         if (decision.selected is TRHashBackend.HIP and hidden_states.ndim == 3 and not grad and not self._fp8
                 and eps > 0.0):

@@ -926,8 +926,8 @@ size_t trmoe_weight_grad_mapped_workspace_bytes(int act_dtype, int64_t m, int64_
 
 int trmoe_weight_grad_mapped(int act_dtype, const void* a, int64_t lda, int64_t a_rows, const void* b, int64_t ldb,
                              int64_t b_rows, int64_t m, int64_t n, int64_t n_rows, int map_mode,
-                             const int64_t* map_off, const int64_t* map_stride, void* out, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             const int64_t* map_off, const int64_t* map_stride, void* out, int64_t out_elems,
+                             void* workspace, size_t workspace_bytes, void* stream) {
     TRMOE_REQUIRE(act_dtype == TRMOE_BF16, "weight_grad_mapped: bf16 only");
     TRMOE_REQUIRE(m > 0 && n > 0 && n_rows >= 0, "weight_grad_mapped: bad dimensions");
     TRMOE_REQUIRE(m % 8 == 0 && n % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0,
@@ -935,6 +935,7 @@ int trmoe_weight_grad_mapped(int act_dtype, const void* a, int64_t lda, int64_t 
     TRMOE_REQUIRE(lda >= m && ldb >= n, "weight_grad_mapped: bad leading dimension");
     TRMOE_REQUIRE(map_mode == 1 || map_mode == 2, "weight_grad_mapped: map_mode must be 1 (rows) or 2 (columns)");
     TRMOE_REQUIRE(a && b && out && map_off && map_stride && workspace, "weight_grad_mapped: null pointer");
+    TRMOE_REQUIRE(out_elems > 0, "weight_grad_mapped: out_elems must be positive");
     TRMOE_REQUIRE(aligned16(a) && aligned16(b) && aligned16(workspace),
                   "weight_grad_mapped: operands and workspace must be 16-byte aligned");
     if (a_rows * lda * 2 >= ((int64_t)1 << 31) || b_rows * ldb * 2 >= ((int64_t)1 << 31))
@@ -963,6 +964,7 @@ int trmoe_weight_grad_mapped(int act_dtype, const void* a, int64_t lda, int64_t 
     w.map_mode = map_mode;
     w.map_off = map_off;
     w.map_stride = map_stride;
+    w.out_elems = out_elems;
     return launch_wgrad(act_dtype, w, as_stream(stream));
 }
 

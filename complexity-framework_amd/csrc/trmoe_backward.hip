@@ -23,6 +23,7 @@
 #include "trmoe_gemm.h"
 #include "trmoe_tiles.h"
 #include "trmoe_pp.h"
+#include "trmoe_map.h"
 
 #include <stdlib.h>
 
@@ -863,15 +864,17 @@ __global__ __launch_bounds__(256) void k_wgrad_reduce(WgradArgs a) {
         T* out = static_cast<T*>(a.out);
         if (a.map_mode == 1) {
             const int64_t o = a.map_off[m];
-            if (o < 0) continue;
             const int64_t st = a.map_stride[m];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) out[o + (n + c) * st] = from_f32<T>(s[c]);
+            for (int c = 0; c < 4; ++c) {
+                const int64_t d = mapped_dest(o, n + c, st, a.out_elems);
+                if (d >= 0) out[d] = from_f32<T>(s[c]);
+            }
         } else if (a.map_mode == 2) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int64_t o = a.map_off[n + c];
-                if (o >= 0) out[o + m * a.map_stride[n + c]] = from_f32<T>(s[c]);
+                const int64_t d = mapped_dest(a.map_off[n + c], m, a.map_stride[n + c], a.out_elems);
+                if (d >= 0) out[d] = from_f32<T>(s[c]);
             }
         } else {
             const int64_t dst = e * a.out_expert_stride + m * a.ldo + n;

@@ -221,10 +221,12 @@ struct WgradArgs {
     float* partial;              // [E][splits][M][N] when splits > 1
     // Destination map of the summed tile (E == 1, through the reduction):
     // 0 none (out[m * ldo + n]); 1 rows: out[map_off[m] + n * map_stride[m]];
-    // 2 columns: out[map_off[n] + m * map_stride[n]]; negative offsets skip.
+    // 2 columns: out[map_off[n] + m * map_stride[n]]; negative offsets skip,
+    // and so do destinations outside [0, out_elems).
     int map_mode;
     const int64_t* map_off;
     const int64_t* map_stride;
+    int64_t out_elems;
 };
 
 int launch_pack(const PackArgs& p, hipStream_t stream);

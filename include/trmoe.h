@@ -465,14 +465,16 @@ int trmoe_weight_grad(int act_dtype, const void* a, int64_t lda, int64_t a_rows,
  * arrive as one packed [m, n] product.  The summed fp32 tile goes to
  *     map_mode 1 (rows):    out[map_off[i] + j * map_stride[i]]
  *     map_mode 2 (columns): out[map_off[j] + i * map_stride[j]]
- * in act_dtype elements; a negative map_off skips the row (column).  The
- * workspace (trmoe_weight_grad_mapped_workspace_bytes) is required.
+ * in act_dtype elements; a negative map_off skips the row (column), and a
+ * destination outside [0, out_elems) is not written (out holds out_elems
+ * elements).  The workspace (trmoe_weight_grad_mapped_workspace_bytes) is
+ * required.
  */
 size_t trmoe_weight_grad_mapped_workspace_bytes(int act_dtype, int64_t m, int64_t n, int64_t n_rows);
 int trmoe_weight_grad_mapped(int act_dtype, const void* a, int64_t lda, int64_t a_rows, const void* b, int64_t ldb,
                              int64_t b_rows, int64_t m, int64_t n, int64_t n_rows, int map_mode,
-                             const int64_t* map_off, const int64_t* map_stride, void* out, void* workspace,
-                             size_t workspace_bytes, void* stream);
+                             const int64_t* map_off, const int64_t* map_stride, void* out, int64_t out_elems,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Grouped plain GEMM over a K1 partition: y[r, :] = h[r, :] . W_e^T for the

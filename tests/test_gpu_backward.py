@@ -362,6 +362,27 @@ def test_layer_backward_active_capacity_and_residual(gpu, strategy):
     assert got["expert_down"][:, 20:].abs().max().item() == 0
 
 
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+def test_layer_backward_active_capacity_bf16_saved(gpu, strategy):
+    """bf16 at reduced active capacity above the decode sizes: the forward
+    saves g|u (and h), and the dense strategy's weight gradients come from
+    the flat mapped buffer as views, copied into full-size zero tensors."""
+    print(f"layer backward active bf16 saved {strategy}", flush=True)
+    torch.manual_seed(5)
+    engine = _engine(gpu, "bf16", 8, 2, 256, 64, 128, None, strategy)
+    engine.set_active_capacity(num_experts=4, expert_width=40)
+    ids = torch.randint(0, 5000, (2, 150), device=gpu)              # 300 tokens > 128
+    x = torch.randn(2, 150, 128, device=gpu, dtype=torch.bfloat16)
+    dout = (torch.randn(2, 150, 128, device=gpu) * 0.1).to(torch.bfloat16)
+    out, got = _hip_grads(engine, x, ids, dout)
+    assert engine._packed.strategy == strategy
+    _check(got, _oracle_grads(engine, x, ids, dout), "bf16")
+    assert got["expert_gate"][4:].abs().max().item() == 0
+    assert got["expert_up"][:, :, 40:].abs().max().item() == 0
+    assert got["expert_down"][:, 40:].abs().max().item() == 0
+    assert got["expert_down"][4:].abs().max().item() == 0
+
+
 def test_layer_backward_frozen_weights_and_no_grad_x(gpu):
     """needs_input_grad: only the requested gradients are produced."""
     torch.manual_seed(4)

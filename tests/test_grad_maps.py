@@ -68,3 +68,35 @@ def test_dense_grad_maps_skip_padding_rows_and_columns():
     c = torch.arange(coff.numel())
     cpad = ((c >= S) & (c < s_pad)) | ((c >= s_pad) & ((c - s_pad) % w_pad >= W))
     assert bool((coff[cpad] < 0).all()) and bool((coff[~cpad] >= 0).all())
+
+
+def test_mapped_destination_guard(tmp_path):
+    """trmoe::mapped_dest, the reduction's write guard, built for the host:
+    real destinations pass; a skipped row, a destination at or past out_elems
+    and a negative one (bad maps from a C-ABI caller) are not written."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc is not installed")
+    root = Path(__file__).resolve().parents[1]
+    exe = tmp_path / "map_guard"
+    subprocess.run([hipcc, "-x", "hip", "--offload-host-only", "-O1", "-I", str(root / "complexity-framework_amd/csrc"),
+                    str(root / "tests/map_guard_check.cpp"), "-o", str(exe)], check=True)
+    S, E, W, H = 256, 4, 64, 32
+    roff, rstride, coff, cstride, offs = ops._dense_grad_maps(S, E, W, H, "cpu")
+    total = int(offs[-1])
+    cases, want = [], []
+    for i in range(roff.numel()):              # every real row destination, first and last column
+        o, st = int(roff[i]), int(rstride[i])
+        for j in (0, H - 1):
+            cases.append((o, j, st, total))
+            want.append(o + j * st if o >= 0 else -1)
+    cases += [(-1, 0, 1, total), (total - 1, 0, 5, total), (total - 1, 1, 1, total), (0, total, 1, total),
+              (5, 1, -6, total), (5, 1, -5, total), (0, 3, 2, 7)]
+    want += [-1, total - 1, -1, -1, -1, 0, 6]
+    out = subprocess.run([str(exe)], input="\n".join(" ".join(map(str, c)) for c in cases), capture_output=True,
+                         text=True, check=True).stdout.split()
+    assert [int(v) for v in out] == want

@@ -520,8 +520,9 @@ def test_mlp_adapter_exposes_dynamic_capacity_controls():
 
 
 def test_shared_lora_adapters_resolve_to_pytorch_with_reason(monkeypatch):
-    """LoRA adapters on the shared linears (reference engine.py:337-345) keep
-    the layer on the universal path; an explicit HIP request raises."""
+    """A shared adapter without LoRALinear's surface (reference
+    engine.py:337-345, lora.py:37-90) keeps the layer on the universal path;
+    an explicit HIP request raises."""
     import types
 
     from complexity_amd.tr_hash import TRHashEngine
@@ -549,6 +550,129 @@ def test_shared_lora_adapters_resolve_to_pytorch_with_reason(monkeypatch):
         hip = TRHashEngine(_config(backend=TRHashBackend.HIP))
         hip.shared_up = _Adapter(hip.shared_up)
         with pytest.raises(RuntimeError, match="LoRA"):
+            hip._decide(fake_cuda)
+
+
+class _LinearLoRA(torch.nn.Module):
+    """LoRALinear's surface (reference complexity/training/lora.py:37-90)."""
+
+    is_lora_adapter = True
+
+    def __init__(self, base, rank=3, alpha=6.0, dropout=0.0, dtype=torch.float64):
+        super().__init__()
+        self.base = base.to(dtype)
+        self.scaling = alpha / rank
+        self.dropout = torch.nn.Dropout(dropout) if dropout else torch.nn.Identity()
+        self.lora_A = torch.nn.Parameter(torch.randn(rank, base.in_features, dtype=dtype))
+        self.lora_B = torch.nn.Parameter(torch.randn(base.out_features, rank, dtype=dtype))
+        self.base.requires_grad_(False)
+
+    def forward(self, x):
+        return self.base(x) + torch.nn.functional.linear(
+            torch.nn.functional.linear(self.dropout(x), self.lora_A), self.lora_B) * self.scaling
+
+
+class _ExpertLoRA(torch.nn.Module):
+    """LoRAExpertTensor's parametrization surface (lora.py:93-165)."""
+
+    def __init__(self, base, rank=2):
+        super().__init__()
+        E, fan_in, fan_out = base.shape
+        self.lora_A = torch.nn.Parameter(torch.randn(E, fan_in, rank))
+        self.lora_B = torch.nn.Parameter(torch.randn(E, rank, fan_out))
+        self.calls = 0
+
+    def forward(self, base):
+        self.calls += 1
+        return torch.baddbmm(base, self.lora_A, self.lora_B, alpha=0.5)
+
+
+def test_merged_lora_weight_equals_the_adapter():
+    """The HIP backend serves a shared LoRALinear by base + scaling * B @ A:
+    same output and same factor gradients as the adapter's own two-step
+    forward (f64, eval)."""
+    from complexity_amd.tr_hash import weights as Wt
+
+    torch.manual_seed(3)
+    a = _LinearLoRA(torch.nn.Linear(24, 40, bias=False))
+    x = torch.randn(7, 24, dtype=torch.float64)
+    dy = torch.randn(7, 40, dtype=torch.float64)
+    direct = a(x)
+    gA, gB = torch.autograd.grad(direct, [a.lora_A, a.lora_B], dy)
+    merged = torch.nn.functional.linear(x, Wt.merged_lora_weight(a))
+    mA, mB = torch.autograd.grad(merged, [a.lora_A, a.lora_B], dy)
+    assert torch.allclose(merged, direct, rtol=0, atol=1e-12)
+    assert torch.allclose(mA, gA, rtol=0, atol=1e-10) and torch.allclose(mB, gB, rtol=0, atol=1e-10)
+
+
+def test_weights_key_follows_parametrized_factors_without_materialising():
+    """The pack cache key changes when a parametrization's factor changes in
+    place, never materialises a weight, and is None (not cacheable) while a
+    parametrization is in training mode; materialize() runs each once."""
+    from torch.nn.utils import parametrize
+
+    from complexity_amd.tr_hash import weights as Wt
+
+    engine = TRHashEngine(_config())
+    engine.requires_grad_(False)
+    adapters = {}
+    for name in Wt.EXPERT_NAMES:
+        adapters[name] = _ExpertLoRA(getattr(engine, name))
+        parametrize.register_parametrization(engine, name, adapters[name])
+        adapters[name].calls = 0                     # registration evaluates it once
+    engine.eval()
+    k1 = Wt.weights_key(engine)
+    assert k1 is not None and Wt.weights_key(engine) == k1
+    assert all(a.calls == 0 for a in adapters.values())
+    assert Wt.stored_dtype(engine, "expert_gate") == torch.float32
+    with torch.no_grad():
+        adapters["expert_up"].lora_B.add_(1.0)
+    k2 = Wt.weights_key(engine)
+    assert k2 != k1
+    with torch.no_grad():
+        engine.parametrizations["expert_down"].original.mul_(2.0)
+    assert Wt.weights_key(engine) != k2
+    got = Wt.materialize(engine)
+    assert [a.calls for a in adapters.values()] == [1, 1, 1]
+    assert torch.equal(got["expert_up"], adapters["expert_up"](engine.parametrizations["expert_up"].original))
+    engine.train()
+    assert Wt.weights_key(engine) is None
+
+    # shared LoRA adapters: keyed on base and factors
+    plain = TRHashEngine(_config()).eval()
+    plain.shared_gate = _LinearLoRA(plain.shared_gate, dtype=torch.float32)
+    k3 = Wt.weights_key(plain)
+    with torch.no_grad():
+        plain.shared_gate.lora_A.mul_(0.5)
+    assert Wt.weights_key(plain) != k3
+
+
+def test_shared_lora_with_merged_weights_selects_hip(monkeypatch):
+    """LoRALinear adapters keep the HIP backend while their dropout is
+    inactive; active dropout (training mode, p > 0) resolves to PYTORCH with a
+    reason, and an explicit HIP request raises."""
+    import types
+
+    from complexity_amd.tr_hash import capabilities as caps
+
+    monkeypatch.setattr(caps, "_hip_available", lambda: True)
+    fake_cuda = types.SimpleNamespace(device=types.SimpleNamespace(type="cuda"), requires_grad=False)
+    with torch.no_grad():
+        engine = TRHashEngine(_config())
+        for name in ("shared_gate", "shared_up", "shared_down"):
+            setattr(engine, name, _LinearLoRA(getattr(engine, name), dropout=0.1, dtype=torch.float32))
+        engine.eval()
+        assert engine._decide(fake_cuda).selected is TRHashBackend.HIP
+        engine.train()
+        d = engine._decide(fake_cuda)
+        assert d.selected is TRHashBackend.PYTORCH and any("LoRA dropout" in r for r in d.reasons)
+        engine.shared_up.dropout = torch.nn.Identity()
+        engine.shared_gate.dropout.p = 0.0
+        engine.shared_down.dropout.p = 0.0
+        assert engine._decide(fake_cuda).selected is TRHashBackend.HIP
+        hip = TRHashEngine(_config(backend=TRHashBackend.HIP))
+        hip.shared_gate = _LinearLoRA(hip.shared_gate, dropout=0.1, dtype=torch.float32)
+        with pytest.raises(RuntimeError, match="LoRA dropout"):
             hip._decide(fake_cuda)
 
 

@@ -64,9 +64,11 @@ def test_no_alloc_route_sort_matches_the_workspace_call(gpu, order):
     rng = np.random.default_rng(41 + order)
     table16 = torch.from_numpy(O.multi_hash_table(32000, 16, 2, 0)).to(gpu)
     table4 = torch.from_numpy(O.multi_hash_table(32000, 4, 2, 0)).to(gpu)
-    # multi-block (256 blocks x 16 experts of histogram), a smaller
-    # multi-block call, then one block (no scratch)
-    cases = [(70000, table16, 16), (20000, table4, 4), (300, table16, 16)]
+    # 32768 tokens x 2 slots = 256 chunks of 256 items: 256 blocks x 16
+    # experts, the whole 16 KiB scratch; then 70000 tokens (547 chunks, 3 per
+    # block, 183 blocks), 20000 tokens at E = 4 (157 blocks), and one block
+    # (no scratch)
+    cases = [(32768, table16, 16), (70000, table16, 16), (20000, table4, 4), (300, table16, 16)]
     for n, table, E in cases:
         ids = torch.from_numpy(rng.integers(-5, 32005, n)).to(gpu)
         want = _with_workspace(lib, ids, table, E, order)

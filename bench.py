@@ -194,6 +194,7 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
         torch.cuda.synchronize()
         gc.collect()
         gc.disable()
+        sustain(torch, fn, 3)
         s, t = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for _ in range(n):
@@ -216,8 +217,6 @@ def decode_hbm(torch, workloads, dev, w=None, layers: int = 16, steps: int = 50,
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             fn()
-        for _ in range(warmup):
-            graph.replay()
         return graph
 
     with torch.no_grad():
@@ -286,6 +285,30 @@ def c5_layer(torch, workloads, ops, dev, steps: int = 10, warmup: int = 3):
             "kernels": kernels, "roofline": roof}
 
 
+def c1_layer(torch, workloads, ops, dev, steps: int = 50, warmup: int = 10, cpu: bool = True):
+    """C1: the fp32 layer at 2048 tokens (4 x 512, uniform ids), the
+    reference's CPU-runnable case, on the HIP backend.  The fp32 GEMMs run on
+    v_mfma_f32_32x32x2f32, so the roofline uses the fp32 matrix peak; the CPU
+    oracle runs beside it on all 2048 tokens."""
+    w = workloads.C1
+    engine = workloads.build_engine(w, dev, backend="hip")
+    x = workloads.make_hidden(w).to(dev)
+    ids = workloads.make_token_ids(w).to(dev)
+    timer = KernelTimer(ops, torch)
+    try:
+        ms, kernel_ms, _, strategy = time_engine(torch, engine, x, ids, steps, warmup, timer)
+    finally:
+        timer.restore()
+    kernels, _, roof = kernel_report(w, kernel_ms, strategy)
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    out = {"workload": w.name, "dtype": "f32", "ms_per_layer": ms, "tokens_per_s": w.tokens / (ms * 1e-3),
+           "layer_tflops": tflops, "layer_mfma_frac": tflops / PEAK["fp32"], "strategy": strategy,
+           "kernels": kernels, "roofline": roof}
+    if cpu:
+        out["cpu_baseline"] = cpu_baseline(w, w.tokens)
+    return out
+
+
 def c4_e2e(torch, dev, steps: int = 128, reps: int = 3):
     """C4 end to end: the 16-layer TR-GQA 200M decoder (complexity_amd.decoder,
     random-init bf16, HIP TR-MoE layer in every block, SDPA attention).
@@ -312,10 +335,10 @@ def c4_e2e(torch, dev, steps: int = 128, reps: int = 3):
         return torch.cuda.Event(enable_timing=True)
 
     with torch.no_grad():
-        prefill()
-        torch.cuda.synchronize()
         gc.collect()
         gc.disable()
+        prefill()
+        torch.cuda.synchronize()
         pre = []
         for _ in range(reps):
             s, e = ev(), ev()
@@ -358,8 +381,7 @@ def c4_e2e(torch, dev, steps: int = 128, reps: int = 3):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             mlps()
-        for _ in range(5):
-            graph.replay()
+        sustain(torch, graph.replay, 5)
         s, e = ev(), ev()
         s.record()
         for _ in range(steps):
@@ -403,12 +425,10 @@ def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
         out = engine(xg, ids)
         out.backward(dout)
 
-    for _ in range(warmup):
-        step()
-    assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
-    torch.cuda.synchronize()
     gc.collect()
     gc.disable()
+    warm = sustain(torch, step, warmup)
+    assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -419,7 +439,32 @@ def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
     ms = start.elapsed_time(stop) / steps
     engine.zero_grad(set_to_none=True)
     return {"workload": w.name, "steps": steps, "ms_per_step_fwd_bwd": ms,
-            "tokens_per_s": w.tokens / (ms * 1e-3), "useful_tflops": 3 * w.flops() / (ms * 1e-3) / 1e12}
+            "tokens_per_s": w.tokens / (ms * 1e-3), "useful_tflops": 3 * w.flops() / (ms * 1e-3) / 1e12, **warm}
+
+
+# The MI355X raises its clocks over the first tens of ms of sustained load
+# (measured: a C2 layer step takes 338 us right after five warm-up steps and
+# 277-280 us once ~60 steps have run back to back; after 1 s idle it ramps
+# again).  Every leg therefore warms up for at least W steps AND at least
+# WARM_S seconds of back-to-back work before its timed region, so that the
+# timed steps measure the steady state, not the ramp.
+WARM_S = 0.3
+
+
+def sustain(torch, fn, min_iters: int, min_s: float = WARM_S) -> dict:
+    """Run fn at least min_iters times and until min_s seconds have passed;
+    returns {"warmup_iters": n, "warmup_s": t}."""
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn()
+        n += 1
+        if n >= min_iters and n % 4 == 0:
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= min_s:
+                break
+    torch.cuda.synchronize()
+    return {"warmup_iters": n, "warmup_s": time.perf_counter() - t0}
 
 
 def time_engine(torch, engine, x, ids, steps, warmup, timer):
@@ -431,15 +476,14 @@ def time_engine(torch, engine, x, ids, steps, warmup, timer):
 
     timer.events = {n: [] for n in timer.NAMES}
     with torch.no_grad():
-        for _ in range(warmup):
-            engine(x, ids)
-        assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
-        torch.cuda.synchronize()
         # a full collection of the interpreter's heap (torch's import leaves
         # millions of objects) stalls the host for ~40 ms; keep it out of the
-        # timed region, as timeit does
+        # timed region, as timeit does, and before the warm-up: the GPU idles
+        # meanwhile and its clocks drop
         gc.collect()
         gc.disable()
+        warm = sustain(torch, lambda: engine(x, ids), warmup)
+        assert engine.last_backend.selected is TRHashBackend.HIP, engine.last_backend
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         start.record()
@@ -454,6 +498,7 @@ def time_engine(torch, engine, x, ids, steps, warmup, timer):
         torch.cuda.synchronize()
         timer.enabled = False
         gc.enable()
+    time_engine.last_warm = warm
     return start.elapsed_time(stop) / steps, timer.averages_ms(), wall, engine._packed.strategy
 
 
@@ -516,6 +561,7 @@ def main():
     ap.add_argument("--no-train", action="store_true", help="skip the forward+backward (autograd) timing")
     ap.add_argument("--no-c4", action="store_true", help="skip the 16-layer TR-GQA decoder (C4) end to end")
     ap.add_argument("--no-c5", action="store_true", help="skip the fp8 W8A16 layer (C5)")
+    ap.add_argument("--no-c1", action="store_true", help="skip the fp32 C1 layer (2048 tokens) and its CPU leg")
     ap.add_argument("--no-block", action="store_true",
                     help="skip the decode block legs (the C3 MLP half with its norm fused / unfused)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -543,6 +589,7 @@ def main():
 
     timer = KernelTimer(ops, torch)
     ms_per_step, kernel_ms, wall, strategy = time_engine(torch, engine, x, ids, args.steps, args.warmup, timer)
+    head_warm = time_engine.last_warm
     kernels, dominant, roof = kernel_report(w, kernel_ms, strategy)
     secondary = {}
     other = "grouped" if strategy == "dense" and not args.no_other else None
@@ -564,6 +611,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": head_warm["warmup_iters"],
+        "warmup_s": head_warm["warmup_s"],
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -602,6 +651,8 @@ def main():
             }
     if not args.no_c4:
         result["c4_e2e"] = c4_e2e(torch, dev)
+    if not args.no_c1 and w.name != workloads.C1.name:
+        result["c1"] = c1_layer(torch, workloads, ops, dev, cpu=not args.no_cpu)
     if not args.no_c5 and w.name != workloads.C5.name:
         result["c5"] = c5_layer(torch, workloads, ops, dev)
     if not args.no_cpu:

@@ -1012,6 +1012,26 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     }
 }
 
+// Tile of a 1-D down launch over tiles_m x tiles_n 256 x 256 tiles.
+// Workgroups go to the 8 XCDs round-robin (id % 8).  With tiles_m a multiple
+// of 8, XCD x takes row tiles x, x + 8, ..., each with every column tile in
+// consecutive ids, so a round reads each row panel of h into one L2 once
+// and all its column tiles use it there (C5: 128 x 8 tiles, 4 rounds; in
+// row-fastest order each h panel came back in all four rounds from HBM, 369 MB
+// of h being more than the 256 MB Infinity Cache).  Other shapes: row tiles
+// fastest.
+__device__ __forceinline__ void down_tile(uint32_t id, uint32_t tiles_m, uint32_t tiles_n, uint32_t& mt,
+                                          uint32_t& nt) {
+    if ((tiles_m & 7) == 0) {
+        const uint32_t x = id & 7, j = id >> 3;
+        nt = j % tiles_n;
+        mt = x + 8 * (j / tiles_n);
+    } else {
+        mt = id % tiles_m;
+        nt = id / tiles_m;
+    }
+}
+
 // K4 on the ping-pong main loop (bf16 activations; bf16 or, FP8, e4m3
 // weights expanded at the fragment read; K a multiple of 64): 256x256 tiles
 // over the hidden columns; weight rows past the hidden size load as zero (the
@@ -1028,8 +1048,10 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     const int group = wave >> 2, wig = wave & 3;
     const int wm0 = group * (BM / 2), wn0 = wig * 64;
     const int lane = threadIdx.x & 63;
-    const int64_t m0 = (int64_t)blockIdx.x * BM;
-    const int64_t n0 = (int64_t)blockIdx.y * BN;
+    uint32_t mt, nt;
+    down_tile(blockIdx.x, (uint32_t)((a.M + BM - 1) / BM), (uint32_t)((a.N + BN - 1) / BN), mt, nt);
+    const int64_t m0 = (int64_t)mt * BM;
+    const int64_t n0 = (int64_t)nt * BN;
 
     // y row of each (tile row, slot), clamped so that a malformed inverse
     // cannot become a wild read; gathered before any direct load is issued
@@ -1470,7 +1492,7 @@ static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
 // ping-pong main loop.
 template <bool FP8>
 static int launch_down_pp(const DownArgs& a, hipStream_t stream) {
-    const dim3 grid((unsigned)((a.M + 255) / 256), (unsigned)((a.N + 255) / 256));
+    const dim3 grid((unsigned)(((a.M + 255) / 256) * ((a.N + 255) / 256)));
     using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
     constexpr int kEpi = 256 * (256 * 2 + 16);   // the bf16 output tile, over the stages
     constexpr int kLds = kEpi > 2 * Lay::kStage ? kEpi : 2 * Lay::kStage;

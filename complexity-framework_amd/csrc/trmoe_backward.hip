@@ -313,8 +313,8 @@ __device__ __forceinline__ void swiglu_bwd_pairs(const SwigluBwdArgs& a, const f
                     mult = tw;
                 }
             }
-            const bf16x2 g2 = __builtin_bit_cast(bf16x2, gv[buf][p]);
-            const bf16x2 u2 = __builtin_bit_cast(bf16x2, uv[buf][p]);
+            const bf16x2 g2 = __builtin_bit_cast(bf16x2, (uint32_t)gv[buf][p]);
+            const bf16x2 u2 = __builtin_bit_cast(bf16x2, (uint32_t)uv[buf][p]);
             float dg[2], du[2], hv[2];
 #pragma unroll
             for (int q = 0; q < 2; ++q) {

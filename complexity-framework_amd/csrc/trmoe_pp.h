@@ -565,19 +565,25 @@ __device__ __forceinline__ void store_bf16_pairs(__amdgpu_buffer_rsrc_t rsrc, in
 // Tile i of a persistent launch over tiles_m x tiles_n tiles -> (row tile,
 // column tile).  Workgroups are dispatched to the 8 XCDs round-robin, so tile
 // i runs on XCD i % 8.  With xcd_rows, XCD x owns the row tiles
-// [x mpx, x mpx + mpx), mpx = tiles_m / 8, and walks them in groups of bm
-// (4 when mpx allows): row fastest within a group, then every column tile,
-// then the next group.  The 32 workgroups of an XCD that run together then
-// hold bm row panels x 32 / bm column panels (4 x 8), which read each K slice
-// of 12 panels per round instead of 18 for 16 x 2.  Other shapes walk row
+// [x mpx, x mpx + mpx), mpx = tiles_m / 8, in groups of bm (4 when mpx
+// allows), so that the 32 workgroups of an XCD that run together hold
+// bm row panels x 32 / bm column panels (4 x 8), which read each K slice of
+// 12 panels per round instead of 18 for 16 x 2.  The column tiles are walked
+// in bands of 32 / bm; within a band the row groups alternate fastest, so
+// consecutive rounds of an XCD keep their weight panels and change only the
+// activation panels (C2 gate|up: 178 -> 175 us).  Other shapes walk row
 // tiles first.
 __device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, uint32_t tiles_n, bool xcd_rows,
                                          uint32_t& mt, uint32_t& nt) {
     if (xcd_rows) {
         const uint32_t mpx = tiles_m >> 3, j = i >> 3;
         const uint32_t bm = (mpx & 3) == 0 ? 4 : ((mpx & 1) == 0 ? 2 : 1);
-        const uint32_t rest = j / bm, mg = rest / tiles_n;
-        nt = rest - mg * tiles_n;
+        const uint32_t ng = mpx / bm, cb = 32 / bm;
+        const uint32_t rest = j / bm;                          // (row group, column) pair in walk order
+        const uint32_t band = rest / (cb * ng), in = rest - band * cb * ng;
+        const uint32_t wb = tiles_n - band * cb < cb ? tiles_n - band * cb : cb;   // the last band may be narrower
+        const uint32_t mg = in / wb;
+        nt = band * cb + (in - mg * wb);
         mt = (i & 7) * mpx + mg * bm + (j - rest * bm);
     } else {
         nt = i / tiles_m;

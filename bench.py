@@ -442,6 +442,60 @@ def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
             "tokens_per_s": w.tokens / (ms * 1e-3), "useful_tflops": 3 * w.flops() / (ms * 1e-3) / 1e12, **warm}
 
 
+def norm_train(torch, engine, w, x, ids, steps: int = 20, warmup: int = 5):
+    """The block's MLP half under autograd (forward_norm_residual, whose
+    RMSNorm runs on trmoe_rmsnorm_forward/_backward there), and the norm
+    alone on those kernels against the reference's torch formula
+    (norms.py:53-55 under autograd), forward + backward each.  The norm's
+    HBM roofline: x and y (forward), then x, dy and dx (backward) once each,
+    5 N H element bytes."""
+    from complexity_amd.tr_hash.hip_autograd import RMSNormFunction
+
+    h = x.shape[-1]
+    nw = (torch.rand(h, device=x.device) + 0.5).to(x.dtype).requires_grad_(True)
+    xg = x.detach().clone().requires_grad_(True)
+    dout = (torch.randn(x.shape, device=x.device) * 0.1).to(x.dtype)
+    flat = xg.detach().reshape(-1, h).requires_grad_(True)
+    dflat = dout.reshape(-1, h)
+
+    def block():
+        engine.zero_grad(set_to_none=True)
+        xg.grad = None
+        nw.grad = None
+        engine.forward_norm_residual(xg, ids, nw, 1e-6).backward(dout)
+
+    def norm_hip():
+        flat.grad = None
+        nw.grad = None
+        RMSNormFunction.apply(flat, nw, 1e-6).backward(dflat)
+
+    def norm_torch():
+        flat.grad = None
+        nw.grad = None
+        var = flat.pow(2).mean(-1, keepdim=True)
+        (nw * (flat * torch.rsqrt(var + 1e-6))).backward(dflat)
+
+    out = {"workload": w.name, "steps": steps}
+    gc.collect()
+    gc.disable()
+    for name, fn in (("block_ms_per_step_fwd_bwd", block), ("norm_hip_ms_fwd_bwd", norm_hip),
+                     ("norm_torch_ms_fwd_bwd", norm_torch)):
+        sustain(torch, fn, warmup)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        out[name] = start.elapsed_time(stop) / steps
+    gc.enable()
+    out["norm_path"] = engine.last_norm
+    nbytes = 5 * x.numel() * x.element_size()
+    out["norm_hip_hbm_frac"] = nbytes / (out["norm_hip_ms_fwd_bwd"] * 1e-3) / (HBM_PEAK * 1e9)
+    engine.zero_grad(set_to_none=True)
+    return out
+
+
 # The MI355X raises its clocks over the first tens of ms of sustained load
 # (measured: a C2 layer step takes 338 us right after five warm-up steps and
 # 277-280 us once ~60 steps have run back to back; after 1 s idle it ramps
@@ -636,6 +690,7 @@ def main():
         train = train_step(torch, engine, w, x, ids)
         train["backward_ms"] = train["ms_per_step_fwd_bwd"] - ms_per_step
         result["train"] = train
+        result["train_block"] = norm_train(torch, engine, w, x, ids)
     if not args.no_decode:
         result["decode"] = decode_hbm(torch, workloads, dev)
         result["decode_c4"] = decode_hbm(torch, workloads, dev, w=workloads.C4_DECODE, per_layer_tables=True)

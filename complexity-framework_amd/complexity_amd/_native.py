@@ -92,6 +92,14 @@ SIGNATURES = {
          _c_vp, _c_i64, _c_vp],
     ),
     "trmoe_rms_row_scale": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _c_vp, _c_vp]),
+    "trmoe_rmsnorm_forward": (
+        _c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_float, _c_vp, _c_i64, _c_vp, _c_vp]),
+    "trmoe_rmsnorm_backward_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "trmoe_rmsnorm_backward": (
+        _c_int,
+        [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
+         _c_vp, _c_vp, _c_size, _c_vp],
+    ),
     "trmoe_shared_gate_up_rms": (
         _c_int,
         [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_float, _c_vp, _c_i64,

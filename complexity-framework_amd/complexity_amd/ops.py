@@ -380,6 +380,85 @@ def rms_row_scale(x: torch.Tensor, eps: float) -> torch.Tensor:
     return r
 
 
+# Largest hidden size of the RMSNorm kernels (one row per wave, in registers).
+RMSNORM_MAX_HIDDEN = {torch.bfloat16: 4096, torch.float32: 2048}
+
+
+def rmsnorm_unsupported(x: torch.Tensor, weight: torch.Tensor) -> Optional[str]:
+    """Why trmoe_rmsnorm_* cannot take (x, weight) (None when it can)."""
+    if x.dtype not in RMSNORM_MAX_HIDDEN:
+        return f"RMSNorm kernels take bf16 or f32 activations, not {x.dtype}"
+    if weight.dtype != x.dtype:
+        return f"RMSNorm kernels need the norm weight in the activation dtype ({weight.dtype} vs {x.dtype})"
+    hidden = x.shape[-1]
+    if (hidden * x.element_size()) % 16 or hidden > RMSNORM_MAX_HIDDEN[x.dtype]:
+        return (f"RMSNorm kernels need hidden to be a multiple of 16 bytes of elements and at most "
+                f"{RMSNORM_MAX_HIDDEN[x.dtype]} ({hidden})")
+    return None
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    """x[n, k] with unit column stride, 16-byte aligned rows and a row stride
+    that is a multiple of 16 bytes (k * elem is one already)."""
+    if x.stride(1) == 1 and x.data_ptr() % 16 == 0 and (x.stride(0) * x.element_size()) % 16 == 0:
+        return x
+    return x.contiguous() if x.data_ptr() % 16 == 0 else x.clone(memory_format=torch.contiguous_format)
+
+
+def _vec16(w: torch.Tensor) -> torch.Tensor:
+    w = w.contiguous()
+    return w if w.data_ptr() % 16 == 0 else w.clone()
+
+
+@_on_tensor_device
+def rmsnorm_forward(x: torch.Tensor, weight: torch.Tensor, eps: float):
+    """(y, r): y = T(x * r) * weight with r[N] fp32 = 1 / sqrt(mean(x^2) + eps),
+    the reference's RMSNorm (complexity/core/normalization/norms.py:46-55, the
+    liger-kernel "llama" casting it calls on CUDA); r is what the backward
+    needs."""
+    lib = _lib()
+    _require_cuda(x)
+    reason = rmsnorm_unsupported(x, weight)
+    if reason:
+        raise ValueError(reason)
+    x = _rows(x)
+    weight = _vec16(weight)
+    n, hidden = x.shape
+    y = torch.empty(n, hidden, dtype=x.dtype, device=x.device)
+    r = torch.empty(n, dtype=torch.float32, device=x.device)
+    st = lib.trmoe_rmsnorm_forward(dtype_code(x.dtype), _p(x), n, hidden, x.stride(0), _p(weight), float(eps),
+                                   _p(y), hidden, _p(r), _stream(x))
+    N.check(st, "trmoe_rmsnorm_forward")
+    return y, r
+
+
+@_on_tensor_device
+def rmsnorm_backward(x: torch.Tensor, weight: torch.Tensor, r: torch.Tensor, dy: torch.Tensor,
+                     dres: Optional[torch.Tensor] = None):
+    """(dx, dweight) of rmsnorm_forward for the output gradient dy; dres, when
+    given, is added to dx (the residual branch's gradient of the same x)."""
+    lib = _lib()
+    _require_cuda(x)
+    reason = rmsnorm_unsupported(x, weight)
+    if reason:
+        raise ValueError(reason)
+    x, dy = _rows(x), _rows(dy.to(x.dtype))
+    dres = None if dres is None else _rows(dres.to(x.dtype))
+    weight = _vec16(weight)
+    r = r.contiguous()
+    n, hidden = x.shape
+    code = dtype_code(x.dtype)
+    dx = torch.empty(n, hidden, dtype=x.dtype, device=x.device)
+    dw = torch.empty(hidden, dtype=x.dtype, device=x.device)
+    ws_bytes = lib.trmoe_rmsnorm_backward_workspace_bytes(code, n, hidden)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    st = lib.trmoe_rmsnorm_backward(code, _p(x), n, hidden, x.stride(0), _p(weight), _p(r), _p(dy), dy.stride(0),
+                                    _p(dres), dres.stride(0) if dres is not None else 0, _p(dx), hidden, _p(dw),
+                                    _p(ws), ws_bytes, _stream(x))
+    N.check(st, "trmoe_rmsnorm_backward")
+    return dx, dw
+
+
 def _extras(row_scale: Optional[torch.Tensor] = None, rms_eps: float = 0.0, w_frag=None):
     """trmoe_call_extras for the *_ex calls; w_frag = (fragment copy, cols)."""
     e = N.CallExtras()

@@ -35,7 +35,7 @@ import torch.nn.functional as F
 
 from .. import ops
 from .buckets import GraphBucketPlanner
-from .hip_autograd import _LayerPlan, hip_layer_autograd
+from .hip_autograd import RMSNormFunction, _LayerPlan, hip_layer_autograd
 from .capabilities import (
     PARTITION_ASSIGNMENT,
     BackendDecision,
@@ -138,6 +138,7 @@ class TRHashEngine(nn.Module):
         self.reset_parameters()
 
         self.last_backend: Optional[BackendDecision] = None
+        self.last_norm: Optional[str] = None
         self._graph_pool: Dict[GraphBucket, "_CapturedTRHashGraph"] = {}
         self._bucket_planner = GraphBucketPlanner(config.graph_buckets) if config.graph_buckets else None
         self._active_num_experts = config.num_experts
@@ -628,8 +629,12 @@ class TRHashEngine(nn.Module):
         bf16/f32 weights, the norm weight is folded into the packed gate/up
         weights, each token's 1/rms scales its gate and up accumulators (the
         decode kernels compute it from the activations they already stage),
-        and the residual add runs in the down epilogue.  Otherwise the norm
-        runs as the reference writes it, then forward_with_residual."""
+        and the residual add runs in the down epilogue.  Under autograd, or
+        with fp8 weights, the norm runs on the RMSNorm kernels
+        (``RMSNormFunction``: differentiable in hidden and norm_weight) and
+        then forward_with_residual.  Otherwise (another backend, or a dtype or
+        hidden size the kernels do not take) it runs as the reference writes
+        it.  ``last_norm`` records which: "fused", "rmsnorm" or "torch"."""
         if norm_weight.shape != (hidden_states.shape[-1],):
             raise ValueError("norm_weight must have shape (hidden_size,)")
         decision = self._decide(hidden_states)
@@ -639,8 +644,17 @@ class TRHashEngine(nn.Module):
             or norm_weight.requires_grad
             or weights.any_requires_grad(self)
         )
-        if (decision.selected is TRHashBackend.HIP and hidden_states.ndim == 3 and not grad and not self._fp8
-                and eps > 0.0):
+        hip = decision.selected is TRHashBackend.HIP and hidden_states.ndim == 3 and eps > 0.0
+        if hip and (grad or self._fp8) and ops.rmsnorm_unsupported(hidden_states, norm_weight) is None:
+            b, t, h = hidden_states.shape
+            flat = hidden_states.reshape(-1, h)
+            if grad:
+                normed = RMSNormFunction.apply(flat, norm_weight, float(eps))
+            else:
+                normed, _ = ops.rmsnorm_forward(flat, norm_weight, float(eps))
+            self.last_norm = "rmsnorm"
+            return self.forward_with_residual(normed.view(b, t, h), token_ids, hidden_states)
+        if hip and not grad and not self._fp8:
             b, t, h = hidden_states.shape
             if token_ids.shape != hidden_states.shape[:2]:
                 raise ValueError("token_ids must match hidden batch/sequence dimensions")
@@ -661,9 +675,11 @@ class TRHashEngine(nn.Module):
                 norm_eps=float(eps),
             )
             out = out if out.dtype == hidden_states.dtype else out.to(hidden_states.dtype)
+            self.last_norm = "fused"
             return out.view(b, t, h)
         variance = hidden_states.pow(2).mean(-1, keepdim=True)
         normed = norm_weight * (hidden_states * torch.rsqrt(variance + eps))
+        self.last_norm = "torch"
         return self.forward_with_residual(normed, token_ids, hidden_states)
 
     def _forward_cuda_graph(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:

@@ -101,5 +101,24 @@ class HIPLayerFunction(torch.autograd.Function):
         return (None, dx if need_dx else None, dout if need_dres else None, *out_params)
 
 
+class RMSNormFunction(torch.autograd.Function):
+    """``weight * rmsnorm(x)`` (complexity/core/normalization/norms.py:46-55)
+    on the HIP kernels, differentiable in x and weight: the forward saves
+    x and each token's fp32 1/rms, the backward writes dx and the weight
+    gradient (summed over tokens in a fixed order)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
+        y, r = ops.rmsnorm_forward(x, weight, eps)
+        ctx.save_for_backward(x, weight, r)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        x, weight, r = ctx.saved_tensors
+        dx, dw = ops.rmsnorm_backward(x, weight, r, dy)
+        return (dx if ctx.needs_input_grad[0] else None, dw if ctx.needs_input_grad[1] else None, None)
+
+
 def hip_layer_autograd(plan: _LayerPlan, x: torch.Tensor, residual: Optional[torch.Tensor], params) -> torch.Tensor:
     return HIPLayerFunction.apply(plan, x, residual, *params)

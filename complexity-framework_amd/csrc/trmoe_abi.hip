@@ -287,6 +287,64 @@ int trmoe_rms_row_scale(int act_dtype, const void* x, int64_t n_tokens, int64_t 
     return launch_rms_row_scale(act_dtype, x, n_tokens, hidden, ldx, eps, row_scale, as_stream(stream));
 }
 
+static bool rmsnorm_hidden_ok(int act_dtype, int64_t hidden) {
+    return hidden > 0 && (hidden * elem_bytes(act_dtype)) % 16 == 0 && hidden <= rmsnorm_max_hidden(act_dtype);
+}
+
+int trmoe_rmsnorm_forward(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                          const void* weight, float eps, void* y, int64_t ldy, float* row_scale, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "rmsnorm_forward: bf16 or f32 activations");
+    TRMOE_REQUIRE(n_tokens >= 0, "rmsnorm_forward: n_tokens < 0");
+    TRMOE_REQUIRE(rmsnorm_hidden_ok(act_dtype, hidden),
+                  "rmsnorm_forward: hidden must be a positive multiple of 16 bytes of elements, at most 4096 bf16 "
+                  "or 2048 f32");
+    TRMOE_REQUIRE(ldx >= hidden && ldy >= hidden, "rmsnorm_forward: row stride < hidden");
+    TRMOE_REQUIRE(eps >= 0.0f, "rmsnorm_forward: eps must be non-negative");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x && weight && y && row_scale, "rmsnorm_forward: null pointer");
+    const int eb = elem_bytes(act_dtype);
+    TRMOE_REQUIRE(rows_ok(x, ldx, eb) && rows_ok(y, ldy, eb) && aligned16(weight),
+                  "rmsnorm_forward: x, y and weight must be 16-byte aligned with row strides that are multiples of "
+                  "16 bytes");
+    return launch_rmsnorm_forward(act_dtype, x, n_tokens, hidden, ldx, weight, eps, y, ldy, row_scale,
+                                  as_stream(stream));
+}
+
+size_t trmoe_rmsnorm_backward_workspace_bytes(int act_dtype, int64_t n_tokens, int64_t hidden) {
+    if ((act_dtype != TRMOE_F32 && act_dtype != TRMOE_BF16) || n_tokens < 0 || !rmsnorm_hidden_ok(act_dtype, hidden))
+        return 0;
+    return (size_t)rmsnorm_groups(n_tokens) * (size_t)hidden * sizeof(float);
+}
+
+int trmoe_rmsnorm_backward(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                           const void* weight, const float* row_scale, const void* dy, int64_t lddy,
+                           const void* dres, int64_t lddres, void* dx, int64_t lddx, void* dweight,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "rmsnorm_backward: bf16 or f32 activations");
+    TRMOE_REQUIRE(n_tokens >= 0, "rmsnorm_backward: n_tokens < 0");
+    TRMOE_REQUIRE(rmsnorm_hidden_ok(act_dtype, hidden),
+                  "rmsnorm_backward: hidden must be a positive multiple of 16 bytes of elements, at most 4096 bf16 "
+                  "or 2048 f32");
+    TRMOE_REQUIRE(ldx >= hidden && lddy >= hidden && lddx >= hidden && (dres == nullptr || lddres >= hidden),
+                  "rmsnorm_backward: row stride < hidden");
+    TRMOE_REQUIRE(dres == nullptr || dres != dx || lddres == lddx,
+                  "rmsnorm_backward: dres in place of dx needs the same row stride");
+    TRMOE_REQUIRE(weight && dweight && workspace, "rmsnorm_backward: null pointer");
+    TRMOE_REQUIRE(workspace_bytes >= trmoe_rmsnorm_backward_workspace_bytes(act_dtype, n_tokens, hidden),
+                  "rmsnorm_backward: workspace smaller than trmoe_rmsnorm_backward_workspace_bytes()");
+    const int eb = elem_bytes(act_dtype);
+    if (n_tokens > 0) {
+        TRMOE_REQUIRE(x && row_scale && dy && dx, "rmsnorm_backward: null pointer");
+        TRMOE_REQUIRE(rows_ok(x, ldx, eb) && rows_ok(dy, lddy, eb) && rows_ok(dx, lddx, eb) &&
+                          (dres == nullptr || rows_ok(dres, lddres, eb)),
+                      "rmsnorm_backward: x, dy, dres and dx must be 16-byte aligned with row strides that are "
+                      "multiples of 16 bytes");
+    }
+    TRMOE_REQUIRE(aligned16(weight), "rmsnorm_backward: weight must be 16-byte aligned");
+    return launch_rmsnorm_backward(act_dtype, x, ldx, weight, row_scale, dy, lddy, dres, lddres, n_tokens, hidden,
+                                   dx, lddx, dweight, static_cast<float*>(workspace), as_stream(stream));
+}
+
 int trmoe_shared_gate_up_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
                              int64_t ldx, const void* w_packed, const float* w_scale, int64_t shared_width,
                              const float* row_scale, float eps, void* h, int64_t ldh, void* stream) {

@@ -243,6 +243,16 @@ int launch_pack_fragments(const void* src, int64_t rows, int64_t kbytes, int64_t
 // row_scale[t] = 1 / sqrt(mean_k x[t, k]^2 + eps) in fp32 for t < n.
 int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, float eps, float* row_scale,
                          hipStream_t stream);
+// RMSNorm with its backward (trmoe_norm.hip): y = T(x * r) * w with r saved;
+// dx = r (dy w) - (r^3 / H) ((dy w) . x) x (+ dres); dw from one fp32 partial
+// per backward workgroup (rmsnorm_groups(n) of them) summed in order.
+int rmsnorm_groups(int64_t n);
+int64_t rmsnorm_max_hidden(int act);
+int launch_rmsnorm_forward(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, const void* w, float eps,
+                           void* y, int64_t ldy, float* rs, hipStream_t stream);
+int launch_rmsnorm_backward(int act, const void* x, int64_t ldx, const void* w, const float* rs, const void* dy,
+                            int64_t lddy, const void* dres, int64_t lddres, int64_t n, int64_t hidden, void* dx,
+                            int64_t lddx, void* dw, float* part, hipStream_t stream);
 int launch_down_combine(int act, int wdt, const DownArgs& a, hipStream_t stream);
 int routed_lds_bytes(int act, int64_t f_pad);
 int launch_routed(int act, int wdt, const RoutedArgs& a, int64_t assignments, hipStream_t stream);

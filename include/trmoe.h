@@ -302,6 +302,33 @@ int trmoe_dense_routed_gate_up_rms(int act_dtype, int w_dtype, const void* x, in
                                    const int64_t* route_table, int64_t vocab_size, int top_k,
                                    const float* route_weights, float shared_scale, float routed_scale,
                                    const float* row_scale, float eps, void* h, int64_t ldh, void* stream);
+/* ---------------------------------------------------------------------------
+ * RMSNorm for training (and for the fp8 layers, whose packs cannot take the
+ * norm weight).  Replaces RMSNorm.forward (complexity/core/normalization/
+ * norms.py:46-55), which on CUDA calls liger-kernel's RMSNorm
+ * (LigerRMSNormFunction.apply(x, weight, eps, 0.0, "llama", False);
+ * pyproject.toml pins liger-kernel>=0.5.0), with its autograd backward:
+ *
+ *   r_t = 1 / sqrt(mean_k x_t,k^2 + eps)       (fp32, saved to row_scale)
+ *   y_t,k = T(x_t,k * r_t) * w_k               (rounded to T twice, "llama")
+ *   dx_t,k = r_t m_t,k - (r_t^3 / hidden) (sum_j m_t,j x_t,j) x_t,k [+ dres_t,k],
+ *            m = dy * w
+ *   dw_k = sum_t dy_t,k * T(x_t,k * r_t)       (fp32 partials summed in a
+ *                                               fixed order: deterministic)
+ *
+ * act_dtype f32 or bf16 for x, weight, y, dy, dres, dx and dweight alike;
+ * rows 16-byte aligned, strides multiples of 16 bytes, hidden a multiple of
+ * 16 bytes of elements and at most 4096 (bf16) / 2048 (f32).  dres (NULL:
+ * none) is added to dx and may be dx itself (same stride).  workspace: device
+ * scratch of trmoe_rmsnorm_backward_workspace_bytes() bytes.
+ * ------------------------------------------------------------------------- */
+int trmoe_rmsnorm_forward(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                          const void* weight, float eps, void* y, int64_t ldy, float* row_scale, void* stream);
+size_t trmoe_rmsnorm_backward_workspace_bytes(int act_dtype, int64_t n_tokens, int64_t hidden);
+int trmoe_rmsnorm_backward(int act_dtype, const void* x, int64_t n_tokens, int64_t hidden, int64_t ldx,
+                           const void* weight, const float* row_scale, const void* dy, int64_t lddy,
+                           const void* dres, int64_t lddres, void* dx, int64_t lddx, void* dweight,
+                           void* workspace, size_t workspace_bytes, void* stream);
 /* row_scale required; the workspace of trmoe_routed_experts_workspace_bytes() too. */
 int trmoe_routed_experts_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
                              int64_t ldx, const int64_t* sorted_indices, const int32_t* expert_offsets,

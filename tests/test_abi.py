@@ -74,3 +74,22 @@ def test_invalid_arguments_fail_before_touching_a_device(lib):
     assert lib.trmoe_last_error()
     with pytest.raises(ValueError):
         _native.check(st, "trmoe_shared_gate_up")
+
+
+def test_rmsnorm_workspace_and_validation_without_a_device(lib):
+    """One fp32 weight partial per backward workgroup (4 rows each, at most
+    1024 of them); unsupported hidden sizes size to 0 and are rejected."""
+    bf, f32 = _native.BF16, _native.F32
+    assert lib.trmoe_rmsnorm_backward_workspace_bytes(bf, 0, 896) == 896 * 4
+    assert lib.trmoe_rmsnorm_backward_workspace_bytes(bf, 5, 896) == 2 * 896 * 4
+    assert lib.trmoe_rmsnorm_backward_workspace_bytes(bf, 16384, 896) == 1024 * 896 * 4
+    assert lib.trmoe_rmsnorm_backward_workspace_bytes(f32, 4096, 2048) == 1024 * 2048 * 4
+    for dt, hidden in ((bf, 100), (bf, 4104), (f32, 2052), (f32, 6)):
+        assert lib.trmoe_rmsnorm_backward_workspace_bytes(dt, 64, hidden) == 0
+        st = lib.trmoe_rmsnorm_forward(dt, None, 16, hidden, hidden, None, 1e-6, None, hidden, None, None)
+        assert st == _native.ERR_INVALID
+    st = lib.trmoe_rmsnorm_forward(bf, None, 16, 896, 896, None, 1e-6, None, 896, None, None)
+    assert st == _native.ERR_INVALID and b"null" in lib.trmoe_last_error()
+    st = lib.trmoe_rmsnorm_backward(bf, None, 16, 896, 896, None, None, None, 896, None, 0, None, 896, None,
+                                    None, 0, None)
+    assert st == _native.ERR_INVALID

@@ -158,3 +158,85 @@ def test_shared_gate_up_rms(gpu, dtype, n):
     else:
         with pytest.raises(ValueError, match="128"):
             ops.shared_gate_up(xg, pg, None, S, rms_eps=eps)
+
+
+def _small_engine(gpu, dtype, strategy, fp8=False):
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=256, vocab_size=5000, num_experts=4, top_k=2,
+                                             shared_width=384, expert_width=64,
+                                             routing_strategy="token_id_multi_hash", routed_output_scale=2.0,
+                                             shared_output_scale=0.5, precision="fp8" if fp8 else dtype,
+                                             backend="hip")).to(gpu)
+    if dtype != "fp32":
+        engine = engine.to(torch.bfloat16)
+    engine.routed_strategy = strategy
+    if fp8:
+        engine.quantize_fp8_()
+    return engine
+
+
+@pytest.mark.parametrize("dtype,strategy,tokens", [
+    ("fp32", "dense", 300), ("bf16", "dense", 300), ("bf16", "grouped", 300), ("bf16", "dense", 40),
+])
+def test_norm_residual_backward_on_rmsnorm_kernels(gpu, dtype, strategy, tokens):
+    """Under autograd the norm runs on the RMSNorm kernels and the MLP on the
+    HIP autograd Function: the output and the gradients of x, the norm weight
+    and two layer weights match f64 autograd of the oracle."""
+    print(f"norm residual backward {dtype} {strategy} {tokens}", flush=True)
+    dt = torch.float32 if dtype == "fp32" else torch.bfloat16
+    engine = _small_engine(gpu, dtype, strategy)
+    g = torch.Generator().manual_seed(tokens)
+    ids = torch.randint(0, 5000, (2, tokens // 2), generator=g).to(gpu)
+    x = (torch.randn(2, tokens // 2, 256, generator=g) * 2.5).to(gpu, dt)
+    nw = _norm_weight(256, gpu, dt).requires_grad_(True)
+    dout = (torch.randn(2, tokens // 2, 256, generator=g) * 0.1).to(gpu, dt)
+    xg = x.detach().clone().requires_grad_(True)
+    out = engine.forward_norm_residual(xg, ids, nw, 1e-6)
+    assert engine.last_norm == "rmsnorm"
+    out.backward(dout)
+    torch.cuda.synchronize()
+
+    cfg = engine.config
+    d = torch.float64
+    leaves = {"x": x.detach().cpu().to(d).requires_grad_(True), "nw": nw.detach().cpu().to(d).requires_grad_(True)}
+    p = {k: v.to(d) for k, v in _params(engine).items()}
+    for k in ("shared_down", "expert_gate"):
+        p[k] = leaves[k] = p[k].clone().requires_grad_(True)
+    ref = O.engine_forward_norm_residual(
+        leaves["x"], ids.cpu(), engine._active_route_table.cpu(), p, leaves["nw"], 1e-6,
+        route_weights=cfg.route_weights, shared_scale=cfg.shared_output_scale, routed_scale=cfg.routed_output_scale)
+    names = list(leaves)
+    grads = dict(zip(names, torch.autograd.grad(ref, [leaves[n] for n in names], dout.detach().cpu().to(d))))
+    got = {"x": xg.grad, "nw": nw.grad, "shared_down": engine.shared_down.weight.grad,
+           "expert_gate": engine.expert_gate.grad}
+    bound = BOUND[dtype]
+    assert O.normwise_rel_err(out.detach(), ref.detach()) <= bound
+    for n in names:
+        assert got[n] is not None, n
+        assert O.normwise_rel_err(got[n].float().cpu(), grads[n]) <= bound, (n, O.normwise_rel_err(got[n], grads[n]))
+
+
+def test_norm_residual_fp8_runs_the_rmsnorm_kernel(gpu):
+    """fp8 weights cannot take the norm weight in their packs: the norm runs on
+    the RMSNorm kernel, then the fp8 layer (against the oracle on the
+    dequantised weights, bound 5e-2)."""
+    engine = _small_engine(gpu, "bf16", "grouped", fp8=True)
+    g = torch.Generator().manual_seed(8)
+    ids = torch.randint(0, 5000, (1, 700), generator=g).to(gpu)
+    # small x (the norm is scale-free) so that out - x keeps the MLP term's bits
+    x = (torch.randn(1, 700, 256, generator=g) * 0.02).to(gpu, torch.bfloat16)
+    nw = _norm_weight(256, gpu, torch.bfloat16)
+    with torch.no_grad():
+        out = engine.forward_norm_residual(x, ids, nw, 1e-6)
+    torch.cuda.synchronize()
+    assert engine.last_norm == "rmsnorm"
+    p = {}
+    for n in ("expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up", "shared_down"):
+        p[n] = O.dequantize_e4m3(getattr(engine, n + "_fp8").cpu(), getattr(engine, n + "_scale").cpu(), 1)
+    cfg = engine.config
+    ref = O.engine_forward(O.rms_norm(x.float().cpu(), nw.float().cpu(), 1e-6), ids.cpu(),
+                           engine._active_route_table.cpu(), p, route_weights=cfg.route_weights,
+                           shared_scale=cfg.shared_output_scale, routed_scale=cfg.routed_output_scale)
+    mlp = out.float().cpu() - x.float().cpu()
+    assert O.normwise_rel_err(mlp, ref) <= 5e-2

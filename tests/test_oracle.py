@@ -405,6 +405,35 @@ def test_rms_norm_constant_rows_closed_form():
     assert torch.allclose(y[1], -w, atol=1e-12)
 
 
+@pytest.mark.parametrize("eps", [1e-6, 0.5])
+def test_rms_norm_gradients_match_central_differences(eps):
+    """The RMSNorm kernels' backward is checked against autograd of the
+    oracle; that autograd is pinned here by central differences of
+    <rms_norm(x, w), dout> in f64, entry by entry in x and w (a large eps
+    keeps its term visible)."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(3, 8, generator=g, dtype=torch.float64) * 2.0).requires_grad_(True)
+    w = (torch.rand(8, generator=g, dtype=torch.float64) + 0.5).requires_grad_(True)
+    dout = torch.randn(3, 8, generator=g, dtype=torch.float64)
+    gx, gw = torch.autograd.grad((O.rms_norm(x, w, eps) * dout).sum(), (x, w))
+
+    def f(xv, wv):
+        return float((O.rms_norm(xv, wv, eps) * dout).sum())
+
+    h = 1e-6
+    with torch.no_grad():
+        for t, grad in ((x, gx), (w, gw)):
+            flat, gflat = t.view(-1), grad.reshape(-1)
+            for i in range(flat.numel()):
+                keep = float(flat[i])
+                flat[i] = keep + h
+                up = f(x, w)
+                flat[i] = keep - h
+                down = f(x, w)
+                flat[i] = keep
+                assert abs((up - down) / (2 * h) - float(gflat[i])) <= 1e-7 * max(1.0, abs(float(gflat[i])))
+
+
 def test_norm_residual_oracle_composes():
     """engine_forward_norm_residual is x + engine_forward(rms_norm(x))."""
     g = torch.Generator().manual_seed(3)

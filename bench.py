@@ -280,9 +280,50 @@ def c5_layer(torch, workloads, ops, dev, steps: int = 10, warmup: int = 3):
         timer.restore()
     kernels, _, roof = kernel_report(w, kernel_ms, strategy)
     tflops = w.flops() / (ms * 1e-3) / 1e12
-    return {"workload": w.name, "ms_per_layer": ms, "tokens_per_s": w.tokens / (ms * 1e-3),
-            "layer_tflops": tflops, "layer_mfma_frac": tflops / PEAK["fp8"], "strategy": strategy,
-            "kernels": kernels, "roofline": roof}
+    out = {"workload": w.name, "ms_per_layer": ms, "tokens_per_s": w.tokens / (ms * 1e-3),
+           "layer_tflops": tflops, "layer_mfma_frac": tflops / PEAK["fp8"], "strategy": strategy,
+           "kernels": kernels, "roofline": roof}
+    out["w8a8"] = c5_w8a8(torch, engine, w, x, ids, ops, steps, warmup)
+    return out
+
+
+def c5_w8a8(torch, engine, w, x, ids, ops, steps: int, warmup: int):
+    """The same C5 layer with fp8_activations: x quantized per token to e4m3
+    and the shared gate|up on the e4m3 MFMA (W8A8; no reference counterpart,
+    and not C5's W8A16 configuration, so reported beside it).  The shared
+    gate|up op (quantizer + GEMM) is priced against the 5.0 PFLOP/s fp8 peak."""
+    flat = x.reshape(-1, w.hidden)
+    packed = engine._hip_packed()
+
+    def ev(fn, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    engine.fp8_activations = True
+    try:
+        with torch.no_grad():
+            gc.collect()
+            gc.disable()
+            sustain(torch, lambda: engine(x, ids), warmup)
+            layer_ms = ev(lambda: engine(x, ids), steps)
+            xq, xs = ops.quantize_rows_e4m3(flat)
+            quant_ms = ev(lambda: ops.quantize_rows_e4m3(flat), steps)
+            gemm_ms = ev(lambda: ops.shared_gate_up_a8(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale,
+                                                        packed.shared_width), steps)
+            gc.enable()
+    finally:
+        engine.fp8_activations = False
+    flops = 4.0 * w.tokens * w.hidden * w.shared
+    return {"ms_per_layer": layer_ms, "tokens_per_s": w.tokens / (layer_ms * 1e-3),
+            "quantize_us": quant_ms * 1e3, "shared_gate_up_a8_us": gemm_ms * 1e3,
+            "shared_gate_up_a8_tflops": flops / (gemm_ms * 1e-3) / 1e12,
+            "shared_gate_up_a8_fp8_frac": flops / (gemm_ms * 1e-3) / 5.0e15,
+            "shared_gate_up_a8_with_quantize_fp8_frac": flops / ((gemm_ms + quant_ms) * 1e-3) / 5.0e15}
 
 
 def c1_layer(torch, workloads, ops, dev, steps: int = 50, warmup: int = 10, cpu: bool = True):

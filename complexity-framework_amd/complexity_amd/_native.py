@@ -95,6 +95,10 @@ SIGNATURES = {
     "trmoe_rmsnorm_forward": (
         _c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_float, _c_vp, _c_i64, _c_vp, _c_vp]),
     "trmoe_rmsnorm_backward_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "trmoe_quantize_rows_e4m3": (
+        _c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp]),
+    "trmoe_shared_gate_up_a8": (
+        _c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
     "trmoe_rmsnorm_backward": (
         _c_int,
         [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,

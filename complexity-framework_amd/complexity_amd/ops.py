@@ -333,6 +333,45 @@ def shared_gate_up(x: torch.Tensor, w_packed: torch.Tensor, w_scale: Optional[to
     return h
 
 
+@_on_tensor_device
+def quantize_rows_e4m3(x: torch.Tensor):
+    """(q float8_e4m3fn [N, K], scale fp32 [N]): each row of x quantized as
+    the engine quantizes weight rows (scale = amax / 448, 1 for a zero row;
+    q = e4m3(clamp(x / scale, +-448)), ties to even)."""
+    lib = _lib()
+    _require_cuda(x)
+    if x.dtype not in RMSNORM_MAX_HIDDEN:
+        raise ValueError(f"quantize_rows_e4m3: bf16 or f32 rows, not {x.dtype}")
+    x = _rows(x)
+    n, k = x.shape
+    ldq = _round_up(k, 16)
+    q = torch.empty(n, ldq, dtype=torch.float8_e4m3fn, device=x.device)[:, :k]
+    scale = torch.empty(n, dtype=torch.float32, device=x.device)
+    st = lib.trmoe_quantize_rows_e4m3(dtype_code(x.dtype), _p(x), n, k, x.stride(0), _p(q), ldq, _p(scale),
+                                      _stream(x))
+    N.check(st, "trmoe_quantize_rows_e4m3")
+    return q, scale
+
+
+@_on_tensor_device
+def shared_gate_up_a8(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                      shared_width: int) -> torch.Tensor:
+    """W8A8 shared gate|up: h[N, round_up(S,128)] bf16 = silu(g) * u with
+    [g|u] = (x_scale * xq) (w_scale * W8)^T on the e4m3 MFMA; xq, x_scale from
+    quantize_rows_e4m3, w_packed / w_scale the layer's e4m3 pack."""
+    lib = _lib()
+    _require_cuda(xq, w_packed)
+    if xq.dtype != torch.float8_e4m3fn or w_packed.dtype != torch.float8_e4m3fn:
+        raise ValueError("shared_gate_up_a8: e4m3 activations and weights")
+    n, hidden = xq.shape
+    ldh = _round_up(shared_width, 128)
+    h = torch.empty(n, ldh, dtype=torch.bfloat16, device=xq.device)
+    st = lib.trmoe_shared_gate_up_a8(_p(xq), _p(x_scale.contiguous()), n, hidden, xq.stride(0), _p(w_packed),
+                                     _p(w_scale), shared_width, _p(h), ldh, _stream(xq))
+    N.check(st, "trmoe_shared_gate_up_a8")
+    return h
+
+
 def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Tensor, num_experts: int,
                    top_k: int, w_gate_up: torch.Tensor, s_gate_up, w_down: torch.Tensor, s_down,
                    expert_width: int, two_pass: bool = True,
@@ -665,7 +704,7 @@ class PackedLayer:
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
                   route_weights: Sequence[float], shared_scale: float, routed_scale: float,
                   order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None, save: bool = False,
-                  norm_eps: Optional[float] = None):
+                  norm_eps: Optional[float] = None, act_fp8: bool = False):
     """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual).
 
     grouped: K1 partition, K3 grouped experts, K2 shared gate|up, K4 down with
@@ -676,7 +715,9 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
     kernels themselves up to 128 tokens (dense strategy), else from
     rms_row_scale.  save: returns (out, gu, h): the raw gate|up outputs and,
     for the dense strategy, the down GEMM's input h (else None), which the
-    backward reuses."""
+    backward reuses.  act_fp8 (e4m3 packs, grouped strategy, above decode
+    sizes, hidden a multiple of 128): the shared gate|up runs W8A8 on x
+    quantized per token (quantize_rows_e4m3, shared_gate_up_a8)."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
     if save and packed.fp8:
@@ -712,9 +753,14 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
                        packed.expert_gate_up_scale, packed.expert_down, packed.expert_down_scale,
                        packed.expert_width, row_scale=rscale)
     if packed.shared_width > 0:
-        h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width, save=save,
-                           row_scale=rscale,
-                           w_frag=packed.fragments("shared_gate_up", hidden) if decode else None)
+        if (act_fp8 and packed.shared_gate_up.dtype == torch.float8_e4m3fn and rscale is None and not decode
+                and hidden % 128 == 0 and hidden <= RMSNORM_MAX_HIDDEN.get(x.dtype, 0)):
+            xq, xs = quantize_rows_e4m3(x)
+            h = shared_gate_up_a8(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width)
+        else:
+            h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width,
+                               save=save, row_scale=rscale,
+                               w_frag=packed.fragments("shared_gate_up", hidden) if decode else None)
         if save:
             h, gu = h
         out = shared_down_combine(h, packed.shared_width, packed.shared_down, packed.shared_down_scale,

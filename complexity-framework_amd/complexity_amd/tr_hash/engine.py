@@ -139,6 +139,12 @@ class TRHashEngine(nn.Module):
 
         self.last_backend: Optional[BackendDecision] = None
         self.last_norm: Optional[str] = None
+        # W8A8: with e4m3 weights (quantize_fp8_), also quantize each token's
+        # activations to e4m3 (per-token scale) for the shared gate|up, which
+        # then runs on the e4m3 MFMA (prefill sizes, grouped strategy).  Off
+        # by default: the reference has no fp8 path and keeps activations in
+        # the compute dtype.
+        self.fp8_activations = False
         self._graph_pool: Dict[GraphBucket, "_CapturedTRHashGraph"] = {}
         self._bucket_planner = GraphBucketPlanner(config.graph_buckets) if config.graph_buckets else None
         self._active_num_experts = config.num_experts
@@ -506,6 +512,7 @@ class TRHashEngine(nn.Module):
                 self.config.routed_output_scale,
                 order=order,
                 residual=res,
+                act_fp8=self.fp8_activations and self._fp8,
             )
         return out if out.dtype == flat_x.dtype else out.to(flat_x.dtype)
 

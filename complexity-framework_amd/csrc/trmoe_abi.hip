@@ -287,6 +287,55 @@ int trmoe_rms_row_scale(int act_dtype, const void* x, int64_t n_tokens, int64_t 
     return launch_rms_row_scale(act_dtype, x, n_tokens, hidden, ldx, eps, row_scale, as_stream(stream));
 }
 
+int trmoe_quantize_rows_e4m3(int act_dtype, const void* x, int64_t n_rows, int64_t k, int64_t ldx, void* q,
+                             int64_t ldq, float* scale, void* stream) {
+    TRMOE_REQUIRE(act_dtype == TRMOE_F32 || act_dtype == TRMOE_BF16, "quantize_rows_e4m3: bf16 or f32 rows");
+    TRMOE_REQUIRE(n_rows >= 0, "quantize_rows_e4m3: n_rows < 0");
+    TRMOE_REQUIRE(k > 0 && (k * elem_bytes(act_dtype)) % 16 == 0 && k <= rmsnorm_max_hidden(act_dtype),
+                  "quantize_rows_e4m3: k must be a positive multiple of 16 bytes of elements, at most 4096 bf16 "
+                  "or 2048 f32");
+    TRMOE_REQUIRE(ldx >= k && ldq >= k, "quantize_rows_e4m3: row stride < k");
+    if (n_rows == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x && q && scale, "quantize_rows_e4m3: null pointer");
+    TRMOE_REQUIRE(rows_ok(x, ldx, elem_bytes(act_dtype)) && rows_ok(q, ldq, 1),
+                  "quantize_rows_e4m3: x and q must be 16-byte aligned with row strides that are multiples of 16 "
+                  "bytes");
+    return launch_quantize_rows_e4m3(act_dtype, x, n_rows, k, ldx, q, ldq, scale, as_stream(stream));
+}
+
+int trmoe_shared_gate_up_a8(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t hidden, int64_t ldxq,
+                            const void* w_packed, const float* w_scale, int64_t shared_width, void* h, int64_t ldh,
+                            void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_gate_up_a8: bad dimensions");
+    TRMOE_REQUIRE(hidden % 128 == 0 && hidden < (int64_t)1 << 30, "shared_gate_up_a8: hidden must be a multiple of 128");
+    TRMOE_REQUIRE(ldxq >= hidden, "shared_gate_up_a8: ldxq < hidden");
+    TRMOE_REQUIRE(ldh >= round_up(shared_width, 128), "shared_gate_up_a8: ldh < round_up(shared_width, 128)");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(x_q && x_scale && w_packed && w_scale && h, "shared_gate_up_a8: null pointer");
+    TRMOE_REQUIRE(aligned16(w_packed), "shared_gate_up_a8: packed weights must be 16-byte aligned");
+    TRMOE_REQUIRE(rows_ok(x_q, ldxq, 1),
+                  "shared_gate_up_a8: x_q rows must be 16-byte aligned with a row stride that is a multiple of 16 "
+                  "bytes");
+    TRMOE_REQUIRE(aligned16(h) && (ldh * 2) % 16 == 0,
+                  "shared_gate_up_a8: h must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+    GateUpArgs a{};
+    a.x = x_q;
+    a.ldx = ldxq;
+    a.M = n_tokens;
+    a.K = (int)hidden;
+    a.w = w_packed;
+    a.ldw = hidden;
+    a.w_scale = w_scale;
+    a.h = h;
+    a.ldh = ldh;
+    a.shared_mult = 1.0f;
+    a.shared_feats = 0;
+    a.expert_feats = 1;
+    a.vocab = 1;
+    a.row_scale = x_scale;
+    return launch_gate_up_a8(a, 2 * round_up(shared_width, 128), as_stream(stream));
+}
+
 static bool rmsnorm_hidden_ok(int act_dtype, int64_t hidden) {
     return hidden > 0 && (hidden * elem_bytes(act_dtype)) % 16 == 0 && hidden <= rmsnorm_max_hidden(act_dtype);
 }

@@ -241,12 +241,19 @@ int launch_gate_up(int act, int wdt, const GateUpArgs& a, int64_t packed_rows, h
 int launch_pack_fragments(const void* src, int64_t rows, int64_t kbytes, int64_t ld_bytes, void* dst,
                           hipStream_t stream);
 // row_scale[t] = 1 / sqrt(mean_k x[t, k]^2 + eps) in fp32 for t < n.
+// W8A8 shared gate|up (persistent stream, e4m3 MFMA): a.x e4m3 codes with row
+// stride a.ldx bytes, a.row_scale their per-token scales, a.w e4m3 packed
+// weights with a.w_scale; needs a.K % 128 == 0 and whole 256-row column tiles.
+int launch_gate_up_a8(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
 int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, float eps, float* row_scale,
                          hipStream_t stream);
 // RMSNorm with its backward (trmoe_norm.hip): y = T(x * r) * w with r saved;
 // dx = r (dy w) - (r^3 / H) ((dy w) . x) x (+ dres); dw from one fp32 partial
 // per backward workgroup (rmsnorm_groups(n) of them) summed in order.
 int rmsnorm_groups(int64_t n);
+// Per-row e4m3 codes and scales (scale = amax / 448) of x[n, k] (trmoe_norm.hip).
+int launch_quantize_rows_e4m3(int act, const void* x, int64_t n, int64_t k, int64_t ldx, void* q, int64_t ldq,
+                              float* scale, hipStream_t stream);
 int64_t rmsnorm_max_hidden(int act);
 int launch_rmsnorm_forward(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, const void* w, float eps,
                            void* y, int64_t ldy, float* rs, hipStream_t stream);

@@ -305,7 +305,9 @@ __global__ __launch_bounds__(Shape::NT) void k_gate_up_swiglu(GateUpArgs a) {
 // PAIRS: adjacent lanes pair their values into 4-byte stores
 // (store_bf16_pairs), else one 2-byte store per value.  Rows at or past M
 // fall past the buffer's range and are dropped.
-template <int TMW, bool PAIRS = true>
+// RS: the gate and up values of each row are also multiplied by
+// a.row_scale[row] (the per-token scale of e4m3 activations).
+template <int TMW, bool PAIRS = true, bool RS = false>
 __device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
                                                    int64_t n0, int wm0, int wn0) {
     const int lane = threadIdx.x & 63, r = lane & 31;
@@ -324,12 +326,29 @@ __device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f3
         const int lb = pair_lane_offset(wm0, col, ld2);
 #pragma unroll
         for (int tm = 0; tm < TMW; ++tm) {
+            // RS: lane l loads the scale of row wm0 + 32 tm + (l % 32) (clamped
+            // into the tile: rows at or past M are not stored), and element i
+            // takes its row's, acc_row(lane, i), from that lane
+            float rsl = 1.0f;
+            if constexpr (RS) {
+                const int rrow = wm0 + tm * 32 + r;
+                rsl = a.row_scale[m0 + (rrow < mlim ? rrow : mlim - 1)];
+            }
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = silu_f(acc[tm][0][i] * sg) * (acc[tm][1][i] * su);
+            for (int i = 0; i < 16; ++i) {
+                float g = acc[tm][0][i] * sg, u = acc[tm][1][i] * su;
+                if constexpr (RS) {
+                    const float rs = __shfl(rsl, 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3));
+                    g *= rs;
+                    u *= rs;
+                }
+                v[i] = silu_f(g) * u;
+            }
             store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
         }
     } else {
+        static_assert(!RS, "row scales are applied on the paired-store path");
         // one 2-byte store per value (fewer live registers: the e4m3 kernels
         // keep their loader state out of scratch this way)
         const int lb = (wm0 + 4 * (lane >> 5)) * ld2 + col * 2;
@@ -485,8 +504,12 @@ __device__ __forceinline__ void gate_up_save_direct(const GateUpArgs& a, const f
 // the tiles_m x (n_tiles / tiles_m) 256-row tiles as one stream of K stages
 // (pp_stream), writing each tile's h from registers while the next tile's
 // stages load and multiply.  SAVE: also the raw gate|up outputs (a.gu).
-template <int TMW, bool SAVE, bool FP8>
+// A8 (with FP8): e4m3 activations too, a.x holding the codes (row stride
+// a.ldx bytes) and a.row_scale their per-token scales: 128 K values per
+// stage on the e4m3 MFMA (W8A8).
+template <int TMW, bool SAVE, bool FP8, bool A8 = false>
 __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t tiles_m, int64_t n_tiles) {
+    static_assert(!A8 || (FP8 && !SAVE), "W8A8 is the inference form of the e4m3 weights");
     constexpr int BM = 64 * TMW;
     extern __shared__ __align__(16) char lds[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -503,11 +526,11 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
         m0 = (int64_t)mt * BM;
         n0 = a.n_base + (int64_t)nt * 256;
     };
-    const int64_t ldx_b = a.ldx * (int64_t)sizeof(bf16_t);
+    const int64_t ldx_b = A8 ? a.ldx : a.ldx * (int64_t)sizeof(bf16_t);
     const int64_t ldw_b = FP8 ? a.ldw : a.ldw * (int64_t)sizeof(bf16_t);
 
     PPRows<BM> ap;
-    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    std::conditional_t<FP8 && !A8, PPRows64, PPRows<256>> bp;
     int64_t m0, n0;
     coords(0, m0, n0);
     if (group == 1) {
@@ -520,9 +543,10 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
     }
     f32x16 acc[TMW][2];
     zero_acc<KindBF16>(acc);
-    using Lay = std::conditional_t<FP8, PPLayoutF8<TMW, true>, PPLayoutK<TMW, true>>;
+    using Lay = std::conditional_t<A8, PPLayoutK8<TMW, true>,
+                                   std::conditional_t<FP8, PPLayoutF8<TMW, true>, PPLayoutK<TMW, true>>>;
     pp_stream<TMW, Lay>(
-        ap, bp, a.K / 64, ntiles, lds, group, wm0, wn0, acc,
+        ap, bp, A8 ? a.K / 128 : a.K / 64, ntiles, lds, group, wm0, wn0, acc,
         [&](int i) {   // i >= ntiles: no rows (the refills past the last stage load zeros)
             int64_t tm0, tn0;
             coords(i, tm0, tn0);
@@ -537,7 +561,10 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
             int64_t tm0, tn0;
             coords(i, tm0, tn0);
             if constexpr (SAVE) gate_up_save_direct<TMW>(a, c, tm0, tn0, wm0, wn0);
-            gate_up_epi_direct<TMW, !FP8>(a, c, tm0, tn0, wm0, wn0);
+            if constexpr (A8)
+                gate_up_epi_direct<TMW, true, true>(a, c, tm0, tn0, wm0, wn0);
+            else
+                gate_up_epi_direct<TMW, !FP8>(a, c, tm0, tn0, wm0, wn0);
         });
 }
 
@@ -1404,6 +1431,23 @@ static int launch_gate_up_pps(const GateUpArgs& a, int64_t packed_rows, hipStrea
     if (grid <= 0) return TRMOE_OK;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), kLds, stream, a, tiles_m, n_tiles);
     return check_launch("shared_gate_up");
+}
+
+// W8A8 shared gate|up: every tile on the persistent stream (a last round
+// that leaves CUs idle is not split off: there is no e4m3-activation tile
+// kernel).  The caller checks K % 128 == 0 and whole 256-row column tiles.
+int launch_gate_up_a8(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
+    const int64_t tiles_m = (a.M + 255) / 256;
+    const int64_t n_tiles = tiles_m * ((packed_rows - a.n_base) / 256);
+    const int64_t cus = device_cus();
+    const int64_t grid = n_tiles < cus ? n_tiles : cus;
+    constexpr int kLds = 2 * PPLayoutK8<4>::kStage;
+    auto kern = k_gate_up_pps<4, false, true, true>;
+    const int st = ensure_lds(kern, kLds);
+    if (st) return st;
+    if (grid <= 0) return TRMOE_OK;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), kLds, stream, a, tiles_m, n_tiles);
+    return check_launch("shared_gate_up_a8");
 }
 
 // 256-row tiles; when their last round would leave at least half of the CUs

@@ -1,4 +1,5 @@
-// RMSNorm of the block MLP's input for training and for the fp8 layers:
+// Row-wise kernels over token rows: the block MLP's RMSNorm (training and
+// fp8 layers) and the per-token e4m3 quantizer of the W8A8 gate|up.
 //
 //   k_rmsnorm_fwd   one wave per token row: r = 1 / sqrt(mean(x^2) + eps) in
 //                   fp32, y = T(x * r) * w (the rounding of the "llama"
@@ -11,6 +12,9 @@
 //                   fp32 sum of dy * T(x * r) over its rows (the weight
 //                   gradient's partial).
 //   k_rmsnorm_dw    sums the partials in workgroup order (deterministic).
+//   k_quantize_rows one wave per row: scale = amax / 448 (1 for a zero row,
+//                   or one holding a NaN) and codes e4m3(clamp(x / scale)),
+//                   the oracle's quantize_e4m3 over each row, bit for bit.
 //
 // HBM-bound: a row is read once into registers (16-byte loads, chunk c of a
 // row on lane c % 64), so hidden sizes up to 64 * kMaxChunks chunks per row.
@@ -220,6 +224,79 @@ __global__ __launch_bounds__(256) void k_rmsnorm_dw(const float* __restrict__ pa
     }
 }
 
+template <class T, int MC>
+__global__ __launch_bounds__(64 * kNormWaves) void k_quantize_rows(const T* __restrict__ x, int64_t n, int k,
+                                                                    int64_t ldx, uint8_t* __restrict__ q,
+                                                                    int64_t ldq, float* __restrict__ scale) {
+    constexpr int kV = 16 / (int)sizeof(T);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kNormWaves + wave;
+    if (row >= n) return;
+    const int nch = k / kV;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * ldx);
+    u32x4 xv[MC];
+#pragma unroll
+    for (int j = 0; j < MC; ++j) {
+        const int c = lane + 64 * j;
+        xv[j] = c < nch ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+    }
+    float amax = 0.f;
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < MC; ++j)
+#pragma unroll
+        for (int e = 0; e < kV; ++e) {
+            const float f = chunk_elem<T>(xv[j], e);
+            nan |= f != f;
+            amax = fmaxf(amax, fabsf(f));
+        }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    nan = __ballot(nan) != 0;
+    // a row holding a NaN has a NaN amax, which is not > 0: scale 1
+    const float sc = (!nan && amax > 0.f) ? amax / 448.0f : 1.0f;
+    uint8_t* qr = q + row * ldq;
+#pragma unroll
+    for (int j = 0; j < MC; ++j) {
+        const int c = lane + 64 * j;
+        if (c >= nch) continue;
+        // four codes per word: v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest
+        // even -- torch's conversion, matched bit for bit over every bf16
+        // value by the GPU tests) of the correctly rounded quotients
+        uint32_t w[kV / 4];
+#pragma unroll
+        for (int t = 0; t < kV / 4; ++t) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float f = chunk_elem<T>(xv[j], 4 * t + u) / sc;
+                v[u] = f > 448.0f ? 448.0f : (f < -448.0f ? -448.0f : f);   // NaN stays NaN
+            }
+            int packed = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+            packed = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], packed, true);
+            w[t] = (uint32_t)packed;
+        }
+        if constexpr (kV == 8)
+            *reinterpret_cast<u32x2*>(qr + c * kV) = u32x2{w[0], w[1]};
+        else
+            *reinterpret_cast<uint32_t*>(qr + c * kV) = w[0];
+    }
+    if (lane == 0) scale[row] = sc;
+}
+
+template <class T, int MC>
+int quant_mc(const void* x, int64_t n, int64_t k, int64_t ldx, void* q, int64_t ldq, float* scale,
+             hipStream_t stream) {
+    const dim3 grid((unsigned)((n + kNormWaves - 1) / kNormWaves));
+    hipLaunchKernelGGL((k_quantize_rows<T, MC>), grid, dim3(64 * kNormWaves), 0, stream, static_cast<const T*>(x), n,
+                       (int)k, ldx, static_cast<uint8_t*>(q), ldq, scale);
+    return check_launch("quantize_rows_e4m3");
+}
+
+template <class T>
+int quant_kind(const void* x, int64_t n, int64_t k, int64_t ldx, void* q, int64_t ldq, float* scale,
+               hipStream_t stream);
+
 template <class T>
 int chunks_per_lane(int64_t hidden) {
     constexpr int kV = 16 / (int)sizeof(T);
@@ -286,7 +363,27 @@ int bwd_kind(const void* x, int64_t ldx, const void* w, const float* rs, const v
     }
 }
 
+template <class T>
+int quant_kind(const void* x, int64_t n, int64_t k, int64_t ldx, void* q, int64_t ldq, float* scale,
+               hipStream_t stream) {
+    switch (chunks_per_lane<T>(k)) {
+    case 1: return quant_mc<T, 1>(x, n, k, ldx, q, ldq, scale, stream);
+    case 2: return quant_mc<T, 2>(x, n, k, ldx, q, ldq, scale, stream);
+    case 4: return quant_mc<T, 4>(x, n, k, ldx, q, ldq, scale, stream);
+    case 8: return quant_mc<T, 8>(x, n, k, ldx, q, ldq, scale, stream);
+    default: return set_error(TRMOE_ERR_UNSUPPORTED, "quantize_rows_e4m3: row too long for one row per wave");
+    }
+}
+
 }  // namespace
+
+int launch_quantize_rows_e4m3(int act, const void* x, int64_t n, int64_t k, int64_t ldx, void* q, int64_t ldq,
+                              float* scale, hipStream_t stream) {
+    if (n <= 0) return TRMOE_OK;
+    if (act == TRMOE_BF16) return quant_kind<bf16_t>(x, n, k, ldx, q, ldq, scale, stream);
+    if (act == TRMOE_F32) return quant_kind<float>(x, n, k, ldx, q, ldq, scale, stream);
+    return set_error(TRMOE_ERR_UNSUPPORTED, "quantize_rows_e4m3: bf16 or f32 activations");
+}
 
 int rmsnorm_groups(int64_t n) {
     const int64_t g = (n + kNormWaves - 1) / kNormWaves;

@@ -220,6 +220,108 @@ __device__ __forceinline__ void pp_mma_load(const u32x4 (&fa)[4][TM], const u32x
     }
 }
 
+// e4m3 x e4m3 stages (W8A8): a 128-byte stage row holds 128 K values, two
+// v_mfma_scale_f32_32x32x64_f8f6f4 steps (unit scales).  That MFMA takes 32
+// bytes of K per lane (row lane % 32, the two lane halves disjoint K); any
+// assignment of the stage's bytes to (lane half, operand register) works as
+// long as A and B use the same one.  K step q takes the 16-byte chunks that
+// the bf16 reads give K groups 2q and 2q + 1 (chunks 4q + h and 4q + 2 + h of
+// lane half h), read straight into the two halves of one 8-register operand.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x8 lds_pair(const char* p0, const char* p1) {
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(p0);
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(p1);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int TM, bool PAT = false>
+__device__ __forceinline__ void pp_read_f8(const char* st, int a_rows, int wm0, int wn0, i32x8 (&fa)[2][TM],
+                                           i32x8 (&fb)[2][2]) {
+    if constexpr (PAT) {
+        int pat[4][2];
+        pp_patterns(pat);
+        const char* As = st + wm0 * kRowBytes;
+        const char* Bs = st + (a_rows + wn0) * kRowBytes;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+                fa[q][tm] = lds_pair(As + tm * 32 * kRowBytes + pat[2 * q][tm & 1],
+                                     As + tm * 32 * kRowBytes + pat[2 * q + 1][tm & 1]);
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+                fb[q][tn] = lds_pair(Bs + tn * 32 * kRowBytes + pat[2 * q][tn & 1],
+                                     Bs + tn * 32 * kRowBytes + pat[2 * q + 1][tn & 1]);
+        }
+    } else {
+        const int lane = threadIdx.x & 63;
+        const int r = lane & 31, h = lane >> 5;
+        const char* As = st;
+        const char* Bs = st + a_rows * kRowBytes;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+                fa[q][tm] = lds_pair(As + lds_byte(wm0 + tm * 32 + r, 4 * q + h),
+                                     As + lds_byte(wm0 + tm * 32 + r, 4 * q + 2 + h));
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+                fb[q][tn] = lds_pair(Bs + lds_byte(wn0 + tn * 32 + r, 4 * q + h),
+                                     Bs + lds_byte(wn0 + tn * 32 + r, 4 * q + 2 + h));
+        }
+    }
+}
+
+__device__ __forceinline__ void mfma_f8(const i32x8& a, const i32x8& b, f32x16& acc) {
+    // formats 0 / 0: e4m3 operands; scales 127: 2^0 in E8M0
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, 127);
+}
+
+template <int TM>
+__device__ __forceinline__ void pp_mma_f8(const i32x8 (&fa)[2][TM], const i32x8 (&fb)[2][2],
+                                          f32x16 (&acc)[TM][2]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) mfma_f8(fa[q][tm], fb[q][tn], acc[tm][tn]);
+}
+
+// pp_mma_f8 with one stage of an operand's loads spread over its MFMAs (as
+// pp_mma_load does for bf16).
+template <int TM, class LD>
+__device__ __forceinline__ void pp_mma_load_f8(const i32x8 (&fa)[2][TM], const i32x8 (&fb)[2][2],
+                                               f32x16 (&acc)[TM][2], const LD& ld, int kt, char* dst) {
+    constexpr int kMfma = 4 * TM;
+    constexpr int kEvery = kMfma / LD::kInstr;
+    static_assert(kEvery >= 1 && kMfma % LD::kInstr == 0, "loads must spread evenly over the MFMAs");
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const int i = (q * TM + tm) * 2 + tn;
+                mfma_f8(fa[q][tm], fb[q][tn], acc[tm][tn]);
+                if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
+            }
+#pragma unroll
+    for (int j = 0; j < LD::kInstr; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);            // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x008, kEvery - 1, 0);   // MFMA
+    }
+}
+
+// Layouts whose stages hold e4m3 A and B (kF8Mma) multiply with pp_mma_f8.
+template <class L, class = void>
+struct F8Mma : std::false_type {};
+template <class L>
+struct F8Mma<L, std::void_t<decltype(L::kF8Mma)>> : std::integral_constant<bool, L::kF8Mma> {};
+
 // Tile of the ping-pong kernel: 64 * TMW rows x 256 packed columns, waves
 // 2 x 4 of 32 * TMW rows x 64 columns (the epilogue's layout).
 template <int TMW>
@@ -236,6 +338,19 @@ struct PPLayoutK {
     __device__ __forceinline__ static void read(const char* st, int wm0, int wn0, u32x4 (&fa)[4][TMW],
                                                 u32x4 (&fb)[4][2]) {
         pp_read<TMW, PAT>(st, 64 * TMW, wm0, wn0, fa, fb);
+    }
+};
+
+// e4m3 activations and e4m3 weights (W8A8): the bytes of PPLayoutK, 128 K
+// values per stage row, multiplied by pp_mma_f8.
+template <int TMW, bool PAT = false>
+struct PPLayoutK8 {
+    static constexpr bool kF8Mma = true;
+    static constexpr int kBOff = 64 * TMW * kRowBytes;
+    static constexpr int kStage = (64 * TMW + 256) * kRowBytes;
+    __device__ __forceinline__ static void read(const char* st, int wm0, int wn0, i32x8 (&fa)[2][TMW],
+                                                i32x8 (&fb)[2][2]) {
+        pp_read_f8<TMW, PAT>(st, 64 * TMW, wm0, wn0, fa, fb);
     }
 };
 
@@ -616,7 +731,11 @@ __device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, ch
     constexpr int kAI = LA::kInstr, kBI = LB::kInstr;
     const int S = nk * ntiles;
 
-    u32x4 fa[4][TMW], fb[4][2];
+    // fragments of one stage: 16-byte chunks per K group, or 32-byte e4m3
+    // operands per K step
+    constexpr bool kF8 = F8Mma<Lay>::value;
+    std::conditional_t<kF8, i32x8[2][TMW], u32x4[4][TMW]> fa;
+    std::conditional_t<kF8, i32x8[2][2], u32x4[4][2]> fb;
 
     // The issuing group's next load: stage `ld_kt` of tile `ld_tile`,
     // advanced by counting (no division in the loop); the loader is pointed
@@ -672,7 +791,10 @@ __device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, ch
                     advance(retarget_b);
                 }
                 pp_barrier();
-                pp_mma<TMW>(fa, fb, acc);
+                if constexpr (kF8)
+                    pp_mma_f8<TMW>(fa, fb, acc);
+                else
+                    pp_mma<TMW>(fa, fb, acc);
                 __builtin_amdgcn_sched_barrier(0);   // B(s+1) and the epilogue's stores waited for after the MFMAs
                 wait_vmcnt<0>();
                 pp_barrier();
@@ -699,7 +821,10 @@ __device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, ch
                 wait_vmcnt<0>();   // A(s+1), issued in the previous phase, has landed (and the epilogue's stores)
                 const int kt2 = ld_kt;
                 pp_barrier();
-                pp_mma_load<TMW>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
+                if constexpr (kF8)
+                    pp_mma_load_f8<TMW>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
+                else
+                    pp_mma_load<TMW>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
                 __builtin_amdgcn_sched_barrier(0);
                 advance(retarget_a);   // the loader's registers are read at issue, so it may move now
                 pp_barrier();

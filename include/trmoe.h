@@ -329,6 +329,28 @@ int trmoe_rmsnorm_backward(int act_dtype, const void* x, int64_t n_tokens, int64
                            const void* weight, const float* row_scale, const void* dy, int64_t lddy,
                            const void* dres, int64_t lddres, void* dx, int64_t lddx, void* dweight,
                            void* workspace, size_t workspace_bytes, void* stream);
+/* ---------------------------------------------------------------------------
+ * W8A8 shared gate|up: e4m3 activations with per-token scales on the e4m3
+ * MFMA.  No counterpart in the reference, which has no fp8 path: this is the
+ * e4m3-activation form of trmoe_shared_gate_up (the shared_gate/shared_up
+ * linears and silu*mul, complexity/tr_hash/engine.py:333-349) for layers
+ * whose weights are e4m3 already (trmoe_pack_weight with TRMOE_FP8_E4M3).
+ *
+ * trmoe_quantize_rows_e4m3: for each row t of x (f32 or bf16, k a multiple
+ *   of 16 bytes of elements, at most 4096 bf16 / 2048 f32)
+ *     scale_t = amax_k |x_t,k| / 448   (1 when that is 0, or the row holds a NaN)
+ *     q_t,k   = e4m3(clamp(x_t,k / scale_t, -448, 448)), round to nearest even
+ *   -- the weights' per-output-channel quantizer applied to token rows.
+ * trmoe_shared_gate_up_a8: h (bf16) = silu(g) * u with
+ *     [g | u]_t,c = scale_t * w_scale_c * sum_k q_t,k * W8_c,k
+ *   hidden a multiple of 128; x_q rows 16-byte aligned (ldxq bytes apart, a
+ *   multiple of 16); h as for trmoe_shared_gate_up.
+ * ------------------------------------------------------------------------- */
+int trmoe_quantize_rows_e4m3(int act_dtype, const void* x, int64_t n_rows, int64_t k, int64_t ldx, void* q,
+                             int64_t ldq, float* scale, void* stream);
+int trmoe_shared_gate_up_a8(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t hidden, int64_t ldxq,
+                            const void* w_packed, const float* w_scale, int64_t shared_width, void* h, int64_t ldh,
+                            void* stream);
 /* row_scale required; the workspace of trmoe_routed_experts_workspace_bytes() too. */
 int trmoe_routed_experts_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
                              int64_t ldx, const int64_t* sorted_indices, const int32_t* expert_offsets,

@@ -36,7 +36,12 @@ Pinning (what checks each function beyond retyping it):
   against central finite differences in f64 (``torch.autograd.gradcheck``);
   the closed-form ``swiglu_backward`` against that autograd.
 * ``rms_norm`` -- torch's own ``F.rms_norm`` (an independent implementation)
-  and the closed form of a constant row (every element becomes sign * weight).
+  and the closed form of a constant row (every element becomes sign * weight);
+  its autograd against central differences.
+* ``engine_forward_w8a8`` -- equal to ``engine_forward`` on activations that
+  quantize exactly (e4m3 grid values whose row maximum is 448 * 2^j), equal
+  to it when the layer has no shared branch, and within e4m3's relative error
+  of it otherwise.
 """
 
 from __future__ import annotations
@@ -428,6 +433,25 @@ def quantize_e4m3(weight: torch.Tensor, reduce_dim: int):
 
 def dequantize_e4m3(q: torch.Tensor, scale: torch.Tensor, reduce_dim: int) -> torch.Tensor:
     return q.to(torch.float32) * scale.unsqueeze(reduce_dim)
+
+
+def engine_forward_w8a8(x, token_ids, table, params: dict, **kw):
+    """engine_forward with the shared gate|up fed per-token e4m3 activations
+    (the W8A8 path, which has no reference counterpart: the reference has no
+    fp8): the shared branch sees dequantize(quantize_e4m3(x over each row)),
+    the routed experts and the down projection see x and h as before."""
+    shape = x.shape
+    flat = x.reshape(-1, shape[-1]).to(torch.float32)
+    q, s = quantize_e4m3(flat, 1)
+    xq = dequantize_e4m3(q, s, 1).to(x.dtype)
+    g = params.get("shared_gate")
+    shared_params = {k: v for k, v in params.items() if not k.startswith("shared_")}
+    routed = engine_forward(x, token_ids, table, shared_params, **kw)
+    if g is None or g.numel() == 0:
+        return routed
+    h = silu_mul(F.linear(xq, g), F.linear(xq, params["shared_up"]))
+    shared = F.linear(h, params["shared_down"]).view(shape)
+    return routed + kw.get("shared_scale", 1.0) * shared
 
 
 def e4m3_decode_table() -> np.ndarray:

@@ -1,0 +1,170 @@
+"""W8A8 shared gate|up (e4m3 activations with per-token scales, e4m3 MFMA).
+
+The reference has no fp8 path; the oracle is the engine's own weight
+quantizer applied to token rows (``quantize_e4m3`` over each row) followed by
+the layer's formula (``engine_forward_w8a8``), pinned in tests/test_oracle.py.
+
+* trmoe_quantize_rows_e4m3 is byte work: codes and scales bit for bit.
+* trmoe_shared_gate_up_a8 multiplies the same e4m3 values the oracle
+  dequantizes, so only fp32 summation order and the bf16 rounding of h
+  differ: normwise bound 1e-2.
+* The C5 layer with fp8_activations: 2e-2 against the W8A8 oracle and the
+  north-star 5e-2 against the plain (W8A16) oracle, on sampled rows.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import trmoe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _special_rows(k, dtype):
+    """A zero row, a row with one large value and the rest in e4m3's
+    subnormal range after scaling, a row holding a NaN, and a row of ties."""
+    rows = torch.zeros(4, k)
+    rows[1] = torch.linspace(-0.02, 0.02, k)                # / (300 / 448): subnormal and small normal codes
+    rows[1, 3] = 300.0
+    rows[2] = torch.linspace(-2.0, 2.0, k)
+    rows[2, 5] = float("nan")
+    # x / scale lands halfway between e4m3 neighbours: scale 1 (max 448),
+    # values 1.0625 and 17 (ties between 1.0 / 1.125 and 16 / 18)
+    rows[3, 0] = 448.0
+    rows[3, 1::2] = 1.0625
+    rows[3, 2::2] = -17.0
+    return rows.to(dtype)
+
+
+@pytest.mark.parametrize("dtype,n,k", [
+    (torch.bfloat16, 1, 128), (torch.bfloat16, 300, 2048), (torch.bfloat16, 4097, 896),
+    (torch.bfloat16, 33, 4096), (torch.float32, 5, 2048), (torch.float32, 64, 256),
+])
+def test_quantize_rows_bit_exact(gpu, dtype, n, k):
+    from complexity_amd import ops
+
+    print(f"quantize rows {dtype} {n}x{k}", flush=True)
+    g = torch.Generator().manual_seed(n + k)
+    x = (torch.randn(n, k, generator=g) * torch.exp2(torch.randint(-8, 8, (n, 1), generator=g).float())).to(dtype)
+    x = torch.cat([x, _special_rows(k, dtype)])
+    q, s = ops.quantize_rows_e4m3(x.to(gpu))
+    torch.cuda.synchronize()
+    ref_q, ref_s = O.quantize_e4m3(x.float(), 1)
+    got, ref = q.cpu().view(torch.uint8), ref_q.view(torch.uint8)
+    nan_row = n + 2
+    keep = torch.ones(x.shape[0], dtype=torch.bool)
+    keep[nan_row] = False
+    assert torch.equal(s.cpu(), ref_s)
+    assert torch.equal(got[keep], ref[keep])
+    finite = ~torch.isnan(x[nan_row].float())
+    assert torch.equal(got[nan_row][finite], ref[nan_row][finite])
+    assert bool(((got[nan_row][~finite] & 0x7F) == 0x7F).all())
+
+
+def test_quantize_rows_every_bf16_value(gpu):
+    """Rows whose maximum is 448 have scale 1, so every finite bf16 value
+    (clamped to +-448) is its own quotient: the conversion's rounding against
+    torch's over all of them (every e4m3 value, the subnormal steps, the ties
+    and both zeros)."""
+    from complexity_amd import ops
+
+    bits = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    vals = torch.where(torch.isfinite(bits), bits, torch.zeros_like(bits)).clamp(-448, 448).reshape(32, 2048)
+    vals[:, 0] = 448.0
+    q, s = ops.quantize_rows_e4m3(vals.to(gpu))
+    torch.cuda.synchronize()
+    ref_q, ref_s = O.quantize_e4m3(vals.float(), 1)
+    assert torch.equal(s.cpu(), ref_s) and bool((ref_s == 1.0).all())
+    assert torch.equal(q.cpu().view(torch.uint8), ref_q.view(torch.uint8))
+
+
+def _engine(gpu, hidden, shared, experts=4, width=64):
+    from complexity_amd.tr_hash import TRHashEngine, TRHashEngineConfig
+
+    engine = TRHashEngine(TRHashEngineConfig(hidden_size=hidden, vocab_size=5000, num_experts=experts, top_k=2,
+                                             shared_width=shared, expert_width=width,
+                                             routing_strategy="token_id_multi_hash", routed_output_scale=2.0,
+                                             shared_output_scale=0.5, precision="fp8", backend="hip")).to(gpu)
+    engine = engine.to(torch.bfloat16)
+    engine.routed_strategy = "grouped"
+    engine.quantize_fp8_()
+    return engine.eval()
+
+
+def _deq(engine, name):
+    return O.dequantize_e4m3(getattr(engine, name + "_fp8").cpu(), getattr(engine, name + "_scale").cpu(), 1)
+
+
+@pytest.mark.parametrize("hidden,shared,n", [(256, 384, 300), (128, 128, 1), (2048, 5632, 4096), (896, 3072, 777)])
+def test_shared_gate_up_a8(gpu, hidden, shared, n):
+    """h against silu(xq Wgq^T) * (xq Wuq^T) in f64 on the same e4m3 values
+    (rows sampled above 1024 tokens)."""
+    from complexity_amd import ops
+
+    print(f"gate_up a8 H={hidden} S={shared} n={n}", flush=True)
+    engine = _engine(gpu, hidden, shared)
+    g = torch.Generator().manual_seed(hidden + n)
+    x = (torch.randn(n, hidden, generator=g) * 1.5).to(gpu, torch.bfloat16)
+    packed = engine._hip_packed()
+    xq, xs = ops.quantize_rows_e4m3(x)
+    h = ops.shared_gate_up_a8(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale, shared)
+    torch.cuda.synchronize()
+    rows = torch.arange(n) if n <= 1024 else torch.randperm(n, generator=g)[:1024]
+    xd = O.dequantize_e4m3(xq.cpu()[rows], xs.cpu()[rows], 1).double()
+    ref = O.silu_mul(F.linear(xd, _deq(engine, "shared_gate").double()),
+                     F.linear(xd, _deq(engine, "shared_up").double()))
+    got = h[:, :shared].cpu()[rows].double()
+    assert O.normwise_rel_err(got, ref) <= 1e-2, O.normwise_rel_err(got, ref)
+
+
+def test_c5_layer_with_fp8_activations(gpu):
+    """C5 (hidden 2048, shared 5632, 16 x 256 experts, 32768 tokens) with
+    fp8_activations against the W8A8 oracle and the plain W8A16 oracle."""
+    from complexity_amd import workloads as Wl
+    from complexity_amd.tr_hash import TRHashBackend
+
+    from complexity_amd import ops
+
+    w = Wl.C5
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    engine.fp8_activations = True
+    x = Wl.make_hidden(w).to(gpu).to(torch.bfloat16)
+    ids = Wl.make_token_ids(w).to(gpu)
+    calls = []
+    a8 = ops.shared_gate_up_a8
+
+    def counted(*a, **k):
+        calls.append(1)
+        return a8(*a, **k)
+
+    ops.shared_gate_up_a8 = counted
+    try:
+        with torch.no_grad():
+            out = engine(x, ids)
+            assert len(calls) == 1
+            engine.fp8_activations = False
+            plain = engine(x, ids)
+            assert len(calls) == 1
+    finally:
+        ops.shared_gate_up_a8 = a8
+    torch.cuda.synchronize()
+    assert engine.last_backend.selected is TRHashBackend.HIP
+    rows = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(2))[:1024]
+    xr = x.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu()
+    ir = ids.reshape(-1)[rows.to(gpu)].cpu()
+    p = {n: _deq(engine, n) for n in ("expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up",
+                                      "shared_down")}
+    cfg = engine.config
+    kw = dict(route_weights=cfg.route_weights, shared_scale=cfg.shared_output_scale,
+              routed_scale=cfg.routed_output_scale)
+    table = engine._active_route_table.cpu()
+    ref8 = O.engine_forward_w8a8(xr, ir, table, p, **kw)
+    ref = O.engine_forward(xr, ir, table, p, **kw)
+    got = out.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu()
+    e8, e = O.normwise_rel_err(got, ref8), O.normwise_rel_err(got, ref)
+    print(f"C5 W8A8: {e8:.3e} vs the W8A8 oracle, {e:.3e} vs the W8A16 oracle", flush=True)
+    assert e8 <= 2e-2
+    assert e <= 5e-2
+    # the flag changes only the shared gate|up: without it the layer is the W8A16 one
+    assert O.normwise_rel_err(plain.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu(), ref) <= 5e-2

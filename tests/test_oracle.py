@@ -452,3 +452,47 @@ def test_norm_residual_oracle_composes():
     xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * nw
     want = x + O.engine_forward(xn, ids, table, params, route_weights=(0.6, 0.4))
     assert torch.allclose(got, want, atol=1e-6)
+
+
+# --------------------------------------------------------------------------- W8A8 (e4m3 activations)
+
+
+def _w8a8_params(g, H=64, S=96, E=4, W=16):
+    return {
+        "shared_gate": torch.randn(S, H, generator=g) * 0.1, "shared_up": torch.randn(S, H, generator=g) * 0.1,
+        "shared_down": torch.randn(H, S, generator=g) * 0.1,
+        "expert_gate": torch.randn(E, H, W, generator=g) * 0.1, "expert_up": torch.randn(E, H, W, generator=g) * 0.1,
+        "expert_down": torch.randn(E, W, H, generator=g) * 0.1,
+    }
+
+
+def test_w8a8_oracle_is_exact_on_representable_rows():
+    """Rows of e4m3 grid values times 2^j whose maximum magnitude is 448 * 2^j
+    quantize exactly (scale 2^j), so the W8A8 forward equals the plain one."""
+    g = torch.Generator().manual_seed(21)
+    params = _w8a8_params(g)
+    grid = torch.from_numpy(O.e4m3_decode_table()).float()
+    grid = grid[torch.isfinite(grid)]
+    rows = grid[torch.randint(0, grid.numel(), (10, 64), generator=g)]
+    rows[:, 0] = 448.0
+    x = rows * torch.exp2(torch.randint(-12, -6, (10, 1), generator=g).float())
+    ids = torch.randint(0, 50, (10,), generator=g)
+    table = torch.from_numpy(O.multi_hash_table(50, 4, 2, 0))
+    kw = dict(route_weights=(0.5, 0.5), shared_scale=0.7, routed_scale=1.3)
+    assert torch.equal(O.engine_forward_w8a8(x, ids, table, params, **kw), O.engine_forward(x, ids, table, params, **kw))
+
+
+def test_w8a8_oracle_quantizes_the_shared_branch_only():
+    g = torch.Generator().manual_seed(22)
+    params = _w8a8_params(g)
+    x = torch.randn(40, 64, generator=g)
+    ids = torch.randint(0, 50, (40,), generator=g)
+    table = torch.from_numpy(O.multi_hash_table(50, 4, 2, 0))
+    kw = dict(route_weights=(0.5, 0.5), shared_scale=0.7, routed_scale=1.3)
+    no_shared = {k: v for k, v in params.items() if not k.startswith("shared_")}
+    assert torch.equal(O.engine_forward_w8a8(x, ids, table, no_shared, **kw),
+                       O.engine_forward(x, ids, table, no_shared, **kw))
+    ref = O.engine_forward(x, ids, table, params, **kw)
+    got = O.engine_forward_w8a8(x, ids, table, params, **kw)
+    err = O.normwise_rel_err(got, ref)
+    assert 0.0 < err < 5e-2, err

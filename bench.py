@@ -485,18 +485,20 @@ def train_step(torch, engine, w, x, ids, steps: int = 10, warmup: int = 3):
 
 def norm_train(torch, engine, w, x, ids, steps: int = 20, warmup: int = 5):
     """The block's MLP half under autograd (forward_norm_residual, whose
-    RMSNorm runs on trmoe_rmsnorm_forward/_backward there), and the norm
-    alone on those kernels against the reference's torch formula
-    (norms.py:53-55 under autograd), forward + backward each.  The norm's
-    HBM roofline: x and y (forward), then x, dy and dx (backward) once each,
-    5 N H element bytes."""
-    from complexity_amd.tr_hash.hip_autograd import RMSNormFunction
+    RMSNorm runs on trmoe_rmsnorm_forward/_backward there), eager; and the
+    norm alone, forward + backward: its kernels replayed as a HIP graph (their
+    few tens of us would otherwise measure the host), and the reference's
+    torch formula (norms.py:53-55) under autograd, eager (about ten kernels
+    over the full tensors: bound by the GPU, and its backward's reductions
+    are not captured into a graph here).  The norm's HBM roofline: x and y
+    (forward), then x, dy and dx (backward) once each, 5 N H element bytes."""
+    from complexity_amd import ops
 
     h = x.shape[-1]
     nw = (torch.rand(h, device=x.device) + 0.5).to(x.dtype).requires_grad_(True)
     xg = x.detach().clone().requires_grad_(True)
     dout = (torch.randn(x.shape, device=x.device) * 0.1).to(x.dtype)
-    flat = xg.detach().reshape(-1, h).requires_grad_(True)
+    flat = xg.detach().reshape(-1, h).clone().requires_grad_(True)
     dflat = dout.reshape(-1, h)
 
     def block():
@@ -506,9 +508,8 @@ def norm_train(torch, engine, w, x, ids, steps: int = 20, warmup: int = 5):
         engine.forward_norm_residual(xg, ids, nw, 1e-6).backward(dout)
 
     def norm_hip():
-        flat.grad = None
-        nw.grad = None
-        RMSNormFunction.apply(flat, nw, 1e-6).backward(dflat)
+        y, r = ops.rmsnorm_forward(flat.detach(), nw.detach(), 1e-6)
+        ops.rmsnorm_backward(flat.detach(), nw.detach(), r, dflat)
 
     def norm_torch():
         flat.grad = None
@@ -516,11 +517,19 @@ def norm_train(torch, engine, w, x, ids, steps: int = 20, warmup: int = 5):
         var = flat.pow(2).mean(-1, keepdim=True)
         (nw * (flat * torch.rsqrt(var + 1e-6))).backward(dflat)
 
-    out = {"workload": w.name, "steps": steps}
-    gc.collect()
-    gc.disable()
-    for name, fn in (("block_ms_per_step_fwd_bwd", block), ("norm_hip_ms_fwd_bwd", norm_hip),
-                     ("norm_torch_ms_fwd_bwd", norm_torch)):
+    def graphed(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g.replay
+
+    def timed(fn):
         sustain(torch, fn, warmup)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
@@ -528,11 +537,18 @@ def norm_train(torch, engine, w, x, ids, steps: int = 20, warmup: int = 5):
             fn()
         stop.record()
         torch.cuda.synchronize()
-        out[name] = start.elapsed_time(stop) / steps
-    gc.enable()
+        return start.elapsed_time(stop) / steps
+
+    out = {"workload": w.name, "steps": steps}
+    gc.collect()
+    gc.disable()
+    out["block_ms_per_step_fwd_bwd"] = timed(block)
     out["norm_path"] = engine.last_norm
+    out["norm_hip_graph_us_fwd_bwd"] = timed(graphed(norm_hip)) * 1e3
+    out["norm_torch_eager_us_fwd_bwd"] = timed(norm_torch) * 1e3
+    gc.enable()
     nbytes = 5 * x.numel() * x.element_size()
-    out["norm_hip_hbm_frac"] = nbytes / (out["norm_hip_ms_fwd_bwd"] * 1e-3) / (HBM_PEAK * 1e9)
+    out["norm_hip_hbm_frac"] = nbytes / (out["norm_hip_graph_us_fwd_bwd"] * 1e-6) / (HBM_PEAK * 1e9)
     engine.zero_grad(set_to_none=True)
     return out
 

@@ -191,35 +191,34 @@ __global__ __launch_bounds__(64 * kNormWaves) void k_rmsnorm_bwd(const T* __rest
     }
 }
 
-// dw[k] = sum over workgroups b (in order) of part[b][k]: 16 columns x 16
-// strided groups of partials per workgroup, the groups added in order.
+// dw[k] = sum over workgroups b (in order) of part[b][k]: 32 columns (whole
+// 128-byte lines) x 32 strided groups of partials per workgroup (a group
+// sums every 32nd partial, eight loads in flight), the groups then added in
+// order.  Latency-bound: the chain per thread is what sets the time.
 template <class T>
-__global__ __launch_bounds__(256) void k_rmsnorm_dw(const float* __restrict__ part, int groups, int hidden,
-                                                     T* __restrict__ dw) {
-    __shared__ float s[16][17];
-    const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
-    const int col = (int)blockIdx.x * 16 + c;
+__global__ __launch_bounds__(1024) void k_rmsnorm_dw(const float* __restrict__ part, int groups, int hidden,
+                                                      T* __restrict__ dw) {
+    __shared__ float s[32][33];
+    const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int col = (int)blockIdx.x * 32 + c;
     float t = 0.f;
     if (col < hidden) {
         int b = g;
-        for (; b + 48 < groups; b += 64) {           // four partials in flight
-            const float v0 = part[(int64_t)b * hidden + col];
-            const float v1 = part[(int64_t)(b + 16) * hidden + col];
-            const float v2 = part[(int64_t)(b + 32) * hidden + col];
-            const float v3 = part[(int64_t)(b + 48) * hidden + col];
-            t += v0;
-            t += v1;
-            t += v2;
-            t += v3;
+        for (; b + 224 < groups; b += 256) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(b + 32 * u) * hidden + col];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t += v[u];
         }
-        for (; b < groups; b += 16) t += part[(int64_t)b * hidden + col];
+        for (; b < groups; b += 32) t += part[(int64_t)b * hidden + col];
     }
     s[g][c] = t;
     __syncthreads();
     if (g == 0 && col < hidden) {
         float u = s[0][c];
 #pragma unroll
-        for (int v = 1; v < 16; ++v) u += s[v][c];
+        for (int v = 1; v < 32; ++v) u += s[v][c];
         dw[col] = from_f32<T>(u);
     }
 }
@@ -339,7 +338,7 @@ int bwd_mc(const T* x, int64_t ldx, const T* w, const float* rs, const T* dy, in
                        rs, dy, lddy, dres, lddres, n, (int)hidden, dx, lddx, part);
     st = check_launch("rmsnorm_backward");
     if (st) return st;
-    hipLaunchKernelGGL((k_rmsnorm_dw<T>), dim3((unsigned)((hidden + 15) / 16)), dim3(256), 0, stream,
+    hipLaunchKernelGGL((k_rmsnorm_dw<T>), dim3((unsigned)((hidden + 31) / 32)), dim3(1024), 0, stream,
                        (const float*)part, groups, (int)hidden, dw);
     return check_launch("rmsnorm_backward (weight gradient)");
 }

@@ -46,7 +46,7 @@ struct PPRows {
     __device__ __forceinline__ void init(const void* base, int64_t first_row, int64_t rows_total, int64_t ld_bytes,
                                          int wave_in_group) {
         const int64_t avail = rows_total - first_row;
-        nrows = (int)(avail < ROWS ? avail : ROWS);
+        nrows = (int)(avail < 0 ? 0 : (avail < ROWS ? avail : ROWS));   // the descriptor's range: never negative
         rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
         const int lane = threadIdx.x & 63;
         wig = wave_in_group;
@@ -59,19 +59,21 @@ struct PPRows {
     __device__ __forceinline__ void retarget(const void* base, int64_t first_row, int64_t rows_total,
                                              int64_t ld_bytes) {
         const int64_t avail = rows_total - first_row;
-        nrows = (int)(avail < ROWS ? avail : ROWS);
+        nrows = (int)(avail < 0 ? 0 : (avail < ROWS ? avail : ROWS));   // the descriptor's range: never negative
         rsrc = make_rsrc(static_cast<const char*>(base) + first_row * ld_bytes, (uint32_t)(nrows * ld_bytes));
     }
     // stage kt (bytes [128 kt, 128 kt + 128) of every row) into `dst` (the
     // operand's part of an LDS stage).  LDS slot (lane % 8) of row r holds K
     // chunk slot ^ swz(r); the rows of instruction j have r / 8 = kInstr *
     // wave_in_group + j, so swz(r) = (lane / 8) ^ (kInstr * wave_in_group + j).
+    // A row at or past nrows starts at or past the descriptor's range
+    // (nrows * row_bytes), so it loads zeros without a select; the stage's K
+    // offset goes in the scalar offset.
     __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
         const int r = row0 + 8 * j;
         const int chunk = (c0 ^ (kInstr * wig + j)) & 7;
-        const int o = r < nrows ? r * row_bytes + kt * kRowBytes + (chunk << 4) : kOutOfRange;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (kInstr * wig + j) * 8 * kRowBytes), 16,
-                                                o, 0, 0, 0);
+                                                r * row_bytes + (chunk << 4), kt * kRowBytes, 0, 0);
     }
     __device__ __forceinline__ void issue(int kt, char* dst) const {
 #pragma unroll

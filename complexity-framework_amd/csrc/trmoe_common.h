@@ -77,11 +77,11 @@ __device__ __forceinline__ void mfma_group(KindF32, u32x4 a, u32x4 b, f32x16& ac
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[3], fb[3], acc, 0, 0, 0);
 }
 
-// Accumulator element i of a 32x32 MFMA tile held by `lane`.
+// Row of accumulator element i of a 32x32 MFMA tile held by `lane` (its
+// column is lane % 32).
 __device__ __forceinline__ int acc_row(int lane, int i) {
     return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
 }
-__device__ __forceinline__ int acc_col(int lane) { return lane & 31; }
 
 // ---------------------------------------------------------------------------
 // buffer loads

@@ -120,13 +120,17 @@ __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_r
                                               __amdgpu_buffer_rsrc_t wr, const int (&w_row0)[NU], int ldw_b,
                                               const int (&w_off)[NU], int s0, int s1, int kb_a,
                                               f32x4 (&acc)[MT][NU], bool ssq_on = false,
-                                              float* ssq = nullptr) {
+                                              float* ssq = nullptr, int w_half = -1) {
     static_assert(!(SW && FP8), "e4m3 weight rows are 64 bytes per span: not staged");
     using WF = WFrag<Kind, FP8>;
     constexpr int kRowsA = MT * 16;
     constexpr int kRows = kRowsA + (SW ? NU * 16 : 0);
     const int lane = threadIdx.x & 63;
     const int q = lane >> 4;
+    // fragment-major weights, w_half >= 0: the tile uses rows 8 w_half ..
+    // 8 w_half + 7 of each 16-row block, so the lanes holding the other half
+    // (row lane % 16) load nothing (zeros: their products are never stored)
+    const bool w_live = w_half < 0 || ((lane & 15) >> 3) == w_half;
     int xo[MT * 2];   // the lane's row offset + chunk for each 8-row copy instruction
 #pragma unroll
     for (int j = 0; j < MT * 2; ++j) {
@@ -173,7 +177,8 @@ __device__ __forceinline__ void staged_k_loop(__amdgpu_buffer_rsrc_t ar, int a_r
                                 // 1 KiB, and lane l's 16 bytes sit at 16 l
                                 const int G = (kb_a + 63) / 64;
                                 wv[j][h][u] = buffer_load16(
-                                    wr, 64 * gg < kb_a ? ((w_row0[u] >> 4) * G + gg) * 1024 + 16 * lane : kOutOfRange);
+                                    wr, (64 * gg < kb_a && w_live) ? ((w_row0[u] >> 4) * G + gg) * 1024 + 16 * lane
+                                                                   : kOutOfRange);
                             } else {
                                 wv[j][h][u] = WF::load(wr, w_off[u], gg, q, kb_a);
                             }
@@ -403,12 +408,28 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up_skinny(GateUpArgs a) {
     }
 }
 
-// Split-K partial of the down GEMM: block (x = COLS-column tile, y = K
-// split) writes part[(split * M + row) * N + col] for its rows and columns;
-// with a single split it finishes the output itself.  COLS = 8 uses half of
-// a 16-row weight block (twice the workgroups for the same columns).
+// Workgroup L of the down's 1-D grid -> (column tile, K split).  Workgroups
+// go to the 8 XCDs round-robin; with 2, 4 or 8 splits (and whole rounds)
+// XCD x takes split x % S only, so each XCD's L2 fetches one K range of h
+// instead of all of it.
+__device__ __forceinline__ void down_tile_split(int L, int ncol, int S, int& ct, int& sp) {
+    if (S > 1 && 8 % S == 0 && (ncol * S) % 8 == 0 && ncol % (8 / S) == 0) {
+        const int x = L & 7, j = L >> 3;
+        sp = x % S;
+        ct = j * (8 / S) + x / S;
+    } else {
+        ct = L % ncol;
+        sp = L / ncol;
+    }
+}
+
+// Split-K partial of the down GEMM: block (COLS-column tile, K split) writes
+// part[(split * M + row) * N + col] for its rows and columns; with a single
+// split it finishes the output itself.  COLS = 8 uses half of a 16-row
+// weight block (twice the workgroups for the same columns).
 template <class Kind, bool FP8, int MT, int COLS, int NW, bool FRAG = false>
-__global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int spans_per_split) {
+__global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part, int spans_per_split, int ncol,
+                                                        int splits) {
     using T = typename Kind::T;
     constexpr int NT = 64 * NW;
     constexpr int kWB = FP8 ? 1 : (int)sizeof(T);
@@ -417,8 +438,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     extern __shared__ __align__(16) float red[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15;
-    const int64_t n0 = (int64_t)blockIdx.x * kCols;
-    const int split = blockIdx.y;
+    int ct, split;
+    down_tile_split((int)blockIdx.x, ncol, splits, ct, split);
+    const int64_t n0 = (int64_t)ct * kCols;
 
     const int kb_a = a.K * (int)sizeof(T);
     const auto ar = make_rsrc(a.h, (uint32_t)(a.M * a.ldh * (int64_t)sizeof(T)));
@@ -450,12 +472,12 @@ __global__ __launch_bounds__(64 * NW) void k_down_skinny(DownArgs a, float* part
     char* region = reinterpret_cast<char*>(red) + wave * SB * kRows * kRowBytes;
     staged_k_loop<Kind, FP8, MT, NU, SB, SW, (COLS < 16 ? 8 : 16), FRAG>(
         ar, (int)a.M, (int)(a.ldh * (int64_t)sizeof(T)), region, wr, w_row0, (int)(a.ldw * kWB), w_off, s0, s1, kb_a,
-        acc);
+        acc, false, nullptr, (FRAG && COLS < 16) ? (int)((n0 >> 3) & 1) : -1);
     __syncthreads();   // every wave is done with its staging region
     skinny_stash<MT, NU>(red, acc);
     __syncthreads();
 
-    const bool single = gridDim.y == 1;
+    const bool single = splits == 1;
     float* dst = part + (int64_t)split * a.M * a.N;
     for (int qi = threadIdx.x; qi < MT * NU * 4 * 64; qi += NT) {
         const int l = qi & 63, i = (qi >> 6) & 3, u = (qi >> 8) % NU, tm = (qi >> 8) / NU;
@@ -565,8 +587,8 @@ int down_skinny_mt(const DownArgs& a, float* part, int sps, int splits, hipStrea
     constexpr int kLds = std::max(red_bytes(MT, NU, NW), staged_lds_bytes<skinny_rows<FP8, MT, NU, NW, FRAG>(), NW>());
     int st = set_lds(kern, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + COLS - 1) / COLS), (unsigned)splits), dim3(64 * NW), kLds, stream,
-                       a, part, sps);
+    const int ncol = (int)((a.N + COLS - 1) / COLS);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(ncol * splits)), dim3(64 * NW), kLds, stream, a, part, sps, ncol, splits);
     st = check_launch("shared_down_combine (skinny)");
     if (st || splits == 1) return st;
     const bool vec = a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0;

@@ -35,7 +35,7 @@ import torch.nn.functional as F
 
 from .. import ops
 from .buckets import GraphBucketPlanner
-from .hip_autograd import RMSNormFunction, _LayerPlan, hip_layer_autograd
+from .hip_autograd import RMSNormResidualFunction, _LayerPlan, hip_layer_autograd
 from .capabilities import (
     PARTITION_ASSIGNMENT,
     BackendDecision,
@@ -638,8 +638,9 @@ class TRHashEngine(nn.Module):
         decode kernels compute it from the activations they already stage),
         and the residual add runs in the down epilogue.  Under autograd, or
         with fp8 weights, the norm runs on the RMSNorm kernels
-        (``RMSNormFunction``: differentiable in hidden and norm_weight) and
-        then forward_with_residual.  Otherwise (another backend, or a dtype or
+        (``RMSNormResidualFunction``: differentiable in hidden and
+        norm_weight, with the residual's gradient added inside the norm's
+        backward kernel) and then forward_with_residual.  Otherwise (another backend, or a dtype or
         hidden size the kernels do not take) it runs as the reference writes
         it.  ``last_norm`` records which: "fused", "rmsnorm" or "torch"."""
         if norm_weight.shape != (hidden_states.shape[-1],):
@@ -655,11 +656,12 @@ class TRHashEngine(nn.Module):
         if hip and (grad or self._fp8) and ops.rmsnorm_unsupported(hidden_states, norm_weight) is None:
             b, t, h = hidden_states.shape
             flat = hidden_states.reshape(-1, h)
-            if grad:
-                normed = RMSNormFunction.apply(flat, norm_weight, float(eps))
-            else:
-                normed, _ = ops.rmsnorm_forward(flat, norm_weight, float(eps))
             self.last_norm = "rmsnorm"
+            if grad:
+                # the residual's gradient joins dx inside the norm's backward
+                normed, res = RMSNormResidualFunction.apply(flat, norm_weight, float(eps))
+                return self.forward_with_residual(normed.view(b, t, h), token_ids, res.view(b, t, h))
+            normed, _ = ops.rmsnorm_forward(flat, norm_weight, float(eps))
             return self.forward_with_residual(normed.view(b, t, h), token_ids, hidden_states)
         if hip and not grad and not self._fp8:
             b, t, h = hidden_states.shape

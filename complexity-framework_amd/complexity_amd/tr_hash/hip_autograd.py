@@ -120,5 +120,26 @@ class RMSNormFunction(torch.autograd.Function):
         return (dx if ctx.needs_input_grad[0] else None, dw if ctx.needs_input_grad[1] else None, None)
 
 
+class RMSNormResidualFunction(torch.autograd.Function):
+    """``(weight * rmsnorm(x), x)`` for the block's MLP half
+    (block.py:271-278): the second output is x again (a view), the residual
+    the layer adds.  Its gradient (the layer's dout) is added to dx inside
+    the norm's backward kernel instead of by a separate sum over [N, H]."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
+        y, r = ops.rmsnorm_forward(x, weight, eps)
+        ctx.save_for_backward(x, weight, r)
+        return y, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dy: Optional[torch.Tensor], dres: Optional[torch.Tensor]):
+        x, weight, r = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(x)
+        dx, dw = ops.rmsnorm_backward(x, weight, r, dy, dres=dres)
+        return (dx if ctx.needs_input_grad[0] else None, dw if ctx.needs_input_grad[1] else None, None)
+
+
 def hip_layer_autograd(plan: _LayerPlan, x: torch.Tensor, residual: Optional[torch.Tensor], params) -> torch.Tensor:
     return HIPLayerFunction.apply(plan, x, residual, *params)

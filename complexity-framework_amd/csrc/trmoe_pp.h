@@ -381,15 +381,16 @@ struct PPRows64 {
     }
     __device__ __forceinline__ void retarget(const void* base, int64_t row0, int64_t rows_total, int64_t ld_bytes) {
         const int64_t avail = rows_total - row0;
-        nrows = (int)(avail < 256 ? avail : 256);
+        nrows = (int)(avail < 0 ? 0 : (avail < 256 ? avail : 256));   // the descriptor's range: never negative
         ld = (int)ld_bytes;
         rsrc = make_rsrc(static_cast<const char*>(base) + row0 * ld_bytes, (uint32_t)(nrows * ld_bytes));
     }
+    // A row at or past nrows starts at or past the descriptor's range, so it
+    // loads zeros without a select; the stage's K offset is the scalar offset.
     __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
         const int r = row + 16 * j;
-        const int o = (r * ld + koff + kt * kRow64) | (r < nrows ? 0 : kOutOfRange);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (wig * kInstr + j) * 16 * kRow64), 16, o,
-                                                0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (wig * kInstr + j) * 16 * kRow64), 16,
+                                                r * ld + koff, kt * kRow64, 0, 0);
     }
     __device__ __forceinline__ void issue(int kt, char* dst) const {
 #pragma unroll

@@ -101,12 +101,13 @@ struct PPGather {
         row0 = 64 * wave_in_group + (lane >> 3);
         c0 = ((lane & 7) ^ (lane >> 3)) & 7;
     }
+    // an absent row's kOutOfRange (2^31) stays past the operand's range with
+    // its chunk added; the stage's K offset is the scalar offset
     __device__ __forceinline__ void issue_one(int j, int kt, char* dst) const {
         const int chunk = (c0 ^ (kInstr * wig + j)) & 7;
         const int g = goff[row0 + 8 * j];
-        const int o = g < 0 ? kOutOfRange : g + kt * kRowBytes + (chunk << 4);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TRMOE_LDS_PTR(dst + (kInstr * wig + j) * 8 * kRowBytes), 16,
-                                                o, 0, 0, 0);
+                                                g + (chunk << 4), kt * kRowBytes, 0, 0);
     }
     __device__ __forceinline__ void issue(int kt, char* dst) const {
 #pragma unroll

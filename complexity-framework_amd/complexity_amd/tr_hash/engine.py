@@ -749,7 +749,8 @@ class _CapturedTRHashGraph:
     the engine's packed copies, so the runner keeps the pack it captured
     (and its split-K scratch) alive and captures again at replay when the
     engine's current pack is another one: after load_state_dict, an in-place
-    weight update or a change of routing strategy.
+    weight update or a change of routing strategy.  The same holds for the
+    engine's fp8_activations switch, which picks other kernels.
     """
 
     def __init__(self, engine: TRHashEngine, bucket: GraphBucket, sample: torch.Tensor):
@@ -779,6 +780,7 @@ class _CapturedTRHashGraph:
         self.graph = None
         self.output = None
         self.packed = self._current_pack()
+        self.act_fp8 = engine.fp8_activations
         self.scratch = ops.workspace_scope()
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
@@ -793,7 +795,8 @@ class _CapturedTRHashGraph:
 
     def replay(self, hidden_states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
         batch, sequence, _ = hidden_states.shape
-        if self.inner is TRHashBackend.HIP and self._current_pack() is not self.packed:
+        if self.inner is TRHashBackend.HIP and (self._current_pack() is not self.packed
+                                                or self.engine.fp8_activations != self.act_fp8):
             self._capture()
         self.hidden.zero_()
         self.token_ids.zero_()

@@ -8,8 +8,11 @@ the layer's formula (``engine_forward_w8a8``), pinned in tests/test_oracle.py.
 * trmoe_shared_gate_up_a8 multiplies the same e4m3 values the oracle
   dequantizes, so only fp32 summation order and the bf16 rounding of h
   differ: normwise bound 1e-2.
-* The C5 layer with fp8_activations: 2e-2 against the W8A8 oracle and the
-  north-star 5e-2 against the plain (W8A16) oracle, on sampled rows.
+* The C5 layer with fp8_activations (full and active capacity): 2e-2
+  against the W8A8 oracle and the north-star 5e-2 against the plain (W8A16)
+  oracle, on sampled rows.
+* The CUDA_GRAPH backend with fp8_activations: replays equal the eager HIP
+  layer bit for bit, and flipping the switch after capture re-captures.
 """
 
 import pytest
@@ -118,15 +121,17 @@ def test_shared_gate_up_a8(gpu, hidden, shared, n):
     assert O.normwise_rel_err(got, ref) <= 1e-2, O.normwise_rel_err(got, ref)
 
 
-def test_c5_layer_with_fp8_activations(gpu):
-    """C5 (hidden 2048, shared 5632, 16 x 256 experts, 32768 tokens) with
-    fp8_activations against the W8A8 oracle and the plain W8A16 oracle."""
+@pytest.mark.parametrize("name", ["c5_fp8_32768", "c5_fp8_32768_active_8x128"])
+def test_c5_layer_with_fp8_activations(gpu, name):
+    """C5 (hidden 2048, shared 5632, 16 x 256 experts, 32768 tokens; the
+    active variant runs 8 experts x 128 features) with fp8_activations
+    against the W8A8 oracle and the plain W8A16 oracle."""
+    from complexity_amd import ops
     from complexity_amd import workloads as Wl
     from complexity_amd.tr_hash import TRHashBackend
 
-    from complexity_amd import ops
-
-    w = Wl.C5
+    print(f"W8A8 layer {name}", flush=True)
+    w = Wl.WORKLOADS[name]
     engine = Wl.build_engine(w, gpu, backend="hip")
     engine.fp8_activations = True
     x = Wl.make_hidden(w).to(gpu).to(torch.bfloat16)
@@ -157,7 +162,8 @@ def test_c5_layer_with_fp8_activations(gpu):
                                       "shared_down")}
     cfg = engine.config
     kw = dict(route_weights=cfg.route_weights, shared_scale=cfg.shared_output_scale,
-              routed_scale=cfg.routed_output_scale)
+              routed_scale=cfg.routed_output_scale, active_experts=w.active_experts,
+              active_width=w.active_width)
     table = engine._active_route_table.cpu()
     ref8 = O.engine_forward_w8a8(xr, ir, table, p, **kw)
     ref = O.engine_forward(xr, ir, table, p, **kw)
@@ -168,3 +174,39 @@ def test_c5_layer_with_fp8_activations(gpu):
     assert e <= 5e-2
     # the flag changes only the shared gate|up: without it the layer is the W8A16 one
     assert O.normwise_rel_err(plain.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu(), ref) <= 5e-2
+
+
+def test_graph_backend_with_fp8_activations(gpu):
+    """CUDA_GRAPH over an e4m3 layer above decode sizes (256 tokens): replays
+    with eager work between them equal the eager HIP layer with the same
+    switch, before and after fp8_activations is flipped on the captured
+    engine (the runner captures again), and the W8A8 replays differ from the
+    W8A16 ones (the switch reached the captured kernels)."""
+    from complexity_amd.tr_hash import GraphBucket, TRHashEngine, TRHashEngineConfig
+
+    torch.manual_seed(19)
+    common = dict(hidden_size=256, vocab_size=997, num_experts=4, top_k=2, shared_width=384, expert_width=64,
+                  precision="fp8", phase="inference", routing_strategy="token_id_multi_hash")
+    graph = TRHashEngine(TRHashEngineConfig(**common, backend="cuda_graph",
+                                            graph_buckets=(GraphBucket(2, 128),))).to(gpu).to(torch.bfloat16)
+    eager = TRHashEngine(TRHashEngineConfig(**common, backend="hip")).to(gpu).to(torch.bfloat16)
+    eager.load_state_dict(graph.state_dict())
+    for e in (graph, eager):
+        e.routed_strategy = "grouped"
+        e.quantize_fp8_()
+        e.eval()
+    results = {}
+    with torch.no_grad():
+        for flag in (True, False, True):
+            graph.fp8_activations = eager.fp8_activations = flag
+            for step in range(3):
+                g = torch.Generator().manual_seed(step)
+                ids = torch.randint(0, 997, (2, 100 + 14 * step), generator=g).to(gpu)
+                x = torch.randn(2, 100 + 14 * step, 256, generator=g).to(gpu, torch.bfloat16)
+                got = graph(x, ids)
+                _ = torch.randn(1 << 16, device=gpu).sum()  # unrelated eager work
+                torch.cuda.synchronize()
+                want = eager(x, ids)
+                assert torch.equal(got, want), (flag, step)
+                results[(flag, step)] = got
+    assert not torch.equal(results[(True, 0)], results[(False, 0)])

@@ -858,8 +858,10 @@ __device__ __forceinline__ void pps_grouped_rows(const int32_t* offsets, int E, 
 // tile j - q n_ct with j = t / 8, q = j / n_ct: the column tiles of a row
 // tile run on one XCD (workgroups go to XCD t % 8), next to each other, so
 // its h rows are read once into that XCD's L2.  Padding tiles load nothing
-// and store nothing.  K (the expert width) is a multiple of 64.
-template <bool FP8>
+// and store nothing.  K (the expert width) is a multiple of 64.  STREAM: the
+// y rows are stored with the non-temporal hint (y is read only by the shared
+// down, after the shared gate|up; see launch_down_grouped_pps).
+template <bool FP8, bool STREAM>
 __global__ __launch_bounds__(512, 1) void k_down_grouped_pps(DownArgs a) {
     extern __shared__ __align__(16) char lds[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -930,7 +932,7 @@ __global__ __launch_bounds__(512, 1) void k_down_grouped_pps(DownArgs a) {
                     float v[16];
 #pragma unroll
                     for (int q = 0; q < 16; ++q) v[q] = c[tm][tn][q] * cs;
-                    store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+                    store_bf16_pairs<STREAM ? kStoreStream : 0>(rsrc, lb + tm * 32 * ld2, ld2, v);
                 }
             }
         });
@@ -1646,21 +1648,29 @@ static int launch_down_grouped_shape(const DownArgs& a, int64_t assignments, hip
 }
 
 // Persistent expert-grouped down: one workgroup per CU (K a multiple of 64,
-// bf16 activations, every shape; column and row tails are masked).
+// bf16 activations, every shape; column and row tails are masked).  A y of
+// at least half the 256 MB Infinity Cache does not stay cached until the
+// shared down reads it, so its rows are streamed (C5, 268 MB: routed experts
+// 333 -> 295 us; C2's grouped strategy, 58 MB: the layer 307 -> 311 us with
+// the hint, so it keeps the default policy).  The hint on the h of either
+// gate|up was no faster at C5, and slower for the grouped one.
 template <bool FP8>
-static int launch_down_grouped_pps(const DownArgs& a, hipStream_t stream) {
+static int launch_down_grouped_pps(const DownArgs& a, int64_t assignments, hipStream_t stream) {
     using Lay = std::conditional_t<FP8, PPLayoutF8<4, true>, PPLayoutK<4, true>>;
     constexpr int kLds = 2 * Lay::kStage;
-    const int st = ensure_lds(k_down_grouped_pps<FP8>, kLds);
+    const bool stream_y = assignments * a.N * 2 >= (int64_t{128} << 20);
+    auto kern = stream_y ? k_down_grouped_pps<FP8, true> : k_down_grouped_pps<FP8, false>;
+    const int st = ensure_lds(kern, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(k_down_grouped_pps<FP8>, dim3((unsigned)device_cus()), dim3(512), kLds, stream, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)device_cus()), dim3(512), kLds, stream, a);
     return check_launch("routed_experts (down)");
 }
 
 template <class Kind, bool FP8>
 static int down_grouped_kind(const DownArgs& a, int64_t assignments, hipStream_t stream) {
     if constexpr (std::is_same_v<Kind, KindBF16>) {
-        if (a.K > 0 && a.K % 64 == 0 && a.y == nullptr && a.residual == nullptr) return launch_down_grouped_pps<FP8>(a, stream);
+        if (a.K > 0 && a.K % 64 == 0 && a.y == nullptr && a.residual == nullptr)
+            return launch_down_grouped_pps<FP8>(a, assignments, stream);
     }
     const bool fits224 = a.N % ShapeDown224::BN == 0;
     if constexpr (FP8) {

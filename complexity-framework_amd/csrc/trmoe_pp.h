@@ -659,7 +659,11 @@ __device__ __forceinline__ void zero_acc_opaque(f32x16 (&acc)[TM][TN]) {
 // lane columns c - 1, c of row i + 1.  v[i] is the value of row i; `lb` the
 // lane's byte offset of its pair (its row for i = 0, plus 1 for odd lanes,
 // times the row stride, plus 2 (c & ~1)); rows advance by ld2 bytes.
-// Offsets at or past the buffer's range are dropped.
+// Offsets at or past the buffer's range are dropped.  POLICY is the buffer
+// store's cache-policy operand: 0, or kStoreStream (the nt bit, a
+// non-temporal hint) for outputs that no kernel reads soon.
+constexpr int kStoreStream = 2;
+
 __device__ __forceinline__ float dpp_swap_pairs(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
 }
@@ -669,6 +673,7 @@ __device__ __forceinline__ int pair_lane_offset(int row0, int col, int ld2) {
     return (row0 + 4 * (lane >> 5) + (lane & 1)) * ld2 + (col & ~1) * 2;
 }
 
+template <int POLICY = 0>
 __device__ __forceinline__ void store_bf16_pairs(__amdgpu_buffer_rsrc_t rsrc, int lb, int ld2, const float (&v)[16]) {
     const bool odd = threadIdx.x & 1;
 #pragma unroll
@@ -677,7 +682,7 @@ __device__ __forceinline__ void store_bf16_pairs(__amdgpu_buffer_rsrc_t rsrc, in
         const float other = dpp_swap_pairs(odd ? v0 : v1);
         const bf16x2 pr = odd ? bf16x2{(bf16_t)other, (bf16_t)v1} : bf16x2{(bf16_t)v0, (bf16_t)other};
         const int off = lb + (8 * (p >> 1) + 2 * (p & 1)) * ld2;   // row acc_row(lane, 2 p) - acc_row(lane, 0)
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, pr), rsrc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, pr), rsrc, off, 0, POLICY);
     }
 }
 

@@ -475,7 +475,9 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pp(GateUpArgs a) {
 
 // gate_up_save for the persistent kernel: the raw gate|up outputs of the
 // calling wave (times the e4m3 scale) to a.gu, offsets built like
-// gate_up_epi_direct's so that none is hoisted out of the tile loop.
+// gate_up_epi_direct's so that none is hoisted out of the tile loop.  gu is
+// read only by the backward, so it is stored with the non-temporal hint
+// (C2 training step, 218 MB of gu: forward + backward 1.116 -> 1.095 ms).
 template <int TMW>
 __device__ __forceinline__ void gate_up_save_direct(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
                                                     int64_t n0, int wm0, int wn0) {
@@ -494,7 +496,7 @@ __device__ __forceinline__ void gate_up_save_direct(const GateUpArgs& a, const f
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = acc[tm][tn][i] * sc;
-            store_bf16_pairs(rsrc, lb + tm * 32 * ld2, ld2, v);
+            store_bf16_pairs<kStoreStream>(rsrc, lb + tm * 32 * ld2, ld2, v);
         }
     }
 }

@@ -99,6 +99,13 @@ SIGNATURES = {
         _c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp]),
     "trmoe_shared_gate_up_a8": (
         _c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "trmoe_shared_gate_up_a8_mx": (
+        _c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "trmoe_shared_down_combine_a8": (
+        _c_int,
+        [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_vp,
+         _c_float, _c_float, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp],
+    ),
     "trmoe_rmsnorm_backward": (
         _c_int,
         [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,

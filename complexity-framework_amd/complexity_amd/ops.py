@@ -372,6 +372,53 @@ def shared_gate_up_a8(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.T
     return h
 
 
+@_on_tensor_device
+def shared_gate_up_a8_mx(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                         shared_width: int):
+    """W8A8 shared gate|up with h left as block-scaled e4m3: (h_q, h_scale)
+    with h_q [N, round_up(S,128)] e4m3 codes and h_scale [N, round_up(S,128)
+    / 32] uint8 E8M0 exponents, h = h_q * 2^(h_scale - 127) per block of 32
+    features (trmoe_shared_gate_up_a8_mx: the smallest power of two that
+    brings the block's maximum to 448 or below)."""
+    lib = _lib()
+    _require_cuda(xq, w_packed)
+    if xq.dtype != torch.float8_e4m3fn or w_packed.dtype != torch.float8_e4m3fn:
+        raise ValueError("shared_gate_up_a8_mx: e4m3 activations and weights")
+    n, hidden = xq.shape
+    f_pad = _round_up(shared_width, 128)
+    h_q = torch.empty(n, f_pad, dtype=torch.float8_e4m3fn, device=xq.device)
+    h_s = torch.empty(n, f_pad // 32, dtype=torch.uint8, device=xq.device)
+    st = lib.trmoe_shared_gate_up_a8_mx(_p(xq), _p(x_scale.contiguous()), n, hidden, xq.stride(0), _p(w_packed),
+                                        _p(w_scale), shared_width, _p(h_q), f_pad, _p(h_s), f_pad // 32, _stream(xq))
+    N.check(st, "trmoe_shared_gate_up_a8_mx")
+    return h_q, h_s
+
+
+@_on_tensor_device
+def shared_down_combine_a8(h_q: torch.Tensor, h_scale: torch.Tensor, shared_width: int, w_down: torch.Tensor,
+                           w_scale: torch.Tensor, hidden: int, y: Optional[torch.Tensor],
+                           inverse: Optional[torch.Tensor], top_k: int, route_weights: Sequence[float],
+                           shared_scale: float, routed_scale: float,
+                           residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """shared_down_combine on block-scaled e4m3 h (shared_gate_up_a8_mx's
+    outputs) and the layer's e4m3 down pack: bf16 out [N, hidden]; S a
+    multiple of 128."""
+    lib = _lib()
+    _require_cuda(h_q, h_scale, w_down, y, inverse, residual)
+    if h_q.dtype != torch.float8_e4m3fn or w_down.dtype != torch.float8_e4m3fn or h_scale.dtype != torch.uint8:
+        raise ValueError("shared_down_combine_a8: e4m3 h and weights, uint8 scales")
+    n = h_q.shape[0]
+    out = torch.empty(n, hidden, dtype=torch.bfloat16, device=h_q.device)
+    rw = _weights_arg(route_weights)
+    st = lib.trmoe_shared_down_combine_a8(
+        _p(h_q), _p(h_scale), n, shared_width, h_q.stride(0), h_scale.stride(0), _p(w_down), _p(w_scale), hidden,
+        _p(y), hidden, _p(inverse), top_k, ctypes.cast(rw, ctypes.c_void_p), float(shared_scale),
+        float(routed_scale), _p(residual), residual.stride(0) if residual is not None else 0, _p(out), hidden,
+        _stream(h_q))
+    N.check(st, "trmoe_shared_down_combine_a8")
+    return out
+
+
 def routed_experts(x: torch.Tensor, sorted_idx: torch.Tensor, offsets: torch.Tensor, num_experts: int,
                    top_k: int, w_gate_up: torch.Tensor, s_gate_up, w_down: torch.Tensor, s_down,
                    expert_width: int, two_pass: bool = True,
@@ -700,11 +747,19 @@ class PackedLayer:
         return got
 
 
+def fp8_activation_mode(mode):
+    """The W8A8 switch: False, True (the shared gate|up and down on e4m3
+    activations) or "gate_up" (the shared gate|up only)."""
+    if mode is False or mode is True or mode == "gate_up":
+        return mode
+    raise ValueError(f"fp8_activations: False, True or 'gate_up', not {mode!r}")
+
+
 @_on_tensor_device
 def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.Tensor, packed: PackedLayer,
                   route_weights: Sequence[float], shared_scale: float, routed_scale: float,
                   order: int = ORDER_TOKEN, residual: Optional[torch.Tensor] = None, save: bool = False,
-                  norm_eps: Optional[float] = None, act_fp8: bool = False):
+                  norm_eps: Optional[float] = None, act_fp8=False):
     """out[N, H] = shared_scale*shared(x) + routed_scale*routed(x) (+ residual).
 
     grouped: K1 partition, K3 grouped experts, K2 shared gate|up, K4 down with
@@ -716,10 +771,14 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
     rms_row_scale.  save: returns (out, gu, h): the raw gate|up outputs and,
     for the dense strategy, the down GEMM's input h (else None), which the
     backward reuses.  act_fp8 (e4m3 packs, grouped strategy, above decode
-    sizes, hidden a multiple of 128): the shared gate|up runs W8A8 on x
-    quantized per token (quantize_rows_e4m3, shared_gate_up_a8)."""
+    sizes, hidden a multiple of 128): True or "gate_up": the shared gate|up
+    runs W8A8 on x quantized per token (quantize_rows_e4m3,
+    shared_gate_up_a8); True with S a multiple of 128: its h leaves as
+    block-scaled e4m3 and the shared down runs W8A8 too
+    (shared_gate_up_a8_mx, shared_down_combine_a8)."""
     n, hidden = x.shape
     top_k = route_table.shape[0]
+    act_fp8 = fp8_activation_mode(act_fp8)
     if save and packed.fp8:
         raise ValueError("layer_forward: e4m3 weights are inference-only (no saved pre-activations, no backward)")
     if n == 0:
@@ -756,6 +815,13 @@ def layer_forward(x: torch.Tensor, token_ids: torch.Tensor, route_table: torch.T
         if (act_fp8 and packed.shared_gate_up.dtype == torch.float8_e4m3fn and rscale is None and not decode
                 and hidden % 128 == 0 and hidden <= RMSNORM_MAX_HIDDEN.get(x.dtype, 0)):
             xq, xs = quantize_rows_e4m3(x)
+            if act_fp8 is True and packed.shared_width % 128 == 0:
+                # h stays e4m3 (one power-of-two scale per 32 features) into the down
+                h_q, h_s = shared_gate_up_a8_mx(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale,
+                                                packed.shared_width)
+                return shared_down_combine_a8(h_q, h_s, packed.shared_width, packed.shared_down,
+                                              packed.shared_down_scale, hidden, y, inverse, top_k, route_weights,
+                                              shared_scale, routed_scale, residual)
             h = shared_gate_up_a8(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width)
         else:
             h = shared_gate_up(x, packed.shared_gate_up, packed.shared_gate_up_scale, packed.shared_width,

@@ -139,11 +139,14 @@ class TRHashEngine(nn.Module):
 
         self.last_backend: Optional[BackendDecision] = None
         self.last_norm: Optional[str] = None
-        # W8A8: with e4m3 weights (quantize_fp8_), also quantize each token's
-        # activations to e4m3 (per-token scale) for the shared gate|up, which
-        # then runs on the e4m3 MFMA (prefill sizes, grouped strategy).  Off
-        # by default: the reference has no fp8 path and keeps activations in
-        # the compute dtype.
+        # W8A8: with e4m3 weights (quantize_fp8_), also quantize activations
+        # to e4m3 so the shared GEMMs run on the e4m3 MFMA (prefill sizes,
+        # grouped strategy).  True: each token's x (per-token scale) into the
+        # shared gate|up, and its h as e4m3 with a power-of-two scale per 32
+        # features into the shared down (shared width a multiple of 128, else
+        # the down keeps bf16 h); "gate_up": the gate|up only.  Off by
+        # default: the reference has no fp8 path and keeps activations in the
+        # compute dtype.
         self.fp8_activations = False
         self._graph_pool: Dict[GraphBucket, "_CapturedTRHashGraph"] = {}
         self._bucket_planner = GraphBucketPlanner(config.graph_buckets) if config.graph_buckets else None
@@ -512,7 +515,7 @@ class TRHashEngine(nn.Module):
                 self.config.routed_output_scale,
                 order=order,
                 residual=res,
-                act_fp8=self.fp8_activations and self._fp8,
+                act_fp8=ops.fp8_activation_mode(self.fp8_activations) if self._fp8 else False,
             )
         return out if out.dtype == flat_x.dtype else out.to(flat_x.dtype)
 

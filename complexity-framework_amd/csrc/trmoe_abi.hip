@@ -336,6 +336,48 @@ int trmoe_shared_gate_up_a8(const void* x_q, const float* x_scale, int64_t n_tok
     return launch_gate_up_a8(a, 2 * round_up(shared_width, 128), as_stream(stream));
 }
 
+int trmoe_shared_gate_up_a8_mx(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t hidden, int64_t ldxq,
+                               const void* w_packed, const float* w_scale, int64_t shared_width, void* h_q,
+                               int64_t ldhq, void* h_scale, int64_t ldhs, void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && shared_width > 0, "shared_gate_up_a8_mx: bad dimensions");
+    TRMOE_REQUIRE(hidden % 128 == 0 && hidden < (int64_t)1 << 30,
+                  "shared_gate_up_a8_mx: hidden must be a multiple of 128");
+    TRMOE_REQUIRE(ldxq >= hidden, "shared_gate_up_a8_mx: ldxq < hidden");
+    const int64_t f_pad = round_up(shared_width, 128);
+    // a 256-row tile's bytes stay below 2^31 (32-bit buffer offsets)
+    TRMOE_REQUIRE(ldhq >= f_pad && ldhq % 16 == 0 && ldhq < (int64_t)1 << 23,
+                  "shared_gate_up_a8_mx: ldhq must be a multiple of 16, at least round_up(shared_width, 128)");
+    TRMOE_REQUIRE(ldhs >= f_pad / 32 && ldhs % 4 == 0 && ldhs < (int64_t)1 << 23,
+                  "shared_gate_up_a8_mx: ldhs must be a multiple of 4, at least round_up(shared_width, 128) / 32");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(n_tokens * ldhq < (int64_t)1 << 40, "shared_gate_up_a8_mx: h_q too large");
+    TRMOE_REQUIRE(x_q && x_scale && w_packed && w_scale && h_q && h_scale, "shared_gate_up_a8_mx: null pointer");
+    TRMOE_REQUIRE(aligned16(w_packed), "shared_gate_up_a8_mx: packed weights must be 16-byte aligned");
+    TRMOE_REQUIRE(rows_ok(x_q, ldxq, 1),
+                  "shared_gate_up_a8_mx: x_q rows must be 16-byte aligned with a row stride that is a multiple of 16 "
+                  "bytes");
+    TRMOE_REQUIRE(aligned16(h_q) && reinterpret_cast<uintptr_t>(h_scale) % 4 == 0,
+                  "shared_gate_up_a8_mx: h_q must be 16-byte and h_scale 4-byte aligned");
+    GateUpArgs a{};
+    a.x = x_q;
+    a.ldx = ldxq;
+    a.M = n_tokens;
+    a.K = (int)hidden;
+    a.w = w_packed;
+    a.ldw = hidden;
+    a.w_scale = w_scale;
+    a.h = h_q;
+    a.ldh = ldhq;
+    a.hs = h_scale;
+    a.ldhs = ldhs;
+    a.shared_mult = 1.0f;
+    a.shared_feats = 0;
+    a.expert_feats = 1;
+    a.vocab = 1;
+    a.row_scale = x_scale;
+    return launch_gate_up_a8(a, 2 * f_pad, as_stream(stream));
+}
+
 static bool rmsnorm_hidden_ok(int act_dtype, int64_t hidden) {
     return hidden > 0 && (hidden * elem_bytes(act_dtype)) % 16 == 0 && hidden <= rmsnorm_max_hidden(act_dtype);
 }
@@ -713,6 +755,59 @@ int trmoe_shared_down_combine(int act_dtype, int w_dtype, const void* h, int64_t
     return shared_down_combine_impl(act_dtype, w_dtype, h, n_tokens, shared_width, ldh, w_down, w_scale, hidden, y,
                                     ldy, inverse, top_k, route_weights, shared_scale, routed_scale, residual, ldr,
                                     out, ldo, workspace, workspace_bytes, stream, nullptr);
+}
+
+int trmoe_shared_down_combine_a8(const void* h_q, const void* h_scale, int64_t n_tokens, int64_t shared_width,
+                                 int64_t ldhq, int64_t ldhs, const void* w_down, const float* w_scale, int64_t hidden,
+                                 const void* y, int64_t ldy, const int64_t* inverse, int top_k,
+                                 const float* route_weights, float shared_scale, float routed_scale,
+                                 const void* residual, int64_t ldr, void* out, int64_t ldo, void* stream) {
+    TRMOE_REQUIRE(n_tokens >= 0 && hidden > 0 && hidden < (int64_t)1 << 30, "shared_down_combine_a8: bad dimensions");
+    TRMOE_REQUIRE(shared_width > 0 && shared_width % 128 == 0 && shared_width < (int64_t)1 << 30,
+                  "shared_down_combine_a8: shared_width must be a positive multiple of 128");
+    // a 256-row tile's bytes stay below 2^31 (32-bit buffer offsets)
+    TRMOE_REQUIRE(ldhq >= shared_width && ldhq % 16 == 0 && ldhq < (int64_t)1 << 23,
+                  "shared_down_combine_a8: ldhq must be a multiple of 16, at least shared_width");
+    TRMOE_REQUIRE(ldhs >= shared_width / 32 && ldhs % 4 == 0 && ldhs < (int64_t)1 << 23,
+                  "shared_down_combine_a8: ldhs must be a multiple of 4, at least shared_width / 32");
+    TRMOE_REQUIRE(ldo >= hidden, "shared_down_combine_a8: ldo < hidden");
+    TRMOE_REQUIRE((y == nullptr) == (inverse == nullptr), "shared_down_combine_a8: y and inverse go together");
+    if (y != nullptr) {
+        TRMOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, "shared_down_combine_a8: bad top_k");
+        TRMOE_REQUIRE(route_weights != nullptr, "shared_down_combine_a8: null route_weights");
+        TRMOE_REQUIRE(ldy >= hidden, "shared_down_combine_a8: ldy < hidden");
+    }
+    TRMOE_REQUIRE(residual == nullptr || ldr >= hidden, "shared_down_combine_a8: ldr < hidden");
+    if (n_tokens == 0) return TRMOE_OK;
+    TRMOE_REQUIRE(n_tokens * ldhq < (int64_t)1 << 40, "shared_down_combine_a8: h_q too large");
+    TRMOE_REQUIRE(h_q && h_scale && w_down && w_scale && out, "shared_down_combine_a8: null pointer");
+    TRMOE_REQUIRE(aligned16(w_down) && aligned16(h_q) && reinterpret_cast<uintptr_t>(h_scale) % 4 == 0,
+                  "shared_down_combine_a8: w_down and h_q must be 16-byte, h_scale 4-byte aligned");
+    DownArgs a{};
+    a.h = h_q;
+    a.ldh = ldhq;
+    a.hs = h_scale;
+    a.ldhs = ldhs;
+    a.M = n_tokens;
+    a.K = (int)shared_width;
+    a.w = w_down;
+    a.ldw = round_up(shared_width, 8);
+    a.w_scale = w_scale;
+    a.N = (int)hidden;
+    a.y = y;
+    a.ldy = ldy;
+    a.inverse = inverse;
+    a.top_k = (y != nullptr) ? top_k : 0;
+    for (int j = 0; j < 4; ++j) a.rw[j] = (y != nullptr && j < top_k) ? route_weights[j] : 0.f;
+    a.shared_scale = shared_scale;
+    a.routed_scale = routed_scale;
+    a.residual = residual;
+    a.ldr = ldr;
+    a.out = out;
+    a.ldo = ldo;
+    a.vec_ok = aligned16(out) && (ldo * 2) % 16 == 0 && (y == nullptr || (aligned16(y) && (ldy * 2) % 16 == 0)) &&
+               (residual == nullptr || (aligned16(residual) && (ldr * 2) % 16 == 0));
+    return launch_down_combine_a8(a, as_stream(stream));
 }
 
 size_t trmoe_fragment_bytes(int dtype, int64_t rows, int64_t cols) {

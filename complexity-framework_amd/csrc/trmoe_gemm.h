@@ -73,6 +73,11 @@ struct GateUpArgs {
     int64_t gather_mod;
     int64_t w_expert_stride;
     int64_t scale_expert_stride;
+    // Block-scaled e4m3 h (W8A8 with launch_gate_up_a8 only; null: h is
+    // bf16): h holds e4m3 codes (row stride ldh bytes) and hs one E8M0
+    // exponent per token and 32 features (row stride ldhs bytes).
+    void* hs;
+    int64_t ldhs;
 };
 
 struct DownArgs {
@@ -109,6 +114,11 @@ struct DownArgs {
     int64_t gather_mod;
     int64_t w_expert_stride;
     int64_t scale_expert_stride;
+    // Block-scaled e4m3 h (launch_down_combine_a8 only): h holds e4m3 codes
+    // (row stride ldh bytes), hs one E8M0 exponent per token and 32 K values
+    // (row stride ldhs bytes, a multiple of 4).
+    const void* hs;
+    int64_t ldhs;
 };
 
 struct RoutedArgs {
@@ -245,6 +255,9 @@ int launch_pack_fragments(const void* src, int64_t rows, int64_t kbytes, int64_t
 // stride a.ldx bytes, a.row_scale their per-token scales, a.w e4m3 packed
 // weights with a.w_scale; needs a.K % 128 == 0 and whole 256-row column tiles.
 int launch_gate_up_a8(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream);
+// K4 on block-scaled e4m3 h and e4m3 weights (the e4m3 MFMA with one E8M0
+// scale per 32 K values of each row of h); K a multiple of 128.
+int launch_down_combine_a8(const DownArgs& a, hipStream_t stream);
 int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int64_t ldx, float eps, float* row_scale,
                          hipStream_t stream);
 // RMSNorm with its backward (trmoe_norm.hip): y = T(x * r) * w with r saved;

@@ -364,6 +364,74 @@ __device__ __forceinline__ void gate_up_epi_direct(const GateUpArgs& a, const f3
     }
 }
 
+// W8A8 h as block-scaled e4m3 (a.hs != nullptr), from transposed
+// accumulator blocks (pp_mma_f8<TM, true>): acc[tm][0][i] / acc[tm][1][i]
+// are the gate / up outputs of feature f0 + acc_row(lane, i), f0 = the
+// wave's first feature, for token wm0 + 32 tm + lane % 32.  So a lane holds
+// 16 of the 32 features of its token's block and lane l ^ 32 the other 16.
+// h = silu(g) * u with the activations' per-token scale and the weights'
+// per-row scales; then per token and block the exponent e: the smallest
+// integer with amax <= 448 * 2^e (amax = m * 2^k by frexp, m in [0.5, 1):
+// e = k - 9, plus 1 when m > 0.875 = 448 / 2^9), clamped to [-126, 126], and
+// 0 for a block without a positive finite maximum (all zeros, or NaN or
+// infinite values).  The codes e4m3(h * 2^-e) (round to nearest even,
+// clamped to +-448, NaN stays NaN) go to a.h (ldh bytes per row, four
+// features per 4-byte store), the E8M0 bytes e + 127 to a.hs (ldhs bytes per
+// row, byte feature / 32).
+__device__ __forceinline__ int mx_exponent(float amax) {
+    if (!(amax > 0.0f) || !__builtin_isfinite(amax)) return 0;
+    int k;
+    const float m = frexpf(amax, &k);
+    const int e = k - 9 + (m > 0.875f ? 1 : 0);
+    return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+template <int TMW>
+__device__ __forceinline__ void gate_up_epi_mx(const GateUpArgs& a, const f32x16 (&acc)[TMW][2], int64_t m0,
+                                               int64_t n0, int wm0, int wn0) {
+    const int lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
+    const int64_t pbase = n0 + wn0;   // packed row of the wave's gate block
+    const float* ws = a.w_scale + pbase;
+    const int64_t mlim = a.M - m0 < 64 * TMW ? a.M - m0 : 64 * TMW;
+    int ldq = (int)a.ldh;   // opaque row strides: no offset below is hoisted out of a caller's loop
+    asm volatile("" : "+s"(ldq));
+    int ldsc = (int)a.ldhs;
+    asm volatile("" : "+s"(ldsc));
+    const auto rq = make_rsrc(static_cast<uint8_t*>(a.h) + m0 * a.ldh, (uint32_t)(mlim * ldq));
+    const auto rs = make_rsrc(static_cast<uint8_t*>(a.hs) + m0 * a.ldhs, (uint32_t)(mlim * ldsc));
+    const int f0 = (int)(pbase >> 1);
+    const int blk = (int)(pbase >> 6);
+#pragma unroll
+    for (int tm = 0; tm < TMW; ++tm) {
+        const int row = wm0 + tm * 32 + r;   // the lane's token in the tile
+        const float rsc = a.row_scale[m0 + (row < mlim ? row : mlim - 1)];
+        float v[16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int fr = 8 * (i >> 2) + 4 * half + (i & 3);   // acc_row(lane, i)
+            v[i] = silu_f(acc[tm][0][i] * ws[fr] * rsc) * (acc[tm][1][i] * (ws[32 + fr] * a.shared_mult) * rsc);
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const int e = mx_exponent(amax);
+        if (half == 0) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(e + 127), rs, row * ldsc + blk, 0, 0);
+        const int rowb = row * ldq + f0 + 4 * half;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {   // features f0 + 8 b + 4 half + 0..3
+            float q[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float t = ldexpf(v[4 * b + u], -e);
+                q[u] = t > 448.0f ? 448.0f : (t < -448.0f ? -448.0f : t);   // NaN stays NaN
+            }
+            int pk = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+            pk = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
+            __builtin_amdgcn_raw_buffer_store_b32((uint32_t)pk, rq, rowb + 8 * b, 0, 0);
+        }
+    }
+}
+
 // gate_up_epi_direct for a tile that may hold dense-routed expert features:
 // the calling wave's 32-feature block is wholly shared (gate_up_epi_direct)
 // or wholly one expert's, whose h is silu(g) * u times the token's route
@@ -508,10 +576,12 @@ __device__ __forceinline__ void gate_up_save_direct(const GateUpArgs& a, const f
 // stages load and multiply.  SAVE: also the raw gate|up outputs (a.gu).
 // A8 (with FP8): e4m3 activations too, a.x holding the codes (row stride
 // a.ldx bytes) and a.row_scale their per-token scales: 128 K values per
-// stage on the e4m3 MFMA (W8A8).
-template <int TMW, bool SAVE, bool FP8, bool A8 = false>
+// stage on the e4m3 MFMA (W8A8).  MXH (with A8): transposed accumulator
+// blocks, and h leaves as block-scaled e4m3 (gate_up_epi_mx).
+template <int TMW, bool SAVE, bool FP8, bool A8 = false, bool MXH = false>
 __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t tiles_m, int64_t n_tiles) {
     static_assert(!A8 || (FP8 && !SAVE), "W8A8 is the inference form of the e4m3 weights");
+    static_assert(!MXH || A8, "block-scaled h is written by the W8A8 kernel");
     constexpr int BM = 64 * TMW;
     extern __shared__ __align__(16) char lds[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -547,7 +617,7 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
     zero_acc<KindBF16>(acc);
     using Lay = std::conditional_t<A8, PPLayoutK8<TMW, true>,
                                    std::conditional_t<FP8, PPLayoutF8<TMW, true>, PPLayoutK<TMW, true>>>;
-    pp_stream<TMW, Lay>(
+    pp_stream<TMW, Lay, MXH>(
         ap, bp, A8 ? a.K / 128 : a.K / 64, ntiles, lds, group, wm0, wn0, acc,
         [&](int i) {   // i >= ntiles: no rows (the refills past the last stage load zeros)
             int64_t tm0, tn0;
@@ -563,7 +633,9 @@ __global__ __launch_bounds__(512, 1) void k_gate_up_pps(GateUpArgs a, int64_t ti
             int64_t tm0, tn0;
             coords(i, tm0, tn0);
             if constexpr (SAVE) gate_up_save_direct<TMW>(a, c, tm0, tn0, wm0, wn0);
-            if constexpr (A8)
+            if constexpr (MXH)
+                gate_up_epi_mx<TMW>(a, c, tm0, tn0, wm0, wn0);
+            else if constexpr (A8)
                 gate_up_epi_direct<TMW, true, true>(a, c, tm0, tn0, wm0, wn0);
             else
                 gate_up_epi_direct<TMW, !FP8>(a, c, tm0, tn0, wm0, wn0);
@@ -1069,9 +1141,13 @@ __device__ __forceinline__ void down_tile(uint32_t id, uint32_t tiles_m, uint32_
 // last tile of H = 896 multiplies 128 of them).  Epilogue: each
 // group writes shared_scale * column scale * acc for its rows to LDS as bf16
 // (the tile kernel's rounding), then every thread adds the route-weighted y
-// rows and the residual over 16-byte chunks and stores.
-template <bool FP8>
+// rows and the residual over 16-byte chunks and stores.  A8 (with FP8): h
+// holds block-scaled e4m3 codes (a.h, ldh bytes per row; a.hs the E8M0
+// scales), multiplied on the e4m3 MFMA with the scales in its operand, 128 K
+// values per stage.
+template <bool FP8, bool A8 = false>
 __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
+    static_assert(!A8 || FP8, "block-scaled h goes with e4m3 weights");
     constexpr int BM = 256, BN = 256;
     using T = bf16_t;
     extern __shared__ __align__(16) char lds[];
@@ -1100,9 +1176,9 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     }
 
     PPRows<BM> ap;
-    std::conditional_t<FP8, PPRows64, PPRows<256>> bp;
+    std::conditional_t<FP8 && !A8, PPRows64, PPRows<256>> bp;
     if (group == 1) {
-        ap.init(a.h, m0, a.M, a.ldh * (int64_t)sizeof(T), wig);
+        ap.init(a.h, m0, a.M, A8 ? a.ldh : a.ldh * (int64_t)sizeof(T), wig);
     } else {   // rows past N load as zero
         if constexpr (FP8)
             bp.init(a.w, n0, a.N, a.ldw, wig);
@@ -1112,13 +1188,15 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     f32x16 acc[4][2];
     zero_acc<KindBF16>(acc);
     constexpr int kORowBytes = BN * 2 + 16;
-    using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
+    using Lay = std::conditional_t<A8, PPLayoutK8<4, true>, std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>>;
+    std::conditional_t<A8, PPBlockScales, PPNoScales> sc;
+    if constexpr (A8) sc.init(a.hs, a.ldhs, m0, a.M, wm0);
     // nothing to add to the product (no routed rows, no residual): each
     // group stores its rows straight from the accumulators as bf16 pairs
     // (group 0 while group 1 multiplies the last stage), with no LDS tile
     // and no copy-out pass
     const bool direct = a.y == nullptr && a.residual == nullptr && a.vec_ok;
-    pp_main<4, Lay>(ap, bp, a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
+    pp_main<4, Lay>(ap, bp, A8 ? a.K / 128 : a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
         const int r = lane & 31;
         float cs[2];
 #pragma unroll
@@ -1154,7 +1232,7 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
                     *reinterpret_cast<T*>(lds + rl * kORowBytes + (wn0 + tn * 32 + r) * 2) =
                         from_f32<T>(c[tm][tn][i] * cs[tn]);
             }
-    });
+    }, sc);
     if (direct) return;
 
     const T* y = static_cast<const T*>(a.y);
@@ -1446,7 +1524,7 @@ int launch_gate_up_a8(const GateUpArgs& a, int64_t packed_rows, hipStream_t stre
     const int64_t cus = device_cus();
     const int64_t grid = n_tiles < cus ? n_tiles : cus;
     constexpr int kLds = 2 * PPLayoutK8<4>::kStage;
-    auto kern = k_gate_up_pps<4, false, true, true>;
+    auto kern = a.hs != nullptr ? k_gate_up_pps<4, false, true, true, true> : k_gate_up_pps<4, false, true, true>;
     const int st = ensure_lds(kern, kLds);
     if (st) return st;
     if (grid <= 0) return TRMOE_OK;
@@ -1538,16 +1616,21 @@ static int launch_down_shape(const DownArgs& a, hipStream_t stream) {
 
 // bf16 down GEMMs with at least a full round of 256x256 tiles run on the
 // ping-pong main loop.
-template <bool FP8>
+template <bool FP8, bool A8 = false>
 static int launch_down_pp(const DownArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)(((a.M + 255) / 256) * ((a.N + 255) / 256)));
-    using Lay = std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>;
+    using Lay = std::conditional_t<A8, PPLayoutK8<4, true>, std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>>;
     constexpr int kEpi = 256 * (256 * 2 + 16);   // the bf16 output tile, over the stages
     constexpr int kLds = kEpi > 2 * Lay::kStage ? kEpi : 2 * Lay::kStage;
-    const int st = ensure_lds(k_down_pp<FP8>, kLds);
+    const int st = ensure_lds(k_down_pp<FP8, A8>, kLds);
     if (st) return st;
-    hipLaunchKernelGGL(k_down_pp<FP8>, grid, dim3(512), kLds, stream, a);
-    return check_launch("shared_down_combine");
+    hipLaunchKernelGGL((k_down_pp<FP8, A8>), grid, dim3(512), kLds, stream, a);
+    return check_launch(A8 ? "shared_down_combine_a8" : "shared_down_combine");
+}
+
+int launch_down_combine_a8(const DownArgs& a, hipStream_t stream) {
+    if (a.M <= 0) return TRMOE_OK;
+    return launch_down_pp<true, true>(a, stream);
 }
 
 // The packed down weights have round_up(N, 256) rows, so every tile choice

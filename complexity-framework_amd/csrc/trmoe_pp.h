@@ -282,7 +282,9 @@ __device__ __forceinline__ void mfma_f8(const i32x8& a, const i32x8& b, f32x16& 
     acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, 127);
 }
 
-template <int TM>
+// TR: transposed accumulator blocks, B times A: block (tm, tn) holds row
+// 32 tn + acc_row(lane, i) of B's rows against A's row 32 tm + lane % 32.
+template <int TM, bool TR = false>
 __device__ __forceinline__ void pp_mma_f8(const i32x8 (&fa)[2][TM], const i32x8 (&fb)[2][2],
                                           f32x16 (&acc)[TM][2]) {
 #pragma unroll
@@ -290,12 +292,17 @@ __device__ __forceinline__ void pp_mma_f8(const i32x8 (&fa)[2][TM], const i32x8 
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn) mfma_f8(fa[q][tm], fb[q][tn], acc[tm][tn]);
+            for (int tn = 0; tn < 2; ++tn) {
+                if constexpr (TR)
+                    mfma_f8(fb[q][tn], fa[q][tm], acc[tm][tn]);
+                else
+                    mfma_f8(fa[q][tm], fb[q][tn], acc[tm][tn]);
+            }
 }
 
 // pp_mma_f8 with one stage of an operand's loads spread over its MFMAs (as
 // pp_mma_load does for bf16).
-template <int TM, class LD>
+template <int TM, class LD, bool TR = false>
 __device__ __forceinline__ void pp_mma_load_f8(const i32x8 (&fa)[2][TM], const i32x8 (&fb)[2][2],
                                                f32x16 (&acc)[TM][2], const LD& ld, int kt, char* dst) {
     constexpr int kMfma = 4 * TM;
@@ -308,7 +315,10 @@ __device__ __forceinline__ void pp_mma_load_f8(const i32x8 (&fa)[2][TM], const i
 #pragma unroll
             for (int tn = 0; tn < 2; ++tn) {
                 const int i = (q * TM + tm) * 2 + tn;
-                mfma_f8(fa[q][tm], fb[q][tn], acc[tm][tn]);
+                if constexpr (TR)
+                    mfma_f8(fb[q][tn], fa[q][tm], acc[tm][tn]);
+                else
+                    mfma_f8(fa[q][tm], fb[q][tn], acc[tm][tn]);
                 if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
             }
 #pragma unroll
@@ -318,6 +328,103 @@ __device__ __forceinline__ void pp_mma_load_f8(const i32x8 (&fa)[2][TM], const i
         __builtin_amdgcn_sched_group_barrier(0x008, kEvery - 1, 0);   // MFMA
     }
 }
+
+// Block-scaled A (W8A8 with e4m3 h): the A operand's E8M0 scales, one per
+// row and 32 K values, in the MFMA's scale operand.  A K step's 64 K values
+// are two blocks: bytes [0, 32) of the step (registers 0-3 of both lane
+// halves) take the scale of lane half 0 (the row's lane l), bytes [32, 64)
+// (registers 4-7) that of lane half 1 (lane l + 32); the operand's byte
+// OPSEL holds it.  B's scale is 2^0.  sa[tm]: the row's four block scales
+// of the stage shifted right by 8 (lane / 32), so that byte 0 is the lane
+// half's block of step 0 and byte 2 its block of step 1.
+template <int OPSEL>
+__device__ __forceinline__ void mfma_f8s(const i32x8& a, const i32x8& b, f32x16& acc, uint32_t sa) {
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, OPSEL, (int)sa, 0, 127);
+}
+
+template <int TM>
+__device__ __forceinline__ void pp_mma_f8s(const i32x8 (&fa)[2][TM], const i32x8 (&fb)[2][2], f32x16 (&acc)[TM][2],
+                                           const uint32_t (&sa)[TM]) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) mfma_f8s<0>(fa[0][tm], fb[0][tn], acc[tm][tn], sa[tm]);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) mfma_f8s<2>(fa[1][tm], fb[1][tn], acc[tm][tn], sa[tm]);
+}
+
+// pp_mma_f8s with one stage of an operand's loads spread over its MFMAs.
+template <int TM, class LD>
+__device__ __forceinline__ void pp_mma_load_f8s(const i32x8 (&fa)[2][TM], const i32x8 (&fb)[2][2],
+                                                f32x16 (&acc)[TM][2], const uint32_t (&sa)[TM], const LD& ld, int kt,
+                                                char* dst) {
+    constexpr int kMfma = 4 * TM;
+    constexpr int kEvery = kMfma / LD::kInstr;
+    static_assert(kEvery >= 1 && kMfma % LD::kInstr == 0, "loads must spread evenly over the MFMAs");
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int i = tm * 2 + tn;
+            mfma_f8s<0>(fa[0][tm], fb[0][tn], acc[tm][tn], sa[tm]);
+            if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
+        }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int i = 2 * TM + tm * 2 + tn;
+            mfma_f8s<2>(fa[1][tm], fb[1][tn], acc[tm][tn], sa[tm]);
+            if (i % kEvery == 0) ld.issue_one(i / kEvery, kt, dst);
+        }
+#pragma unroll
+    for (int j = 0; j < LD::kInstr; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);            // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x008, kEvery - 1, 0);   // MFMA
+    }
+}
+
+// Scale sources of pp_main: none (unit scales), or the E8M0 block scales of
+// the wave's A rows (a byte array of ldhs bytes per row, 4 bytes per 128-K
+// stage): the dword of stage t of rows wm0 + 32 tm + lane % 32 of the tile.
+// Rows past the descriptor's range (rows_total) read 0, a scale of 2^-127
+// on rows whose codes load as zero.
+struct PPNoScales {
+    static constexpr bool kOn = false;
+    template <int TM>
+    __device__ __forceinline__ void load(int, uint32_t (&)[TM]) const {}
+};
+
+struct PPBlockScales {
+    static constexpr bool kOn = true;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int off;      // byte offset of the lane's row for tm = 0
+    int step;     // 32 rows
+    int shift;    // 8 (lane / 32)
+    __device__ __forceinline__ void init(const void* hs, int64_t ldhs, int64_t first_row, int64_t rows_total,
+                                         int wm0) {
+        const int64_t avail = rows_total - first_row;
+        const int64_t nrows = avail < 0 ? 0 : (avail < 256 ? avail : 256);
+        rsrc = make_rsrc(static_cast<const char*>(hs) + first_row * ldhs, (uint32_t)(nrows * ldhs));
+        const int lane = threadIdx.x & 63;
+        off = (wm0 + (lane & 31)) * (int)ldhs;
+        step = 32 * (int)ldhs;
+        shift = 8 * (lane >> 5);
+    }
+    template <int TM>
+    __device__ __forceinline__ void load(int t, uint32_t (&dst)[TM]) const {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) dst[tm] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off + tm * step, 4 * t, 0);
+    }
+    template <int TM>
+    __device__ __forceinline__ void take(const uint32_t (&src)[TM], uint32_t (&dst)[TM]) const {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) dst[tm] = src[tm] >> shift;
+    }
+};
 
 // Layouts whose stages hold e4m3 A and B (kF8Mma) multiply with pp_mma_f8.
 template <class L, class = void>
@@ -557,18 +664,36 @@ struct PPLayoutT {
 // group 0 in the phase after its last multiply, while group 1 multiplies the
 // last stage, and group 1 after it.  Every wave leaves after a barrier that
 // follows both groups' rows_out, so the tile can be read right away.
-template <int TMW, class Lay, class LA, class LB, class RowsOut>
+// e4m3 layouts (kF8Mma) multiply with pp_mma_f8, or with sc's block scales
+// (SC::kOn, pp_mma_f8s): each wave loads the scale dwords of stage t + 1
+// while it multiplies stage t (group 0 with its B refill, group 1 after the
+// phase barrier), and they land by the wait that ends that phase.
+template <int TMW, class Lay, class LA, class LB, class RowsOut, class SC = PPNoScales>
 __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char* lds, int group, int wm0, int wn0,
-                                        f32x16 (&acc)[TMW][2], RowsOut&& rows_out) {
+                                        f32x16 (&acc)[TMW][2], RowsOut&& rows_out, const SC& sc = SC{}) {
     constexpr int kStage = Lay::kStage;
     constexpr int kBOff = Lay::kBOff;
     char* st0 = lds;
     char* st1 = lds + kStage;
     constexpr int kAI = LA::kInstr, kBI = LB::kInstr;
+    constexpr bool kF8 = F8Mma<Lay>::value;
+    static_assert(kF8 || !SC::kOn, "block scales are for e4m3 stages");
 
-    u32x4 fa[4][TMW], fb[4][2];
+    std::conditional_t<kF8, i32x8[2][TMW], u32x4[4][TMW]> fa;
+    std::conditional_t<kF8, i32x8[2][2], u32x4[4][2]> fb;
+    uint32_t sa[TMW] = {}, sn[TMW] = {};   // block scales of the stage multiplied next / of the one after
+    auto mma = [&]() {
+        if constexpr (SC::kOn)
+            pp_mma_f8s<TMW>(fa, fb, acc, sa);
+        else if constexpr (kF8)
+            pp_mma_f8<TMW>(fa, fb, acc);
+        else
+            pp_mma<TMW>(fa, fb, acc);
+    };
 
-    // prologue: stages 0 and 1 requested, stage 0 landed everywhere
+    // prologue: stages 0 and 1 requested, stage 0 landed everywhere (and
+    // the scales of stage 0, requested before them)
+    if constexpr (SC::kOn) sc.template load<TMW>(0, sn);
     if (group == 1) {
         ap.issue(0, st0);
         if (nk > 1) {
@@ -586,6 +711,7 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
             wait_vmcnt<0>();
         }
     }
+    if constexpr (SC::kOn) sc.take(sn, sa);
     pp_barrier();
 
     if (group == 0) {
@@ -597,10 +723,13 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
             // behind a wave's own buffer->LDS loads wait for those loads
             __builtin_amdgcn_sched_barrier(0);
             if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
+            if constexpr (SC::kOn)
+                if (t + 1 < nk) sc.template load<TMW>(t + 1, sn);
             pp_barrier();
-            pp_mma<TMW>(fa, fb, acc);
+            mma();
             __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
             wait_vmcnt<0>();
+            if constexpr (SC::kOn) sc.take(sn, sa);
             pp_barrier();
         }
         // phase 2nk: group 1 multiplies the last stage, group 0 writes its
@@ -619,14 +748,24 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
             Lay::read(st, wm0, wn0, fa, fb);
             wait_lgkmcnt0();
             wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
+            if constexpr (SC::kOn)
+                if (t >= 1) sc.take(sn, sa);   // stage t's scales, requested in the previous phase
             pp_barrier();
+            if constexpr (SC::kOn)
+                if (t + 1 < nk) sc.template load<TMW>(t + 1, sn);
             // Both groups are done with stage t only now: the other waves of
             // this group read it in the phase that just ended, so A(t+2)
             // cannot be issued into it before this barrier.
-            if constexpr (decltype(load)::value)
-                pp_mma_load<TMW>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
-            else
-                pp_mma<TMW>(fa, fb, acc);
+            if constexpr (decltype(load)::value) {
+                if constexpr (SC::kOn)
+                    pp_mma_load_f8s<TMW>(fa, fb, acc, sa, ap, t + 2, (t & 1) ? st1 : st0);
+                else if constexpr (kF8)
+                    pp_mma_load_f8<TMW>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+                else
+                    pp_mma_load<TMW>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+            } else {
+                mma();
+            }
             pp_barrier();
         };
         int t = 0;
@@ -728,8 +867,9 @@ __device__ __forceinline__ void pps_tile(uint32_t i, uint32_t tiles_m, uint32_t 
 // that operand before its first load of tile i (the caller has pointed both
 // at tile 0); for i == ntiles the loader must load nothing (zeros): group 1
 // issues its refills unconditionally, so the last two stages request two
-// stages past the end into buffers nobody reads again.
-template <int TMW, class Lay, class LA, class LB, class RA, class RB, class Epi>
+// stages past the end into buffers nobody reads again.  TR (e4m3 stages):
+// transposed accumulator blocks (pp_mma_f8<TM, true>).
+template <int TMW, class Lay, bool TR = false, class LA, class LB, class RA, class RB, class Epi>
 __device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, char* lds, int group, int wm0,
                                           int wn0, f32x16 (&acc)[TMW][2], RA&& retarget_a, RB&& retarget_b,
                                           Epi&& epi) {
@@ -801,7 +941,7 @@ __device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, ch
                 }
                 pp_barrier();
                 if constexpr (kF8)
-                    pp_mma_f8<TMW>(fa, fb, acc);
+                    pp_mma_f8<TMW, TR>(fa, fb, acc);
                 else
                     pp_mma<TMW>(fa, fb, acc);
                 __builtin_amdgcn_sched_barrier(0);   // B(s+1) and the epilogue's stores waited for after the MFMAs
@@ -831,7 +971,7 @@ __device__ __forceinline__ void pp_stream(LA& ap, LB& bp, int nk, int ntiles, ch
                 const int kt2 = ld_kt;
                 pp_barrier();
                 if constexpr (kF8)
-                    pp_mma_load_f8<TMW>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
+                    pp_mma_load_f8<TMW, LA, TR>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
                 else
                     pp_mma_load<TMW>(fa, fb, acc, ap, kt2, (s & 1) ? st1 : st0);
                 __builtin_amdgcn_sched_barrier(0);

@@ -351,6 +351,36 @@ int trmoe_quantize_rows_e4m3(int act_dtype, const void* x, int64_t n_rows, int64
 int trmoe_shared_gate_up_a8(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t hidden, int64_t ldxq,
                             const void* w_packed, const float* w_scale, int64_t shared_width, void* h, int64_t ldh,
                             void* stream);
+/* ---------------------------------------------------------------------------
+ * W8A8 shared down on block-scaled e4m3 h.  No counterpart in the reference
+ * (no fp8 path there): the e4m3-activation forms of trmoe_shared_gate_up's h
+ * and of trmoe_shared_down_combine (shared_down and the combine,
+ * complexity/tr_hash/engine.py:333-349, 578), for layers with e4m3 weights.
+ *
+ * trmoe_shared_gate_up_a8_mx: h as in trmoe_shared_gate_up_a8 (in fp32),
+ *   written as e4m3 codes with one power-of-two scale per token and block of
+ *   32 features, b = f / 32:
+ *     e_t,b  = the smallest integer with max_{f in b} |h_t,f| <= 448 * 2^e,
+ *              clamped to [-126, 126]; 0 when that maximum is 0 or not
+ *              finite
+ *     h_q    = e4m3(h * 2^-e), round to nearest even, clamped to +-448
+ *     h_scale[t * ldhs + b] = e + 127 (E8M0)
+ *   h_q: [n, ldhq] bytes, ldhq a multiple of 16 and >= round_up(S, 128),
+ *   16-byte aligned; the padding features are written as code 0, scale 127.
+ *   h_scale: [n, ldhs] bytes, ldhs a multiple of 4 and >= round_up(S, 128)/32.
+ * trmoe_shared_down_combine_a8: trmoe_shared_down_combine (bf16 y, residual
+ *   and out) with h = h_q * 2^(h_scale - 127) per block, on the e4m3 MFMA
+ *   with the block scales in its operand: S a multiple of 128, w_down the
+ *   PLAIN-packed e4m3 shared_down.weight with its per-row scales w_scale.
+ * ------------------------------------------------------------------------- */
+int trmoe_shared_gate_up_a8_mx(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t hidden, int64_t ldxq,
+                               const void* w_packed, const float* w_scale, int64_t shared_width, void* h_q,
+                               int64_t ldhq, void* h_scale, int64_t ldhs, void* stream);
+int trmoe_shared_down_combine_a8(const void* h_q, const void* h_scale, int64_t n_tokens, int64_t shared_width,
+                                 int64_t ldhq, int64_t ldhs, const void* w_down, const float* w_scale, int64_t hidden,
+                                 const void* y, int64_t ldy, const int64_t* inverse, int top_k,
+                                 const float* route_weights, float shared_scale, float routed_scale,
+                                 const void* residual, int64_t ldr, void* out, int64_t ldo, void* stream);
 /* row_scale required; the workspace of trmoe_routed_experts_workspace_bytes() too. */
 int trmoe_routed_experts_rms(int act_dtype, int w_dtype, const void* x, int64_t n_tokens, int64_t hidden,
                              int64_t ldx, const int64_t* sorted_indices, const int32_t* expert_offsets,

@@ -42,6 +42,11 @@ Pinning (what checks each function beyond retyping it):
   quantize exactly (e4m3 grid values whose row maximum is 448 * 2^j), equal
   to it when the layer has no shared branch, and within e4m3's relative error
   of it otherwise.
+* ``block_exponents_e4m3`` / ``quantize_blocks_e4m3`` -- the exponent rule
+  against a brute-force search for the smallest e with amax <= 448 * 2^e in
+  float64, over random and boundary maxima (448 * 2^j and its float32
+  neighbours, zero, non-finite, the clamps); every block's largest code in
+  [224, 448]; exactly representable blocks round-trip unchanged.
 """
 
 from __future__ import annotations
@@ -435,11 +440,46 @@ def dequantize_e4m3(q: torch.Tensor, scale: torch.Tensor, reduce_dim: int) -> to
     return q.to(torch.float32) * scale.unsqueeze(reduce_dim)
 
 
-def engine_forward_w8a8(x, token_ids, table, params: dict, **kw):
+def block_exponents_e4m3(amax) -> np.ndarray:
+    """Power-of-two block scale exponents for e4m3 codes (the block-scaled
+    W8A8 h; no reference counterpart): the smallest integer e with
+    amax <= 448 * 2^e, from frexp (amax = m * 2^k, m in [0.5, 1): e = k - 9,
+    plus 1 when m > 0.875 = 448 / 2^9), clamped to [-126, 126]; 0 where amax
+    is 0 or not finite."""
+    a = np.asarray(amax, dtype=np.float32)
+    m, k = np.frexp(a)
+    e = k.astype(np.int64) - 9 + (m > np.float32(0.875))
+    e = np.clip(e, -126, 126)
+    return np.where((a > 0) & np.isfinite(a), e, 0)
+
+
+def quantize_blocks_e4m3(h: torch.Tensor, block: int = 32):
+    """h [n, f] (f a multiple of ``block``) as e4m3 codes with one exponent
+    per row and block of ``block`` columns: (codes float8_e4m3fn [n, f],
+    exponents int64 [n, f / block]); code = e4m3(clamp(h * 2^-e, +-448)),
+    round to nearest even.  A block's maximum ignores NaN."""
+    hf = h.detach().to(torch.float32)
+    n, f = hf.shape
+    hb = hf.reshape(n, f // block, block)
+    amax = torch.nan_to_num(hb.abs(), nan=0.0).amax(dim=-1)
+    e = torch.from_numpy(block_exponents_e4m3(amax.numpy()))
+    scaled = hb * torch.exp2(-e.to(torch.float32)).unsqueeze(-1)
+    q = torch.where(scaled > E4M3_MAX, E4M3_MAX, torch.where(scaled < -E4M3_MAX, -E4M3_MAX, scaled))
+    return q.to(torch.float8_e4m3fn).reshape(n, f), e
+
+
+def dequantize_blocks_e4m3(q: torch.Tensor, e: torch.Tensor, block: int = 32) -> torch.Tensor:
+    n, f = q.shape
+    qb = q.to(torch.float32).reshape(n, f // block, block)
+    return (qb * torch.exp2(e.to(torch.float32)).unsqueeze(-1)).reshape(n, f)
+
+
+def engine_forward_w8a8(x, token_ids, table, params: dict, *, h_blocks: bool = False, **kw):
     """engine_forward with the shared gate|up fed per-token e4m3 activations
     (the W8A8 path, which has no reference counterpart: the reference has no
     fp8): the shared branch sees dequantize(quantize_e4m3(x over each row)),
-    the routed experts and the down projection see x and h as before."""
+    the routed experts see x.  h_blocks: the down projection sees h through
+    quantize_blocks_e4m3 (blocks of 32 features), else h itself."""
     shape = x.shape
     flat = x.reshape(-1, shape[-1]).to(torch.float32)
     q, s = quantize_e4m3(flat, 1)
@@ -450,6 +490,9 @@ def engine_forward_w8a8(x, token_ids, table, params: dict, **kw):
     if g is None or g.numel() == 0:
         return routed
     h = silu_mul(F.linear(xq, g), F.linear(xq, params["shared_up"]))
+    if h_blocks:
+        hq, he = quantize_blocks_e4m3(h)
+        h = dequantize_blocks_e4m3(hq, he).to(h.dtype)
     shared = F.linear(h, params["shared_down"]).view(shape)
     return routed + kw.get("shared_scale", 1.0) * shared
 

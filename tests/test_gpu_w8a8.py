@@ -8,9 +8,17 @@ the layer's formula (``engine_forward_w8a8``), pinned in tests/test_oracle.py.
 * trmoe_shared_gate_up_a8 multiplies the same e4m3 values the oracle
   dequantizes, so only fp32 summation order and the bf16 rounding of h
   differ: normwise bound 1e-2.
-* The C5 layer with fp8_activations (full and active capacity): 2e-2
-  against the W8A8 oracle and the north-star 5e-2 against the plain (W8A16)
-  oracle, on sampled rows.
+* trmoe_shared_gate_up_a8_mx (h as block-scaled e4m3): every block's largest
+  code in [224, 448] (the exponent is the smallest that fits), padding
+  features code 0 / exponent 0, and the oracle's block quantizer applied to
+  the same kernel's bf16 h (trmoe_shared_gate_up_a8, pinned to f64 above)
+  agrees up to what bf16 rounding moves.
+* trmoe_shared_down_combine_a8 on oracle-quantized h: 1e-2 against f64 on
+  the dequantized values (only fp32 summation order and bf16 outputs differ).
+* The C5 layer with fp8_activations True (its h block-scaled e4m3 into the
+  W8A8 down) and "gate_up" (W8A8 gate|up only), full and active capacity:
+  2e-2 against the W8A8 oracle of that mode and the north-star 5e-2 against
+  the plain (W8A16) oracle, on sampled rows.
 * The CUDA_GRAPH backend with fp8_activations: replays equal the eager HIP
   layer bit for bit, and flipping the switch after capture re-captures.
 """
@@ -121,8 +129,98 @@ def test_shared_gate_up_a8(gpu, hidden, shared, n):
     assert O.normwise_rel_err(got, ref) <= 1e-2, O.normwise_rel_err(got, ref)
 
 
+@pytest.mark.parametrize("hidden,shared,n", [(256, 384, 300), (128, 300, 1), (2048, 5632, 4096), (896, 3072, 777)])
+def test_shared_gate_up_a8_block_scaled_h(gpu, hidden, shared, n):
+    """The block quantizer on the kernel's own h: trmoe_shared_gate_up_a8
+    gives the same accumulators rounded to bf16 (its h is pinned against the
+    f64 oracle by test_shared_gate_up_a8), so the codes and exponents are
+    checked against the oracle's rule applied to that bf16 h: exactly, except
+    where the bf16 rounding of h lands exactly on a boundary of the rule
+    (a block maximum of 448 * 2^e, an e4m3 rounding midpoint), where the
+    kernel's fp32 h may fall on either side."""
+    from complexity_amd import ops
+
+    print(f"gate_up a8 mx H={hidden} S={shared} n={n}", flush=True)
+    engine = _engine(gpu, hidden, shared)
+    g = torch.Generator().manual_seed(hidden + n + 1)
+    x = (torch.randn(n, hidden, generator=g) * 1.5).to(gpu, torch.bfloat16)
+    packed = engine._hip_packed()
+    xq, xs = ops.quantize_rows_e4m3(x)
+    hq, hs = ops.shared_gate_up_a8_mx(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale, shared)
+    hb = ops.shared_gate_up_a8(xq, xs, packed.shared_gate_up, packed.shared_gate_up_scale, shared)
+    torch.cuda.synchronize()
+    f_pad = hq.shape[1]
+    assert f_pad == -(-shared // 128) * 128 and hs.shape == (n, f_pad // 32)
+    rows = torch.arange(n) if n <= 1024 else torch.randperm(n, generator=g)[:1024]
+    q = hq.cpu()[rows]
+    e = hs.cpu()[rows].long() - 127
+    h = hb.cpu()[rows].float()
+    # padding features: code 0, exponent 0
+    assert bool((q.float()[:, shared:] == 0).all())
+    assert bool((e[:, -(-shared // 32):] == 0).all())
+    # the exponent is the smallest that fits: every block's largest code in [224, 448]
+    qb = q.float().reshape(len(rows), -1, 32).abs().amax(-1)
+    nz = qb > 0
+    assert bool(((qb[nz] >= 224) & (qb[nz] <= 448)).all())
+    _, want_e = O.quantize_blocks_e4m3(h)
+    # 448 * 2^e is a bf16 number: the kernel's fp32 maximum may lie just above
+    # a bf16 maximum that equals it, and then the kernel's exponent is one more
+    bmax = h.abs().reshape(len(rows), -1, 32).amax(-1)
+    edge = bmax == 448.0 * torch.exp2(want_e.float())
+    assert bool(((e == want_e) | (edge & (e == want_e + 1))).all())
+
+    def e4m3(v):
+        return torch.where(v > 448, 448.0, torch.where(v < -448, -448.0, v)).to(torch.float8_e4m3fn)
+
+    # codes under the kernel's own exponents.  e4m3 rounding midpoints are
+    # bf16 numbers too, so bf16 h can only round differently from the
+    # kernel's fp32 h where it sits exactly on one: there either neighbour
+    scaled = h * torch.exp2(-e.repeat_interleave(32, dim=1).float())
+    own = e4m3(scaled)
+    tie = e4m3(scaled * (1 + 2.0 ** -20)).view(torch.uint8) != e4m3(scaled * (1 - 2.0 ** -20)).view(torch.uint8)
+    same = q.view(torch.uint8) == own.view(torch.uint8)
+    assert bool((same | tie).all())
+    lo, hi = e4m3(scaled * (1 - 2.0 ** -20)).float(), e4m3(scaled * (1 + 2.0 ** -20)).float()
+    assert bool((same | (q.float() == torch.minimum(lo, hi)) | (q.float() == torch.maximum(lo, hi))).all())
+    got = O.dequantize_blocks_e4m3(q, e)
+    assert O.normwise_rel_err(got[:, :shared].double(), h[:, :shared].double()) <= 2.0 ** -4
+
+
+@pytest.mark.parametrize("hidden,shared,n,routed,residual", [
+    (256, 384, 300, True, False), (128, 128, 1, False, True), (2048, 5632, 4096, True, False),
+    (896, 3072, 777, True, True)])
+def test_shared_down_combine_a8(gpu, hidden, shared, n, routed, residual):
+    from complexity_amd import ops
+
+    print(f"down a8 H={hidden} S={shared} n={n} routed={routed} residual={residual}", flush=True)
+    engine = _engine(gpu, hidden, shared)
+    packed = engine._hip_packed()
+    g = torch.Generator().manual_seed(hidden + shared + n)
+    h = torch.randn(n, shared, generator=g) * torch.exp2(torch.randint(-6, 6, (n, shared // 32), generator=g)
+                                                         .float()).repeat_interleave(32, dim=1)
+    hq, he = O.quantize_blocks_e4m3(h)
+    hd = O.dequantize_blocks_e4m3(hq, he).double()
+    rw = (0.6, 0.4)
+    y = inv = res = None
+    ref = 0.5 * (hd @ _deq(engine, "shared_down").double().T)
+    if routed:
+        y = torch.randn(2 * n, hidden, generator=g).to(torch.bfloat16)
+        inv = torch.randperm(2 * n, generator=g).reshape(2, n)
+        ref = ref + 2.0 * (rw[0] * y.double()[inv[0]] + rw[1] * y.double()[inv[1]])
+    if residual:
+        res = torch.randn(n, hidden, generator=g).to(torch.bfloat16)
+        ref = ref + res.double()
+    out = ops.shared_down_combine_a8(
+        hq.to(gpu), (he + 127).to(torch.uint8).to(gpu), shared, packed.shared_down, packed.shared_down_scale, hidden,
+        None if y is None else y.to(gpu), None if inv is None else inv.to(gpu), 2, rw, 0.5, 2.0,
+        None if res is None else res.to(gpu))
+    torch.cuda.synchronize()
+    assert O.normwise_rel_err(out.cpu().double(), ref) <= 1e-2, O.normwise_rel_err(out.cpu().double(), ref)
+
+
+@pytest.mark.parametrize("mode", [True, "gate_up"])
 @pytest.mark.parametrize("name", ["c5_fp8_32768", "c5_fp8_32768_active_8x128"])
-def test_c5_layer_with_fp8_activations(gpu, name):
+def test_c5_layer_with_fp8_activations(gpu, name, mode):
     """C5 (hidden 2048, shared 5632, 16 x 256 experts, 32768 tokens; the
     active variant runs 8 experts x 128 features) with fp8_activations
     against the W8A8 oracle and the plain W8A16 oracle."""
@@ -130,29 +228,35 @@ def test_c5_layer_with_fp8_activations(gpu, name):
     from complexity_amd import workloads as Wl
     from complexity_amd.tr_hash import TRHashBackend
 
-    print(f"W8A8 layer {name}", flush=True)
+    print(f"W8A8 layer {name} mode {mode}", flush=True)
     w = Wl.WORKLOADS[name]
     engine = Wl.build_engine(w, gpu, backend="hip")
-    engine.fp8_activations = True
+    engine.fp8_activations = mode
     x = Wl.make_hidden(w).to(gpu).to(torch.bfloat16)
     ids = Wl.make_token_ids(w).to(gpu)
     calls = []
-    a8 = ops.shared_gate_up_a8
+    names = ("shared_gate_up_a8_mx", "shared_down_combine_a8", "shared_gate_up_a8")
+    saved = {k: getattr(ops, k) for k in names}
 
-    def counted(*a, **k):
-        calls.append(1)
-        return a8(*a, **k)
+    def counted(k):
+        def f(*a, **kw):
+            calls.append(k)
+            return saved[k](*a, **kw)
+        return f
 
-    ops.shared_gate_up_a8 = counted
+    for k in names:
+        setattr(ops, k, counted(k))
     try:
         with torch.no_grad():
             out = engine(x, ids)
-            assert len(calls) == 1
+            want = ["shared_gate_up_a8_mx", "shared_down_combine_a8"] if mode is True else ["shared_gate_up_a8"]
+            assert calls == want
             engine.fp8_activations = False
             plain = engine(x, ids)
-            assert len(calls) == 1
+            assert calls == want
     finally:
-        ops.shared_gate_up_a8 = a8
+        for k in names:
+            setattr(ops, k, saved[k])
     torch.cuda.synchronize()
     assert engine.last_backend.selected is TRHashBackend.HIP
     rows = torch.randperm(w.tokens, generator=torch.Generator().manual_seed(2))[:1024]
@@ -165,11 +269,11 @@ def test_c5_layer_with_fp8_activations(gpu, name):
               routed_scale=cfg.routed_output_scale, active_experts=w.active_experts,
               active_width=w.active_width)
     table = engine._active_route_table.cpu()
-    ref8 = O.engine_forward_w8a8(xr, ir, table, p, **kw)
+    ref8 = O.engine_forward_w8a8(xr, ir, table, p, h_blocks=mode is True, **kw)
     ref = O.engine_forward(xr, ir, table, p, **kw)
     got = out.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu()
     e8, e = O.normwise_rel_err(got, ref8), O.normwise_rel_err(got, ref)
-    print(f"C5 W8A8: {e8:.3e} vs the W8A8 oracle, {e:.3e} vs the W8A16 oracle", flush=True)
+    print(f"C5 W8A8 ({mode}): {e8:.3e} vs the W8A8 oracle, {e:.3e} vs the W8A16 oracle", flush=True)
     assert e8 <= 2e-2
     assert e <= 5e-2
     # the flag changes only the shared gate|up: without it the layer is the W8A16 one
@@ -179,9 +283,9 @@ def test_c5_layer_with_fp8_activations(gpu, name):
 def test_graph_backend_with_fp8_activations(gpu):
     """CUDA_GRAPH over an e4m3 layer above decode sizes (256 tokens): replays
     with eager work between them equal the eager HIP layer with the same
-    switch, before and after fp8_activations is flipped on the captured
-    engine (the runner captures again), and the W8A8 replays differ from the
-    W8A16 ones (the switch reached the captured kernels)."""
+    switch, before and after fp8_activations is changed on the captured
+    engine (the runner captures again), and the replays of the three modes
+    differ (the switch reached the captured kernels)."""
     from complexity_amd.tr_hash import GraphBucket, TRHashEngine, TRHashEngineConfig
 
     torch.manual_seed(19)
@@ -197,7 +301,7 @@ def test_graph_backend_with_fp8_activations(gpu):
         e.eval()
     results = {}
     with torch.no_grad():
-        for flag in (True, False, True):
+        for flag in (True, False, "gate_up", True):
             graph.fp8_activations = eager.fp8_activations = flag
             for step in range(3):
                 g = torch.Generator().manual_seed(step)
@@ -210,3 +314,4 @@ def test_graph_backend_with_fp8_activations(gpu):
                 assert torch.equal(got, want), (flag, step)
                 results[(flag, step)] = got
     assert not torch.equal(results[(True, 0)], results[(False, 0)])
+    assert not torch.equal(results[(True, 0)], results[("gate_up", 0)])

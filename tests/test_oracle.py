@@ -496,3 +496,66 @@ def test_w8a8_oracle_quantizes_the_shared_branch_only():
     got = O.engine_forward_w8a8(x, ids, table, params, **kw)
     err = O.normwise_rel_err(got, ref)
     assert 0.0 < err < 5e-2, err
+
+
+# --------------------------------------------------------------------------- block-scaled e4m3 h
+
+
+def _smallest_exponent(a: float) -> int:
+    """Brute force in float64 (448 * 2^e is exact there): the smallest e with a <= 448 * 2^e."""
+    e = -140
+    while a > 448.0 * 2.0 ** e:
+        e += 1
+    return e
+
+
+def test_block_exponents_against_brute_force():
+    rng = np.random.default_rng(5)
+    vals = [np.float32(v) for v in rng.lognormal(0.0, 12.0, 3000)]
+    for j in range(-120, 121, 7):   # the boundaries 448 * 2^j and their float32 neighbours
+        b = np.float32(448.0 * 2.0 ** j)
+        vals += [b, np.nextafter(b, np.float32(np.inf)), np.nextafter(b, np.float32(0))]
+    vals += [np.float32(224.0), np.float32(224.5), np.float32(1e-40), np.float32(3e38)]
+    got = O.block_exponents_e4m3(np.array(vals, dtype=np.float32))
+    for v, e in zip(vals, got):
+        want = min(max(_smallest_exponent(float(v)), -126), 126)
+        assert e == want, (float(v), int(e), want)
+    special = O.block_exponents_e4m3(np.array([0.0, np.inf, np.nan, -0.0], dtype=np.float32))
+    assert special.tolist() == [0, 0, 0, 0]
+
+
+def test_quantize_blocks_codes_in_range_and_exact_blocks():
+    g = torch.Generator().manual_seed(31)
+    h = torch.randn(50, 128, generator=g) * torch.exp2(torch.randint(-20, 20, (50, 1), generator=g).float())
+    h[3, 32:64] = 0.0   # an all-zero block
+    q, e = O.quantize_blocks_e4m3(h)
+    qb = q.float().reshape(50, 4, 32).abs().amax(-1)
+    nz = qb > 0
+    # the exponent is the smallest that fits: the block's largest code is in [224, 448]
+    assert bool(((qb[nz] >= 224) & (qb[nz] <= 448)).all())
+    assert e[3, 1] == 0 and not bool(nz[3, 1])
+    d = O.dequantize_blocks_e4m3(q, e)
+    big = h.abs() >= 2.0 ** -6 * 2.0 ** e.repeat_interleave(32, dim=1).float()   # e4m3 normals
+    assert bool(((d - h).abs()[big] <= h.abs()[big] * 2.0 ** -4).all())       # half an e4m3 ulp
+    # blocks of e4m3 grid values with maximum 448 * 2^j come back unchanged
+    grid = torch.from_numpy(O.e4m3_decode_table()).float()
+    grid = grid[torch.isfinite(grid)]
+    exact = grid[torch.randint(0, grid.numel(), (6, 64), generator=g)]
+    exact[:, 0] = 448.0
+    exact[:, 32] = -448.0
+    exact = exact * torch.exp2(torch.randint(-30, 30, (6, 1), generator=g).float())
+    q2, e2 = O.quantize_blocks_e4m3(exact)
+    assert torch.equal(O.dequantize_blocks_e4m3(q2, e2), exact)
+
+
+def test_w8a8_oracle_with_block_scaled_h():
+    g = torch.Generator().manual_seed(23)
+    params = _w8a8_params(g, S=128)
+    x = torch.randn(40, 64, generator=g)
+    ids = torch.randint(0, 50, (40,), generator=g)
+    table = torch.from_numpy(O.multi_hash_table(50, 4, 2, 0))
+    kw = dict(route_weights=(0.5, 0.5), shared_scale=0.7, routed_scale=1.3)
+    a = O.engine_forward_w8a8(x, ids, table, params, **kw)
+    b = O.engine_forward_w8a8(x, ids, table, params, h_blocks=True, **kw)
+    err = O.normwise_rel_err(b, a)
+    assert 0.0 < err < 4e-2, err

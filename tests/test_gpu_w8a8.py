@@ -21,6 +21,8 @@ the layer's formula (``engine_forward_w8a8``), pinned in tests/test_oracle.py.
   the plain (W8A16) oracle, on sampled rows.
 * The CUDA_GRAPH backend with fp8_activations: replays equal the eager HIP
   layer bit for bit, and flipping the switch after capture re-captures.
+* Shapes the W8A8 kernels do not take fall back (bf16 h into the W8A16 down,
+  or the whole layer W8A16), checked against the oracle of the path taken.
 """
 
 import pytest
@@ -315,3 +317,52 @@ def test_graph_backend_with_fp8_activations(gpu):
                 results[(flag, step)] = got
     assert not torch.equal(results[(True, 0)], results[(False, 0)])
     assert not torch.equal(results[(True, 0)], results[("gate_up", 0)])
+
+
+@pytest.mark.parametrize("hidden,shared,want", [
+    (256, 300, ["shared_gate_up_a8"]),                                 # S % 128 != 0: bf16 h, W8A16 down
+    (192, 384, []),                                                    # hidden % 128 != 0: W8A16
+    (256, 384, ["shared_gate_up_a8_mx", "shared_down_combine_a8"]),
+])
+def test_fp8_activations_falls_back_by_shape(gpu, hidden, shared, want):
+    """fp8_activations=True takes the W8A8 kernels the shapes allow, and the
+    output matches the oracle of the path taken (2e-2)."""
+    from complexity_amd import ops
+
+    print(f"W8A8 fallback H={hidden} S={shared}", flush=True)
+    engine = _engine(gpu, hidden, shared)
+    engine.fp8_activations = True
+    g = torch.Generator().manual_seed(hidden + shared)
+    x = torch.randn(2, 150, hidden, generator=g).to(gpu, torch.bfloat16)
+    ids = torch.randint(0, 5000, (2, 150), generator=g).to(gpu)
+    names = ("shared_gate_up_a8_mx", "shared_down_combine_a8", "shared_gate_up_a8")
+    saved = {k: getattr(ops, k) for k in names}
+    calls = []
+
+    def counted(k):
+        def f(*a, **kw):
+            calls.append(k)
+            return saved[k](*a, **kw)
+        return f
+
+    for k in names:
+        setattr(ops, k, counted(k))
+    try:
+        with torch.no_grad():
+            out = engine(x, ids)
+    finally:
+        for k in names:
+            setattr(ops, k, saved[k])
+    torch.cuda.synchronize()
+    assert calls == want
+    p = {n: _deq(engine, n) for n in ("expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up",
+                                      "shared_down")}
+    cfg = engine.config
+    kw = dict(route_weights=cfg.route_weights, shared_scale=cfg.shared_output_scale,
+              routed_scale=cfg.routed_output_scale)
+    xr, ir, table = x.float().cpu(), ids.cpu(), engine._active_route_table.cpu()
+    if want:
+        ref = O.engine_forward_w8a8(xr, ir, table, p, h_blocks=len(want) == 2, **kw)
+    else:
+        ref = O.engine_forward(xr, ir, table, p, **kw)
+    assert O.normwise_rel_err(out.float().cpu(), ref) <= 2e-2, O.normwise_rel_err(out.float().cpu(), ref)

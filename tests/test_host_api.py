@@ -244,6 +244,19 @@ def test_save_refuses_e4m3_packs():
                           packed, (0.5, 0.5), 1.0, 1.0, save=True)
 
 
+def test_fp8_activation_modes_are_validated():
+    from complexity_amd import ops
+
+    assert [ops.fp8_activation_mode(m) for m in (False, True, "gate_up")] == [False, True, "gate_up"]
+    for bad in ("all", 1, None, "down"):
+        with pytest.raises(ValueError, match="fp8_activations"):
+            ops.fp8_activation_mode(bad)
+    with pytest.raises(ValueError, match="fp8_activations"):
+        ops.layer_forward(torch.zeros(2, 64), torch.zeros(2, dtype=torch.long), torch.zeros(2, 8, dtype=torch.long),
+                          ops.PackedLayer(act_dtype=torch.bfloat16, num_experts=4, expert_width=64), (0.5, 0.5),
+                          1.0, 1.0, act_fp8="both")
+
+
 def test_missing_library_on_gpu_fails_loudly(monkeypatch):
     monkeypatch.delenv("TRMOE_ALLOW_PYTORCH_FALLBACK", raising=False)
     with pytest.raises(RuntimeError):

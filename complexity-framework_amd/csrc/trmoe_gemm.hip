@@ -1348,6 +1348,9 @@ static int launch_gate_up_kind(const GateUpArgs& a, int64_t packed_rows, hipStre
         else
             return launch_gate_up_dma_balanced<Kind>(a, packed_rows, stream);
     }
+    // fewer 128x128 tiles than CUs: 64x128 (bf16 at 512 tokens: the op 36.5 -> 27.6 us)
+    if (packed_rows % 128 == 0 && ((a.M + 127) / 128) * (packed_rows / 128) < device_cus())
+        return launch_gate_up_shape<Kind, FP8, SmallShape<FP8, 128>>(a, packed_rows, stream);
     return launch_gate_up_shape<Kind, FP8, ShapeMain>(a, packed_rows, stream);
 }
 
@@ -1367,11 +1370,12 @@ static int launch_gate_up_routed_cols_shape(const GateUpArgs& a, int64_t packed_
 
 template <class Kind, bool FP8>
 static int launch_gate_up_routed_cols(const GateUpArgs& a, int64_t packed_rows, hipStream_t stream) {
-    if constexpr (std::is_same_v<Kind, KindF32>) {
-        // C1's 512 expert columns at 2048 tokens: 32 tiles of 128x256, 128 of 64x128 (op 300 -> 217 us)
+    {
+        // fewer 128x256 tiles than CUs: 64x128 (C1's 512 expert columns at 2048
+        // tokens: 32 -> 128 workgroups, the op 300 -> 217 us)
         const int64_t cols = packed_rows - a.n_base;
         if (cols % 128 == 0 && ((a.M + 127) / 128) * (cols / 256) < device_cus())
-            return launch_gate_up_routed_cols_shape<Kind, FP8, ShapeSmallWideDma>(a, packed_rows, stream);
+            return launch_gate_up_routed_cols_shape<Kind, FP8, SmallShape<FP8, 128>>(a, packed_rows, stream);
     }
     if (!FP8 && (packed_rows - a.n_base) % 256 == 0)
         return launch_gate_up_routed_cols_shape<Kind, FP8, std::conditional_t<FP8, ShapeMain, ShapeTallDma>>(
@@ -1652,11 +1656,10 @@ static int launch_down_kind(const DownArgs& a, hipStream_t stream) {
         if (a.N % 256 == 0 && mt * (a.N / 256) >= 256) return launch_down_shape<Kind, FP8, ShapeBigF8Dma>(a, stream);
     }
     const bool big = (fits224 && mt * (a.N / ShapeDown224::BN) >= 256) || mt * ((a.N + 255) / 256) >= kBigTileMinBlocks;
-    if constexpr (std::is_same_v<Kind, KindF32>) {
-        // C1 (2048 x 896): 112 tiles of 128x128 on 256 CUs, 448 of 64x64 (237 -> 124 us)
-        if (!big && ((a.M + 127) / 128) * ((a.N + 127) / 128) < device_cus())
-            return launch_down_shape<Kind, FP8, ShapeSmallDma>(a, stream);
-    }
+    // fewer 128x128 tiles than CUs: 64x64 tiles (C1, 2048 x 896 f32: 112 -> 448
+    // workgroups, 237 -> 124 us; bf16 at 512 / 2048 tokens: 40 -> 19, 41 -> 24 us)
+    if (!big && ((a.M + 127) / 128) * ((a.N + 127) / 128) < device_cus())
+        return launch_down_shape<Kind, FP8, SmallShape<FP8, 64>>(a, stream);
     if (!big) return launch_down_shape<Kind, FP8, ShapeMain>(a, stream);
     if constexpr (FP8) {
         if (fits224) return launch_down_shape<Kind, FP8, ShapeDown224>(a, stream);

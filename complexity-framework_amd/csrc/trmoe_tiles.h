@@ -76,12 +76,12 @@ using ShapeDown224Dma = TileShape<256, 224, 4, 1, 4>;
 using ShapeBigF8Dma = TileShape<256, 256, 2, 4, 6>;  // e4m3 weights loaded straight into LDS
 using ShapeGroupNarrowDma = TileShape<256, 128, 4, 2, 4>;   // 256x128 direct-load tiles
 using ShapeTallDma = TileShape<128, 256, 1, 4, 4>;          // 128x256: 4 waves of 128x64
-// f32 launches whose larger tiles would leave CUs idle (the fp32 MFMA is
-// slow enough that the smaller tiles' extra LDS reads do not matter): 4
-// waves of 32x32 for the down, 4 waves of 32x64 for gate|up columns (the
-// SwiGLU epilogue needs 64 packed columns, 32 gate + 32 up, per wave)
-using ShapeSmallDma = TileShape<64, 64, 2, 2, 4>;
-using ShapeSmallWideDma = TileShape<64, 128, 2, 2, 4>;
+// Launches whose larger tiles would leave CUs idle: 64 x BN tiles of 4 waves,
+// 32x32 each for the down (BN 64), 32x64 for gate|up columns (BN 128: the
+// SwiGLU epilogue needs 64 packed columns, 32 gate + 32 up, per wave);
+// direct loads, or the register path that expands e4m3 weights.
+template <bool FP8, int BN>
+using SmallShape = std::conditional_t<FP8, TileShape<64, BN, 2, 2>, TileShape<64, BN, 2, 2, 4>>;
 
 // ---------------------------------------------------------------------------
 // expert-grouped tiles

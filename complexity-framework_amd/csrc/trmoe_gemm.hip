@@ -1715,6 +1715,14 @@ static int gate_up_grouped_kind(const GateUpArgs& a, int64_t assignments, int64_
             return launch_gate_up_grouped_pps<FP8>(a, stream);
     }
     const bool wide = packed_rows % 256 == 0;
+    {
+        // fewer tiles of the shapes below than CUs: 64x128 (C2 grouped, 4 x 64
+        // experts: 132 -> 516 workgroups, routed experts 47.5 -> 44.6 us)
+        const int64_t bn = wide ? 256 : 128;
+        const int64_t bm = FP8 ? (wide ? 256 : 128) : 256;
+        if (packed_rows % 128 == 0 && ((assignments + bm - 1) / bm + a.E) * (packed_rows / bn) < device_cus())
+            return launch_gate_up_grouped_shape<Kind, FP8, SmallShape<FP8, 128>>(a, assignments, packed_rows, stream);
+    }
     if constexpr (FP8) {
         if (wide) return launch_gate_up_grouped_shape<Kind, FP8, ShapeBigF8Dma>(a, assignments, packed_rows, stream);
         return launch_gate_up_grouped_shape<Kind, FP8, ShapeMain>(a, assignments, packed_rows, stream);

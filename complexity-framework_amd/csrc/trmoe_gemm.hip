@@ -1300,6 +1300,12 @@ static int ensure_lds(F* fn, int bytes) {
 // no padded columns).  bf16/f32 operands take the direct buffer->LDS loads
 // (PGR 4); e4m3 weights the register-staged loop that expands them.
 constexpr int64_t kBigTileMinBlocks = 512;
+// The ping-pong gate|up keeps its 256x256 tiles down to half a wave of
+// workgroups: its two 4-wave groups hide the loads that an underfilled grid of
+// the plain 256x256 loop cannot (bf16 layer, 2048 tokens: gate|up 43.6 ->
+// 34.7 us at 128 tiles; the down keeps kBigTileMinBlocks, where a lower bound
+// made 8192 tokens slower).
+constexpr int64_t kPPGateUpMinBlocks = 128;
 
 static int device_cus() { return current_device_cus(); }
 
@@ -1484,12 +1490,12 @@ int launch_rms_row_scale(int act, const void* x, int64_t n, int64_t hidden, int6
 
 // bf16 prefill-sized gate|up (shared or dense-routed, every column tile in
 // one launch) on the ping-pong tiles: 256x256 tiles over whole 64-element K
-// stages, at least kBigTileMinBlocks tiles.
+// stages, at least kPPGateUpMinBlocks tiles.
 static bool pp_eligible(int act, int wdt, const GateUpArgs& a, int64_t packed_rows) {
     const int64_t cols = packed_rows - a.n_base;
     const bool types = act == TRMOE_BF16 && (wdt == TRMOE_BF16 || (wdt == TRMOE_FP8_E4M3 && a.gu == nullptr));
     return types && a.K > 0 && a.K % 64 == 0 && cols > 0 && cols % 256 == 0 &&
-           ((a.M + 255) / 256) * (cols / 256) >= kBigTileMinBlocks;
+           ((a.M + 255) / 256) * (cols / 256) >= kPPGateUpMinBlocks;
 }
 
 template <bool ROUTED, int TMW, bool SAVE, bool FP8>

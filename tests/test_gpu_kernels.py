@@ -248,6 +248,37 @@ def test_shared_down_combine_big_tiles(gpu, dtype, N, S, H):
     assert nerr(out[rows], ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("with_y,with_res", [(False, False), (False, True), (True, True)])
+def test_shared_down_combine_ping_pong_every_row(gpu, with_y, with_res):
+    """bf16 down at H = 896 on the ping-pong kernel (at least 256 tiles of
+    256 x 256, the last column tile half zero weight rows).  Every row is
+    checked against a float64 product, so a block stored at the wrong rows
+    or columns, or one never stored, fails; 16384 + 37 rows leave a ragged
+    last row tile.  Both epilogues: stores from the accumulators (no y, no
+    residual) and the LDS tile that adds y and the residual."""
+    from complexity_amd import ops
+
+    N, S, H, k = 16384 + 37, 3072, 896, 2
+    h, wd, hpad, y, perm, res = _down_case(N, S, H, k, torch.bfloat16, 60)
+    pd, _ = ops.pack_linear_down(wd.to(gpu))
+    rw = (0.7, 0.3)
+    out = ops.shared_down_combine(hpad.to(gpu), S, pd, None, H, y.to(gpu) if with_y else None,
+                                  perm.to(gpu) if with_y else None, k, rw, 0.5, 2.0,
+                                  res.to(gpu) if with_res else None).cpu()
+    ref = 0.5 * (h.double() @ wd.double().T)
+    if with_y:
+        yr = y.double()
+        ref = ref + 2.0 * (rw[0] * yr[perm[:N]] + rw[1] * yr[perm[N:]])
+    if with_res:
+        ref = ref + res.double()
+    row_err = (out.double() - ref).norm(dim=1) / ref.norm(dim=1)
+    assert row_err.max().item() <= TOL[torch.bfloat16], int(row_err.argmax())
+    # per 32-column block of every row tile: catches a block written to the
+    # wrong place even where a row's norm would dilute it
+    blk = (out.double() - ref).reshape(N, H // 32, 32).norm(dim=2) / ref.reshape(N, H // 32, 32).norm(dim=2)
+    assert blk.max().item() <= 4 * TOL[torch.bfloat16]
+
+
 # --------------------------------------------------------------------------- decode-shape kernels
 
 

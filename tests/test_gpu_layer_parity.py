@@ -152,6 +152,30 @@ def test_bf16_layer_full_size(gpu, name):
     assert err16 <= BOUND["bf16"]
 
 
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("tokens", [512, 2048, 4096, 8192])
+def test_bf16_layer_between_decode_and_c2(gpu, strategy, tokens):
+    """C2's layer at token counts where the launch shapes change: 64-row
+    tiles where larger ones leave CUs idle (512, 2048), the ping-pong gate|up
+    from half a round of 256 x 256 tiles (2048: 192 tiles, 4096: 384), the
+    256 x 256 down from 512 tiles (8192).  Every row against the fp32 oracle
+    fed the same bf16 inputs."""
+    from dataclasses import replace
+
+    from complexity_amd import workloads as Wl
+
+    w = replace(Wl.C2, name=f"bf16_{tokens}", batch=max(1, tokens // 2048), seq=min(tokens, 2048))
+    assert w.tokens == tokens
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    engine.routed_strategy = strategy
+    x, ids = Wl.make_hidden(w).to(gpu).to(torch.bfloat16), Wl.make_token_ids(w).to(gpu)
+    out = _run(engine, x, ids)
+    assert engine._packed.strategy == strategy
+    err = O.normwise_rel_err(out, _oracle(engine, x, ids))
+    print(f"\nbf16 {tokens} tokens {strategy}: normwise error vs fp32 oracle {err:.3e}")
+    assert err <= BOUND["bf16"]
+
+
 @pytest.mark.parametrize("layer", [0, 7, 15])
 def test_c4_decode_layers(gpu, layer):
     """C4's MLP in greedy decode: 8 tokens, the route table of layer `layer`

@@ -19,6 +19,8 @@ the layer's formula (``engine_forward_w8a8``), pinned in tests/test_oracle.py.
   W8A8 down) and "gate_up" (W8A8 gate|up only), full and active capacity:
   2e-2 against the W8A8 oracle of that mode and the north-star 5e-2 against
   the plain (W8A16) oracle, on sampled rows.
+* C5's layer at 512, 2048 and 8192 tokens (the small e4m3 tiles, one round
+  of 256 x 256): W8A16 and W8A8 with block-scaled h against their oracles.
 * The CUDA_GRAPH backend with fp8_activations: replays equal the eager HIP
   layer bit for bit, and flipping the switch after capture re-captures.
 * Shapes the W8A8 kernels do not take fall back (bf16 h into the W8A16 down,
@@ -280,6 +282,49 @@ def test_c5_layer_with_fp8_activations(gpu, name, mode):
     assert e <= 5e-2
     # the flag changes only the shared gate|up: without it the layer is the W8A16 one
     assert O.normwise_rel_err(plain.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu(), ref) <= 5e-2
+
+
+@pytest.mark.parametrize("tokens", [512, 2048, 8192])
+def test_fp8_layer_between_decode_and_c5(gpu, tokens):
+    """C5's layer (e4m3 weights, hidden 2048, shared 5632, 16 x 256 experts)
+    at token counts where the launch shapes change: 64-row tiles for e4m3
+    weights where larger ones leave CUs idle (512, 2048), one round or more
+    of 256 x 256 tiles (8192).  W8A16 against the dequantised-weight oracle,
+    then W8A8 with block-scaled h against the W8A8 oracle, on the same engine
+    and inputs (up to 1024 sampled rows).  e4m3 weights take the grouped
+    strategy (the dense-routed one needs bf16/f32 weights)."""
+    from dataclasses import replace
+
+    from complexity_amd import workloads as Wl
+
+    print(f"fp8 layer {tokens} tokens", flush=True)
+    w = replace(Wl.C5, name=f"fp8_{tokens}", batch=max(1, tokens // 2048), seq=min(tokens, 2048))
+    assert w.tokens == tokens
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    x = Wl.make_hidden(w).to(gpu).to(torch.bfloat16)
+    ids = Wl.make_token_ids(w).to(gpu)
+    with torch.no_grad():
+        out16 = engine(x, ids)
+        engine.fp8_activations = True
+        out8 = engine(x, ids)
+    torch.cuda.synchronize()
+    assert engine._packed.strategy == "grouped"
+    rows = torch.randperm(tokens, generator=torch.Generator().manual_seed(3))[:1024]
+    xr = x.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu()
+    ir = ids.reshape(-1)[rows.to(gpu)].cpu()
+    p = {n: _deq(engine, n) for n in ("expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up",
+                                      "shared_down")}
+    cfg = engine.config
+    kw = dict(route_weights=cfg.route_weights, shared_scale=cfg.shared_output_scale,
+              routed_scale=cfg.routed_output_scale)
+    table = engine._active_route_table.cpu()
+    ref = O.engine_forward(xr, ir, table, p, **kw)
+    ref8 = O.engine_forward_w8a8(xr, ir, table, p, h_blocks=True, **kw)
+    e16 = O.normwise_rel_err(out16.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu(), ref)
+    e8 = O.normwise_rel_err(out8.reshape(-1, w.hidden)[rows.to(gpu)].float().cpu(), ref8)
+    print(f"fp8 {tokens}: W8A16 {e16:.3e}, W8A8 {e8:.3e}", flush=True)
+    assert e16 <= 5e-2
+    assert e8 <= 2e-2
 
 
 def test_graph_backend_with_fp8_activations(gpu):

@@ -176,6 +176,25 @@ def test_bf16_layer_between_decode_and_c2(gpu, strategy, tokens):
     assert err <= BOUND["bf16"]
 
 
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("tokens", [512, 8192])
+def test_fp32_layer_between_decode_and_c2(gpu, strategy, tokens):
+    """C1's fp32 layer at 512 tokens (64 x 64 down and 64 x 128 gate|up
+    tiles) and 8192 (the large fp32 tiles), every row against the oracle."""
+    from dataclasses import replace
+
+    from complexity_amd import workloads as Wl
+
+    w = replace(Wl.C1, name=f"fp32_{tokens}", batch=max(1, tokens // 2048), seq=min(tokens, 2048))
+    assert w.tokens == tokens
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    engine.routed_strategy = strategy
+    x, ids = Wl.make_hidden(w).to(gpu), Wl.make_token_ids(w).to(gpu)
+    out = _run(engine, x, ids)
+    assert engine._packed.strategy == strategy
+    assert O.normwise_rel_err(out, _oracle(engine, x, ids)) <= BOUND["fp32"]
+
+
 @pytest.mark.parametrize("layer", [0, 7, 15])
 def test_c4_decode_layers(gpu, layer):
     """C4's MLP in greedy decode: 8 tokens, the route table of layer `layer`

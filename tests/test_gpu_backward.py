@@ -418,6 +418,30 @@ def test_c2_bf16_layer_backward_full_size(gpu):
 
 
 @pytest.mark.parametrize("strategy", ["dense", "grouped"])
+@pytest.mark.parametrize("tokens", [2048, 8192])
+def test_c2_shape_layer_backward_mid_sizes(gpu, strategy, tokens):
+    """C2's layer (bf16, Zipf ids) at 2048 and 8192 tokens through autograd,
+    both routed strategies: the weight gradients' split counts and the
+    persistent SwiGLU backward's grid differ from C2's 16384 tokens."""
+    from dataclasses import replace
+
+    from complexity_amd import workloads as Wl
+
+    print(f"layer backward C2 shape {tokens} tokens {strategy}", flush=True)
+    w = replace(Wl.C2, name=f"bf16_{tokens}", batch=tokens // 2048, seq=2048)
+    engine = Wl.build_engine(w, gpu, backend="hip")
+    engine.routed_strategy = strategy
+    x = Wl.make_hidden(w).to(gpu).to(torch.bfloat16)
+    ids = Wl.make_token_ids(w).to(gpu)
+    dout = (torch.randn(x.shape, device=gpu, generator=torch.Generator(device=gpu).manual_seed(tokens)) *
+            0.1).to(torch.bfloat16)
+    _, got = _hip_grads(engine, x, ids, dout)
+    assert engine._packed.strategy == strategy
+    ref = _oracle_grads(engine, x, ids, dout, device=gpu, dtype=torch.float32)
+    _check(got, ref, "bf16")
+
+
+@pytest.mark.parametrize("strategy", ["dense", "grouped"])
 @pytest.mark.parametrize("n", [1, 5, 64, 129])
 def test_layer_backward_decode_sizes(gpu, strategy, n):
     """Few tokens: the data gradient runs on the decode-shape down kernels

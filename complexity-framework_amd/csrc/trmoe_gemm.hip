@@ -1135,6 +1135,12 @@ __device__ __forceinline__ void down_tile(uint32_t id, uint32_t tiles_m, uint32_
     }
 }
 
+// LDS stages of k_down_pp: three with e4m3 weights and bf16 h (48 KiB each;
+// C5's h does not fit the Infinity Cache, and its HBM reads need the longer
+// lead), else two.
+template <bool FP8, bool A8>
+constexpr int kDownPPStages = (FP8 && !A8) ? 3 : 2;
+
 // K4 on the ping-pong main loop (bf16 activations; bf16 or, FP8, e4m3
 // weights expanded at the fragment read; K a multiple of 64): 256x256 tiles
 // over the hidden columns; weight rows past the hidden size load as zero (the
@@ -1196,7 +1202,8 @@ __global__ __launch_bounds__(512, 1) void k_down_pp(DownArgs a) {
     // (group 0 while group 1 multiplies the last stage), with no LDS tile
     // and no copy-out pass
     const bool direct = a.y == nullptr && a.residual == nullptr && a.vec_ok;
-    pp_main<4, Lay>(ap, bp, A8 ? a.K / 128 : a.K / 64, lds, group, wm0, wn0, acc, [&](const f32x16 (&c)[4][2]) {
+    pp_main<4, Lay, kDownPPStages<FP8, A8>>(ap, bp, A8 ? a.K / 128 : a.K / 64, lds, group, wm0, wn0, acc,
+                                             [&](const f32x16 (&c)[4][2]) {
         const int r = lane & 31;
         float cs[2];
 #pragma unroll
@@ -1637,7 +1644,8 @@ static int launch_down_pp(const DownArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)(((a.M + 255) / 256) * ((a.N + 255) / 256)));
     using Lay = std::conditional_t<A8, PPLayoutK8<4, true>, std::conditional_t<FP8, PPLayoutF8<4>, PPLayoutK<4>>>;
     constexpr int kEpi = 256 * (256 * 2 + 16);   // the bf16 output tile, over the stages
-    constexpr int kLds = kEpi > 2 * Lay::kStage ? kEpi : 2 * Lay::kStage;
+    constexpr int kBufs = kDownPPStages<FP8, A8> * Lay::kStage;
+    constexpr int kLds = kEpi > kBufs ? kEpi : kBufs;
     const int st = ensure_lds(k_down_pp<FP8, A8>, kLds);
     if (st) return st;
     hipLaunchKernelGGL((k_down_pp<FP8, A8>), grid, dim3(512), kLds, stream, a);

@@ -672,16 +672,34 @@ struct PPLayoutT {
 // (SC::kOn, pp_mma_f8s): each wave loads the scale dwords of stage t + 1
 // while it multiplies stage t (group 0 with its B refill, group 1 after the
 // phase barrier), and they land by the wait that ends that phase.
-template <int TMW, class Lay, class LA, class LB, class RowsOut, class SC = PPNoScales>
+//
+// NB = 3 (stages that fit three times in LDS: e4m3 weights, 48 KiB): stage
+// t lives in buffer t % 3 and each group requests its operand three stages
+// ahead, A(t + 3) between group 1's MFMAs of stage t and B(t + 2) after
+// group 0's reads of stage t (buffer (t + 2) % 3 held stage t - 1, read by
+// both groups before the barrier that opened the phase).  A load then has
+// about three phases to land instead of one and a half; each wait leaves the
+// newest stage's loads in flight (vmcnt counts in issue order).
+template <int TMW, class Lay, int NB = 2, class LA, class LB, class RowsOut, class SC = PPNoScales>
 __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char* lds, int group, int wm0, int wn0,
                                         f32x16 (&acc)[TMW][2], RowsOut&& rows_out, const SC& sc = SC{}) {
     constexpr int kStage = Lay::kStage;
     constexpr int kBOff = Lay::kBOff;
+    static_assert(NB == 2 || NB == 3, "two or three LDS stages");
+    // one scalar buffer offset per stage (kept opaque, so that t % 3 is not
+    // strength-reduced into per-fragment vector arithmetic)
+    auto buf = [&](int t) -> char* {
+        if constexpr (NB == 2)
+            return lds + (t & 1) * kStage;
+        else
+            return lds + __builtin_amdgcn_readfirstlane((t % 3) * kStage);
+    };
     char* st0 = lds;
     char* st1 = lds + kStage;
     constexpr int kAI = LA::kInstr, kBI = LB::kInstr;
     constexpr bool kF8 = F8Mma<Lay>::value;
     static_assert(kF8 || !SC::kOn, "block scales are for e4m3 stages");
+    static_assert(NB == 2 || !SC::kOn, "block scales take two stages");
 
     std::conditional_t<kF8, i32x8[2][TMW], u32x4[4][TMW]> fa;
     std::conditional_t<kF8, i32x8[2][2], u32x4[4][2]> fb;
@@ -698,7 +716,29 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
     // prologue: stages 0 and 1 requested, stage 0 landed everywhere (and
     // the scales of stage 0, requested before them)
     if constexpr (SC::kOn) sc.template load<TMW>(0, sn);
-    if (group == 1) {
+    if constexpr (NB == 3) {
+        // stages 0..2 requested, stage 0 landed
+        const int pre = nk < 3 ? nk : 3;
+        for (int s = 0; s < pre; ++s) {
+            if (group == 1)
+                ap.issue(s, buf(s));
+            else
+                bp.issue(s, buf(s) + kBOff);
+        }
+        if (pre == 3) {
+            if (group == 1)
+                wait_vmcnt<2 * kAI>();
+            else
+                wait_vmcnt<2 * kBI>();
+        } else if (pre == 2) {
+            if (group == 1)
+                wait_vmcnt<kAI>();
+            else
+                wait_vmcnt<kBI>();
+        } else {
+            wait_vmcnt<0>();
+        }
+    } else if (group == 1) {
         ap.issue(0, st0);
         if (nk > 1) {
             ap.issue(1, st1);
@@ -720,13 +760,13 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
 
     if (group == 0) {
         for (int t = 0; t < nk; ++t) {
-            const char* st = (t & 1) ? st1 : st0;
+            const char* st = buf(t);
             Lay::read(st, wm0, wn0, fa, fb);
             wait_lgkmcnt0();
-            // B(t+1) goes out after this wave's reads: LDS reads issued
+            // B(t+NB-1) goes out after this wave's reads: LDS reads issued
             // behind a wave's own buffer->LDS loads wait for those loads
             __builtin_amdgcn_sched_barrier(0);
-            if (t >= 1 && t + 1 < nk) bp.issue(t + 1, ((t + 1) & 1 ? st1 : st0) + kBOff);
+            if (t >= 1 && t + NB - 1 < nk) bp.issue(t + NB - 1, buf(t + NB - 1) + kBOff);
             if constexpr (SC::kOn)
                 if (t + 1 < nk) sc.template load<TMW>(t + 1, sn);
             pp_barrier();
@@ -734,7 +774,14 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
             mma();
             __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);   // B(t+1) is waited for after the MFMAs, not among them
-            wait_vmcnt<0>();
+            if constexpr (NB == 3) {
+                if (t + 2 < nk)
+                    wait_vmcnt<kBI>();   // B(t+2) may stay in flight
+                else
+                    wait_vmcnt<0>();
+            } else {
+                wait_vmcnt<0>();
+            }
             if constexpr (SC::kOn) sc.take(sn, sa);
             pp_barrier();
         }
@@ -750,10 +797,19 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
         // A(t+2) while t + 2 < nk (two loops rather than a branch around the
         // MFMAs, which would give each branch its own accumulator registers)
         auto step = [&](int t, auto load) {
-            const char* st = (t & 1) ? st1 : st0;
+            const char* st = buf(t);
             Lay::read(st, wm0, wn0, fa, fb);
             wait_lgkmcnt0();
-            wait_vmcnt<0>();   // A(t+1), issued at the start of the previous phase, has landed
+            // A(t+1), issued at the start of the previous phase (NB = 3: two
+            // phases earlier, A(t+2) staying in flight), has landed
+            if constexpr (NB == 3) {
+                if (t + 2 < nk)
+                    wait_vmcnt<kAI>();
+                else
+                    wait_vmcnt<0>();
+            } else {
+                wait_vmcnt<0>();
+            }
             if constexpr (SC::kOn)
                 if (t >= 1) sc.take(sn, sa);   // stage t's scales, requested in the previous phase
             pp_barrier();
@@ -767,9 +823,9 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
                 if constexpr (SC::kOn)
                     pp_mma_load_f8s<TMW>(fa, fb, acc, sa, ap, t + 2, (t & 1) ? st1 : st0);
                 else if constexpr (kF8)
-                    pp_mma_load_f8<TMW>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+                    pp_mma_load_f8<TMW>(fa, fb, acc, ap, t + NB, buf(t));
                 else
-                    pp_mma_load<TMW>(fa, fb, acc, ap, t + 2, (t & 1) ? st1 : st0);
+                    pp_mma_load<TMW>(fa, fb, acc, ap, t + NB, buf(t));
             } else {
                 mma();
             }
@@ -777,7 +833,7 @@ __device__ __forceinline__ void pp_main(const LA& ap, const LB& bp, int nk, char
             pp_barrier();
         };
         int t = 0;
-        for (; t + 2 < nk; ++t) step(t, BoolC<true>{});
+        for (; t + NB < nk; ++t) step(t, BoolC<true>{});
         for (; t < nk; ++t) step(t, BoolC<false>{});
         rows_out(acc);
         wait_lgkmcnt0();

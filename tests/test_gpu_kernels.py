@@ -248,6 +248,33 @@ def test_shared_down_combine_big_tiles(gpu, dtype, N, S, H):
     assert nerr(out[rows], ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("with_res", [False, True])
+@pytest.mark.parametrize("S", [64, 128, 192, 320])
+def test_fp8_down_three_stage_ring_short_k(gpu, S, with_res):
+    """The ping-pong down with e4m3 weights runs three LDS stages; K = 64,
+    128, 192 and 320 give 1, 2, 3 and 5 stages, covering the prologue that
+    requests fewer than three and the loop's last waits.  8197 tokens x 2048
+    hidden = 33 x 8 tiles (a round and a ragged row tile); with the residual
+    the LDS-tile epilogue, without it the stores from the accumulators."""
+    from complexity_amd import ops
+
+    N, H = 8197, 2048
+    h = _rand(N, S, scale=0.5, seed=70 + S).to(torch.bfloat16)
+    wd = _rand(H, S, scale=0.05, seed=71 + S)
+    q, sc = O.quantize_e4m3(wd, 1)
+    pd, ps = ops.pack_linear_down(q.to(gpu), sc.to(gpu))
+    hpad = torch.zeros(N, (S + 127) // 128 * 128, dtype=torch.bfloat16)
+    hpad[:, :S] = h
+    res = _rand(N, H, seed=72 + S).to(torch.bfloat16)
+    out = ops.shared_down_combine(hpad.to(gpu), S, pd, ps, H, None, None, 1, (1.0,), 0.5, 1.0,
+                                  res.to(gpu) if with_res else None).cpu()
+    ref = 0.5 * (h.double() @ O.dequantize_e4m3(q, sc, 1).double().T)
+    if with_res:
+        ref = ref + res.double()
+    row_err = (out.double() - ref).norm(dim=1) / ref.norm(dim=1)
+    assert row_err.max().item() <= TOL[torch.bfloat16], int(row_err.argmax())
+
+
 @pytest.mark.parametrize("with_y,with_res", [(False, False), (False, True), (True, True)])
 def test_shared_down_combine_ping_pong_every_row(gpu, with_y, with_res):
     """bf16 down at H = 896 on the ping-pong kernel (at least 256 tiles of
